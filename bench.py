@@ -1,0 +1,184 @@
+"""Benchmark of the MI355X DSA-layer hot path: one JSON line on stdout.
+
+Workload (N = 1): BASELINE.json configs[1], the FP8 routed MoE of one GPU's TP=4 share
+(hidden 7168, 256 experts top-8 + 1 shared, intermediate 512, E4M3 weights with 128x128
+f32 block scales) at 8 decode rows, as one persistent launch. A step is one launch
+over one batch of 8 rows, on one of ``--layers`` independently seeded layers in turn
+(about 2.8 GB of experts each, so the 256 MB MALL cannot serve the weights). Inputs are
+resident in HBM before the timed region; the timed region is bracketed by
+``torch.cuda.synchronize()`` and measured with HIP events on the launch stream.
+
+``roofline``: algorithmic bytes per launch = every distinct expert the batch actually
+routed to (shared included) x 11,012,736 B + the router 3,670,016 B + the rows in and
+out, over the average launch time, against 8 TB/s. ``cpu_baseline``: the CPU oracle
+(``oracle/moe.py``) on the same workload, one launch worth (8 rows, only the routed
+experts dequantised), on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "µs per decoder layer at 8 rows; MoE/attn achieved HBM TB/s vs 8 TB/s peak"
+HBM_PEAK_GBS = 8000.0
+EXPERT_BYTES = 7_340_032 + 1_792 + 3_670_016 + 896  # w13 + s13 + w2 + s2 of one expert
+ROUTER_BYTES = 3_670_016
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=40)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--rows", type=int, default=8)
+    p.add_argument("--layers", type=int, default=4)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return p.parse_args()
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    f = ROOT / "profiles" / f"{name}_traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get("bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def cpu_baseline(a_cpu, w, ids, rows):
+    """The oracle's MoE block on the host, one launch worth (bounded sample)."""
+    import numpy as np
+    import torch
+
+    from oracle import moe as omoe
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    experts = {}
+    for e in np.unique(ids):
+        e = int(e)
+        experts[e] = (w.w13[e].view(torch.uint8).cpu().numpy(), w.s13[e].cpu().numpy(),
+                      w.w2[e].view(torch.uint8).cpu().numpy(), w.s2[e].cpu().numpy())
+    args = (a_cpu, w.g_post.cpu(), w.w_r.cpu(), w.bias.cpu(), None, None, None, None)
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        omoe.moe_fp8(*args, experts=experts)
+        times.append(time.perf_counter() - t0)
+    us = min(times) * 1e6
+    return {"value": round(us, 1), "unit": "µs per layer (MoE block, 8 rows)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 MoE block of {rows} rows over its {len(experts)} routed experts, "
+                      f"best of {len(times)}; oracle/moe.py f64 GEMVs on dequantised E4M3"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every GPU box here has one GPU, and the sharded "
+              f"path (TP=4 exchanges) is not built; got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from sgl_amd_mono_amd.dsv32 import synthetic
+    from sgl_amd_mono_amd.dsv32.config import DSV32
+    from sgl_amd_mono_amd.dsv32.moe import MoeFp8Op, MoeRouting
+
+    dev = torch.device("cuda:0")
+    rows, L = args.rows, args.layers
+    print(f"bench: generating {L} layers of FP8 experts", file=sys.stderr, flush=True)
+    weights = [synthetic.moe_fp8_weights(dev, seed=100 + i) for i in range(L)]
+    ops = [MoeFp8Op(w, dev, max_rows=rows) for w in weights]
+    inputs = [synthetic.rows_bf16(rows, DSV32.hidden, dev, seed=200 + i) for i in range(L)]
+    outs = [torch.empty(rows, DSV32.hidden, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+
+    # routing of each (layer, batch): the distinct experts a launch streams
+    distinct = []
+    ids0 = None
+    for i in range(L):
+        rt = MoeRouting(torch.empty(rows, DSV32.experts, device=dev),
+                        torch.empty(rows, 9, dtype=torch.int32, device=dev),
+                        torch.empty(rows, 9, device=dev))
+        ops[i].launch(inputs[i], routing=rt, out=outs[i])
+        ops[i].rt.check()
+        ids = rt.ids.cpu().numpy()
+        distinct.append(len(np.unique(ids)))
+        if i == 0:
+            ids0 = ids
+    act_bytes = rows * DSV32.hidden * 2 * 2
+    bytes_per = [d * EXPERT_BYTES + ROUTER_BYTES + act_bytes for d in distinct]
+
+    stream = torch.cuda.current_stream()
+    for s in range(args.warmup):
+        ops[s % L].launch(inputs[s % L], out=outs[s % L])
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for s in range(args.steps):
+        ops[s % L].launch(inputs[s % L], out=outs[s % L])
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    for op in ops:
+        op.rt.check()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    us = ms * 1e3
+    avg_bytes = sum(bytes_per[s % L] for s in range(args.steps)) / args.steps
+    achieved = avg_bytes / (us * 1e-6) / 1e9  # GB/s
+    print(f"bench: {args.steps} launches, {us:.1f} us each (wall {wall * 1e3 / args.steps:.1f} "
+          f"ms/step), distinct experts {distinct}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(inputs[0].cpu(), weights[0], ids0, rows)
+
+    line = {
+        "metric": METRIC,
+        "value": round(us, 2),
+        "unit": "µs",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE configs[1]: FP8 routed MoE, one GPU's TP=4 share, one "
+                        "persistent launch (post-norm, router, top-8 + shared, W8A8 SwiGLU, "
+                        "down, residual)",
+            "rows": rows, "hidden": DSV32.hidden, "experts": DSV32.experts + 1,
+            "inter": DSV32.inter, "layers_rotated": L,
+            "distinct_experts": distinct,
+        },
+        "rows_per_s": round(rows / (us * 1e-6), 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("moe_fp8_r8"),
+            "algorithmic_bytes": int(avg_bytes),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

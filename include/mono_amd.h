@@ -1,0 +1,116 @@
+/* C ABI of the MI355X (gfx950) DSA decoder-layer monokernel library, libmono_amd.so.
+ *
+ * Plain pointers and sizes only: every tensor is a device address the caller owns,
+ * except the scratch and guard blocks a runtime allocates once (sizes from the
+ * *_scratch_bytes functions). Every entry point returns 0 or a negative MONO_E* code
+ * (never throws); mono_last_error() gives the message of the last failure on the
+ * calling thread. Launches are asynchronous on the given HIP stream, do no host
+ * synchronisation, and hold no host state between calls, so they can be captured in
+ * a HIP graph.
+ *
+ * What each entry point replaces in the reference (yuychang/sgl-amd-mono) is cited on
+ * its declaration. */
+#ifndef MONO_AMD_H
+#define MONO_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* an opaque HIP stream (hipStream_t); 0 is the default stream */
+typedef void* mono_stream_t;
+
+#define MONO_OK 0
+#define MONO_E_ARG (-1)     /* bad argument: null pointer, shape or size */
+#define MONO_E_DEVICE (-2)  /* not a gfx950 device, or the grid cannot be co-resident */
+#define MONO_E_LAUNCH (-3)  /* the HIP runtime refused the launch */
+#define MONO_E_FAILED (-4)  /* an earlier launch on this guard block timed out */
+
+/* The guard block: int32 words, runtime owned, zeroed at allocation. Words 0-5 keep
+ * the meaning of the reference's epoch buffer (sgl_amd_mono/common/guard.py:16-30). */
+#define MONO_GUARD_EPOCH 0        /* launches completed on this block (the tag base) */
+#define MONO_GUARD_DEADLINE_LO 1  /* wait deadline, 100 MHz ticks, low word */
+#define MONO_GUARD_DEADLINE_HI 2  /* ... high word */
+#define MONO_GUARD_ERR_DEADLINE 3 /* 1 + the site of the first wait that timed out */
+#define MONO_GUARD_ERR_PEER 4     /* reserved: a failure seen on another GPU */
+#define MONO_GUARD_ERR_FAULT 5    /* set when the timed-out wait was fault-injected */
+#define MONO_GUARD_EXIT 6         /* CTAs of the running launch that finished */
+#define MONO_GUARD_ABORT 7        /* set on a failure: every other wait gives up */
+#define MONO_GUARD_WORDS 16
+
+#define MONO_CLOCK_HZ 100000000 /* s_memrealtime */
+
+/* Wait sites (the value in MONO_GUARD_ERR_DEADLINE is 1 + site). */
+#define MONO_SITE_LOGITS 1   /* routing waits on the router's logits */
+#define MONO_SITE_MID 2      /* a mid quant task waits on up/gate tiles */
+#define MONO_SITE_MQ 3       /* an expert-down tile waits on a quantised mid block */
+
+int mono_version(void);
+const char* mono_last_error(void);
+
+/* Device facts the host checks at load: gfx950, CU count, LDS per CU.
+ * Replaces the co-residency check of sgl_amd_mono/minimax_m31/residency.py:66-85. */
+typedef struct {
+  int32_t cus;
+  int32_t lds_bytes;
+  int32_t is_gfx950;
+  int32_t grid; /* CTAs of a monokernel launch: one per CU */
+} MonoDeviceInfo;
+int mono_device_info(int32_t device, MonoDeviceInfo* out);
+
+/* Write the wait deadline (seconds -> 100 MHz ticks) into a guard block.
+ * Replaces Glm53Runtime.set_deadline (sgl_amd_mono/glm53/gfx950/runner.py:197-204)
+ * and guard.deadline_ticks (sgl_amd_mono/common/guard.py:69-76). */
+int mono_set_deadline(int32_t* guard, double seconds, mono_stream_t stream);
+
+/* Zero a scratch and guard block with a fill kernel (graph safe): required after a
+ * launch failed, since a failed launch leaves hand-off words half written. The
+ * reference stops the process instead (sgl_amd_mono/common/guard.py:91-97). */
+int mono_reset(void* scratch, size_t scratch_bytes, int32_t* guard, mono_stream_t stream);
+
+/* ------------------------------------------------------------------------------
+ * FP8 routed MoE: the FFN half of the layer as one persistent launch.
+ * post-attention RMSNorm -> router GEMV + sigmoid -> top-8 (+ shared expert) ->
+ * W8A8 expert up/gate + SiLU -> mid per-128 quant -> expert down, route weighting
+ * -> out = a + y (the local residual add of the W == 1 reduce).
+ * Replaces stages 8-10 of the reference layer kernel:
+ * sgl_amd_mono/glm53/gfx950/kernel.py:4199-4330 (norm, router, activation quant),
+ * :1575-1629 + :4332-4350 (routing), :4352-4999 (up/gate), :5001-5187 (down), and
+ * the W == 1 peer_reduce branch :1665-1669. */
+typedef struct {
+  int32_t rows;            /* R, 1..16 */
+  int32_t hidden;          /* 7168 */
+  int32_t inter;           /* expert intermediate per GPU: 512 */
+  int32_t experts;         /* routed experts: 256 (the shared one is id 256) */
+  float eps;               /* RMSNorm epsilon */
+  float route_scale;       /* routed_scaling_factor, 2.5 */
+  const void* a;           /* bf16 [R, H]: the stream after attention */
+  void* out;               /* bf16 [R, H]: a + MoE(a) */
+  const void* g_post;      /* bf16 [H]: post-attention norm weight */
+  const void* w_r;         /* bf16 [E, H]: router */
+  const float* bias;       /* f32 [E]: e_score_correction_bias */
+  const uint8_t* w13;      /* E4M3 [E + 1, 2 I, H]: gate rows then up rows */
+  const float* s13;        /* f32 [E + 1, 2 I / 128, H / 128] */
+  const uint8_t* w2;       /* E4M3 [E + 1, H, I] */
+  const float* s2;         /* f32 [E + 1, H / 128, I / 128] */
+  float* y;                /* optional f32 [R, H]: the MoE sum alone */
+  float* scores;           /* optional f32 [R, E]: sigmoid(logit) */
+  int32_t* ids;            /* optional i32 [R, 9]: slot 0 shared (256), then picks */
+  float* weights;          /* optional f32 [R, 9]: slot 0 1.0, then route weights */
+  void* scratch;           /* runtime owned, mono_moe_fp8_scratch_bytes() */
+  int32_t* guard;          /* runtime owned guard block */
+  uint32_t* host_error;    /* optional pinned host word: 1 + failed site */
+  int32_t fault_site;      /* test fault injection: this wait site stalls (0: none) */
+  int32_t fault_after;     /* ... once the epoch reached this many launches */
+} MonoMoeFp8Args;
+
+size_t mono_moe_fp8_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts);
+int mono_moe_fp8_launch(const MonoMoeFp8Args* args, mono_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MONO_AMD_H */

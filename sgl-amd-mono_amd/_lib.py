@@ -1,0 +1,135 @@
+"""ctypes binding of libmono_amd.so, the C ABI declared in ``include/mono_amd.h``.
+
+The library is the only compute path: if it is missing or was built for another
+target, ``lib()`` raises, and nothing falls back to a CPU or PyTorch implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import threading
+from ctypes import c_double, c_float, c_int32, c_size_t, c_uint32, c_void_p
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libmono_amd.so"
+HEADER = PKG.parent / "include" / "mono_amd.h"
+
+MONO_OK = 0
+MONO_E_ARG = -1
+MONO_E_DEVICE = -2
+MONO_E_LAUNCH = -3
+MONO_E_FAILED = -4
+
+# guard block words (mono_amd.h MONO_GUARD_*)
+GUARD_EPOCH = 0
+GUARD_DEADLINE_LO = 1
+GUARD_DEADLINE_HI = 2
+GUARD_ERR_DEADLINE = 3
+GUARD_ERR_PEER = 4
+GUARD_ERR_FAULT = 5
+GUARD_EXIT = 6
+GUARD_ABORT = 7
+GUARD_WORDS = 16
+
+# wait sites (the deadline error word holds 1 + site)
+SITES = {1: "logits", 2: "mid", 3: "mq"}
+
+
+class MonoDeviceInfo(ctypes.Structure):
+    _fields_ = [("cus", c_int32), ("lds_bytes", c_int32), ("is_gfx950", c_int32), ("grid", c_int32)]
+
+
+class MonoMoeFp8Args(ctypes.Structure):
+    """Mirror of ``MonoMoeFp8Args`` in mono_amd.h (same order and types)."""
+
+    _fields_ = [
+        ("rows", c_int32),
+        ("hidden", c_int32),
+        ("inter", c_int32),
+        ("experts", c_int32),
+        ("eps", c_float),
+        ("route_scale", c_float),
+        ("a", c_void_p),
+        ("out", c_void_p),
+        ("g_post", c_void_p),
+        ("w_r", c_void_p),
+        ("bias", c_void_p),
+        ("w13", c_void_p),
+        ("s13", c_void_p),
+        ("w2", c_void_p),
+        ("s2", c_void_p),
+        ("y", c_void_p),
+        ("scores", c_void_p),
+        ("ids", c_void_p),
+        ("weights", c_void_p),
+        ("scratch", c_void_p),
+        ("guard", c_void_p),
+        ("host_error", c_void_p),
+        ("fault_site", c_int32),
+        ("fault_after", c_int32),
+    ]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "mono_version": (c_int32, []),
+    "mono_last_error": (ctypes.c_char_p, []),
+    "mono_device_info": (c_int32, [c_int32, ctypes.POINTER(MonoDeviceInfo)]),
+    "mono_set_deadline": (c_int32, [c_void_p, c_double, c_void_p]),
+    "mono_reset": (c_int32, [c_void_p, c_size_t, c_void_p, c_void_p]),
+    "mono_moe_fp8_scratch_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
+    "mono_moe_fp8_launch": (c_int32, [ctypes.POINTER(MonoMoeFp8Args), c_void_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def header_functions() -> list[str]:
+    """Every function the C header declares (``int name(`` / ``size_t name(`` ...)."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(mono_\w+)\s*\(", text, flags=re.M)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library with typed entry points; raises if it is not built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with `python -m sgl_amd_mono_amd.build` "
+                    "(there is no fallback path)"
+                )
+            dll = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(dll, name)
+                fn.restype, fn.argtypes = res, args
+            _lib = dll
+        return _lib
+
+
+def last_error() -> str:
+    msg = lib().mono_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero C ABI return code."""
+    if rc == MONO_OK:
+        return
+    err = last_error()
+    if rc == MONO_E_ARG:
+        raise ValueError(f"{what}: {err}")
+    raise RuntimeError(f"{what}: {err} (code {rc})")
+
+
+def stream_handle(stream=None) -> int:
+    """The hipStream_t of a torch stream (the current one by default)."""
+    import torch
+
+    s = torch.cuda.current_stream() if stream is None else stream
+    return int(s.cuda_stream)

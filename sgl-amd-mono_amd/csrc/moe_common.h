@@ -1,0 +1,139 @@
+// Routing shared by the MoE launches: sigmoid + bias top-k with lowest-id ties, the
+// slot tables (slot 0 the shared expert) and the distinct-expert list every CTA
+// derives identically from them.
+#pragma once
+
+#include "mono_device.h"
+
+namespace mono {
+
+constexpr int MOE_MAXR = 16;   // rows a MoE launch takes
+constexpr int MOE_NEXP = 256;  // routed experts
+constexpr int MOE_TOPK = 8;
+constexpr int MOE_SLOTS = MOE_TOPK + 1;
+constexpr int MOE_SHARED = 256;  // the shared expert's id
+constexpr int MOE_NDIST = MOE_NEXP + 1;
+
+// LDS routing state of one CTA
+struct RouteLds {
+  int32_t id[MOE_MAXR][MOE_SLOTS];  // slot 0: shared, then picks in selection order
+  float w[MOE_MAXR][MOE_SLOTS];     // route weights (slot 0: 1)
+  uint32_t mask[MOE_NDIST];         // per expert id: bit t = row t routed to it
+  int32_t uexp[MOE_NDIST];          // distinct experts: u = 0 the shared, then ascending
+  uint32_t umask[MOE_NDIST];
+  int32_t nd;
+};
+
+// The top-k of one row, called by one whole wave. `score_of(i)` gives this lane's
+// i-th candidate score (expert lane + 64 i) and `bias` the matching biases.
+// Order: radix key of f32(score + bias) descending, then lower expert id
+// (sgl_amd_mono/glm53/gfx950/kernel.py:1575-1629). Writes slots 1..8 of row t into
+// `rl` and sets the row's bit in rl.mask. Returns nothing; weights are
+// raw / (sum of the 8 raw, in pick order) * route_scale.
+__device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], const float (&bs)[4],
+                                 float route_scale, float* scores_out, int32_t* ids_out,
+                                 float* weights_out) {
+  const int l = lane_id();
+  uint64_t cand[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = l + 64 * i;
+    const uint32_t key = radix_key(sc[i] + bs[i]);
+    cand[i] = ((uint64_t)key << 32) | (uint32_t)(0xFFFF - e);
+  }
+  float picked_raw[MOE_TOPK];
+  int picked_id[MOE_TOPK];
+#pragma unroll
+  for (int r = 0; r < MOE_TOPK; ++r) {
+    uint64_t mine = cand[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) mine = cand[i] > mine ? cand[i] : mine;
+    const uint64_t best = wave_max_u64(mine);
+    const int e = 0xFFFF - (int)(uint32_t)(best & 0xFFFFFFFFu);
+    // the owner lane of expert e knows its raw score
+    const int owner = e & 63, slot = e >> 6;
+    float raw = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i == slot) raw = sc[i];
+    raw = __shfl(raw, owner, WAVE);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (cand[i] == best) cand[i] = 0;  // 0 is below every live candidate
+    picked_raw[r] = raw;
+    picked_id[r] = e;
+  }
+  float tot = 0.f;
+#pragma unroll
+  for (int r = 0; r < MOE_TOPK; ++r) tot += picked_raw[r];
+  if (l < MOE_TOPK) {
+    float raw = 0.f;
+    int e = 0;
+#pragma unroll
+    for (int r = 0; r < MOE_TOPK; ++r)
+      if (r == l) {
+        raw = picked_raw[r];
+        e = picked_id[r];
+      }
+    const float w = raw / tot * route_scale;
+    rl.id[t][1 + l] = e;
+    rl.w[t][1 + l] = w;
+    atomicOr(&rl.mask[e], 1u << t);
+    if (ids_out) ids_out[t * MOE_SLOTS + 1 + l] = e;
+    if (weights_out) weights_out[t * MOE_SLOTS + 1 + l] = w;
+  }
+  if (l == 0) {
+    rl.id[t][0] = MOE_SHARED;
+    rl.w[t][0] = 1.f;
+    if (ids_out) ids_out[t * MOE_SLOTS] = MOE_SHARED;
+    if (weights_out) weights_out[t * MOE_SLOTS] = 1.f;
+  }
+  if (scores_out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) scores_out[t * MOE_NEXP + l + 64 * i] = sc[i];
+  }
+}
+
+// Compact rl.mask into the distinct list (one whole wave): u = 0 the shared expert,
+// then routed ids ascending.
+__device__ inline void build_distinct(RouteLds& rl, int rows) {
+  const int l = lane_id();
+  uint32_t m[4];
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = rl.mask[4 * l + i];
+    cnt += m[i] != 0;
+  }
+  // inclusive scan of cnt over lanes
+  int inc = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int o = __shfl_up(inc, d, WAVE);
+    if (l >= d) inc += o;
+  }
+  int pos = 1 + inc - cnt;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (m[i]) {
+      rl.uexp[pos] = 4 * l + i;
+      rl.umask[pos] = m[i];
+      ++pos;
+    }
+  if (l == 63) rl.nd = 1 + inc;
+  if (l == 0) {
+    rl.uexp[0] = MOE_SHARED;
+    rl.umask[0] = rows >= 32 ? 0xFFFFFFFFu : ((1u << rows) - 1u);
+  }
+}
+
+// route weight of row t for expert e (0 when e is not among its slots)
+__device__ inline float route_weight(const RouteLds& rl, int t, int e) {
+  float w = 0.f;
+#pragma unroll
+  for (int s = 0; s < MOE_SLOTS; ++s)
+    if (rl.id[t][s] == e) w = rl.w[t][s];
+  return w;
+}
+
+}  // namespace mono

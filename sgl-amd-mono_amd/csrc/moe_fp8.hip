@@ -1,0 +1,541 @@
+// FP8 routed MoE as one persistent gfx950 launch (the FFN half of the DSA layer).
+//
+// Stages, every CTA in order (task t of a stage runs on CTA t mod grid):
+//   0  RMSNorm of the R rows (every CTA, from L2), per-128 E4M3 quant of its wave's
+//      K slice straight into MFMA B-operand registers, and the router logit of its
+//      expert(s), published as (value, tag) pairs.
+//   1  routing: each CTA polls the 256 x R logits and runs sigmoid + bias top-8
+//      itself (one wave a row), then compacts the distinct experts, shared first.
+//   2  up/gate: task (u, c) = 16 gate + 16 up rows of distinct expert u over all of
+//      K, the 8 waves splitting K. W8A8 16x16x128 MFMA per 128-chunk, then the
+//      chunk's weight block scale x activation scale into the f32 accumulator.
+//      Weight chunks stream through a register ring that already holds the next
+//      task's chunks while this one finishes. mid = silu(g) * u goes out as tagged
+//      pairs, so no wave ever drains its loads to publish.
+//   3  mid quant: task (u, kb) polls a 128-block of mid, quantises it per row to
+//      E4M3 with coefficient scale * route weight, publishes, then a ready tag.
+//   4  down: task f = 32 output rows over every distinct expert (wave w takes
+//      experts u = w mod 8), prefetching the next expert's weights, then a fixed
+//      order reduction across waves and out = bf16(a + y).
+// The tag of a launch is the guard block's epoch + 1; the last CTA out advances the
+// epoch. Every wait polls under the guard's deadline.
+//
+// Reference: sgl_amd_mono/glm53/gfx950/kernel.py:4199-4330 (router + quant),
+// :1575-1629 (route_top8), :4352-4999 (up/gate), :5001-5187 (down), :1440-1450
+// (quant_scaled), :1665-1669 (W == 1 residual add).
+#include <hip/hip_runtime.h>
+
+#include "moe_common.h"
+#include "mono_abi.h"
+
+namespace mono {
+
+template <int H, int I>
+struct MoeFp8Geom {
+  static constexpr int WAVES = 16;
+  static constexpr int THREADS = WAVES * WAVE;
+  static constexpr int QW = 8;             // waves that own a K slice (stage 0, B operands)
+  static constexpr int NKC = H / 128;      // 128-K chunks of the hidden dim
+  static constexpr int KCW = NKC / QW;     // chunks a K slice holds
+  static constexpr int NUG = I / 16;       // up/gate tasks per expert
+  static constexpr int NKB = I / 128;      // 128-blocks of the intermediate
+  static constexpr int DNT = 32;           // output rows of a down task
+  static constexpr int NDN = H / DNT;
+  static_assert(NKC % QW == 0, "hidden must split into 8 slices of 128-chunks");
+  static_assert(I % 128 == 0, "intermediate must be whole 128-blocks");
+  static_assert(H % 128 == 0, "hidden must be whole 128-blocks");
+
+  // scratch layout (bytes)
+  static constexpr size_t OFF_LOGIT = 0;
+  static constexpr size_t SZ_LOGIT = (size_t)MOE_MAXR * MOE_NEXP * 8;
+  static constexpr size_t OFF_MID = OFF_LOGIT + SZ_LOGIT;
+  static constexpr size_t SZ_MID = (size_t)MOE_NDIST * MOE_MAXR * I * 8;
+  static constexpr size_t OFF_MQ = OFF_MID + SZ_MID;
+  static constexpr size_t SZ_MQ = (size_t)MOE_NDIST * MOE_MAXR * I;
+  static constexpr size_t OFF_MCOEF = OFF_MQ + SZ_MQ;
+  static constexpr size_t SZ_MCOEF = (size_t)MOE_NDIST * MOE_MAXR * NKB * 4;
+  static constexpr size_t OFF_READY = OFF_MCOEF + SZ_MCOEF;
+  static constexpr size_t SZ_READY = (size_t)MOE_NDIST * NKB * 4;
+  static constexpr size_t BYTES = (OFF_READY + SZ_READY + 255) & ~(size_t)255;
+};
+
+struct MoeFp8Params {
+  int rows;
+  float eps, route_scale;
+  const uint16_t* a;
+  uint16_t* out;
+  const uint16_t* g_post;
+  const uint16_t* w_r;
+  const float* bias;
+  const uint8_t* w13;
+  const float* s13;
+  const uint8_t* w2;
+  const float* s2;
+  float* y;
+  float* scores;
+  int32_t* ids;
+  float* weights;
+  uint8_t* scratch;
+  int32_t* guard;
+  uint32_t* host_err;
+  int fault_site, fault_after;
+};
+
+// bf16 x 8 in a dword4 -> 8 f32
+__device__ inline void bf16x8(v4i v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo((uint32_t)v[i]);
+    f[2 * i + 1] = bf16_hi((uint32_t)v[i]);
+  }
+}
+
+__device__ inline v8i cat8(v4i a, v4i b) {
+  return v8i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+template <int H, int I>
+__global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
+  using G = MoeFp8Geom<H, I>;
+  constexpr int KCW = G::KCW, NUG = G::NUG, NKB = G::NKB, QW = G::QW;
+  const int tid = threadIdx.x, l = tid & 63;
+  // the wave index in an SGPR: every per-wave address term stays scalar
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = l & 15, grp = l >> 4;  // MFMA column (row of the batch) and K group
+  const int half = w / QW, wq = w % QW;  // gate / up (or row group) half, K slice
+  const int R = p.rows;
+  const int nblk = gridDim.x, b = blockIdx.x;
+
+  __shared__ RouteLds rl;
+  // the E4M3 activations as each lane's MFMA B operand: [slice][chunk][half][lane]
+  __shared__ v4i xq_lds[QW * KCW * 2 * 64];
+  __shared__ float xs_lds[QW * KCW][16];  // activation block scale per (chunk, row)
+  __shared__ v4f red[G::WAVES][64];
+  __shared__ float red_small[2][QW][16];
+  __shared__ float rstd_s[MOE_MAXR];
+  __shared__ uint32_t tag_s;
+  __shared__ int ok_s;
+
+  uint64_t* logit_pairs = reinterpret_cast<uint64_t*>(p.scratch + G::OFF_LOGIT);
+  uint64_t* mid_pairs = reinterpret_cast<uint64_t*>(p.scratch + G::OFF_MID);
+  uint8_t* mq = p.scratch + G::OFF_MQ;
+  float* mcoef = reinterpret_cast<float*>(p.scratch + G::OFF_MCOEF);
+  uint32_t* ready = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
+
+  if (tid == 0) tag_s = ld_dev(reinterpret_cast<uint32_t*>(p.guard) + MONO_GUARD_EPOCH) + 1u;
+  for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
+  __syncthreads();
+  const uint32_t tag = tag_s;
+  Guard guard;
+  guard.init(p.guard, p.host_err, p.fault_site, tag - 1u, (uint32_t)p.fault_after);
+  bool ok = true;
+
+  const __amdgpu_buffer_rsrc_t ra = rsrc(p.a, (uint32_t)(R * H * 2));
+  const __amdgpu_buffer_rsrc_t rg = rsrc(p.g_post, H * 2);
+  const __amdgpu_buffer_rsrc_t rw = rsrc(p.w_r, (uint32_t)MOE_NEXP * H * 2);
+
+  // ---------------------------------------------------------------- stage 0
+  // pass 1 (waves 0-7): sum of squares of row t over this slice (rows >= R load 0)
+  if (half == 0) {
+    float ss = 0.f;
+#pragma unroll 1
+    for (int j = 0; j < KCW; ++j) {
+      const uint32_t off = (uint32_t)(t * H + (wq * KCW + j) * 128 + 32 * grp) * 2;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float f[8];
+        bf16x8(ld16<CP_NONE>(ra, off + 16 * q), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+      }
+    }
+    ss += xor_f(ss, 16);
+    ss += xor_f(ss, 32);
+    if (grp == 0) red_small[0][wq][t] = ss;
+  }
+  __syncthreads();
+  if (tid < MOE_MAXR) {
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < QW; ++i) tot += red_small[0][i][tid];
+    rstd_s[tid] = tid < R ? 1.0f / sqrtf(tot / (float)H + p.eps) : 0.f;
+  }
+  __syncthreads();
+  const float rstd = rstd_s[t];
+
+  // pass 2 (waves 0-7): xn = a * rstd * g; E4M3 B operands + scales; router dot
+  // products of this CTA's experts (b, b + grid, ...)
+  for (int e = b, first = 1; first || e < MOE_NEXP; e += nblk, first = 0) {
+    float rpart = 0.f;
+    if (half == 0) {
+#pragma unroll 1
+      for (int j = 0; j < KCW; ++j) {
+        const int k0 = (wq * KCW + j) * 128 + 32 * grp;
+        float xn[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float fa[8], fg[8];
+          bf16x8(ld16<CP_NONE>(ra, (uint32_t)(t * H + k0) * 2 + 16 * q), fa);
+          bf16x8(ld16<CP_NONE>(rg, (uint32_t)k0 * 2 + 16 * q), fg);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xn[8 * q + i] = fa[i] * rstd * fg[i];
+        }
+        if (first) {
+          float am = 0.f;
+#pragma unroll
+          for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(xn[i]));
+          am = fmaxf(am, xor_f(am, 16));
+          am = fmaxf(am, xor_f(am, 32));
+          const bool nz = am > 0.f;
+          if (grp == 0) xs_lds[wq * KCW + j][t] = nz ? am * INV_FP8_MAX : 1.f;
+          const float inv = nz ? FP8_MAX / am : 1.f;
+          v4i q0, q1;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            q0[d] = (int)pack_fp8x4(clamp_fp8(xn[4 * d] * inv), clamp_fp8(xn[4 * d + 1] * inv),
+                                    clamp_fp8(xn[4 * d + 2] * inv),
+                                    clamp_fp8(xn[4 * d + 3] * inv));
+            q1[d] = (int)pack_fp8x4(clamp_fp8(xn[16 + 4 * d] * inv),
+                                    clamp_fp8(xn[17 + 4 * d] * inv),
+                                    clamp_fp8(xn[18 + 4 * d] * inv),
+                                    clamp_fp8(xn[19 + 4 * d] * inv));
+          }
+          xq_lds[((wq * KCW + j) * 2 + 0) * 64 + l] = q0;
+          xq_lds[((wq * KCW + j) * 2 + 1) * 64 + l] = q1;
+        }
+        if (e < MOE_NEXP) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float fw[8];
+            bf16x8(ld16<CP_NT>(rw, (uint32_t)(e * H + k0) * 2 + 16 * q), fw);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rpart += bf16_round(xn[8 * q + i]) * fw[i];
+          }
+        }
+      }
+      rpart += xor_f(rpart, 16);
+      rpart += xor_f(rpart, 32);
+    }
+    if (e >= MOE_NEXP) break;  // CTA-uniform
+    __syncthreads();
+    if (half == 0 && grp == 0) red_small[1][wq][t] = rpart;
+    __syncthreads();
+    if (tid < R) {
+      float lg = 0.f;
+#pragma unroll
+      for (int i = 0; i < QW; ++i) lg += red_small[1][i][tid];
+      st_dev64(&logit_pairs[tid * MOE_NEXP + e], pair(__float_as_uint(lg), tag));
+    }
+  }
+
+  // ---------------------------------------------------------------- stage 1
+  // one wave a row: poll the row's 256 logits, sigmoid, top-8
+  if (w < R) {
+    const int row = w;
+    uint64_t pr[4];
+    ok = wait_until(guard, MONO_SITE_LOGITS, [&]() {
+      bool all = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = ld_dev64(&logit_pairs[row * MOE_NEXP + l + 64 * i]);
+        all &= (uint32_t)(pr[i] >> 32) == tag;
+      }
+      return __all(all);
+    });
+    if (ok) {
+      float sc[4], bs[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lg = __uint_as_float((uint32_t)pr[i]);
+        sc[i] = 1.0f / (1.0f + expf(-lg));
+        bs[i] = p.bias[l + 64 * i];
+      }
+      const bool out0 = b == 0;
+      route_row(rl, row, sc, bs, p.route_scale, out0 ? p.scores : nullptr,
+                out0 ? p.ids : nullptr, out0 ? p.weights : nullptr);
+    }
+  }
+  __syncthreads();
+  if (w == 0) build_distinct(rl, R);
+  ok = cta_ok(ok, guard, ok_s);
+  const int nd = rl.nd;
+
+  // ---------------------------------------------------------------- stage 2
+  // waves 0-7: the 16 gate rows of the task, waves 8-15 the 16 up rows; wave wq's
+  // K slice is chunks [KCW wq, KCW (wq + 1)). Its ring holds one task's KCW chunks:
+  // a slot is refilled with the next task's chunk as soon as its MFMA issued.
+  {
+    const int ntask = ok ? nd * NUG : 0;
+    v4i ring[KCW][2];
+    const uint32_t vo = (uint32_t)(t * H + 32 * grp);  // this lane's row and K group
+    // a task past the end issues through an empty buffer: its loads return 0 with no
+    // memory traffic, so the refill needs no branch
+    auto task_src = [&](int task, uint32_t& so) {
+      const bool live = task < ntask;
+      const int tk = live ? task : 0;
+      const int u = tk / NUG, cc = tk % NUG;
+      const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
+      so = (uint32_t)((half * I + cc * 16) * H + wq * KCW * 128);
+      return rsrc(p.w13 + (size_t)e * (2 * I) * H, live ? 2u * I * H : 0u);
+    };
+    int task = b;
+    {
+      uint32_t so;
+      const __amdgpu_buffer_rsrc_t r = task_src(task, so);
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) {
+        ring[j][0] = ld16s<CP_NT>(r, vo, so + j * 128);
+        ring[j][1] = ld16s<CP_NT>(r, vo + 16, so + j * 128);
+      }
+    }
+    while (task < ntask) {
+      const int u = task / NUG, cc = task % NUG;
+      const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
+      const uint32_t mask = rl.umask[u];
+      const float tok_on = ((mask >> t) & 1u) ? 1.f : 0.f;
+      const int sbase = __builtin_amdgcn_readfirstlane(
+          (e * (2 * I / 128) + (half * I + cc * 16) / 128) * (H / 128) + wq * KCW);
+      const int next = task + nblk;
+      uint32_t son;
+      const __amdgpu_buffer_rsrc_t rn = task_src(next, son);
+      // B operands and scales: the same LDS words every task, read through an opaque
+      // base so they are not hoisted out of the loop (they would hold 56 VGPRs)
+      const int xb = opaque_v(wq * KCW * 2 * 64 + l);
+      const int sb = opaque_v(wq * KCW * 16 + t);
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) {
+        const v8i B = cat8(xq_lds[xb + j * 128], xq_lds[xb + j * 128 + 64]);
+        const v4f zero = {0.f, 0.f, 0.f, 0.f};
+        const v4f d = mfma_fp8(cat8(ring[j][0], ring[j][1]), B, zero);
+        // the slot is free once its MFMA issued: refill it with the next task's chunk
+        ring[j][0] = ld16s<CP_NT>(rn, vo, son + j * 128);
+        ring[j][1] = ld16s<CP_NT>(rn, vo + 16, son + j * 128);
+        acc += d * (sld(p.s13, sbase + j) * ((&xs_lds[0][0])[sb + j * 16] * tok_on));
+        // one chunk per scheduling region keeps the live set to the ring
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      red[w][l] = acc;
+      __syncthreads();
+      if (tid < 256) {
+        const int row = tid & 15, tok = tid >> 4;  // adjacent threads, adjacent features
+        const int L = tok + 16 * (row >> 2), v = row & 3;
+        float gs = 0.f, us = 0.f;
+#pragma unroll
+        for (int i = 0; i < QW; ++i) {
+          gs += red[i][L][v];
+          us += red[QW + i][L][v];
+        }
+        if (tok < R && ((mask >> tok) & 1u)) {
+          const float m = gs / (1.0f + expf(-gs)) * us;
+          st_dev64(&mid_pairs[((size_t)u * MOE_MAXR + tok) * I + cc * 16 + row],
+                   pair(__float_as_uint(m), tag));
+        }
+      }
+      __syncthreads();
+      task = next;
+    }
+  }
+
+  // ---------------------------------------------------------------- stage 3
+  // mid quant: task (u, kb), one wave a row. Trip counts stay CTA-uniform (barriers
+  // per task); a failed wait only skips work.
+  {
+    const int nq = ok ? nd * NKB : 0;
+    for (int q = b; q < nq; q += nblk) {
+      const int u = q / NKB, kb = q % NKB;
+      const int e = rl.uexp[u];
+      const uint32_t mask = rl.umask[u];
+      const int tok = w;
+      if (tok < R && ((mask >> tok) & 1u) && ok) {
+        const size_t base = ((size_t)u * MOE_MAXR + tok) * I + kb * 128 + 2 * l;
+        uint64_t p0 = 0, p1 = 0;
+        ok = wait_until(guard, MONO_SITE_MID, [&]() {
+          p0 = ld_dev64(&mid_pairs[base]);
+          p1 = ld_dev64(&mid_pairs[base + 1]);
+          return __all((uint32_t)(p0 >> 32) == tag && (uint32_t)(p1 >> 32) == tag);
+        });
+        if (ok) {
+          const float v0 = __uint_as_float((uint32_t)p0), v1 = __uint_as_float((uint32_t)p1);
+          const float am = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+          const bool nz = am > 0.f;
+          const float sc = nz ? am * INV_FP8_MAX : 1.f;
+          const float inv = nz ? FP8_MAX / am : 1.f;
+          const uint32_t h = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                                 clamp_fp8(v0 * inv), clamp_fp8(v1 * inv), 0, false) &
+                             0xFFFFu;
+          const uint32_t hn = xor_u(h, 1);
+          if ((l & 1) == 0)
+            st_dev(reinterpret_cast<uint32_t*>(mq + ((size_t)u * MOE_MAXR + tok) * I + kb * 128 +
+                                               2 * l),
+                   h | (hn << 16));
+          if (l == 0)
+            st_devf(&mcoef[((size_t)u * MOE_MAXR + tok) * NKB + kb],
+                    sc * route_weight(rl, tok, e));
+        }
+      }
+      drain();
+      const bool all_ok = cta_ok(ok, guard, ok_s);
+      if (tid == 0 && all_ok) st_dev(&ready[u * NKB + kb], tag);
+    }
+    ok = cta_ok(ok, guard, ok_s);
+  }
+
+  // ---------------------------------------------------------------- stage 4
+  // down: task f = output rows [32 f, 32 f + 32); waves 0-7 the first 16 rows, 8-15
+  // the next 16; wave wq takes experts u = wq, wq + 8, ... and prefetches the next
+  {
+    const int ntask = ok ? G::NDN : 0;
+    const __amdgpu_buffer_rsrc_t rmq = rsrc(mq, (uint32_t)G::SZ_MQ);
+    for (int f = b; f < ntask; f += nblk) {
+      const int r0 = f * G::DNT;
+      const int rg0 = r0 + 16 * half;
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      v4i buf[2][NKB][2];
+      auto issue_dn = [&](int u, int s) {
+        const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
+        const __amdgpu_buffer_rsrc_t r = rsrc(p.w2 + (size_t)e * H * I, (uint32_t)H * I);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const uint32_t o = (uint32_t)(rg0 + t) * I + kb * 128 + 32 * grp;
+          buf[s][kb][0] = ld16<CP_NT>(r, o);
+          buf[s][kb][1] = ld16<CP_NT>(r, o + 16);
+        }
+      };
+      // expert u from slot s: wait for its quantised mid, MFMA into acc
+      auto consume_dn = [&](int u, int s) -> bool {
+        const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
+        const uint32_t mask = rl.umask[u];
+        if (!wait_until(guard, MONO_SITE_MQ, [&]() {
+              const uint32_t rv = l < NKB ? ld_dev(&ready[u * NKB + l]) : tag;
+              return __all(rv == tag);
+            }))
+          return false;
+        const bool on = t < R && ((mask >> t) & 1u);
+        const size_t mrow = ((size_t)u * MOE_MAXR + t) * I;
+        const int s2b = __builtin_amdgcn_readfirstlane((e * (H / 128) + rg0 / 128) * (I / 128));
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const uint32_t mo = (uint32_t)(mrow + kb * 128 + 32 * grp);
+          v4i b0 = ld16<CP_DEV>(rmq, mo), b1 = ld16<CP_DEV>(rmq, mo + 16);
+          const float cf = on ? __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
+                                    &mcoef[((size_t)u * MOE_MAXR + t) * NKB + kb])))
+                              : 0.f;
+          if (!on) {  // rows not routed here: stale bytes could be NaN codes
+            b0 = v4i{0, 0, 0, 0};
+            b1 = v4i{0, 0, 0, 0};
+          }
+          const v4f zero = {0.f, 0.f, 0.f, 0.f};
+          acc += mfma_fp8(cat8(buf[s][kb][0], buf[s][kb][1]), cat8(b0, b1), zero) *
+                 (sld(p.s2, s2b + kb) * cf);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        return true;
+      };
+      // experts u = wq, wq + 8, ...: slot 0 holds even steps, slot 1 odd ones
+      int u = wq;
+      if (u < nd) issue_dn(u, 0);
+      while (u < nd && ok) {
+        if (u + QW < nd) issue_dn(u + QW, 1);
+        ok = consume_dn(u, 0);
+        u += QW;
+        if (u >= nd || !ok) break;
+        if (u + QW < nd) issue_dn(u + QW, 0);
+        ok = consume_dn(u, 1);
+        u += QW;
+      }
+      // fixed-order reduction over each half's 8 waves, then the residual add
+      red[w][l] = acc;
+      __syncthreads();
+      if (tid < 512) {
+        const int row = tid & 31, tok = tid >> 5;  // 32 rows x 16 columns, rows fastest
+        const int h = row >> 4, rr = row & 15;
+        const int L = tok + 16 * (rr >> 2), v = rr & 3;
+        float ys = 0.f;
+#pragma unroll
+        for (int i = 0; i < QW; ++i) ys += red[h * QW + i][L][v];
+        if (tok < R && ok) {
+          const int col = r0 + row;
+          const float av = bf16_lo(p.a[tok * H + col]);
+          p.out[tok * H + col] = (uint16_t)bf16_bits(av + ys);
+          if (p.y) p.y[tok * H + col] = ys;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---------------------------------------------------------------- exit
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
+    drain();
+    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
+    if (old == (uint32_t)nblk - 1u) {
+      st_dev(gw + MONO_GUARD_EXIT, 0u);
+      st_dev(gw + MONO_GUARD_EPOCH, tag);
+    }
+  }
+}
+
+}  // namespace mono
+
+using namespace mono;
+
+extern "C" size_t mono_moe_fp8_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts) {
+  if (experts != MOE_NEXP) return 0;
+  if (hidden == 7168 && inter == 512) return MoeFp8Geom<7168, 512>::BYTES;
+  return 0;
+}
+
+extern "C" int mono_moe_fp8_launch(const MonoMoeFp8Args* a, mono_stream_t stream) {
+  if (!a) return set_error(MONO_E_ARG, "mono_moe_fp8_launch: null args");
+  if (a->rows < 1 || a->rows > MOE_MAXR)
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: rows must be 1..16");
+  if (a->experts != MOE_NEXP)
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: experts must be 256");
+  if (!a->a || !a->out || !a->g_post || !a->w_r || !a->bias || !a->w13 || !a->s13 || !a->w2 ||
+      !a->s2 || !a->scratch || !a->guard)
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: null tensor");
+  MoeFp8Params p;
+  p.rows = a->rows;
+  p.eps = a->eps;
+  p.route_scale = a->route_scale;
+  p.a = static_cast<const uint16_t*>(a->a);
+  p.out = static_cast<uint16_t*>(a->out);
+  p.g_post = static_cast<const uint16_t*>(a->g_post);
+  p.w_r = static_cast<const uint16_t*>(a->w_r);
+  p.bias = a->bias;
+  p.w13 = a->w13;
+  p.s13 = a->s13;
+  p.w2 = a->w2;
+  p.s2 = a->s2;
+  p.y = a->y;
+  p.scores = a->scores;
+  p.ids = a->ids;
+  p.weights = a->weights;
+  p.scratch = static_cast<uint8_t*>(a->scratch);
+  p.guard = a->guard;
+  p.host_err = nullptr;
+  if (a->host_error) {
+    void* dptr = nullptr;
+    if (hipHostGetDevicePointer(&dptr, a->host_error, 0) != hipSuccess || !dptr)
+      return set_error(MONO_E_ARG, "mono_moe_fp8_launch: host_error is not pinned host memory");
+    p.host_err = static_cast<uint32_t*>(dptr);
+  }
+  p.fault_site = a->fault_site;
+  p.fault_after = a->fault_after;
+  int grid = 0;
+  int rc = monokernel_grid(&grid);
+  if (rc) return rc;
+  if (a->hidden == 7168 && a->inter == 512) {
+    rc = check_coresident(moe_fp8_kernel<7168, 512>, 1024, 0,
+                          "mono_moe_fp8_launch: one 1024-thread CTA per CU does not fit");
+    if (rc) return rc;
+    hipLaunchKernelGGL((moe_fp8_kernel<7168, 512>), dim3(grid), dim3(1024), 0,
+                       (hipStream_t)stream, p);
+  } else {
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: unsupported hidden/inter");
+  }
+  return check_launch("mono_moe_fp8_launch");
+}

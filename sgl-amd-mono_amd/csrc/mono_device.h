@@ -1,0 +1,246 @@
+// Device helpers shared by the gfx950 monokernel stages.
+//
+// Everything here is CDNA4 (gfx950) specific: wave64, the f8f6f4 matrix cores, buffer
+// resources with CDNA cache-policy bits, and the 100 MHz s_memrealtime clock.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mono_amd.h"
+
+namespace mono {
+
+typedef int32_t v8i __attribute__((ext_vector_type(8)));
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v2i __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+constexpr float FP8_MAX = 448.0f;
+constexpr float INV_FP8_MAX = 1.0f / 448.0f;
+
+// ------------------------------------------------------------------ cache policies
+// aux bits of the buffer intrinsics on gfx950: sc0 = 1, nt = 2, sc1 = 16
+constexpr int CP_NONE = 0;
+constexpr int CP_NT = 2;    // streamed once: weights
+constexpr int CP_DEV = 16;  // device coherent (sc1): mailboxes written by other CTAs
+
+// raw buffer resource over [base, base + bytes); loads past the end return 0
+__device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+template <int CP>
+__device__ inline v4i ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP);
+}
+// per-lane offset `voff` (VGPR) + wave-uniform offset `soff` (SGPR)
+template <int CP>
+__device__ inline v4i ld16s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CP);
+}
+// a wave-uniform read through the constant address space: an s_load, counted by
+// lgkmcnt, so waiting for it never waits on the vector loads in flight
+template <class T>
+__device__ inline T sld(const T* p, int i) {
+  typedef const __attribute__((address_space(4))) T* cptr;
+  return ((cptr)(p))[i];
+}
+
+// an int the compiler cannot see through (kept in a VGPR): indexing LDS from it keeps
+// a load inside its loop while the constant parts fold into the instruction offset
+__device__ inline int opaque_v(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+template <int CP>
+__device__ inline v2i ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP);
+}
+template <int CP>
+__device__ inline int32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP);
+}
+
+// device-coherent (sc1) scalar-width accesses through the memory model
+__device__ inline uint32_t ld_dev(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t ld_dev64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_dev64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_devf(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t add_dev(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// wait until this wave's earlier memory operations (sc1 stores included) completed
+__device__ inline void drain() { __builtin_amdgcn_s_waitcnt(0); }
+
+// (value, tag) pair: one 8-byte store publishes a 32-bit word with its launch tag
+__device__ inline uint64_t pair(uint32_t v, uint32_t tag) {
+  return (uint64_t)v | ((uint64_t)tag << 32);
+}
+
+// ------------------------------------------------------------------ wave ops
+// a zero the compiler cannot see through: indexing with it keeps a load inside its loop
+__device__ inline int opaque_zero() {
+  int z;
+  asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+  return z;
+}
+
+__device__ inline int lane_id() { return __lane_id(); }
+
+__device__ inline float xor_f(float v, int m) { return __shfl_xor(v, m, WAVE); }
+__device__ inline uint32_t xor_u(uint32_t v, int m) {
+  return (uint32_t)__shfl_xor((int)v, m, WAVE);
+}
+
+template <int MAXM = 32>
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m <= MAXM; m <<= 1) v += xor_f(v, m);
+  return v;
+}
+template <int MAXM = 32>
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int m = 1; m <= MAXM; m <<= 1) v = fmaxf(v, xor_f(v, m));
+  return v;
+}
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 1; m <= 32; m <<= 1) {
+    uint32_t lo = xor_u((uint32_t)v, m), hi = xor_u((uint32_t)(v >> 32), m);
+    uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// ------------------------------------------------------------------ number formats
+// f32 -> bf16 bits, round to nearest even (finite inputs)
+__device__ inline uint32_t bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ inline float bf16_round(float f) { return __uint_as_float(bf16_bits(f) << 16); }
+__device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// 4 f32 (already within +-448) -> 4 E4M3 bytes in one dword, round to nearest even
+__device__ inline uint32_t pack_fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+// E4M3 byte pair (low or high 16 bits of w) -> 2 f32, exact
+__device__ inline v2f fp8x2_lo(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false); }
+__device__ inline v2f fp8x2_hi(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true); }
+
+__device__ inline float clamp_fp8(float v) { return fminf(fmaxf(v, -FP8_MAX), FP8_MAX); }
+
+// radix order key of f32 bits: larger key ranks first (+0 above -0)
+__device__ inline uint32_t radix_key(float f) {
+  uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b ^ 0x80000000u);
+}
+
+// ------------------------------------------------------------------ matrix cores
+// 16x16x128 E4M3 x E4M3 -> f32 (the scaled form at unit E8M0 scales). Lane l holds
+// row l % 16 of A (column l % 16 of B) and 32 K values of group l / 16; D lane l
+// holds rows 4 (l / 16) + v, column l % 16.
+__device__ inline v4f mfma_fp8(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+// 16x16x128 E2M1 x E2M1 with E8M0 scales per 32 K (lane l: row/column l % 16, K
+// group l / 16); only the low 4 dwords of a and b carry data
+__device__ inline v4f mfma_fp4_scaled(v8i a, v8i b, v4f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 4, 0, sa, 0, sb);
+}
+
+// ------------------------------------------------------------------ guard
+// The guard block (int32 words, runtime owned): see mono_amd.h MONO_GUARD_*.
+struct Guard {
+  int32_t* words;
+  uint32_t* host_err;  // pinned host mirror of the first error (may be null)
+  uint64_t deadline;   // ticks of the 100 MHz clock
+  int fault_site;      // test fault injection: this wait site never completes
+  uint64_t t0;
+
+  __device__ void init(int32_t* w, uint32_t* he, int fsite, uint32_t epoch, uint32_t fafter) {
+    words = w;
+    host_err = he;
+    uint32_t lo = ld_dev(reinterpret_cast<uint32_t*>(w) + MONO_GUARD_DEADLINE_LO);
+    uint32_t hi = ld_dev(reinterpret_cast<uint32_t*>(w) + MONO_GUARD_DEADLINE_HI);
+    deadline = ((uint64_t)hi << 32) | lo;
+    fault_site = (fsite > 0 && epoch >= fafter) ? fsite : 0;
+    t0 = 0;
+  }
+  __device__ bool aborted() const {
+    return ld_dev(reinterpret_cast<uint32_t*>(words) + MONO_GUARD_ABORT) != 0;
+  }
+  // a wait at `site` passed its deadline: record 1 + site (first failure sticks),
+  // raise the abort flag every other wait checks, mirror the word to the host
+  __device__ void fail(int site) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(words);
+    uint32_t expect = 0;
+    __hip_atomic_compare_exchange_strong(w + MONO_GUARD_ERR_DEADLINE, &expect, (uint32_t)(site + 1),
+                                         __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    if (fault_site) st_dev(w + MONO_GUARD_ERR_FAULT, 1u);
+    st_dev(w + MONO_GUARD_ABORT, 1u);
+    if (host_err)
+      __hip_atomic_store(host_err, (uint32_t)(site + 1), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+    drain();
+  }
+};
+
+// CTA-uniform success: false if any thread of the CTA failed or the launch aborted.
+// Call from every thread (three barriers); `ok_s` is a __shared__ int.
+__device__ inline bool cta_ok(bool mine, Guard& g, int& ok_s) {
+  __syncthreads();
+  if (threadIdx.x == 0) ok_s = g.aborted() ? 0 : 1;
+  __syncthreads();
+  if (!mine) ok_s = 0;
+  __syncthreads();
+  return ok_s != 0;
+}
+
+// Poll `ready()` (wave-uniform result expected) until true. Every 64 polls: check the
+// abort flag and the deadline. Returns false if the launch is failing; the caller then
+// skips its remaining work so every wave still reaches the end of the kernel.
+template <class F>
+__device__ inline bool wait_until(Guard& g, int site, F ready) {
+  const bool stalled = (site == g.fault_site);
+  uint32_t polls = 0;
+  uint64_t start = 0;
+  while (true) {
+    if (!stalled && ready()) return true;
+    if ((++polls & 63) == 0) {
+      if (g.aborted()) return false;
+      uint64_t now = wall_clock64();
+      if (start == 0) start = now;
+      if (now - start > g.deadline) {
+        g.fail(site);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+}  // namespace mono

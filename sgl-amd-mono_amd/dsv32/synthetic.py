@@ -1,0 +1,73 @@
+"""Seeded synthetic inputs of the benchmark configs (no checkpoints here).
+
+Distributions follow the reference's kernel tests: router ~N(0,1)*2/sqrt(H) and bias
+0.1*N(0,1) (``test/kernels/glm53/check_layer.py:96-99``), expert weights ``randn`` cast
+to E4M3 (``check_layer.py:56-59``), norm weights 1 + 0.1*N(0,1) (``:67-68``); block
+scales ~U(0.5, 2)/448; MXFP4 codes random bytes with E8M0 scales in [119, 122]
+(``test/kernels/test_minimax_m31_ffn.py:44-51``). Each tensor family draws from its own
+``torch.Generator`` seeded from (seed, family) in a fixed order.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .config import DSV32, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
+from .moe import MoeFp8Weights
+
+FP8 = torch.float8_e4m3fn
+
+
+def _gen(device, seed: int, family: int) -> torch.Generator:
+    return torch.Generator(device=device).manual_seed(1_000_003 * seed + 7919 * family + 17)
+
+
+def moe_fp8_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
+                    experts: int | None = None) -> MoeFp8Weights:
+    """Config 2 weights; ``experts`` limits how many expert slots get random values
+    (the rest stay zero) to keep CPU-side fixtures small."""
+    dev = torch.device(device)
+    h, i, e = cfg.hidden, cfg.inter, cfg.experts
+    n = e + 1
+    g = _gen(dev, seed, 1)
+    w_r = (torch.randn(e, h, generator=g, device=dev) * (2.0 / h ** 0.5)).to(torch.bfloat16)
+    bias = torch.randn(e, generator=_gen(dev, seed, 2), device=dev) * 0.1
+    g_post = (1 + 0.1 * torch.randn(h, generator=_gen(dev, seed, 3), device=dev)).to(torch.bfloat16)
+    w13 = torch.zeros(n, 2 * i, h, dtype=FP8, device=dev)
+    w2 = torch.zeros(n, h, i, dtype=FP8, device=dev)
+    gw = _gen(dev, seed, 4)
+    live = range(n) if experts is None else sorted(set(range(min(experts, n))) | {n - 1})
+    for x in live:
+        w13[x] = torch.randn(2 * i, h, generator=gw, device=dev).to(FP8)
+        w2[x] = torch.randn(h, i, generator=gw, device=dev).to(FP8)
+    gs = _gen(dev, seed, 5)
+    s13 = (0.5 + 1.5 * torch.rand(n, 2 * i // 128, h // 128, generator=gs, device=dev)) / 448.0
+    s2 = (0.5 + 1.5 * torch.rand(n, h // 128, i // 128, generator=gs, device=dev)) / 448.0
+    return MoeFp8Weights(g_post=g_post, w_r=w_r, bias=bias, w13=w13, s13=s13, w2=w2, s2=s2)
+
+
+def rows_bf16(rows: int, hidden: int, device, seed: int = 0) -> torch.Tensor:
+    """Activation rows ~N(0,1), bf16."""
+    g = _gen(torch.device(device), seed, 100 + rows)
+    return torch.randn(rows, hidden, generator=g, device=device).to(torch.bfloat16)
+
+
+def mxfp4_moe_weights(device, seed: int = 0, cfg: Mxfp4MoeConfig = MXFP4_MOE):
+    """Config 4: E2M1 codes (random bytes, even index in the low nibble) with E8M0
+    scales per 32 in [119, 122]; w13 [E+1, 2I, H/2] + [E+1, 2I, H/32], w2 [E+1, H, I/2] +
+    [E+1, H, I/32]; router bias f32 0.01*N(0,1)."""
+    dev = torch.device(device)
+    h, i, n = cfg.hidden, cfg.inter, cfg.experts + 1
+    g = _gen(dev, seed, 11)
+    u8 = dict(dtype=torch.uint8, device=dev, generator=g)
+    w13 = torch.randint(0, 256, (n, 2 * i, h // 2), **u8)
+    s13 = torch.randint(119, 123, (n, 2 * i, h // 32), **u8)
+    w2 = torch.randint(0, 256, (n, h, i // 2), **u8)
+    s2 = torch.randint(119, 123, (n, h, i // 32), **u8)
+    bias = torch.randn(cfg.experts, generator=_gen(dev, seed, 12), device=dev) * 0.01
+    return dict(w13=w13, s13=s13, w2=w2, s2=s2, bias=bias)
+
+
+def logits_f32(rows: int, experts: int, device, seed: int = 0) -> torch.Tensor:
+    g = _gen(torch.device(device), seed, 200 + rows)
+    return torch.randn(rows, experts, generator=g, device=device)

@@ -1,0 +1,82 @@
+"""The C ABI: the library loads, exports every function the header declares, and the
+ctypes mirrors have the C layout (no GPU needed: no compute call is made)."""
+
+import ctypes
+import subprocess
+
+import pytest
+
+from sgl_amd_mono_amd import _lib, guard
+
+
+def test_library_exports_every_header_function():
+    dll = _lib.lib()
+    names = _lib.header_functions()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(dll, n), n
+    assert set(names) == set(_lib.SIGNATURES), "every declared function has a typed binding"
+    assert dll.mono_version() == 1
+
+
+def _c_layout(struct, fields, tmp_path):
+    src = tmp_path / "layout.c"
+    body = "".join(f'printf("%zu ", offsetof({struct}, {f}));' for f in fields)
+    src.write_text(f'#include <stdio.h>\n#include <stddef.h>\n#include "mono_amd.h"\n'
+                   f'int main(void) {{ {body} printf("%zu\\n", sizeof({struct})); return 0; }}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(_lib.HEADER.parent), str(src), "-o", str(exe)], check=True)
+    return [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                            check=True).stdout.split()]
+
+
+@pytest.mark.parametrize("cls,cname", [(_lib.MonoMoeFp8Args, "MonoMoeFp8Args"),
+                                        (_lib.MonoDeviceInfo, "MonoDeviceInfo")])
+def test_ctypes_mirrors_match_the_c_layout(cls, cname, tmp_path):
+    fields = [f for f, _ in cls._fields_]
+    want = _c_layout(cname, fields, tmp_path)
+    got = [getattr(cls, f).offset for f in fields] + [ctypes.sizeof(cls)]
+    assert got == want
+
+
+def test_null_args_are_refused_without_a_gpu():
+    rc = _lib.lib().mono_moe_fp8_launch(None, None)
+    assert rc == _lib.MONO_E_ARG and "null" in _lib.last_error()
+    args = _lib.MonoMoeFp8Args(rows=0, experts=256)
+    assert _lib.lib().mono_moe_fp8_launch(ctypes.byref(args), None) == _lib.MONO_E_ARG
+
+
+def test_scratch_bytes_only_for_built_geometries():
+    assert _lib.lib().mono_moe_fp8_scratch_bytes(7168, 512, 256) > 0
+    assert _lib.lib().mono_moe_fp8_scratch_bytes(7168, 384, 256) == 0
+
+
+def test_deadline_ticks_bounds():
+    # the reference refuses deadlines past the 32-bit check (test_guard_hip.py:98-109)
+    assert guard.deadline_ticks(1.0) == 100_000_000
+    # 2^31 units of 2^8 ticks at 100 MHz: 5497 s
+    assert guard.deadline_ticks(5497) <= guard.MAX_DEADLINE_TICKS
+    with pytest.raises(ValueError):
+        guard.deadline_ticks(5498)
+    with pytest.raises(ValueError):
+        guard.deadline_ticks(0)
+    assert guard.watchdog_deadline(300) == 60.0 and guard.watchdog_deadline(30) == 15.0
+
+
+def test_fault_injection_env(monkeypatch):
+    monkeypatch.setenv(guard.FAULT_ENV, "1:3:5")
+    assert guard.fault_injection(1) == (3, 5)
+    assert guard.fault_injection(0) is None
+    monkeypatch.setenv(guard.FAULT_ENV, "0:2")
+    assert guard.fault_injection(0) == (2, 0)
+    monkeypatch.delenv(guard.FAULT_ENV)
+    assert guard.fault_injection(0) is None
+
+
+def test_guard_words_describe():
+    assert guard.describe([0] * 16) is None
+    words = [0] * 16
+    words[_lib.GUARD_ERR_DEADLINE] = 3  # site 2 = mid
+    words[_lib.GUARD_ERR_FAULT] = 1
+    msg = guard.describe(words)
+    assert "mid" in msg and "fault-injected 1" in msg

@@ -1,0 +1,150 @@
+"""FP8 routed MoE launch (config 2) against the CPU oracle on the same seeded inputs.
+
+Bars: router top-8 ids bit-exact given the launch's own sigmoid scores (lowest-id
+ties); scores within f32 accumulation-order error of the oracle's; the MoE sum y within
+1e-2 relative (norm) and cos >= 0.9999 of the oracle run on the launch's routing; the
+layer output a + y within 2e-2 max-abs + 1e-2 relative (bf16, fp32 accumulation)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as omoe
+from sgl_amd_mono_amd.dsv32 import synthetic
+from sgl_amd_mono_amd.dsv32.config import DSV32
+from sgl_amd_mono_amd.dsv32.moe import MoeFp8Op, MoeRouting
+
+pytestmark = pytest.mark.gpu
+H, E = DSV32.hidden, DSV32.experts
+
+
+@pytest.fixture(scope="module")
+def layer(gpu):
+    return synthetic.moe_fp8_weights(gpu, seed=0)
+
+
+def _routing(rows, dev):
+    return MoeRouting(scores=torch.empty(rows, E, dtype=torch.float32, device=dev),
+                      ids=torch.empty(rows, 9, dtype=torch.int32, device=dev),
+                      weights=torch.empty(rows, 9, dtype=torch.float32, device=dev))
+
+
+def _cpu_experts(w, ids):
+    out = {}
+    for e in np.unique(ids):
+        e = int(e)
+        out[e] = (w.w13[e].view(torch.uint8).cpu().numpy(), w.s13[e].cpu().numpy(),
+                  w.w2[e].view(torch.uint8).cpu().numpy(), w.s2[e].cpu().numpy())
+    return out
+
+
+def _run(op, a):
+    rows = a.shape[0]
+    y = torch.full((rows, H), float("nan"), dtype=torch.float32, device=a.device)
+    rt = _routing(rows, a.device)
+    out = op.launch(a, y=y, routing=rt)
+    op.rt.check()
+    return out, y, rt
+
+
+@pytest.mark.parametrize("rows", [1, 4, 8, 16])
+def test_moe_fp8_matches_oracle(layer, gpu, rows):
+    print(f"case rows={rows}", flush=True)
+    op = MoeFp8Op(layer, gpu, max_rows=16)
+    a = synthetic.rows_bf16(rows, H, gpu, seed=rows)
+    out, y, rt = _run(op, a)
+    ids, wts = rt.ids.cpu().numpy(), rt.weights.cpu().numpy()
+    scores = rt.scores.cpu()
+    bias = layer.bias.cpu()
+    # selection: bit-exact against the oracle's top-8 of the launch's own scores
+    sel, sel_w = omoe.route_topk(scores, bias)
+    assert np.array_equal(ids[:, 1:], sel), "router ids differ"
+    assert np.all(ids[:, 0] == 256) and np.all(wts[:, 0] == 1.0)
+    np.testing.assert_allclose(wts[:, 1:], sel_w, rtol=2e-6, atol=1e-7)
+    # the oracle end to end
+    ref = omoe.moe_fp8(a.cpu(), layer.g_post.cpu(), layer.w_r.cpu(), bias, None, None, None,
+                       None, experts=_cpu_experts(layer, np.concatenate([ids, ref_ids(a, layer)])),
+                       routing=(ids, wts))
+    np.testing.assert_allclose(scores.numpy(), ref["scores"].numpy(), rtol=1e-5, atol=1e-6)
+    got, want = y.cpu().double(), ref["y"].double()
+    rel = float((got - want).norm() / want.norm())
+    cos = float(torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0))
+    print(f"rows={rows} y rel={rel:.3e} cos={cos:.6f}", flush=True)
+    assert rel <= 1e-2 and cos >= 0.9999, (rel, cos)
+    o = out.cpu().float()
+    assert torch.all((o - ref["out"]).abs() <= 2e-2 + 1e-2 * ref["out"].abs())
+    # the oracle's own routing agrees wherever the 8th/9th keys are clearly apart
+    own, _ = omoe.route_topk(ref["scores"], bias)
+    key = (ref["scores"] + bias).numpy()
+    srt = -np.sort(-key, 1)
+    clear = (srt[:, 7] - srt[:, 8]) > 1e-4
+    assert np.array_equal(np.sort(own[clear], 1), np.sort(ids[clear, 1:], 1))
+
+
+def ref_ids(a, layer):
+    """The oracle's own routing ids (its experts are needed for the comparison too)."""
+    xn = omoe.rmsnorm(a.cpu(), layer.g_post.cpu())
+    s = omoe.sigmoid(omoe.router_logits(xn, layer.w_r.cpu()))
+    return omoe.slots_with_shared(*omoe.route_topk(s, layer.bias.cpu()))[0]
+
+
+def test_moe_fp8_is_deterministic_and_writes_only_its_rows(layer, gpu):
+    print("case determinism rows=8", flush=True)
+    op = MoeFp8Op(layer, gpu, max_rows=16)
+    a = synthetic.rows_bf16(8, H, gpu, seed=42)
+    full = torch.full((16, H), 7.0, dtype=torch.bfloat16, device=gpu)
+    r1 = op.launch(a, out=full[:8]).clone()
+    r2 = op.launch(a).clone()
+    r3 = op.launch(a).clone()
+    op.rt.check()
+    assert torch.equal(r1, r2) and torch.equal(r2, r3)
+    assert torch.all(full[8:] == 7.0), "wrote past its rows"
+
+
+def test_moe_fp8_graph_replay_matches_eager(layer, gpu):
+    print("case graph replay rows=4", flush=True)
+    op = MoeFp8Op(layer, gpu, max_rows=16)
+    a = synthetic.rows_bf16(4, H, gpu, seed=7)
+    out = torch.empty(4, H, dtype=torch.bfloat16, device=gpu)
+    eager = op.launch(a).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op.launch(a, out=out)  # warm up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        op.launch(a, out=out)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        op.launch(a)  # eager work between replays
+        torch.cuda.synchronize()
+    op.rt.check()
+
+
+def test_moe_fp8_deadline_stops_and_reports(layer, gpu):
+    """Fault injection from the host: the mid-quant wait never completes, so it times
+    out after a 5 ms deadline; every CTA still exits, the host raises, and a reset
+    runtime launches cleanly again."""
+    print("case fault injection site=mid", flush=True)
+    a = synthetic.rows_bf16(2, H, gpu, seed=3)
+    op = MoeFp8Op(layer, gpu, max_rows=16, deadline_s=0.005, fault=(2, 0))
+    op.launch(a)
+    with pytest.raises(RuntimeError, match="mid"):
+        op.rt.check()
+    with pytest.raises(RuntimeError):
+        op.launch(a)  # refused after a failure
+    words = op.rt.guard.cpu().tolist()
+    assert words[3] == 3 and words[5] == 1  # 1 + site, fault-injected
+    op.fault = (0, 0)
+    op.rt.reset()
+    op.rt.set_deadline(10.0)
+    clean = op.launch(a).clone()
+    op.rt.check()
+    ref = MoeFp8Op(layer, gpu, max_rows=16).launch(a)
+    torch.cuda.synchronize()
+    assert torch.equal(clean, ref)
