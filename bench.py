@@ -41,7 +41,25 @@ def parse():
     p.add_argument("--rows", type=int, default=8)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--layout", default="aiter16", choices=("aiter16", "rowmajor"),
+                   help="on-HBM layout of the expert weights (SGLang's gfx950 MoE load "
+                        "leaves them in AITER's (16, 16) shuffle)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a 1 GiB device-to-device copy 5 times (the reference "
+                        "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return p.parse_args()
+
+
+def copy_calibration():
+    import torch
+
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "launches": 5}), flush=True)
 
 
 def traffic_from_profiles(name: str):
@@ -64,10 +82,10 @@ def cpu_baseline(a_cpu, w, ids, rows):
 
     torch.set_num_threads(os.cpu_count() or 1)
     experts = {}
+    from sgl_amd_mono_amd.dsv32 import synthetic
+
     for e in np.unique(ids):
-        e = int(e)
-        experts[e] = (w.w13[e].view(torch.uint8).cpu().numpy(), w.s13[e].cpu().numpy(),
-                      w.w2[e].view(torch.uint8).cpu().numpy(), w.s2[e].cpu().numpy())
+        experts[int(e)] = synthetic.rowmajor_expert(w, int(e))
     args = (a_cpu, w.g_post.cpu(), w.w_r.cpu(), w.bias.cpu(), None, None, None, None)
     times = []
     for _ in range(2):
@@ -83,6 +101,9 @@ def cpu_baseline(a_cpu, w, ids, rows):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every GPU box here has one GPU, and the sharded "
               f"path (TP=4 exchanges) is not built; got --gpus {args.gpus}", file=sys.stderr)
@@ -97,7 +118,7 @@ def main():
     dev = torch.device("cuda:0")
     rows, L = args.rows, args.layers
     print(f"bench: generating {L} layers of FP8 experts", file=sys.stderr, flush=True)
-    weights = [synthetic.moe_fp8_weights(dev, seed=100 + i) for i in range(L)]
+    weights = [synthetic.moe_fp8_weights(dev, seed=100 + i, layout=args.layout) for i in range(L)]
     ops = [MoeFp8Op(w, dev, max_rows=rows) for w in weights]
     inputs = [synthetic.rows_bf16(rows, DSV32.hidden, dev, seed=200 + i) for i in range(L)]
     outs = [torch.empty(rows, DSV32.hidden, dtype=torch.bfloat16, device=dev) for _ in range(L)]
@@ -162,7 +183,7 @@ def main():
                         "persistent launch (post-norm, router, top-8 + shared, W8A8 SwiGLU, "
                         "down, residual)",
             "rows": rows, "hidden": DSV32.hidden, "experts": DSV32.experts + 1,
-            "inter": DSV32.inter, "layers_rotated": L,
+            "inter": DSV32.inter, "layers_rotated": L, "weight_layout": args.layout,
             "distinct_experts": distinct,
         },
         "rows_per_s": round(rows / (us * 1e-6), 1),

@@ -80,11 +80,18 @@ int mono_reset(void* scratch, size_t scratch_bytes, int32_t* guard, mono_stream_
  * sgl_amd_mono/glm53/gfx950/kernel.py:4199-4330 (norm, router, activation quant),
  * :1575-1629 + :4332-4350 (routing), :4352-4999 (up/gate), :5001-5187 (down), and
  * the W == 1 peer_reduce branch :1665-1669. */
+/* On-HBM layouts of FP8 expert weights [.., N, K] */
+#define MONO_LAYOUT_ROWMAJOR 0 /* plain row-major E4M3 */
+#define MONO_LAYOUT_AITER16 1  /* AITER (16, 16) shuffle: [N / 16, K / 32, 2, 16, 16 B],
+                                  SGLang's in-place layout on gfx950
+                                  (sgl_amd_mono/glm53/gfx950/kernel.py:787-808) */
+
 typedef struct {
   int32_t rows;            /* R, 1..16 */
   int32_t hidden;          /* 7168 */
   int32_t inter;           /* expert intermediate per GPU: 512 */
   int32_t experts;         /* routed experts: 256 (the shared one is id 256) */
+  int32_t layout;          /* MONO_LAYOUT_* of w13 and w2 */
   float eps;               /* RMSNorm epsilon */
   float route_scale;       /* routed_scaling_factor, 2.5 */
   const void* a;           /* bf16 [R, H]: the stream after attention */
@@ -105,7 +112,20 @@ typedef struct {
   uint32_t* host_error;    /* optional pinned host word: 1 + failed site */
   int32_t fault_site;      /* test fault injection: this wait site stalls (0: none) */
   int32_t fault_after;     /* ... once the epoch reached this many launches */
+  uint64_t* timeline;      /* optional u64 [grid, 8]: per-CTA s_memrealtime stamps at the
+                              stage boundaries (MONO_TL_*), as the reference's timeline
+                              build (sgl_amd_mono/common/stamps.py:16-33) */
 } MonoMoeFp8Args;
+
+/* timeline marks of the MoE launch */
+#define MONO_TL_START 0
+#define MONO_TL_STAGED 1  /* norm, activation quant and router logits published */
+#define MONO_TL_ROUTED 2  /* routing and the distinct-expert list in LDS */
+#define MONO_TL_UPGATE 3  /* this CTA's up/gate tasks done */
+#define MONO_TL_MIDQ 4    /* this CTA's mid quant tasks done */
+#define MONO_TL_DOWN 5    /* this CTA's down tasks done */
+#define MONO_TL_END 6
+#define MONO_TL_COLS 8
 
 size_t mono_moe_fp8_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts);
 int mono_moe_fp8_launch(const MonoMoeFp8Args* args, mono_stream_t stream);

@@ -33,6 +33,14 @@ GUARD_EXIT = 6
 GUARD_ABORT = 7
 GUARD_WORDS = 16
 
+# on-HBM layouts of FP8 expert weights (MONO_LAYOUT_*)
+LAYOUT_ROWMAJOR = 0
+LAYOUT_AITER16 = 1
+
+# timeline marks of the MoE launch (MONO_TL_*), u64 [grid, TL_COLS]
+TL_MARKS = ("start", "staged", "routed", "upgate", "midq", "down", "end")
+TL_COLS = 8
+
 # wait sites (the deadline error word holds 1 + site)
 SITES = {1: "logits", 2: "mid", 3: "mq"}
 
@@ -49,6 +57,7 @@ class MonoMoeFp8Args(ctypes.Structure):
         ("hidden", c_int32),
         ("inter", c_int32),
         ("experts", c_int32),
+        ("layout", c_int32),
         ("eps", c_float),
         ("route_scale", c_float),
         ("a", c_void_p),
@@ -69,6 +78,7 @@ class MonoMoeFp8Args(ctypes.Structure):
         ("host_error", c_void_p),
         ("fault_site", c_int32),
         ("fault_after", c_int32),
+        ("timeline", c_void_p),
     ]
 
 

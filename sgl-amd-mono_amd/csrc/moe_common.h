@@ -21,6 +21,8 @@ struct RouteLds {
   uint32_t mask[MOE_NDIST];         // per expert id: bit t = row t routed to it
   int32_t uexp[MOE_NDIST];          // distinct experts: u = 0 the shared, then ascending
   uint32_t umask[MOE_NDIST];
+  int32_t uslot[MOE_NDIST];         // first (expert, row) slot of u; rows of u in order
+  int32_t slot_ut[MOE_MAXR * MOE_SLOTS];  // slot -> (u << 8) | row
   int32_t nd;
 };
 
@@ -56,7 +58,7 @@ __device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], cons
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (i == slot) raw = sc[i];
-    raw = __shfl(raw, owner, WAVE);
+    raw = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(raw), owner));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (cand[i] == best) cand[i] = 0;  // 0 is below every live candidate
@@ -125,6 +127,37 @@ __device__ inline void build_distinct(RouteLds& rl, int rows) {
     rl.uexp[0] = MOE_SHARED;
     rl.umask[0] = rows >= 32 ? 0xFFFFFFFFu : ((1u << rows) - 1u);
   }
+  // (expert, row) slots: the rows of each distinct expert, experts in u order. Every
+  // row has 9 distinct slots, so there are exactly 9 R of them; u < 4 * 64 covers nd.
+  const int nd = 1 + __shfl(inc, 63, WAVE);
+  uint32_t um[4];
+  int c2 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = 4 * l + i;
+    um[i] = u < nd ? rl.umask[u] : 0u;
+    c2 += __popc(um[i]);
+  }
+  int inc2 = c2;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int o = __shfl_up(inc2, d, WAVE);
+    if (l >= d) inc2 += o;
+  }
+  int s = inc2 - c2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = 4 * l + i;
+    if (u < nd) {
+      rl.uslot[u] = s;
+      for (uint32_t m = um[i]; m; m &= m - 1) rl.slot_ut[s++] = (u << 8) | (__ffs(m) - 1);
+    }
+  }
+}
+
+// the slot of (u, row t), or -1 when row t is not routed to u
+__device__ inline int slot_of(const RouteLds& rl, int u, uint32_t mask, int t) {
+  return ((mask >> t) & 1u) ? rl.uslot[u] + __popc(mask & ((1u << t) - 1u)) : -1;
 }
 
 // route weight of row t for expert e (0 when e is not among its slots)

@@ -79,6 +79,7 @@ struct MoeFp8Params {
   int32_t* guard;
   uint32_t* host_err;
   int fault_site, fault_after;
+  uint64_t* timeline;
 };
 
 // bf16 x 8 in a dword4 -> 8 f32
@@ -94,7 +95,10 @@ __device__ inline v8i cat8(v4i a, v4i b) {
   return v8i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-template <int H, int I>
+// SHUF: expert weights in AITER's (16, 16) layout, [rows / 16, K / 32, 2, 16 rows, 16 B]
+// (what SGLang's gfx950 MoE load leaves in place): a 16-row x 128-K MFMA tile is then one
+// contiguous 2 KB, and each load instruction reads 8 whole cache lines
+template <int H, int I, bool SHUF>
 __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   using G = MoeFp8Geom<H, I>;
   constexpr int KCW = G::KCW, NUG = G::NUG, NKB = G::NKB, QW = G::QW;
@@ -111,9 +115,8 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   __shared__ v4i xq_lds[QW * KCW * 2 * 64];
   __shared__ float xs_lds[QW * KCW][16];  // activation block scale per (chunk, row)
   __shared__ v4f red[G::WAVES][64];
-  __shared__ float red_small[2][QW][16];
+  __shared__ float red_small[2][2][8];
   __shared__ float rstd_s[MOE_MAXR];
-  __shared__ uint32_t tag_s;
   __shared__ int ok_s;
 
   uint64_t* logit_pairs = reinterpret_cast<uint64_t*>(p.scratch + G::OFF_LOGIT);
@@ -122,113 +125,156 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   float* mcoef = reinterpret_cast<float*>(p.scratch + G::OFF_MCOEF);
   uint32_t* ready = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
 
-  if (tid == 0) tag_s = ld_dev(reinterpret_cast<uint32_t*>(p.guard) + MONO_GUARD_EPOCH) + 1u;
+  __shared__ uint32_t head_s[4];
+  const __amdgpu_buffer_rsrc_t rg = rsrc(p.g_post, H * 2);
+  // the post-attention norm weight, the same for every row, into LDS (over the
+  // reduction buffer, idle until stage 2), ahead of the guard read so both overlap
+  v4i* g_lds = reinterpret_cast<v4i*>(&red[0][0]);
+  static_assert(H * 2 <= (int)sizeof(red), "norm weight staging");
+  for (int i = tid; i < H / 8; i += G::THREADS) g_lds[i] = ld16<CP_NONE>(rg, i * 16);
+  if (tid == 0) {
+    const v4i h = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)h[i];
+  }
   for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
   __syncthreads();
-  const uint32_t tag = tag_s;
+  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
   Guard guard;
-  guard.init(p.guard, p.host_err, p.fault_site, tag - 1u, (uint32_t)p.fault_after);
+  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
   bool ok = true;
 
-  const __amdgpu_buffer_rsrc_t ra = rsrc(p.a, (uint32_t)(R * H * 2));
-  const __amdgpu_buffer_rsrc_t rg = rsrc(p.g_post, H * 2);
-  const __amdgpu_buffer_rsrc_t rw = rsrc(p.w_r, (uint32_t)MOE_NEXP * H * 2);
 
   // ---------------------------------------------------------------- stage 0
-  // pass 1 (waves 0-7): sum of squares of row t over this slice (rows >= R load 0)
-  if (half == 0) {
-    float ss = 0.f;
-#pragma unroll 1
-    for (int j = 0; j < KCW; ++j) {
-      const uint32_t off = (uint32_t)(t * H + (wq * KCW + j) * 128 + 32 * grp) * 2;
+  stamp(p.timeline, MONO_TL_START);
+  // A pair of waves owns a row: wave w takes row w % 8 (+ 8 in the second pass when
+  // R > 8) and column half w / 8. Lane l holds the 8 values at q * 512 + l * 8 of each of
+  // its half's 7 slices q, so the row, the norm weight and the router row come in with
+  // one round trip of 21 loads a lane. The E4M3 codes go to xq_lds in the MFMA B-operand
+  // image of stage 2 (chunk kc = q * 4 + l / 16; K group (l % 16) / 4; byte (l % 4) * 8).
+  {
+    constexpr int NQ = H / 512 / 2;  // slices a half holds
+    static_assert(H % 1024 == 0, "hidden must split into two halves of 512-slices");
+    const int ch = w / 8, wr = w % 8;
+    for (int pass = 0; pass * 8 < R; ++pass) {
+      const int r = pass * 8 + wr;
+      const bool live = r < R;
+      const __amdgpu_buffer_rsrc_t rar = rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
+      v4i av[NQ], wv[NQ];
+      const uint32_t base = (uint32_t)(ch * NQ * 512 + l * 8) * 2;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < NQ; ++q) av[q] = ld16<CP_NONE>(rar, base + q * 1024);
+      const int e0 = b < MOE_NEXP ? b : 0;
+      const __amdgpu_buffer_rsrc_t rwr =
+          rsrc(p.w_r + (size_t)e0 * H, (b < MOE_NEXP && live) ? H * 2 : 0);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) wv[q] = ld16<CP_NT>(rwr, base + q * 1024);
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
         float f[8];
-        bf16x8(ld16<CP_NONE>(ra, off + 16 * q), f);
+        bf16x8(av[q], f);
 #pragma unroll
         for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
       }
-    }
-    ss += xor_f(ss, 16);
-    ss += xor_f(ss, 32);
-    if (grp == 0) red_small[0][wq][t] = ss;
-  }
-  __syncthreads();
-  if (tid < MOE_MAXR) {
-    float tot = 0.f;
+      ss = wave_sum(ss);
+      if (l == 0) red_small[0][ch][wr] = ss;
+      __syncthreads();
+      const float rstd = live ? 1.0f / sqrtf((red_small[0][0][wr] + red_small[0][1][wr]) /
+                                             (float)H + p.eps)
+                              : 0.f;
+      float rp = 0.f;
 #pragma unroll
-    for (int i = 0; i < QW; ++i) tot += red_small[0][i][tid];
-    rstd_s[tid] = tid < R ? 1.0f / sqrtf(tot / (float)H + p.eps) : 0.f;
-  }
-  __syncthreads();
-  const float rstd = rstd_s[t];
-
-  // pass 2 (waves 0-7): xn = a * rstd * g; E4M3 B operands + scales; router dot
-  // products of this CTA's experts (b, b + grid, ...)
-  for (int e = b, first = 1; first || e < MOE_NEXP; e += nblk, first = 0) {
-    float rpart = 0.f;
-    if (half == 0) {
-#pragma unroll 1
-      for (int j = 0; j < KCW; ++j) {
-        const int k0 = (wq * KCW + j) * 128 + 32 * grp;
-        float xn[32];
+      for (int q = 0; q < NQ; ++q) {
+        float fa[8], fg[8], fw[8], xn[8];
+        bf16x8(av[q], fa);
+        bf16x8(g_lds[ch * NQ * 64 + q * 64 + l], fg);
+        bf16x8(wv[q], fw);
+        float am = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float fa[8], fg[8];
-          bf16x8(ld16<CP_NONE>(ra, (uint32_t)(t * H + k0) * 2 + 16 * q), fa);
-          bf16x8(ld16<CP_NONE>(rg, (uint32_t)k0 * 2 + 16 * q), fg);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) xn[8 * q + i] = fa[i] * rstd * fg[i];
+        for (int i = 0; i < 8; ++i) {
+          xn[i] = fa[i] * rstd * fg[i];
+          am = fmaxf(am, fabsf(xn[i]));
+          rp += bf16_round(xn[i]) * fw[i];
         }
-        if (first) {
-          float am = 0.f;
-#pragma unroll
-          for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(xn[i]));
-          am = fmaxf(am, xor_f(am, 16));
-          am = fmaxf(am, xor_f(am, 32));
-          const bool nz = am > 0.f;
-          if (grp == 0) xs_lds[wq * KCW + j][t] = nz ? am * INV_FP8_MAX : 1.f;
-          const float inv = nz ? FP8_MAX / am : 1.f;
-          v4i q0, q1;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            q0[d] = (int)pack_fp8x4(clamp_fp8(xn[4 * d] * inv), clamp_fp8(xn[4 * d + 1] * inv),
-                                    clamp_fp8(xn[4 * d + 2] * inv),
-                                    clamp_fp8(xn[4 * d + 3] * inv));
-            q1[d] = (int)pack_fp8x4(clamp_fp8(xn[16 + 4 * d] * inv),
-                                    clamp_fp8(xn[17 + 4 * d] * inv),
-                                    clamp_fp8(xn[18 + 4 * d] * inv),
-                                    clamp_fp8(xn[19 + 4 * d] * inv));
-          }
-          xq_lds[((wq * KCW + j) * 2 + 0) * 64 + l] = q0;
-          xq_lds[((wq * KCW + j) * 2 + 1) * 64 + l] = q1;
-        }
-        if (e < MOE_NEXP) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float fw[8];
-            bf16x8(ld16<CP_NT>(rw, (uint32_t)(e * H + k0) * 2 + 16 * q), fw);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) rpart += bf16_round(xn[8 * q + i]) * fw[i];
-          }
+        am = row16_max(am);
+        const bool nz = am > 0.f;
+        const float inv = nz ? FP8_MAX / am : 1.f;
+        const int kc = (ch * NQ + q) * 4 + (l >> 4);
+        if (live) {
+          v2i qq;
+          qq[0] = (int)pack_fp8x4(clamp_fp8(xn[0] * inv), clamp_fp8(xn[1] * inv),
+                                  clamp_fp8(xn[2] * inv), clamp_fp8(xn[3] * inv));
+          qq[1] = (int)pack_fp8x4(clamp_fp8(xn[4] * inv), clamp_fp8(xn[5] * inv),
+                                  clamp_fp8(xn[6] * inv), clamp_fp8(xn[7] * inv));
+          const int g4 = (l & 15) >> 2, h = (l & 3) >> 1;
+          char* dst = reinterpret_cast<char*>(xq_lds) +
+                      ((kc * 2 + h) * 64 + r + 16 * g4) * 16 + (l & 1) * 8;
+          *reinterpret_cast<v2i*>(dst) = qq;
+          if ((l & 15) == 0) xs_lds[kc][r] = nz ? am * INV_FP8_MAX : 1.f;
         }
       }
-      rpart += xor_f(rpart, 16);
-      rpart += xor_f(rpart, 32);
+      rp = wave_sum(rp);
+      if (l == 0) red_small[1][ch][wr] = rp;
+      __syncthreads();
+      if (ch == 0 && l == 0 && live && b < MOE_NEXP)
+        st_dev64(&logit_pairs[r * MOE_NEXP + b],
+                 pair(__float_as_uint(red_small[1][0][wr] + red_small[1][1][wr]), tag));
+      __syncthreads();
     }
-    if (e >= MOE_NEXP) break;  // CTA-uniform
-    __syncthreads();
-    if (half == 0 && grp == 0) red_small[1][wq][t] = rpart;
-    __syncthreads();
-    if (tid < R) {
-      float lg = 0.f;
+    // rows past R: zero B operands, unit scales (stage 2 reads all 16 columns)
+    for (int i = tid; i < G::NKC * 16; i += G::THREADS) {
+      const int kc = i / 16, r = i % 16;
+      if (r >= R) {
+        xs_lds[kc][r] = 1.f;
 #pragma unroll
-      for (int i = 0; i < QW; ++i) lg += red_small[1][i][tid];
-      st_dev64(&logit_pairs[tid * MOE_NEXP + e], pair(__float_as_uint(lg), tag));
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) xq_lds[(kc * 2 + h) * 64 + r + 16 * g4] = v4i{0, 0, 0, 0};
+      }
+    }
+    // a grid smaller than the expert count: this CTA's further router experts
+    for (int e = b + nblk; e < MOE_NEXP; e += nblk) {
+      for (int pass = 0; pass * 8 < R; ++pass) {
+        const int r = pass * 8 + wr;
+        const bool live = r < R;
+        const __amdgpu_buffer_rsrc_t rar =
+            rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
+        const __amdgpu_buffer_rsrc_t rwr = rsrc(p.w_r + (size_t)e * H, live ? H * 2 : 0);
+        const uint32_t base = (uint32_t)(ch * NQ * 512 + l * 8) * 2;
+        __syncthreads();
+        float ss = 0.f, rp = 0.f;
+        for (int q = 0; q < NQ; ++q) {
+          float f[8];
+          bf16x8(ld16<CP_NONE>(rar, base + q * 1024), f);
+          for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+        }
+        ss = wave_sum(ss);
+        if (l == 0) red_small[0][ch][wr] = ss;
+        __syncthreads();
+        const float rstd = live ? 1.0f / sqrtf((red_small[0][0][wr] + red_small[0][1][wr]) /
+                                               (float)H + p.eps)
+                                : 0.f;
+        for (int q = 0; q < NQ; ++q) {
+          float fa[8], fg[8], fw[8];
+          bf16x8(ld16<CP_NONE>(rar, base + q * 1024), fa);
+          bf16x8(g_lds[ch * NQ * 64 + q * 64 + l], fg);
+          bf16x8(ld16<CP_NT>(rwr, base + q * 1024), fw);
+          for (int i = 0; i < 8; ++i) rp += bf16_round(fa[i] * rstd * fg[i]) * fw[i];
+        }
+        rp = wave_sum(rp);
+        if (l == 0) red_small[1][ch][wr] = rp;
+        __syncthreads();
+        if (ch == 0 && l == 0 && live)
+          st_dev64(&logit_pairs[r * MOE_NEXP + e],
+                   pair(__float_as_uint(red_small[1][0][wr] + red_small[1][1][wr]), tag));
+      }
     }
   }
+  __syncthreads();
 
   // ---------------------------------------------------------------- stage 1
+  stamp(p.timeline, MONO_TL_STAGED);
   // one wave a row: poll the row's 256 logits, sigmoid, top-8
   if (w < R) {
     const int row = w;
@@ -257,17 +303,21 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   }
   __syncthreads();
   if (w == 0) build_distinct(rl, R);
-  ok = cta_ok(ok, guard, ok_s);
+  ok = cta_all(ok, ok_s);
   const int nd = rl.nd;
 
   // ---------------------------------------------------------------- stage 2
+  stamp(p.timeline, MONO_TL_ROUTED);
   // waves 0-7: the 16 gate rows of the task, waves 8-15 the 16 up rows; wave wq's
   // K slice is chunks [KCW wq, KCW (wq + 1)). Its ring holds one task's KCW chunks:
   // a slot is refilled with the next task's chunk as soon as its MFMA issued.
   {
     const int ntask = ok ? nd * NUG : 0;
     v4i ring[KCW][2];
-    const uint32_t vo = (uint32_t)(t * H + 32 * grp);  // this lane's row and K group
+    // this lane's row and K group; the second 16 bytes of a lane's 32 sit 16 bytes on
+    // (row major) or a 16-row half-tile on (shuffled); a 128-K chunk is CS bytes on
+    const uint32_t vo = SHUF ? (uint32_t)(grp * 512 + t * 16) : (uint32_t)(t * H + 32 * grp);
+    constexpr uint32_t HO = SHUF ? 256 : 16, CS = SHUF ? 2048 : 128;
     // a task past the end issues through an empty buffer: its loads return 0 with no
     // memory traffic, so the refill needs no branch
     auto task_src = [&](int task, uint32_t& so) {
@@ -275,7 +325,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       const int tk = live ? task : 0;
       const int u = tk / NUG, cc = tk % NUG;
       const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
-      so = (uint32_t)((half * I + cc * 16) * H + wq * KCW * 128);
+      const int row0 = half * I + cc * 16;
+      so = SHUF ? (uint32_t)((row0 / 16) * (H / 32) * 512 + wq * KCW * CS)
+                : (uint32_t)(row0 * H + wq * KCW * 128);
       return rsrc(p.w13 + (size_t)e * (2 * I) * H, live ? 2u * I * H : 0u);
     };
     int task = b;
@@ -284,8 +336,8 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       const __amdgpu_buffer_rsrc_t r = task_src(task, so);
 #pragma unroll
       for (int j = 0; j < KCW; ++j) {
-        ring[j][0] = ld16s<CP_NT>(r, vo, so + j * 128);
-        ring[j][1] = ld16s<CP_NT>(r, vo + 16, so + j * 128);
+        ring[j][0] = ld16s<CP_NT>(r, vo, so + j * CS);
+        ring[j][1] = ld16s<CP_NT>(r, vo + HO, so + j * CS);
       }
     }
     while (task < ntask) {
@@ -309,8 +361,8 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         const v4f zero = {0.f, 0.f, 0.f, 0.f};
         const v4f d = mfma_fp8(cat8(ring[j][0], ring[j][1]), B, zero);
         // the slot is free once its MFMA issued: refill it with the next task's chunk
-        ring[j][0] = ld16s<CP_NT>(rn, vo, son + j * 128);
-        ring[j][1] = ld16s<CP_NT>(rn, vo + 16, son + j * 128);
+        ring[j][0] = ld16s<CP_NT>(rn, vo, son + j * CS);
+        ring[j][1] = ld16s<CP_NT>(rn, vo + HO, son + j * CS);
         acc += d * (sld(p.s13, sbase + j) * ((&xs_lds[0][0])[sb + j * 16] * tok_on));
         // one chunk per scheduling region keeps the live set to the ring
         __builtin_amdgcn_sched_barrier(0);
@@ -338,6 +390,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   }
 
   // ---------------------------------------------------------------- stage 3
+  stamp(p.timeline, MONO_TL_UPGATE);
   // mid quant: task (u, kb), one wave a row. Trip counts stay CTA-uniform (barriers
   // per task); a failed wait only skips work.
   {
@@ -364,7 +417,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
           const uint32_t h = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
                                  clamp_fp8(v0 * inv), clamp_fp8(v1 * inv), 0, false) &
                              0xFFFFu;
-          const uint32_t hn = xor_u(h, 1);
+          const uint32_t hn = dpp_u<DPP_XOR1>(h);
           if ((l & 1) == 0)
             st_dev(reinterpret_cast<uint32_t*>(mq + ((size_t)u * MOE_MAXR + tok) * I + kb * 128 +
                                                2 * l),
@@ -382,67 +435,96 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   }
 
   // ---------------------------------------------------------------- stage 4
-  // down: task f = output rows [32 f, 32 f + 32); waves 0-7 the first 16 rows, 8-15
-  // the next 16; wave wq takes experts u = wq, wq + 8, ... and prefetches the next
+  stamp(p.timeline, MONO_TL_MIDQ);
+  // down: task f = output rows [32 f, 32 f + 32); waves 0-7 the first 16 rows, 8-15 the
+  // next 16; wave wq takes experts u = wq, wq + 8, ... One wait for every quantised mid
+  // block (the first weight tile already in flight), then the 9 R (expert, row) mid rows
+  // are copied into LDS over the dead activation operands, so the expert loop streams
+  // weights with no poll and no other global load.
   {
     const int ntask = ok ? G::NDN : 0;
-    const __amdgpu_buffer_rsrc_t rmq = rsrc(mq, (uint32_t)G::SZ_MQ);
-    for (int f = b; f < ntask; f += nblk) {
-      const int r0 = f * G::DNT;
-      const int rg0 = r0 + 16 * half;
+    uint8_t* mql = reinterpret_cast<uint8_t*>(xq_lds);  // [9 R slots][I] E4M3
+    float* mcl = reinterpret_cast<float*>(mql + MOE_MAXR * MOE_SLOTS * I);  // [slots][NKB]
+    static_assert(MOE_MAXR * MOE_SLOTS * (I + NKB * 4) <= (int)sizeof(xq_lds), "mid slots");
+    // one tile of weight chunks a wave; each chunk is refilled with the next step's as
+    // soon as its MFMA issued, the last expert of a task running into the next task
+    v4i buf[NKB][2];
+    const uint32_t vo = SHUF ? (uint32_t)(grp * 512 + t * 16) : (uint32_t)t * I + 32 * grp;
+    constexpr uint32_t HO = SHUF ? 256 : 16, CS = SHUF ? 2048 : 128;
+    auto src_of = [&](int f, int u, uint32_t& so) {
+      const bool live = f < ntask && u < nd;
+      const int e = __builtin_amdgcn_readfirstlane(rl.uexp[live ? u : 0]);
+      const int row0 = (live ? f : 0) * G::DNT + 16 * half;
+      so = SHUF ? (uint32_t)((row0 / 16) * (I / 32) * 512) : (uint32_t)row0 * I;
+      return rsrc(p.w2 + (size_t)e * H * I, live ? (uint32_t)H * I : 0u);
+    };
+    {
+      uint32_t so;
+      const __amdgpu_buffer_rsrc_t r = src_of(b, wq, so);
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        buf[kb][0] = ld16s<CP_NT>(r, vo, so + kb * CS);
+        buf[kb][1] = ld16s<CP_NT>(r, vo, so + kb * CS + HO);
+      }
+    }
+    // every quantised mid block of this launch
+    if (ntask) {
+      const int i = w * 64 + l;
+      ok = wait_until(guard, MONO_SITE_MQ, [&]() {
+        const uint32_t rv = i < nd * NKB ? ld_dev(&ready[i]) : tag;
+        return __all(rv == tag);
+      });
+    }
+    ok = cta_all(ok, ok_s);
+    if (ok && ntask) {
+      // mid rows + coefficients into LDS: 32 lanes of 16 B a slot row
+      const __amdgpu_buffer_rsrc_t rmq = rsrc(mq, (uint32_t)G::SZ_MQ);
+      const int nsl = R * MOE_SLOTS;
+      constexpr int CPR = I / 16;  // 16-byte pieces of a mid row
+      for (int i = tid; i < nsl * CPR; i += G::THREADS) {
+        const int s = i / CPR, c = i % CPR;
+        const int ut = rl.slot_ut[s];
+        const uint32_t src_off = (uint32_t)(((ut >> 8) * MOE_MAXR + (ut & 255)) * I + c * 16);
+        *reinterpret_cast<v4i*>(mql + s * I + c * 16) = ld16<CP_DEV>(rmq, src_off);
+      }
+      for (int i = tid; i < nsl * NKB; i += G::THREADS) {
+        const int s = i / NKB, kb = i % NKB;
+        const int ut = rl.slot_ut[s];
+        mcl[i] = __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
+            &mcoef[((size_t)(ut >> 8) * MOE_MAXR + (ut & 255)) * NKB + kb])));
+      }
+    }
+    __syncthreads();
+    for (int f = b; f < (ok ? ntask : 0); f += nblk) {
+      const int rg0 = f * G::DNT + 16 * half;
       v4f acc = {0.f, 0.f, 0.f, 0.f};
-      v4i buf[2][NKB][2];
-      auto issue_dn = [&](int u, int s) {
-        const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
-        const __amdgpu_buffer_rsrc_t r = rsrc(p.w2 + (size_t)e * H * I, (uint32_t)H * I);
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          const uint32_t o = (uint32_t)(rg0 + t) * I + kb * 128 + 32 * grp;
-          buf[s][kb][0] = ld16<CP_NT>(r, o);
-          buf[s][kb][1] = ld16<CP_NT>(r, o + 16);
+      for (int u = wq; u < nd; u += QW) {
+        int fn = f, un = u + QW;
+        if (un >= nd) {
+          fn = f + nblk;
+          un = wq;
         }
-      };
-      // expert u from slot s: wait for its quantised mid, MFMA into acc
-      auto consume_dn = [&](int u, int s) -> bool {
+        uint32_t son;
+        const __amdgpu_buffer_rsrc_t rn = src_of(fn, un, son);
         const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
-        const uint32_t mask = rl.umask[u];
-        if (!wait_until(guard, MONO_SITE_MQ, [&]() {
-              const uint32_t rv = l < NKB ? ld_dev(&ready[u * NKB + l]) : tag;
-              return __all(rv == tag);
-            }))
-          return false;
-        const bool on = t < R && ((mask >> t) & 1u);
-        const size_t mrow = ((size_t)u * MOE_MAXR + t) * I;
-        const int s2b = __builtin_amdgcn_readfirstlane((e * (H / 128) + rg0 / 128) * (I / 128));
+        const int sl = slot_of(rl, u, rl.umask[u], t);
+        const bool on = sl >= 0;
+        const int bb = (on ? sl : 0) * I + 32 * grp;
+        const int s2b =
+            __builtin_amdgcn_readfirstlane((e * (H / 128) + rg0 / 128) * (I / 128));
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-          const uint32_t mo = (uint32_t)(mrow + kb * 128 + 32 * grp);
-          v4i b0 = ld16<CP_DEV>(rmq, mo), b1 = ld16<CP_DEV>(rmq, mo + 16);
-          const float cf = on ? __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
-                                    &mcoef[((size_t)u * MOE_MAXR + t) * NKB + kb])))
-                              : 0.f;
-          if (!on) {  // rows not routed here: stale bytes could be NaN codes
-            b0 = v4i{0, 0, 0, 0};
-            b1 = v4i{0, 0, 0, 0};
-          }
+          const v4i z = {0, 0, 0, 0};
+          const v4i b0 = on ? *reinterpret_cast<const v4i*>(mql + bb + kb * 128) : z;
+          const v4i b1 = on ? *reinterpret_cast<const v4i*>(mql + bb + kb * 128 + 16) : z;
+          const float cf = on ? mcl[(on ? sl : 0) * NKB + kb] : 0.f;
           const v4f zero = {0.f, 0.f, 0.f, 0.f};
-          acc += mfma_fp8(cat8(buf[s][kb][0], buf[s][kb][1]), cat8(b0, b1), zero) *
-                 (sld(p.s2, s2b + kb) * cf);
+          const v4f d = mfma_fp8(cat8(buf[kb][0], buf[kb][1]), cat8(b0, b1), zero);
+          buf[kb][0] = ld16s<CP_NT>(rn, vo, son + kb * CS);
+          buf[kb][1] = ld16s<CP_NT>(rn, vo, son + kb * CS + HO);
+          acc += d * (sld(p.s2, s2b + kb) * cf);
           __builtin_amdgcn_sched_barrier(0);
         }
-        return true;
-      };
-      // experts u = wq, wq + 8, ...: slot 0 holds even steps, slot 1 odd ones
-      int u = wq;
-      if (u < nd) issue_dn(u, 0);
-      while (u < nd && ok) {
-        if (u + QW < nd) issue_dn(u + QW, 1);
-        ok = consume_dn(u, 0);
-        u += QW;
-        if (u >= nd || !ok) break;
-        if (u + QW < nd) issue_dn(u + QW, 0);
-        ok = consume_dn(u, 1);
-        u += QW;
       }
       // fixed-order reduction over each half's 8 waves, then the residual add
       red[w][l] = acc;
@@ -454,8 +536,8 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         float ys = 0.f;
 #pragma unroll
         for (int i = 0; i < QW; ++i) ys += red[h * QW + i][L][v];
-        if (tok < R && ok) {
-          const int col = r0 + row;
+        if (tok < R) {
+          const int col = f * G::DNT + row;
           const float av = bf16_lo(p.a[tok * H + col]);
           p.out[tok * H + col] = (uint16_t)bf16_bits(av + ys);
           if (p.y) p.y[tok * H + col] = ys;
@@ -466,6 +548,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   }
 
   // ---------------------------------------------------------------- exit
+  stamp(p.timeline, MONO_TL_DOWN);
   __syncthreads();
   if (tid == 0) {
     uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
@@ -476,6 +559,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       st_dev(gw + MONO_GUARD_EPOCH, tag);
     }
   }
+  stamp(p.timeline, MONO_TL_END);
 }
 
 }  // namespace mono
@@ -525,15 +609,19 @@ extern "C" int mono_moe_fp8_launch(const MonoMoeFp8Args* a, mono_stream_t stream
   }
   p.fault_site = a->fault_site;
   p.fault_after = a->fault_after;
+  p.timeline = a->timeline;
   int grid = 0;
   int rc = monokernel_grid(&grid);
   if (rc) return rc;
+  if (a->layout != MONO_LAYOUT_ROWMAJOR && a->layout != MONO_LAYOUT_AITER16)
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: unknown weight layout");
   if (a->hidden == 7168 && a->inter == 512) {
-    rc = check_coresident(moe_fp8_kernel<7168, 512>, 1024, 0,
+    auto k = a->layout == MONO_LAYOUT_AITER16 ? moe_fp8_kernel<7168, 512, true>
+                                              : moe_fp8_kernel<7168, 512, false>;
+    rc = check_coresident(k, 1024, 0,
                           "mono_moe_fp8_launch: one 1024-thread CTA per CU does not fit");
     if (rc) return rc;
-    hipLaunchKernelGGL((moe_fp8_kernel<7168, 512>), dim3(grid), dim3(1024), 0,
-                       (hipStream_t)stream, p);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);
   } else {
     return set_error(MONO_E_ARG, "mono_moe_fp8_launch: unsupported hidden/inter");
   }

@@ -108,24 +108,81 @@ __device__ inline uint32_t xor_u(uint32_t v, int m) {
   return (uint32_t)__shfl_xor((int)v, m, WAVE);
 }
 
-template <int MAXM = 32>
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m <= MAXM; m <<= 1) v += xor_f(v, m);
+// Butterfly reductions on the VALU (no LDS crossbar): DPP quad_perm pairs lanes i^1 and
+// i^2, row_half_mirror i <-> 7-i and row_mirror i <-> 15-i within each row of 16 lanes,
+// then v_permlane16_swap / v_permlane32_swap exchange rows. Every lane of a group ends
+// with the same bits (each step combines the same two operands, commutatively).
+template <int CTRL>
+__device__ inline uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __uint_as_float(dpp_u<CTRL>(__float_as_uint(v)));
+}
+constexpr int DPP_XOR1 = 0xB1;       // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4E;       // quad_perm [2, 3, 0, 1]
+constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_MIRROR = 0x140;
+
+// the partner row's value (rows of 16 lanes paired as 0-1, 2-3), or the other half
+__device__ inline void swap16(float v, float& a, float& b) {
+  auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(s[0]);
+  b = __uint_as_float(s[1]);
+}
+__device__ inline void swap32(float v, float& a, float& b) {
+  auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(s[0]);
+  b = __uint_as_float(s[1]);
+}
+
+// reduction over each row of 16 lanes
+template <class Op>
+__device__ inline float red16(float v, Op op) {
+  v = op(v, dpp_f<DPP_XOR1>(v));
+  v = op(v, dpp_f<DPP_XOR2>(v));
+  v = op(v, dpp_f<DPP_HALF_MIRROR>(v));
+  v = op(v, dpp_f<DPP_MIRROR>(v));
   return v;
 }
-template <int MAXM = 32>
-__device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int m = 1; m <= MAXM; m <<= 1) v = fmaxf(v, xor_f(v, m));
-  return v;
+// reduction over the wave
+template <class Op>
+__device__ inline float red64(float v, Op op) {
+  v = red16(v, op);
+  float a, b;
+  swap16(v, a, b);
+  v = op(a, b);
+  swap32(v, a, b);
+  return op(a, b);
 }
+struct OpAdd {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+__device__ inline float wave_sum(float v) { return red64(v, OpAdd()); }
+__device__ inline float wave_max(float v) { return red64(v, OpMax()); }
+__device__ inline float row16_max(float v) { return red16(v, OpMax()); }
+
+// maximum of a u64 over the wave
 __device__ inline uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 1; m <= 32; m <<= 1) {
-    uint32_t lo = xor_u((uint32_t)v, m), hi = xor_u((uint32_t)(v >> 32), m);
-    uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
+  auto mx = [](uint64_t a, uint64_t b) { return a > b ? a : b; };
+  auto step = [&](uint32_t lo, uint32_t hi) { return ((uint64_t)hi << 32) | lo; };
+  v = mx(v, step(dpp_u<DPP_XOR1>((uint32_t)v), dpp_u<DPP_XOR1>((uint32_t)(v >> 32))));
+  v = mx(v, step(dpp_u<DPP_XOR2>((uint32_t)v), dpp_u<DPP_XOR2>((uint32_t)(v >> 32))));
+  v = mx(v, step(dpp_u<DPP_HALF_MIRROR>((uint32_t)v), dpp_u<DPP_HALF_MIRROR>((uint32_t)(v >> 32))));
+  v = mx(v, step(dpp_u<DPP_MIRROR>((uint32_t)v), dpp_u<DPP_MIRROR>((uint32_t)(v >> 32))));
+  {
+    auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+    v = mx(step(lo[0], hi[0]), step(lo[1], hi[1]));
+  }
+  {
+    auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+    v = mx(step(lo[0], hi[0]), step(lo[1], hi[1]));
   }
   return v;
 }
@@ -178,15 +235,20 @@ struct Guard {
   uint32_t* host_err;  // pinned host mirror of the first error (may be null)
   uint64_t deadline;   // ticks of the 100 MHz clock
   int fault_site;      // test fault injection: this wait site never completes
+  uint64_t slack;      // deadline multiple of the other waits while a fault is injected
   uint64_t t0;
 
-  __device__ void init(int32_t* w, uint32_t* he, int fsite, uint32_t epoch, uint32_t fafter) {
+  // `head` = guard words 0-3 as read once by the CTA (one coherent load, shared in LDS:
+  // every thread reading the block itself would pile thousands of requests on one line)
+  __device__ void init(int32_t* w, uint32_t* he, int fsite, const uint32_t* head, uint32_t fafter) {
     words = w;
     host_err = he;
-    uint32_t lo = ld_dev(reinterpret_cast<uint32_t*>(w) + MONO_GUARD_DEADLINE_LO);
-    uint32_t hi = ld_dev(reinterpret_cast<uint32_t*>(w) + MONO_GUARD_DEADLINE_HI);
-    deadline = ((uint64_t)hi << 32) | lo;
+    const uint32_t epoch = head[MONO_GUARD_EPOCH];
+    deadline = ((uint64_t)head[MONO_GUARD_DEADLINE_HI] << 32) | head[MONO_GUARD_DEADLINE_LO];
     fault_site = (fsite > 0 && epoch >= fafter) ? fsite : 0;
+    // the injected wait times out first: waits downstream of it (which stall as a
+    // consequence) get four times as long, so the error word names the injected site
+    slack = fault_site ? 4 : 1;
     t0 = 0;
   }
   __device__ bool aborted() const {
@@ -209,11 +271,26 @@ struct Guard {
   }
 };
 
+// timeline stamp: thread 0 of the CTA writes the 100 MHz clock at mark k
+__device__ inline void stamp(uint64_t* tl, int k) {
+  if (tl && threadIdx.x == 0) tl[blockIdx.x * MONO_TL_COLS + k] = wall_clock64();
+}
+
 // CTA-uniform success: false if any thread of the CTA failed or the launch aborted.
 // Call from every thread (three barriers); `ok_s` is a __shared__ int.
 __device__ inline bool cta_ok(bool mine, Guard& g, int& ok_s) {
   __syncthreads();
   if (threadIdx.x == 0) ok_s = g.aborted() ? 0 : 1;
+  __syncthreads();
+  if (!mine) ok_s = 0;
+  __syncthreads();
+  return ok_s != 0;
+}
+
+// CTA-uniform AND of the threads' flags, without reading the global abort flag
+__device__ inline bool cta_all(bool mine, int& ok_s) {
+  __syncthreads();
+  if (threadIdx.x == 0) ok_s = 1;
   __syncthreads();
   if (!mine) ok_s = 0;
   __syncthreads();
@@ -234,7 +311,7 @@ __device__ inline bool wait_until(Guard& g, int site, F ready) {
       if (g.aborted()) return false;
       uint64_t now = wall_clock64();
       if (start == 0) start = now;
-      if (now - start > g.deadline) {
+      if (now - start > (stalled ? g.deadline : g.deadline * g.slack)) {
         g.fail(site);
         return false;
       }

@@ -19,7 +19,7 @@ from typing import Optional
 
 import torch
 
-from .. import _lib
+from .. import _lib, layouts
 from ..runtime import MonoRuntime
 from .config import DSV32, MAX_ROWS, LayerConfig
 
@@ -44,6 +44,7 @@ class MoeFp8Weights:
     """One layer's FFN weights in SGLang's loaded layout, read in place.
 
     w13 E4M3 [E + 1, 2 I, H] (gate rows, then up rows; the shared expert is id E),
+    row-major or in AITER's (16, 16) shuffle (``layout``; ``layouts.py``),
     s13 f32 [E + 1, 2 I / 128, H / 128] (``w13_weight_scale_inv``), w2 E4M3 [E + 1, H, I],
     s2 f32 [E + 1, H / 128, I / 128]; router w_r bf16 [E, H], bias f32 [E]
     (``e_score_correction_bias``), post-attention norm g_post bf16 [H]."""
@@ -55,9 +56,12 @@ class MoeFp8Weights:
     s13: torch.Tensor
     w2: torch.Tensor
     s2: torch.Tensor
+    layout: str = layouts.ROWMAJOR  # of w13 and w2: "rowmajor" or "aiter16"
 
     def validate(self, cfg: LayerConfig, device) -> None:
         h, i, e = cfg.hidden, cfg.inter, cfg.experts
+        if self.layout not in layouts.LAYOUTS:
+            raise ValueError(f"layout {self.layout!r}: one of {layouts.LAYOUTS}")
         _need(self.g_post, "g_post", torch.bfloat16, (h,), device)
         _need(self.w_r, "w_r", torch.bfloat16, (e, h), device)
         _need(self.bias, "bias", torch.float32, (e,), device)
@@ -100,7 +104,7 @@ class MoeFp8Op:
 
     def launch(self, a: torch.Tensor, y: Optional[torch.Tensor] = None,
                routing: Optional[MoeRouting] = None, out: Optional[torch.Tensor] = None,
-               stream=None) -> torch.Tensor:
+               stream=None, timeline: Optional[torch.Tensor] = None) -> torch.Tensor:
         """a bf16 [R, H] -> a + MoE(a), bf16 [R, H] (``out`` or a runtime buffer)."""
         cfg = self.cfg
         if a.dim() != 2 or not 1 <= a.shape[0] <= self.max_rows:
@@ -117,10 +121,13 @@ class MoeFp8Op:
             _need(routing.scores, "scores", torch.float32, (r, cfg.experts), self.device)
             _need(routing.ids, "ids", torch.int32, (r, cfg.top_k + 1), self.device)
             _need(routing.weights, "weights", torch.float32, (r, cfg.top_k + 1), self.device)
+        if timeline is not None:
+            _need(timeline, "timeline", torch.int64, (self.rt.grid, _lib.TL_COLS), self.device)
         self.rt.before_launch()
         w = self.w
         args = _lib.MonoMoeFp8Args(
             rows=r, hidden=cfg.hidden, inter=cfg.inter, experts=cfg.experts,
+            layout=_lib.LAYOUT_AITER16 if w.layout == layouts.AITER16 else _lib.LAYOUT_ROWMAJOR,
             eps=cfg.rms_eps, route_scale=cfg.route_scale,
             a=a.data_ptr(), out=out.data_ptr(), g_post=w.g_post.data_ptr(),
             w_r=w.w_r.data_ptr(), bias=w.bias.data_ptr(), w13=w.w13.data_ptr(),
@@ -132,6 +139,7 @@ class MoeFp8Op:
             scratch=self.rt.scratch.data_ptr(), guard=self.rt.guard.data_ptr(),
             host_error=self.rt.host_error.data_ptr(),
             fault_site=int(self.fault[0]), fault_after=int(self.fault[1]),
+            timeline=timeline.data_ptr() if timeline is not None else None,
         )
         with torch.cuda.device(self.device):
             _lib.check(_lib.lib().mono_moe_fp8_launch(ctypes.byref(args),

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import torch
 
+from .. import layouts
 from .config import DSV32, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
 from .moe import MoeFp8Weights
 
@@ -23,9 +24,10 @@ def _gen(device, seed: int, family: int) -> torch.Generator:
 
 
 def moe_fp8_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
-                    experts: int | None = None) -> MoeFp8Weights:
+                    experts: int | None = None, layout: str = layouts.ROWMAJOR) -> MoeFp8Weights:
     """Config 2 weights; ``experts`` limits how many expert slots get random values
-    (the rest stay zero) to keep CPU-side fixtures small."""
+    (the rest stay zero) to keep CPU-side fixtures small; ``layout`` "aiter16" stores the
+    same values in AITER's (16, 16) shuffle."""
     dev = torch.device(device)
     h, i, e = cfg.hidden, cfg.inter, cfg.experts
     n = e + 1
@@ -43,7 +45,20 @@ def moe_fp8_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
     gs = _gen(dev, seed, 5)
     s13 = (0.5 + 1.5 * torch.rand(n, 2 * i // 128, h // 128, generator=gs, device=dev)) / 448.0
     s2 = (0.5 + 1.5 * torch.rand(n, h // 128, i // 128, generator=gs, device=dev)) / 448.0
-    return MoeFp8Weights(g_post=g_post, w_r=w_r, bias=bias, w13=w13, s13=s13, w2=w2, s2=s2)
+    if layout == layouts.AITER16:
+        for x in range(n):  # expert by expert: no 2x peak copy of ~3 GB
+            w13[x] = layouts.shuffle_16x16(w13[x].view(torch.uint8)).view(FP8)
+            w2[x] = layouts.shuffle_16x16(w2[x].view(torch.uint8)).view(FP8)
+    return MoeFp8Weights(g_post=g_post, w_r=w_r, bias=bias, w13=w13, s13=s13, w2=w2, s2=s2,
+                         layout=layout)
+
+
+def rowmajor_expert(w: MoeFp8Weights, e: int):
+    """Expert e's (w13, s13, w2, s2) on the host as numpy, row-major (for the oracle)."""
+    w13, w2 = w.w13[e].view(torch.uint8), w.w2[e].view(torch.uint8)
+    if w.layout == layouts.AITER16:
+        w13, w2 = layouts.unshuffle_16x16(w13), layouts.unshuffle_16x16(w2)
+    return (w13.cpu().numpy(), w.s13[e].cpu().numpy(), w2.cpu().numpy(), w.s2[e].cpu().numpy())
 
 
 def rows_bf16(rows: int, hidden: int, device, seed: int = 0) -> torch.Tensor:

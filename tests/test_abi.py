@@ -80,3 +80,22 @@ def test_guard_words_describe():
     words[_lib.GUARD_ERR_FAULT] = 1
     msg = guard.describe(words)
     assert "mid" in msg and "fault-injected 1" in msg
+
+
+def test_aiter16_shuffle_is_the_reference_index_map():
+    """Element (n, k) of the (16, 16) shuffle sits at byte
+    ((n // 16 * K // 32 + k // 32) * 2 + k % 32 // 16) * 256 + n % 16 * 16 + k % 16
+    (ld_fp8_chunk, glm53/gfx950/kernel.py:787-808), and unshuffle inverts it."""
+    import torch
+
+    from sgl_amd_mono_amd import layouts
+
+    n, k = 48, 96
+    w = torch.arange(n * k, dtype=torch.int64).reshape(n, k)
+    s = layouts.shuffle_16x16(w).reshape(-1)
+    for nn, kk in [(0, 0), (5, 17), (16, 31), (47, 95), (33, 64)]:
+        pos = ((nn // 16 * (k // 32) + kk // 32) * 2 + kk % 32 // 16) * 256 + nn % 16 * 16 + kk % 16
+        assert int(s[pos]) == nn * k + kk
+    assert torch.equal(layouts.unshuffle_16x16(layouts.shuffle_16x16(w)), w)
+    e = torch.randint(0, 255, (3, 32, 64), dtype=torch.uint8)
+    assert torch.equal(layouts.unshuffle_16x16(layouts.shuffle_16x16(e)), e)

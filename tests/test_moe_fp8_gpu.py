@@ -23,6 +23,11 @@ def layer(gpu):
     return synthetic.moe_fp8_weights(gpu, seed=0)
 
 
+@pytest.fixture(scope="module")
+def layer_aiter(gpu):
+    return synthetic.moe_fp8_weights(gpu, seed=0, layout="aiter16")
+
+
 def _routing(rows, dev):
     return MoeRouting(scores=torch.empty(rows, E, dtype=torch.float32, device=dev),
                       ids=torch.empty(rows, 9, dtype=torch.int32, device=dev),
@@ -30,12 +35,7 @@ def _routing(rows, dev):
 
 
 def _cpu_experts(w, ids):
-    out = {}
-    for e in np.unique(ids):
-        e = int(e)
-        out[e] = (w.w13[e].view(torch.uint8).cpu().numpy(), w.s13[e].cpu().numpy(),
-                  w.w2[e].view(torch.uint8).cpu().numpy(), w.s2[e].cpu().numpy())
-    return out
+    return {int(e): synthetic.rowmajor_expert(w, int(e)) for e in np.unique(ids)}
 
 
 def _run(op, a):
@@ -47,9 +47,12 @@ def _run(op, a):
     return out, y, rt
 
 
-@pytest.mark.parametrize("rows", [1, 4, 8, 16])
-def test_moe_fp8_matches_oracle(layer, gpu, rows):
-    print(f"case rows={rows}", flush=True)
+@pytest.mark.parametrize("rows,layout", [(1, "rowmajor"), (4, "rowmajor"), (8, "rowmajor"),
+                                         (16, "rowmajor"), (1, "aiter16"), (8, "aiter16"),
+                                         (16, "aiter16")])
+def test_moe_fp8_matches_oracle(request, gpu, rows, layout):
+    print(f"case rows={rows} layout={layout}", flush=True)
+    layer = request.getfixturevalue("layer" if layout == "rowmajor" else "layer_aiter")
     op = MoeFp8Op(layer, gpu, max_rows=16)
     a = synthetic.rows_bf16(rows, H, gpu, seed=rows)
     out, y, rt = _run(op, a)
