@@ -5,8 +5,9 @@ Workload (N = 1): BASELINE.json configs[1], the FP8 routed MoE of one GPU's TP=4
 f32 block scales) at 8 decode rows, as one persistent launch. A step is one launch
 over one batch of 8 rows, on one of ``--layers`` independently seeded layers in turn
 (about 2.8 GB of experts each, so the 256 MB MALL cannot serve the weights). Inputs are
-resident in HBM before the timed region; the timed region is bracketed by
-``torch.cuda.synchronize()`` and measured with HIP events on the launch stream.
+resident in HBM before the timed region; the timed region replays a HIP graph of one
+launch per layer, is bracketed by ``torch.cuda.synchronize()`` and is measured with HIP
+events on the replay stream.
 
 ``roofline``: algorithmic bytes per launch = every distinct expert the batch actually
 routed to (shared included) x 11,012,736 B + the router 3,670,016 B + the rows in and
@@ -139,24 +140,44 @@ def main():
     act_bytes = rows * DSV32.hidden * 2 * 2
     bytes_per = [d * EXPERT_BYTES + ROUTER_BYTES + act_bytes for d in distinct]
 
-    stream = torch.cuda.current_stream()
+    # One HIP graph holds a launch on each of the L layers in turn (as the reference's
+    # timing harness replays a captured step of launches, test/kernels/glm53/
+    # time_layers.py:38-76); the timed region replays it, so the host issues nothing
+    # per launch. Eager warm-up first, then graph warm-up replays.
     for s in range(args.warmup):
         ops[s % L].launch(inputs[s % L], out=outs[s % L])
     torch.cuda.synchronize()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        for i in range(L):  # warm-up on the capture stream
+            ops[i].launch(inputs[i], out=outs[i])
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=cs):
+        for i in range(L):
+            ops[i].launch(inputs[i], out=outs[i])
+    reps = max(1, args.steps // L)
+    steps = reps * L
+    for _ in range(max(1, args.warmup // L)):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
-    for s in range(args.steps):
-        ops[s % L].launch(inputs[s % L], out=outs[s % L])
+    for _ in range(reps):
+        graph.replay()
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     for op in ops:
         op.rt.check()
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = ev0.elapsed_time(ev1) / steps
     us = ms * 1e3
-    avg_bytes = sum(bytes_per[s % L] for s in range(args.steps)) / args.steps
+    args.steps = steps
+    avg_bytes = sum(bytes_per) / L
     achieved = avg_bytes / (us * 1e-6) / 1e9  # GB/s
     print(f"bench: {args.steps} launches, {us:.1f} us each (wall {wall * 1e3 / args.steps:.1f} "
           f"ms/step), distinct experts {distinct}", file=sys.stderr, flush=True)

@@ -96,8 +96,25 @@ __device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], cons
   }
 }
 
+// exclusive prefix sum over the wave's lanes of a small count v < 2^BITS: one ballot
+// per bit and a masked popcount (v_mbcnt), no cross-lane data movement
+template <int BITS>
+__device__ inline int wave_prefix(int v, int& total) {
+  int pre = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < BITS; ++k) {
+    const uint64_t bal = __ballot((v >> k) & 1);
+    pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                         __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))
+           << k;
+    total += __popcll(bal) << k;
+  }
+  return pre;
+}
+
 // Compact rl.mask into the distinct list (one whole wave): u = 0 the shared expert,
-// then routed ids ascending.
+// then routed ids ascending; then the (expert, row) slots.
 __device__ inline void build_distinct(RouteLds& rl, int rows) {
   const int l = lane_id();
   uint32_t m[4];
@@ -107,51 +124,32 @@ __device__ inline void build_distinct(RouteLds& rl, int rows) {
     m[i] = rl.mask[4 * l + i];
     cnt += m[i] != 0;
   }
-  // inclusive scan of cnt over lanes
-  int inc = cnt;
+  int nroute = 0;
+  int pos = 1 + wave_prefix<3>(cnt, nroute);
+  const int nd = 1 + nroute;
+  const uint32_t shared_mask = rows >= 32 ? 0xFFFFFFFFu : ((1u << rows) - 1u);
+  // (expert, row) slots, experts in u order: slot base of each of this lane's experts
+  int c2 = 0;
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int o = __shfl_up(inc, d, WAVE);
-    if (l >= d) inc += o;
-  }
-  int pos = 1 + inc - cnt;
+  for (int i = 0; i < 4; ++i) c2 += __popc(m[i]);
+  int nslot = 0;
+  int s = __popc(shared_mask) + wave_prefix<7>(c2, nslot);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (m[i]) {
       rl.uexp[pos] = 4 * l + i;
       rl.umask[pos] = m[i];
+      rl.uslot[pos] = s;
+      for (uint32_t mm = m[i]; mm; mm &= mm - 1) rl.slot_ut[s++] = (pos << 8) | (__ffs(mm) - 1);
       ++pos;
     }
-  if (l == 63) rl.nd = 1 + inc;
   if (l == 0) {
+    rl.nd = nd;
     rl.uexp[0] = MOE_SHARED;
-    rl.umask[0] = rows >= 32 ? 0xFFFFFFFFu : ((1u << rows) - 1u);
-  }
-  // (expert, row) slots: the rows of each distinct expert, experts in u order. Every
-  // row has 9 distinct slots, so there are exactly 9 R of them; u < 4 * 64 covers nd.
-  const int nd = 1 + __shfl(inc, 63, WAVE);
-  uint32_t um[4];
-  int c2 = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int u = 4 * l + i;
-    um[i] = u < nd ? rl.umask[u] : 0u;
-    c2 += __popc(um[i]);
-  }
-  int inc2 = c2;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int o = __shfl_up(inc2, d, WAVE);
-    if (l >= d) inc2 += o;
-  }
-  int s = inc2 - c2;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int u = 4 * l + i;
-    if (u < nd) {
-      rl.uslot[u] = s;
-      for (uint32_t m = um[i]; m; m &= m - 1) rl.slot_ut[s++] = (u << 8) | (__ffs(m) - 1);
-    }
+    rl.umask[0] = shared_mask;
+    rl.uslot[0] = 0;
+    int s0 = 0;
+    for (uint32_t mm = shared_mask; mm; mm &= mm - 1) rl.slot_ut[s0++] = __ffs(mm) - 1;
   }
 }
 

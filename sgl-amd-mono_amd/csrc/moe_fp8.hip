@@ -25,6 +25,8 @@
 // (quant_scaled), :1665-1669 (W == 1 residual add).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "moe_common.h"
 #include "mono_abi.h"
 
@@ -56,7 +58,10 @@ struct MoeFp8Geom {
   static constexpr size_t SZ_MCOEF = (size_t)MOE_NDIST * MOE_MAXR * NKB * 4;
   static constexpr size_t OFF_READY = OFF_MCOEF + SZ_MCOEF;
   static constexpr size_t SZ_READY = (size_t)MOE_NDIST * NKB * 4;
-  static constexpr size_t BYTES = (OFF_READY + SZ_READY + 255) & ~(size_t)255;
+  // work-queue counters (zero at launch entry; the last CTA out re-zeroes them)
+  static constexpr size_t OFF_QUEUE = (OFF_READY + SZ_READY + 255) & ~(size_t)255;
+  static constexpr int NQUEUE = 4;
+  static constexpr size_t BYTES = (OFF_QUEUE + NQUEUE * 4 + 255) & ~(size_t)255;
 };
 
 struct MoeFp8Params {
@@ -115,7 +120,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   __shared__ v4i xq_lds[QW * KCW * 2 * 64];
   __shared__ float xs_lds[QW * KCW][16];  // activation block scale per (chunk, row)
   __shared__ v4f red[G::WAVES][64];
-  __shared__ float red_small[2][2][8];
+  __shared__ float red_small[2][2][16];
+  __shared__ v4i wr_lds[H / 8];  // this CTA's router row (bf16), staged like the norm weight
+  __shared__ int next_s;
   __shared__ float rstd_s[MOE_MAXR];
   __shared__ int ok_s;
 
@@ -124,20 +131,41 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   uint8_t* mq = p.scratch + G::OFF_MQ;
   float* mcoef = reinterpret_cast<float*>(p.scratch + G::OFF_MCOEF);
   uint32_t* ready = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
+  uint32_t* queue = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_QUEUE);
 
   __shared__ uint32_t head_s[4];
+  stamp(p.timeline, MONO_TL_START);
+  // the first eight rows: two waves a row, lane l the 8 values at q * 512 + l * 8 of its
+  // half's 7 slices; issued first so they fly with the staging and guard loads below
+  constexpr int NQ0 = H / 1024;
+  v4i av0[NQ0];
+  {
+    const int r = w / 2, ch = w % 2;
+    const bool live = r < R;
+    const __amdgpu_buffer_rsrc_t rar = rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
+    const uint32_t base = (uint32_t)(ch * NQ0 * 512 + l * 8) * 2;
+#pragma unroll
+    for (int q = 0; q < NQ0; ++q) av0[q] = ld16<CP_NONE>(rar, base + q * 1024);
+  }
   const __amdgpu_buffer_rsrc_t rg = rsrc(p.g_post, H * 2);
   // the post-attention norm weight, the same for every row, into LDS (over the
   // reduction buffer, idle until stage 2), ahead of the guard read so both overlap
   v4i* g_lds = reinterpret_cast<v4i*>(&red[0][0]);
   static_assert(H * 2 <= (int)sizeof(red), "norm weight staging");
   for (int i = tid; i < H / 8; i += G::THREADS) g_lds[i] = ld16<CP_NONE>(rg, i * 16);
+  {
+    const bool has = b < MOE_NEXP;
+    const __amdgpu_buffer_rsrc_t rw0 =
+        rsrc(p.w_r + (size_t)(has ? b : 0) * H, has ? H * 2 : 0);
+    for (int i = tid; i < H / 8; i += G::THREADS) wr_lds[i] = ld16<CP_NT>(rw0, i * 16);
+  }
   if (tid == 0) {
     const v4i h = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)h[i];
   }
   for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
+  if (tid == 0) ok_s = 1;
   __syncthreads();
   const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
   Guard guard;
@@ -146,29 +174,18 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
 
 
   // ---------------------------------------------------------------- stage 0
-  stamp(p.timeline, MONO_TL_START);
-  // A pair of waves owns a row: wave w takes row w % 8 (+ 8 in the second pass when
-  // R > 8) and column half w / 8. Lane l holds the 8 values at q * 512 + l * 8 of each of
-  // its half's 7 slices q, so the row, the norm weight and the router row come in with
-  // one round trip of 21 loads a lane. The E4M3 codes go to xq_lds in the MFMA B-operand
-  // image of stage 2 (chunk kc = q * 4 + l / 16; K group (l % 16) / 4; byte (l % 4) * 8).
+  // Each row is owned by WPR waves (2 for R <= 8, else 1), each holding NQ 512-value
+  // slices of it: lane l holds the 8 values at q * 512 + l * 8. One round trip brings the
+  // row; the norm weight and this CTA's router row wait in LDS. The E4M3 codes go to
+  // xq_lds in the MFMA B-operand image of stage 2 (chunk kc = q * 4 + l / 16; K group
+  // (l % 16) / 4; byte (l % 4) * 8).
   {
-    constexpr int NQ = H / 512 / 2;  // slices a half holds
-    static_assert(H % 1024 == 0, "hidden must split into two halves of 512-slices");
-    const int ch = w / 8, wr = w % 8;
-    for (int pass = 0; pass * 8 < R; ++pass) {
-      const int r = pass * 8 + wr;
+    // the row values of pass `row0` (issued at the top of the kernel for the first)
+    auto rows_pass = [&](auto nq_tag, int row0, v4i* av) {
+      constexpr int NQ = decltype(nq_tag)::value;
+      constexpr int WPR = H / 512 / NQ;
+      const int r = row0 + w / WPR, ch = w % WPR;
       const bool live = r < R;
-      const __amdgpu_buffer_rsrc_t rar = rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
-      v4i av[NQ], wv[NQ];
-      const uint32_t base = (uint32_t)(ch * NQ * 512 + l * 8) * 2;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) av[q] = ld16<CP_NONE>(rar, base + q * 1024);
-      const int e0 = b < MOE_NEXP ? b : 0;
-      const __amdgpu_buffer_rsrc_t rwr =
-          rsrc(p.w_r + (size_t)e0 * H, (b < MOE_NEXP && live) ? H * 2 : 0);
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) wv[q] = ld16<CP_NT>(rwr, base + q * 1024);
       float ss = 0.f;
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
@@ -178,29 +195,39 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
       }
       ss = wave_sum(ss);
-      if (l == 0) red_small[0][ch][wr] = ss;
+      if (l == 0 && r < 16) red_small[0][ch][r] = ss;
       __syncthreads();
-      const float rstd = live ? 1.0f / sqrtf((red_small[0][0][wr] + red_small[0][1][wr]) /
-                                             (float)H + p.eps)
-                              : 0.f;
+      float tot = 0.f;
+      if (r < 16) {
+#pragma unroll
+        for (int c = 0; c < WPR; ++c) tot += red_small[0][c][r];
+      }
+      const float rstd = live ? 1.0f / sqrtf(tot / (float)H + p.eps) : 0.f;
+      // widen the packed row again below rather than keep the 8 NQ f32 values of the
+      // sum of squares alive across the barrier
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(av[q]));
       float rp = 0.f;
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
-        float fa[8], fg[8], fw[8], xn[8];
+        const int sl = ch * NQ + q;
+        float fa[8], fg[8], xn[8];
         bf16x8(av[q], fa);
-        bf16x8(g_lds[ch * NQ * 64 + q * 64 + l], fg);
-        bf16x8(wv[q], fw);
+        bf16x8(g_lds[sl * 64 + l], fg);
+        const v4i wv = wr_lds[sl * 64 + l];
         float am = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           xn[i] = fa[i] * rstd * fg[i];
           am = fmaxf(am, fabsf(xn[i]));
-          rp += bf16_round(xn[i]) * fw[i];
         }
+        // router: the normalised row rounded to bf16 pairs, dotted with the bf16 weights
+#pragma unroll
+        for (int d = 0; d < 4; ++d) rp = dot2_bf16(xn[2 * d], xn[2 * d + 1], (uint32_t)wv[d], rp);
         am = row16_max(am);
         const bool nz = am > 0.f;
         const float inv = nz ? FP8_MAX / am : 1.f;
-        const int kc = (ch * NQ + q) * 4 + (l >> 4);
+        const int kc = sl * 4 + (l >> 4);
         if (live) {
           v2i qq;
           qq[0] = (int)pack_fp8x4(clamp_fp8(xn[0] * inv), clamp_fp8(xn[1] * inv),
@@ -213,15 +240,36 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
           *reinterpret_cast<v2i*>(dst) = qq;
           if ((l & 15) == 0) xs_lds[kc][r] = nz ? am * INV_FP8_MAX : 1.f;
         }
+        // one slice per scheduling region: the LDS operands are not hoisted ahead
+        __builtin_amdgcn_sched_barrier(0);
       }
       rp = wave_sum(rp);
-      if (l == 0) red_small[1][ch][wr] = rp;
+      if (l == 0 && r < 16) red_small[1][ch][r] = rp;
       __syncthreads();
-      if (ch == 0 && l == 0 && live && b < MOE_NEXP)
-        st_dev64(&logit_pairs[r * MOE_NEXP + b],
-                 pair(__float_as_uint(red_small[1][0][wr] + red_small[1][1][wr]), tag));
+      if (ch == 0 && l == 0 && live && b < MOE_NEXP) {
+        float lg = 0.f;
+#pragma unroll
+        for (int c = 0; c < WPR; ++c) lg += red_small[1][c][r];
+        st_dev64(&logit_pairs[r * MOE_NEXP + b], pair(__float_as_uint(lg), tag));
+      }
+    };
+    static_assert(H % 1024 == 0, "hidden must split into two halves of 512-slices");
+    // two waves a row, eight rows a pass (the second pass only when R > 8)
+    rows_pass(std::integral_constant<int, NQ0>(), 0, av0);
+    if (R > 8) {
       __syncthreads();
+      const int r = 8 + w / 2, ch = w % 2;
+      const bool live = r < R;
+      const __amdgpu_buffer_rsrc_t rar =
+          rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
+      const uint32_t base = (uint32_t)(ch * NQ0 * 512 + l * 8) * 2;
+      v4i av1[NQ0];
+#pragma unroll
+      for (int q = 0; q < NQ0; ++q) av1[q] = ld16<CP_NONE>(rar, base + q * 1024);
+      rows_pass(std::integral_constant<int, NQ0>(), 8, av1);
     }
+    const int ch = w / 8, wr = w % 8;
+    constexpr int NQ = H / 1024;
     // rows past R: zero B operands, unit scales (stage 2 reads all 16 columns)
     for (int i = tid; i < G::NKC * 16; i += G::THREADS) {
       const int kc = i / 16, r = i % 16;
@@ -301,9 +349,11 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
                 out0 ? p.ids : nullptr, out0 ? p.weights : nullptr);
     }
   }
+  if (!ok) ok_s = 0;
   __syncthreads();
   if (w == 0) build_distinct(rl, R);
-  ok = cta_all(ok, ok_s);
+  __syncthreads();
+  ok = ok_s != 0;
   const int nd = rl.nd;
 
   // ---------------------------------------------------------------- stage 2
@@ -330,6 +380,10 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
                 : (uint32_t)(row0 * H + wq * KCW * 128);
       return rsrc(p.w13 + (size_t)e * (2 * I) * H, live ? 2u * I * H : 0u);
     };
+    // Task hand-out: CTA b starts on task b; later tasks come from a device-wide
+    // counter in order (nblk, nblk + 1, ...), grabbed one task ahead so the ring can be
+    // refilled with the next task while this one runs. Tasks run the same arithmetic on
+    // whichever CTA takes them, so results do not depend on the hand-out.
     int task = b;
     {
       uint32_t so;
@@ -340,6 +394,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         ring[j][1] = ld16s<CP_NT>(r, vo + HO, so + j * CS);
       }
     }
+    if (tid == 0) next_s = task < ntask ? nblk + (int)add_dev(&queue[0], 1u) : ntask;
+    __syncthreads();
+    int next = next_s;
     while (task < ntask) {
       const int u = task / NUG, cc = task % NUG;
       const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
@@ -347,7 +404,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       const float tok_on = ((mask >> t) & 1u) ? 1.f : 0.f;
       const int sbase = __builtin_amdgcn_readfirstlane(
           (e * (2 * I / 128) + (half * I + cc * 16) / 128) * (H / 128) + wq * KCW);
-      const int next = task + nblk;
+      // the task after next (its value lands in LDS before the epilogue barrier)
+      int nn = ntask;
+      if (tid == 0 && next < ntask) nn = nblk + (int)add_dev(&queue[0], 1u);
       uint32_t son;
       const __amdgpu_buffer_rsrc_t rn = task_src(next, son);
       // B operands and scales: the same LDS words every task, read through an opaque
@@ -368,7 +427,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         __builtin_amdgcn_sched_barrier(0);
       }
       red[w][l] = acc;
+      if (tid == 0) next_s = nn;
       __syncthreads();
+      const int after = next_s;
       if (tid < 256) {
         const int row = tid & 15, tok = tid >> 4;  // adjacent threads, adjacent features
         const int L = tok + 16 * (row >> 2), v = row & 3;
@@ -386,6 +447,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       }
       __syncthreads();
       task = next;
+      next = after;
     }
   }
 
@@ -555,6 +617,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
     drain();
     const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
     if (old == (uint32_t)nblk - 1u) {
+      // every other CTA is past its last queue grab: the counters restart at zero
+#pragma unroll
+      for (int i = 0; i < G::NQUEUE; ++i) st_dev(queue + i, 0u);
       st_dev(gw + MONO_GUARD_EXIT, 0u);
       st_dev(gw + MONO_GUARD_EPOCH, tag);
     }

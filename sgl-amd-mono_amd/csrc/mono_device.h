@@ -207,7 +207,16 @@ __device__ inline uint32_t pack_fp8x4(float a, float b, float c, float d) {
 __device__ inline v2f fp8x2_lo(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false); }
 __device__ inline v2f fp8x2_hi(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true); }
 
-__device__ inline float clamp_fp8(float v) { return fminf(fmaxf(v, -FP8_MAX), FP8_MAX); }
+__device__ inline float clamp_fp8(float v) { return __builtin_amdgcn_fmed3f(v, -FP8_MAX, FP8_MAX); }
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+// acc + bf16(a) * w.lo + bf16(b) * w.hi, with a, b rounded to bf16 (nearest even) by
+// v_cvt_pk_bf16_f32 and the products summed by v_dot2c_f32_bf16
+__device__ inline float dot2_bf16(float a, float b, uint32_t w, float acc) {
+  const v2f f = {a, b};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_convertvector(f, v2bf),
+                                        __builtin_bit_cast(v2bf, w), acc, false);
+}
 
 // radix order key of f32 bits: larger key ranks first (+0 above -0)
 __device__ inline uint32_t radix_key(float f) {
