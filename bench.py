@@ -32,6 +32,8 @@ METRIC = "µs per decoder layer at 8 rows; MoE/attn achieved HBM TB/s vs 8 TB/s 
 HBM_PEAK_GBS = 8000.0
 EXPERT_BYTES = 7_340_032 + 1_792 + 3_670_016 + 896  # w13 + s13 + w2 + s2 of one expert
 ROUTER_BYTES = 3_670_016
+# MXFP4 expert of config 4: w13 768 x 1536 B + 768 x 96 scales, w2 3072 x 192 B + 3072 x 12
+MX_EXPERT_BYTES = 1_179_648 + 73_728 + 589_824 + 36_864
 
 
 def parse():
@@ -39,6 +41,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4"),
+                   help="moe_fp8: BASELINE configs[1] (the metric's MoE phase); "
+                        "moe_mxfp4: configs[3], the MXFP4 A16W4 expert block")
     p.add_argument("--rows", type=int, default=8)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -74,6 +79,29 @@ def traffic_from_profiles(name: str):
     return None
 
 
+def cpu_baseline_mxfp4(x_cpu, logits_cpu, w, ids, rows):
+    """The oracle's MXFP4 block on the host, one launch worth (bounded sample)."""
+    import numpy as np
+    import torch
+
+    from oracle import moe as omoe
+    from sgl_amd_mono_amd.dsv32 import synthetic
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    experts = {int(e): synthetic.rowmajor_mxfp4_expert(w, int(e)) for e in np.unique(ids)}
+    parts = [{e: v[k] for e, v in experts.items()} for k in range(4)]
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        omoe.moe_mxfp4(x_cpu, logits_cpu, w.bias.cpu(), *parts, residual=x_cpu)
+        times.append(time.perf_counter() - t0)
+    us = min(times) * 1e6
+    return {"value": round(us, 1), "unit": f"µs per MXFP4 MoE block ({rows} rows)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 MXFP4 block of {rows} rows over its {len(experts)} routed experts, "
+                      f"best of {len(times)}; oracle/moe.py f64 GEMVs on dequantised E2M1"}
+
+
 def cpu_baseline(a_cpu, w, ids, rows):
     """The oracle's MoE block on the host, one launch worth (bounded sample)."""
     import numpy as np
@@ -100,15 +128,45 @@ def cpu_baseline(a_cpu, w, ids, rows):
                       f"best of {len(times)}; oracle/moe.py f64 GEMVs on dequantised E4M3"}
 
 
-def main():
-    args = parse()
-    if args.copy_calibration:
-        copy_calibration()
-        return
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: every GPU box here has one GPU, and the sharded "
-              f"path (TP=4 exchanges) is not built; got --gpus {args.gpus}", file=sys.stderr)
-        sys.exit(2)
+def time_graph(launch, L: int, steps: int, warmup: int):
+    """Average µs of one launch: a HIP graph holds a launch on each of the L layers in
+    turn (as the reference's timing harness replays a captured step of launches,
+    test/kernels/glm53/time_layers.py:38-76) and the timed region replays it, so the
+    host issues nothing per launch. Eager warm-up first, then graph warm-up replays.
+    HIP events bracket the replays on the replay stream. Returns (us, wall_s, steps)."""
+    import torch
+
+    for s in range(warmup):
+        launch(s % L)
+    torch.cuda.synchronize()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        for i in range(L):  # warm-up on the capture stream
+            launch(i)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=cs):
+        for i in range(L):
+            launch(i)
+    reps = max(1, steps // L)
+    for _ in range(max(1, warmup // L)):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) * 1e3 / (reps * L), wall, reps * L
+
+
+def bench_moe_fp8(args):
     import numpy as np
     import torch
 
@@ -140,81 +198,109 @@ def main():
     act_bytes = rows * DSV32.hidden * 2 * 2
     bytes_per = [d * EXPERT_BYTES + ROUTER_BYTES + act_bytes for d in distinct]
 
-    # One HIP graph holds a launch on each of the L layers in turn (as the reference's
-    # timing harness replays a captured step of launches, test/kernels/glm53/
-    # time_layers.py:38-76); the timed region replays it, so the host issues nothing
-    # per launch. Eager warm-up first, then graph warm-up replays.
-    for s in range(args.warmup):
-        ops[s % L].launch(inputs[s % L], out=outs[s % L])
-    torch.cuda.synchronize()
-    cs = torch.cuda.Stream()
-    cs.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(cs):
-        for i in range(L):  # warm-up on the capture stream
-            ops[i].launch(inputs[i], out=outs[i])
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph, stream=cs):
-        for i in range(L):
-            ops[i].launch(inputs[i], out=outs[i])
-    reps = max(1, args.steps // L)
-    steps = reps * L
-    for _ in range(max(1, args.warmup // L)):
-        graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(reps):
-        graph.replay()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    us, wall, steps = time_graph(lambda i: ops[i].launch(inputs[i], out=outs[i]), L,
+                                 args.steps, args.warmup)
     for op in ops:
         op.rt.check()
-    ms = ev0.elapsed_time(ev1) / steps
-    us = ms * 1e3
-    args.steps = steps
-    avg_bytes = sum(bytes_per) / L
-    achieved = avg_bytes / (us * 1e-6) / 1e9  # GB/s
-    print(f"bench: {args.steps} launches, {us:.1f} us each (wall {wall * 1e3 / args.steps:.1f} "
+    print(f"bench: {steps} launches, {us:.1f} us each (wall {wall * 1e3 / steps:.1f} "
           f"ms/step), distinct experts {distinct}", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline(inputs[0].cpu(), weights[0], ids0, rows)
+    config = {
+        "workload": "BASELINE configs[1]: FP8 routed MoE, one GPU's TP=4 share, one "
+                    "persistent launch (post-norm, router, top-8 + shared, W8A8 SwiGLU, "
+                    "down, residual)",
+        "rows": rows, "hidden": DSV32.hidden, "experts": DSV32.experts + 1,
+        "inter": DSV32.inter, "layers_rotated": L, "weight_layout": args.layout,
+        "distinct_experts": distinct,
+    }
+    return us, steps, sum(bytes_per) / L, "fp8", config, "moe_fp8_r8", cpu
 
+
+def bench_moe_mxfp4(args):
+    import numpy as np
+    import torch
+
+    from sgl_amd_mono_amd.dsv32 import synthetic
+    from sgl_amd_mono_amd.dsv32.config import MXFP4_MOE as C
+    from sgl_amd_mono_amd.dsv32.moe import MoeMxfp4Op, MoeRouting
+
+    dev = torch.device("cuda:0")
+    rows, L = args.rows, args.layers
+    print(f"bench: generating {L} layers of MXFP4 experts", file=sys.stderr, flush=True)
+    weights = [synthetic.mxfp4_moe_weights(dev, seed=100 + i, layout=args.layout)
+               for i in range(L)]
+    ops = [MoeMxfp4Op(w, dev, max_rows=rows) for w in weights]
+    xs = [synthetic.rows_bf16(rows, C.hidden, dev, seed=300 + i) for i in range(L)]
+    logits = [synthetic.logits_f32(rows, C.experts, dev, seed=300 + i) for i in range(L)]
+    outs = [torch.empty(rows, C.hidden, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    distinct, ids0 = [], None
+    for i in range(L):
+        rt = MoeRouting(torch.empty(rows, C.experts, device=dev),
+                        torch.empty(rows, 9, dtype=torch.int32, device=dev),
+                        torch.empty(rows, 9, device=dev))
+        ops[i].launch(xs[i], logits[i], res=xs[i], routing=rt, out=outs[i])
+        ops[i].rt.check()
+        ids = rt.ids.cpu().numpy()
+        distinct.append(len(np.unique(ids)))
+        if i == 0:
+            ids0 = ids
+    # rows in, residual in, out; logits
+    act_bytes = rows * C.hidden * 2 * 3 + rows * C.experts * 4
+    bytes_per = [d * MX_EXPERT_BYTES + act_bytes for d in distinct]
+    us, wall, steps = time_graph(
+        lambda i: ops[i].launch(xs[i], logits[i], res=xs[i], out=outs[i]), L, args.steps,
+        args.warmup)
+    for op in ops:
+        op.rt.check()
+    print(f"bench: {steps} launches, {us:.1f} us each (wall {wall * 1e3 / steps:.1f} "
+          f"ms/step), distinct experts {distinct}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(inputs[0].cpu(), weights[0], ids0, rows)
+        cpu = cpu_baseline_mxfp4(xs[0].cpu(), logits[0].cpu(), weights[0], ids0, rows)
+    config = {
+        "workload": "BASELINE configs[3]: MXFP4 (A16W4) routed MoE, one GPU's TP=4 share, "
+                    "one persistent launch (given logits, sigmoid + bias top-8 + shared, "
+                    "E2M1/E8M0 SwiGLU with bf16 mid, down, residual)",
+        "rows": rows, "hidden": C.hidden, "experts": C.experts + 1, "inter": C.inter,
+        "layers_rotated": L, "weight_layout": args.layout, "distinct_experts": distinct,
+    }
+    return us, steps, sum(bytes_per) / L, "bf16 x e2m1", config, f"moe_mxfp4_r{rows}", cpu
 
+
+def main():
+    args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every GPU box here has one GPU, and the sharded "
+              f"path (TP=4 exchanges) is not built; got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    run = bench_moe_fp8 if args.workload == "moe_fp8" else bench_moe_mxfp4
+    us, steps, avg_bytes, dtype, config, prof, cpu = run(args)
+    achieved = avg_bytes / (us * 1e-6) / 1e9  # GB/s
     line = {
         "metric": METRIC,
         "value": round(us, 2),
         "unit": "µs",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": round(us / 1e3, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8",
+        "dtype": dtype,
         "data": "synthetic",
-        "config": {
-            "workload": "BASELINE configs[1]: FP8 routed MoE, one GPU's TP=4 share, one "
-                        "persistent launch (post-norm, router, top-8 + shared, W8A8 SwiGLU, "
-                        "down, residual)",
-            "rows": rows, "hidden": DSV32.hidden, "experts": DSV32.experts + 1,
-            "inter": DSV32.inter, "layers_rotated": L, "weight_layout": args.layout,
-            "distinct_experts": distinct,
-        },
-        "rows_per_s": round(rows / (us * 1e-6), 1),
+        "config": config,
+        "rows_per_s": round(args.rows / (us * 1e-6), 1),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles("moe_fp8_r8"),
+            "traffic": traffic_from_profiles(prof),
             "algorithmic_bytes": int(avg_bytes),
         },
         "cpu_baseline": cpu,

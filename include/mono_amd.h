@@ -130,6 +130,53 @@ typedef struct {
 size_t mono_moe_fp8_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts);
 int mono_moe_fp8_launch(const MonoMoeFp8Args* args, mono_stream_t stream);
 
+/* ------------------------------------------------------------------------------
+ * MXFP4 (A16W4) routed MoE as one persistent launch: the gate logits are given, the
+ * rows x are bf16 and stay bf16 (no activation quant); experts are E2M1 codes (two a
+ * byte, the even K index in the low nibble) with one E8M0 scale per 32 K values.
+ * sigmoid(logits) + bias top-8 (+ the shared expert in slot 0) -> up/gate with each
+ * 32-group dequantised exactly to bf16 -> mid = bf16(silu(g) * u) -> down, route
+ * weighting -> out = bf16(res + y) (or bf16(y) without res).
+ * Replaces the A16W4 expert stage of the reference's FFN launch
+ * (sgl_amd_mono/minimax_m31/a16w4.py:26-92 operands; route as
+ * test/kernels/test_minimax_m31_ffn.py:146-151) and the MXFP4 units of the layer
+ * kernel (sgl_amd_mono/glm53/gfx950/kernel.py:906-995).
+ * Layouts: MONO_LAYOUT_ROWMAJOR = codes [E + 1, N, K / 2], scales [E + 1, N, K / 32];
+ * MONO_LAYOUT_AITER16 = codes in the AITER (16, 16) byte shuffle and scales in the
+ * e8m0 shuffle of sgl_amd_mono/common/mx.py:40-44, [E + 1, N, C] with C = K / 32
+ * rounded up to a multiple of 8 (the map groups columns by 8). */
+typedef struct {
+  int32_t rows;            /* R, 1..16 */
+  int32_t hidden;          /* 3072 */
+  int32_t inter;           /* expert intermediate per GPU: 384 */
+  int32_t experts;         /* routed experts: 256 (the shared one is id 256) */
+  int32_t layout;          /* MONO_LAYOUT_* of the codes and scales */
+  float route_scale;       /* routed_scaling_factor */
+  const void* x;           /* bf16 [R, H]: the expert input rows */
+  const void* res;         /* optional bf16 [R, H]: residual added to y */
+  void* out;               /* bf16 [R, H]: res + y */
+  const float* logits;     /* f32 [R, E]: gate logits */
+  const float* bias;       /* f32 [E]: e_score_correction_bias */
+  const uint8_t* w13;      /* E2M1 x2 [E + 1, 2 I, H / 2]: gate rows then up rows */
+  const uint8_t* s13;      /* E8M0 [E + 1, 2 I, H / 32] (or the AITER16 shuffle) */
+  const uint8_t* w2;       /* E2M1 x2 [E + 1, H, I / 2] */
+  const uint8_t* s2;       /* E8M0 [E + 1, H, I / 32] (or the AITER16 shuffle) */
+  float* y;                /* optional f32 [R, H]: the MoE sum alone */
+  float* scores;           /* optional f32 [R, E]: sigmoid(logit) */
+  int32_t* ids;            /* optional i32 [R, 9]: slot 0 shared (256), then picks */
+  float* weights;          /* optional f32 [R, 9]: slot 0 1.0, then route weights */
+  void* scratch;           /* runtime owned, mono_moe_mxfp4_scratch_bytes() */
+  int32_t* guard;          /* runtime owned guard block */
+  uint32_t* host_error;    /* optional pinned host word: 1 + failed site */
+  int32_t fault_site;      /* test fault injection (MONO_SITE_MID: the down wait) */
+  int32_t fault_after;
+  uint64_t* timeline;      /* optional u64 [grid, 8]: MONO_TL_* stamps (MIDQ: the wait for
+                              every mid tile ended) */
+} MonoMoeMxfp4Args;
+
+size_t mono_moe_mxfp4_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts);
+int mono_moe_mxfp4_launch(const MonoMoeMxfp4Args* args, mono_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

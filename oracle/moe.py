@@ -149,7 +149,7 @@ def moe_fp8(a, g_post, w_r, bias, w13, s13, w2, s2, eps=RMS_EPS, route_scale=ROU
 
 
 def moe_mxfp4(x, logits, bias, w13, s13, w2, s2, route_scale=ROUTE_SCALE, top_k=TOP_K,
-              residual=None):
+              residual=None, routing=None):
     """Config 4: MXFP4 (E2M1 + E8M0 per 32) A16W4 experts on bf16 rows.
 
     x bf16 [R, H]; logits f32 [R, 256] given; route sigmoid + bias top-k as
@@ -157,13 +157,18 @@ def moe_mxfp4(x, logits, bias, w13, s13, w2, s2, route_scale=ROUTE_SCALE, top_k=
     (f32), mid = bf16(silu(gate) * up) (the A16W4 launch keeps mid in bf16,
     ``test_minimax_m31_ffn.py:132-141``), y_e = mid @ W2^T, y = sum_slots w * y_e
     (shared expert slot 0, weight 1). w13 [E, 2*inter, H/2] uint8 + s13 [E, 2*inter,
-    H/32] E8M0; w2 [E, H, inter/2] + s2 [E, H, inter/32]."""
+    H/32] E8M0; w2 [E, H, inter/2] + s2 [E, H, inter/32] (anything indexable by expert
+    id). ``routing`` = (ids [R, 9], weights [R, 9]) replaces the oracle's own routing."""
     xf = torch.as_tensor(x).float().double()
     scores = sigmoid(logits)
-    ids, wts = route_topk(scores, bias, top_k, route_scale)
-    sid, sw = slots_with_shared(ids, wts)
+    if routing is None:
+        ids, wts = route_topk(scores, bias, top_k, route_scale)
+        sid, sw = slots_with_shared(ids, wts)
+    else:
+        sid = np.asarray(routing[0], dtype=np.int64)
+        sw = np.asarray(routing[1], dtype=np.float32)
     r, hdim = xf.shape
-    inter = w2.shape[-1] * 2
+    inter = w2[SHARED].shape[-1] * 2
     y = torch.zeros(r, hdim, dtype=torch.float64)
     for e in np.unique(sid):
         rows, slots = np.nonzero(sid == e)

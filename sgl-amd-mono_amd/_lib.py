@@ -33,7 +33,7 @@ GUARD_EXIT = 6
 GUARD_ABORT = 7
 GUARD_WORDS = 16
 
-# on-HBM layouts of FP8 expert weights (MONO_LAYOUT_*)
+# on-HBM layouts of expert weights (MONO_LAYOUT_*)
 LAYOUT_ROWMAJOR = 0
 LAYOUT_AITER16 = 1
 
@@ -82,6 +82,38 @@ class MonoMoeFp8Args(ctypes.Structure):
     ]
 
 
+class MonoMoeMxfp4Args(ctypes.Structure):
+    """Mirror of ``MonoMoeMxfp4Args`` in mono_amd.h (same order and types)."""
+
+    _fields_ = [
+        ("rows", c_int32),
+        ("hidden", c_int32),
+        ("inter", c_int32),
+        ("experts", c_int32),
+        ("layout", c_int32),
+        ("route_scale", c_float),
+        ("x", c_void_p),
+        ("res", c_void_p),
+        ("out", c_void_p),
+        ("logits", c_void_p),
+        ("bias", c_void_p),
+        ("w13", c_void_p),
+        ("s13", c_void_p),
+        ("w2", c_void_p),
+        ("s2", c_void_p),
+        ("y", c_void_p),
+        ("scores", c_void_p),
+        ("ids", c_void_p),
+        ("weights", c_void_p),
+        ("scratch", c_void_p),
+        ("guard", c_void_p),
+        ("host_error", c_void_p),
+        ("fault_site", c_int32),
+        ("fault_after", c_int32),
+        ("timeline", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mono_version": (c_int32, []),
@@ -91,6 +123,8 @@ SIGNATURES = {
     "mono_reset": (c_int32, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "mono_moe_fp8_scratch_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "mono_moe_fp8_launch": (c_int32, [ctypes.POINTER(MonoMoeFp8Args), c_void_p]),
+    "mono_moe_mxfp4_scratch_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
+    "mono_moe_mxfp4_launch": (c_int32, [ctypes.POINTER(MonoMoeMxfp4Args), c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,449 @@
+// MXFP4 (A16W4) routed MoE as one persistent gfx950 launch.
+//
+// Stages, every CTA in order:
+//   0  the CTA's MFMA B operands (each wave's K slice of the bf16 rows) load into
+//      registers while waves 0..R-1 route one row each from the given logits: sigmoid,
+//      + bias, top-8 with lowest-id ties, weights raw / sum * scale. Every CTA routes
+//      for itself (the logits are inputs), so nothing is handed off before up/gate.
+//   1  up/gate: task (u, c) = 16 gate + 16 up rows of distinct expert u over all of K;
+//      task t runs on CTA t mod grid. Waves 0-7 take the gate rows, 8-15 the up rows,
+//      each wave a 384-K slice. A lane's 16 code bytes are one row's 32-group, which
+//      shares one E8M0 scale: v_cvt_scalef32_pk_bf16_fp4 dequantises them exactly to 32
+//      bf16 for four 16x16x32 bf16 MFMAs. Each wave keeps two tasks of weights in
+//      flight. Wave 0 reduces the task and stores mid = bf16(silu(g) * u) by slot (row,
+//      pick), then the task's ready word gets the launch tag. Only wave 0 stores, so
+//      only wave 0 ever waits for its loads to drain (and it refills after that wait).
+//   2  down: task f = 16 output rows over every distinct expert, wave w taking experts
+//      u = w mod 16. Its first three experts' weights are in flight before the wait for
+//      every ready word; the R x 9 mid slot rows are then copied into LDS. Each
+//      expert's partial is scaled by the row's route weight; a fixed-order reduction
+//      over the 16 waves and out = bf16(res + y).
+// The tag of a launch is the guard block's epoch + 1; the last CTA out advances it.
+//
+// Reference: A16W4 operands sgl_amd_mono/minimax_m31/a16w4.py:26-92 (lane = one row's
+// 32-group, scale folded into the fp4 -> bf16 convert); MXFP4 units
+// sgl_amd_mono/glm53/gfx950/kernel.py:906-995; route as
+// test/kernels/test_minimax_m31_ffn.py:146-151; the e8m0 shuffle index
+// sgl_amd_mono/common/mx.py:40-44.
+#include <hip/hip_runtime.h>
+
+#include "moe_common.h"
+#include "mono_abi.h"
+
+namespace mono {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+template <int H, int I>
+struct MoeMxGeom {
+  static constexpr int WAVES = 16;
+  static constexpr int THREADS = WAVES * WAVE;
+  static constexpr int QW = 8;          // waves of a K split (up/gate)
+  static constexpr int NKS = H / 128;   // 128-K steps of the hidden dim
+  static constexpr int KSW = NKS / QW;  // steps of a wave's slice
+  static constexpr int NUG = I / 16;    // up/gate tasks per expert
+  static constexpr int NDS = I / 128;   // 128-K steps of the intermediate
+  static constexpr int NDN = H / 16;    // down tasks
+  static constexpr int RING = 3;        // experts of down weights a wave keeps in flight
+  static constexpr int MROW = I * 2 + 16;  // LDS bytes of a mid slot row (16 off the banks)
+  static_assert(NKS % QW == 0, "hidden must split into 8 slices of 128-steps");
+  static_assert(I % 128 == 0, "intermediate must be whole 128-steps");
+
+  // scratch layout (bytes)
+  static constexpr size_t OFF_MID = 0;  // bf16 [R x 9 slots][I]
+  static constexpr size_t SZ_MID = (size_t)MOE_MAXR * MOE_SLOTS * I * 2;
+  static constexpr size_t OFF_READY = (OFF_MID + SZ_MID + 255) & ~(size_t)255;
+  static constexpr size_t SZ_READY = (size_t)MOE_NDIST * NUG * 4;
+  static constexpr size_t BYTES = (OFF_READY + SZ_READY + 255) & ~(size_t)255;
+};
+
+// Operand addressing of one MXFP4 weight matrix [N, K] (one expert): a lane's 16 code
+// bytes are row 16 rg + l % 16, K 128 s + 32 (l / 16) .. + 31; its scale is that row's
+// E8M0 of column 4 s + l / 16. Offsets split into a per-lane part (VGPR) and a
+// wave-uniform part (SGPR).
+//   row-major: codes [N, K / 2], scales [N, K / 32];
+//   SHUF: codes in AITER's (16, 16) shuffle, [N / 16, K / 64, 2, 16 rows, 16 B], where a
+//   16-row x 128-K tile is 1 KiB contiguous with lane l at 16 l; scales in the e8m0
+//   shuffle of sgl_amd_mono/common/mx.py:40-44 over CP = K / 32 rounded up to 8 columns:
+//   byte ((((r32 CP/8 + c8) 4 + e) 16 + b) 2 + d) 2 + a for row 32 r32 + 16 a + b and
+//   column 8 c8 + 4 d + e, so lane l's byte of step s sits in dword
+//   (r32 CP/8 + s / 2) 64 + l at byte 2 (s % 2) + rg % 2.
+template <bool SHUF, int K>
+struct MxOperand {
+  static constexpr int C = K / 32;
+  static constexpr int CP = SHUF ? (C + 7) / 8 * 8 : C;
+  static constexpr uint32_t code_bytes(int n) { return (uint32_t)n * (K / 2); }
+  static constexpr uint32_t scale_bytes(int n) { return (uint32_t)n * CP; }
+  __device__ static uint32_t code_v(int l) {
+    return SHUF ? (uint32_t)l * 16 : (uint32_t)((l & 15) * (K / 2) + (l >> 4) * 16);
+  }
+  __device__ static uint32_t code_s(int rg, int s) {
+    return (uint32_t)rg * 8 * K + (uint32_t)s * (SHUF ? 1024 : 64);
+  }
+  __device__ static uint32_t scale_v(int l) {
+    return SHUF ? (uint32_t)l * 4 : (uint32_t)((l & 15) * C + (l >> 4));
+  }
+  __device__ static uint32_t scale_s(int rg, int s) {
+    return SHUF ? (uint32_t)((((rg >> 1) * (CP / 8) + (s >> 1)) * 256) + (s & 1) * 2 + (rg & 1))
+                : (uint32_t)(rg * 16 * C + 4 * s);
+  }
+};
+
+__device__ inline uint32_t ld1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, CP_NT);
+}
+
+// acc += one 128-K step: the lane's 16 code bytes (E8M0 `code`) dequantised to bf16 and
+// multiplied with the four B operands of the step (8 bf16 each, K 8 d .. of the lane's
+// 32-group). The fp4 -> bf16 conversion with the power-of-two scale is exact.
+__device__ inline v4f fp4_step(v4i wv, uint32_t code, const v4i (&B)[4], v4f acc) {
+  const float sc = __uint_as_float((code & 0xFFu) << 23);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t wd = (uint32_t)wv[d];
+    const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 0);
+    const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 1);
+    const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 2);
+    const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 3);
+    const v8bf a = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(v8bf, B[d]), acc, 0, 0,
+                                                  0);
+  }
+  return acc;
+}
+
+struct MoeMxParams {
+  int rows;
+  float route_scale;
+  const uint16_t* x;
+  const uint16_t* res;
+  uint16_t* out;
+  const float* logits;
+  const float* bias;
+  const uint8_t* w13;
+  const uint8_t* s13;
+  const uint8_t* w2;
+  const uint8_t* s2;
+  float* y;
+  float* scores;
+  int32_t* ids;
+  float* weights;
+  uint8_t* scratch;
+  int32_t* guard;
+  uint32_t* host_err;
+  int fault_site, fault_after;
+  uint64_t* timeline;
+};
+
+template <int H, int I, bool SHUF>
+__global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
+  using G = MoeMxGeom<H, I>;
+  using W13 = MxOperand<SHUF, H>;  // [2 I, H]
+  using W2 = MxOperand<SHUF, I>;   // [H, I]
+  constexpr int KSW = G::KSW, NUG = G::NUG, NDS = G::NDS, QW = G::QW, RING = G::RING;
+  const int tid = threadIdx.x, l = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = l & 15, grp = l >> 4;  // MFMA column (row of the batch) and K group
+  const int half = w / QW, wq = w % QW;
+  const int R = p.rows;
+  const int nblk = gridDim.x, b = blockIdx.x;
+
+  __shared__ RouteLds rl;
+  __shared__ v4f red[2][G::WAVES][64];  // up/gate: by task parity; down: [0]
+  __shared__ __attribute__((aligned(16))) uint8_t mid_lds[MOE_MAXR * MOE_SLOTS * G::MROW];
+  __shared__ float wslot[MOE_MAXR * MOE_SLOTS];  // route weight of each (expert, row) slot
+  __shared__ uint32_t head_s[4];
+  __shared__ int ok_s;
+
+  uint16_t* mid = reinterpret_cast<uint16_t*>(p.scratch + G::OFF_MID);
+  uint32_t* ready = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
+
+  stamp(p.timeline, MONO_TL_START);
+  // B operands: x[t][128 s + 32 grp + 8 d ..] for the wave's steps s (0 past row R)
+  v4i xb[KSW][4];
+  {
+    const __amdgpu_buffer_rsrc_t rx = rsrc(p.x, (uint32_t)R * H * 2);
+    const uint32_t vo = (uint32_t)(t * H + 32 * grp) * 2;
+#pragma unroll
+    for (int j = 0; j < KSW; ++j)
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        xb[j][d] = ld16s<CP_NONE>(rx, vo, (uint32_t)(((wq * KSW + j) * 128 + 8 * d) * 2));
+  }
+  if (tid == 0) {
+    const v4i h = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)h[i];
+  }
+  for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
+  if (tid == 0) ok_s = 1;
+  __syncthreads();
+  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
+  Guard guard;
+  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
+
+  // ---------------------------------------------------------------- stage 0: routing
+  stamp(p.timeline, MONO_TL_STAGED);
+  if (w < R) {
+    float sc[4], bs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lg = p.logits[w * MOE_NEXP + l + 64 * i];
+      sc[i] = 1.0f / (1.0f + expf(-lg));
+      bs[i] = p.bias[l + 64 * i];
+    }
+    const bool out0 = b == 0;
+    route_row(rl, w, sc, bs, p.route_scale, out0 ? p.scores : nullptr, out0 ? p.ids : nullptr,
+              out0 ? p.weights : nullptr);
+  }
+  __syncthreads();
+  if (w == 0) build_distinct(rl, R);
+  __syncthreads();
+  const int nd = rl.nd;
+  for (int s = tid; s < R * MOE_SLOTS; s += G::THREADS) {
+    const int ut = rl.slot_ut[s];
+    wslot[s] = route_weight(rl, ut & 255, rl.uexp[ut >> 8]);
+  }
+
+  // ---------------------------------------------------------------- stage 1: up/gate
+  stamp(p.timeline, MONO_TL_ROUTED);
+  {
+    const int ntask = nd * NUG;
+    const uint32_t cv = W13::code_v(l), sv = W13::scale_v(l);
+    // operands of a task for this wave; a task past the end reads through empty
+    // buffers (loads return 0, no memory traffic), so refills need no branch
+    auto issue = [&](int task, int j, v4i& wv, uint32_t& code) {
+      const bool live = task < ntask;
+      const int tk = live ? task : 0;
+      const int u = tk / NUG, cc = tk % NUG;
+      const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
+      const int rg = half * NUG + cc;
+      const int s = wq * KSW + j;
+      const __amdgpu_buffer_rsrc_t rc =
+          rsrc(p.w13 + (size_t)e * W13::code_bytes(2 * I), live ? W13::code_bytes(2 * I) : 0u);
+      const __amdgpu_buffer_rsrc_t rs =
+          rsrc(p.s13 + (size_t)e * W13::scale_bytes(2 * I), live ? W13::scale_bytes(2 * I) : 0u);
+      wv = ld16s<CP_NT>(rc, cv, W13::code_s(rg, s));
+      code = ld1(rs, sv, W13::scale_s(rg, s));
+    };
+    v4i wa[KSW], wb[KSW];
+    uint32_t ca[KSW], cb[KSW];
+#pragma unroll
+    for (int j = 0; j < KSW; ++j) issue(b, j, wa[j], ca[j]);
+#pragma unroll
+    for (int j = 0; j < KSW; ++j) issue(b + nblk, j, wb[j], cb[j]);
+
+    auto run = [&](int task, int par, v4i (&wv)[KSW], uint32_t (&code)[KSW]) {
+      const int u = task / NUG, cc = task % NUG;
+      const int nt = task + 2 * nblk;  // the task this ring slot holds next
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KSW; ++j) {
+        acc = fp4_step(wv[j], code[j], xb[j], acc);
+        if (w != 0) issue(nt, j, wv[j], code[j]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      red[par][w][l] = acc;
+      __syncthreads();
+      if (w == 0) {
+        // lane l: rows 4 (l / 16) + v of the task's 16, batch row l % 16
+        v4f gs = red[par][0][l], us = red[par][QW][l];
+#pragma unroll
+        for (int i = 1; i < QW; ++i) {
+          gs += red[par][i][l];
+          us += red[par][QW + i][l];
+        }
+        const uint32_t mask = rl.umask[u];
+        if (t < R && ((mask >> t) & 1u)) {
+          uint32_t h[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) h[v] = bf16_bits(gs[v] / (1.0f + expf(-gs[v])) * us[v]);
+          const int sl = slot_of(rl, u, mask, t);
+          st_dev64(reinterpret_cast<uint64_t*>(mid + (size_t)sl * I + cc * 16 + 4 * grp),
+                   (uint64_t)(h[0] | (h[1] << 16)) | ((uint64_t)(h[2] | (h[3] << 16)) << 32));
+        }
+        drain();  // the mid stores (and this wave's in-flight loads) completed
+#pragma unroll
+        for (int j = 0; j < KSW; ++j) issue(nt, j, wv[j], code[j]);
+        if (l == 0) st_dev(&ready[u * NUG + cc], tag);
+      }
+    };
+    for (int task = b; task < ntask; task += 2 * nblk) {
+      run(task, 0, wa, ca);
+      if (task + nblk < ntask) run(task + nblk, 1, wb, cb);
+    }
+  }
+
+  // ---------------------------------------------------------------- stage 2: down
+  stamp(p.timeline, MONO_TL_UPGATE);
+  bool ok = true;
+  {
+    const uint32_t cv = W2::code_v(l), sv = W2::scale_v(l);
+    auto issue = [&](int f, int u, int s, v4i& wv, uint32_t& code) {
+      const bool live = u < nd;
+      const int e = __builtin_amdgcn_readfirstlane(rl.uexp[live ? u : 0]);
+      const __amdgpu_buffer_rsrc_t rc =
+          rsrc(p.w2 + (size_t)e * W2::code_bytes(H), live ? W2::code_bytes(H) : 0u);
+      const __amdgpu_buffer_rsrc_t rs =
+          rsrc(p.s2 + (size_t)e * W2::scale_bytes(H), live ? W2::scale_bytes(H) : 0u);
+      wv = ld16s<CP_NT>(rc, cv, W2::code_s(f, s));
+      code = ld1(rs, sv, W2::scale_s(f, s));
+    };
+    bool first = true;
+    for (int f = b; f < G::NDN; f += nblk) {
+      v4i dw[RING][NDS];
+      uint32_t dc[RING][NDS];
+#pragma unroll
+      for (int k = 0; k < RING; ++k)
+#pragma unroll
+        for (int s = 0; s < NDS; ++s) issue(f, w + G::WAVES * k, s, dw[k][s], dc[k][s]);
+      if (first) {
+        first = false;
+        // every up/gate task of this launch, then the mid slot rows into LDS
+        const int nflag = nd * NUG;
+        ok = wait_until(guard, MONO_SITE_MID, [&]() {
+          bool all = true;
+          for (int i = tid; i < nflag; i += G::THREADS) all &= ld_dev(&ready[i]) == tag;
+          return __all(all);
+        });
+        ok = cta_all(ok, ok_s);
+        stamp(p.timeline, MONO_TL_MIDQ);
+        if (ok) {
+          const __amdgpu_buffer_rsrc_t rm = rsrc(mid, (uint32_t)G::SZ_MID);
+          constexpr int CPR = I * 2 / 16;  // 16-byte pieces of a mid row
+          for (int i = tid; i < R * MOE_SLOTS * CPR; i += G::THREADS) {
+            const int s = i / CPR, c = i % CPR;
+            *reinterpret_cast<v4i*>(mid_lds + s * G::MROW + c * 16) =
+                ld16<CP_DEV>(rm, (uint32_t)(s * I * 2 + c * 16));
+          }
+        }
+        __syncthreads();
+      }
+      if (!ok) break;
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      for (int k0 = 0; w + G::WAVES * k0 < nd; k0 += RING) {
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+          const int u = w + G::WAVES * (k0 + k);
+          if (u < nd) {
+            const int sl = slot_of(rl, u, rl.umask[u], t);
+            const bool on = sl >= 0;
+            const float wt = on ? wslot[sl] : 0.f;
+            const uint8_t* mrow = mid_lds + (on ? sl : 0) * G::MROW + 64 * grp;
+            v4f d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NDS; ++s) {
+              v4i B[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const v4i z = {0, 0, 0, 0};
+                B[q] = on ? *reinterpret_cast<const v4i*>(mrow + s * 256 + q * 16) : z;
+              }
+              d = fp4_step(dw[k][s], dc[k][s], B, d);
+              issue(f, u + G::WAVES * RING, s, dw[k][s], dc[k][s]);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            acc += d * wt;
+          }
+        }
+      }
+      red[0][w][l] = acc;
+      __syncthreads();
+      if (w == 0) {
+        v4f ys = red[0][0][l];
+#pragma unroll
+        for (int i = 1; i < G::WAVES; ++i) ys += red[0][i][l];
+        if (t < R) {
+          const int col = f * 16 + 4 * grp;
+          uint32_t h[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            h[v] = bf16_bits((p.res ? bf16_lo(p.res[t * H + col + v]) : 0.f) + ys[v]);
+          *reinterpret_cast<uint64_t*>(p.out + t * H + col) =
+              (uint64_t)(h[0] | (h[1] << 16)) | ((uint64_t)(h[2] | (h[3] << 16)) << 32);
+          if (p.y) *reinterpret_cast<v4f*>(p.y + t * H + col) = ys;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---------------------------------------------------------------- exit
+  stamp(p.timeline, MONO_TL_DOWN);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
+    drain();
+    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
+    if (old == (uint32_t)nblk - 1u) {
+      st_dev(gw + MONO_GUARD_EXIT, 0u);
+      st_dev(gw + MONO_GUARD_EPOCH, tag);
+    }
+  }
+  stamp(p.timeline, MONO_TL_END);
+}
+
+}  // namespace mono
+
+using namespace mono;
+
+extern "C" size_t mono_moe_mxfp4_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts) {
+  if (experts != MOE_NEXP) return 0;
+  if (hidden == 3072 && inter == 384) return MoeMxGeom<3072, 384>::BYTES;
+  return 0;
+}
+
+extern "C" int mono_moe_mxfp4_launch(const MonoMoeMxfp4Args* a, mono_stream_t stream) {
+  if (!a) return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: null args");
+  if (a->rows < 1 || a->rows > MOE_MAXR)
+    return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: rows must be 1..16");
+  if (a->experts != MOE_NEXP)
+    return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: experts must be 256");
+  if (!a->x || !a->out || !a->logits || !a->bias || !a->w13 || !a->s13 || !a->w2 || !a->s2 ||
+      !a->scratch || !a->guard)
+    return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: null tensor");
+  if (a->layout != MONO_LAYOUT_ROWMAJOR && a->layout != MONO_LAYOUT_AITER16)
+    return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: unknown weight layout");
+  MoeMxParams p;
+  p.rows = a->rows;
+  p.route_scale = a->route_scale;
+  p.x = static_cast<const uint16_t*>(a->x);
+  p.res = static_cast<const uint16_t*>(a->res);
+  p.out = static_cast<uint16_t*>(a->out);
+  p.logits = a->logits;
+  p.bias = a->bias;
+  p.w13 = a->w13;
+  p.s13 = a->s13;
+  p.w2 = a->w2;
+  p.s2 = a->s2;
+  p.y = a->y;
+  p.scores = a->scores;
+  p.ids = a->ids;
+  p.weights = a->weights;
+  p.scratch = static_cast<uint8_t*>(a->scratch);
+  p.guard = a->guard;
+  p.host_err = nullptr;
+  if (a->host_error) {
+    void* dptr = nullptr;
+    if (hipHostGetDevicePointer(&dptr, a->host_error, 0) != hipSuccess || !dptr)
+      return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: host_error is not pinned host memory");
+    p.host_err = static_cast<uint32_t*>(dptr);
+  }
+  p.fault_site = a->fault_site;
+  p.fault_after = a->fault_after;
+  p.timeline = a->timeline;
+  int grid = 0;
+  int rc = monokernel_grid(&grid);
+  if (rc) return rc;
+  if (a->hidden == 3072 && a->inter == 384) {
+    auto k = a->layout == MONO_LAYOUT_AITER16 ? moe_mxfp4_kernel<3072, 384, true>
+                                              : moe_mxfp4_kernel<3072, 384, false>;
+    rc = check_coresident(k, 1024, 0,
+                          "mono_moe_mxfp4_launch: one 1024-thread CTA per CU does not fit");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);
+  } else {
+    return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: unsupported hidden/inter");
+  }
+  return check_launch("mono_moe_mxfp4_launch");
+}

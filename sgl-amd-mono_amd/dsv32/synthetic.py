@@ -14,7 +14,7 @@ import torch
 
 from .. import layouts
 from .config import DSV32, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
-from .moe import MoeFp8Weights
+from .moe import MoeFp8Weights, MoeMxfp4Weights
 
 FP8 = torch.float8_e4m3fn
 
@@ -67,10 +67,12 @@ def rows_bf16(rows: int, hidden: int, device, seed: int = 0) -> torch.Tensor:
     return torch.randn(rows, hidden, generator=g, device=device).to(torch.bfloat16)
 
 
-def mxfp4_moe_weights(device, seed: int = 0, cfg: Mxfp4MoeConfig = MXFP4_MOE):
+def mxfp4_moe_weights(device, seed: int = 0, cfg: Mxfp4MoeConfig = MXFP4_MOE,
+                      layout: str = layouts.ROWMAJOR) -> MoeMxfp4Weights:
     """Config 4: E2M1 codes (random bytes, even index in the low nibble) with E8M0
     scales per 32 in [119, 122]; w13 [E+1, 2I, H/2] + [E+1, 2I, H/32], w2 [E+1, H, I/2] +
-    [E+1, H, I/32]; router bias f32 0.01*N(0,1)."""
+    [E+1, H, I/32]; router bias f32 0.01*N(0,1). ``layout`` "aiter16" stores the same
+    values in the (16, 16) code shuffle and the e8m0 scale shuffle."""
     dev = torch.device(device)
     h, i, n = cfg.hidden, cfg.inter, cfg.experts + 1
     g = _gen(dev, seed, 11)
@@ -80,7 +82,20 @@ def mxfp4_moe_weights(device, seed: int = 0, cfg: Mxfp4MoeConfig = MXFP4_MOE):
     w2 = torch.randint(0, 256, (n, h, i // 2), **u8)
     s2 = torch.randint(119, 123, (n, h, i // 32), **u8)
     bias = torch.randn(cfg.experts, generator=_gen(dev, seed, 12), device=dev) * 0.01
-    return dict(w13=w13, s13=s13, w2=w2, s2=s2, bias=bias)
+    if layout == layouts.AITER16:
+        w13, w2 = layouts.shuffle_16x16(w13), layouts.shuffle_16x16(w2)
+        s13, s2 = layouts.shuffle_e8m0(s13), layouts.shuffle_e8m0(s2)
+    return MoeMxfp4Weights(bias=bias, w13=w13, s13=s13, w2=w2, s2=s2, layout=layout)
+
+
+def rowmajor_mxfp4_expert(w: MoeMxfp4Weights, e: int, cfg: Mxfp4MoeConfig = MXFP4_MOE):
+    """Expert e's (w13, s13, w2, s2) bytes on the host as numpy, row-major."""
+    w13, s13, w2, s2 = w.w13[e], w.s13[e], w.w2[e], w.s2[e]
+    if w.layout == layouts.AITER16:
+        w13, w2 = layouts.unshuffle_16x16(w13), layouts.unshuffle_16x16(w2)
+        s13 = layouts.unshuffle_e8m0(s13, cfg.hidden // 32)
+        s2 = layouts.unshuffle_e8m0(s2, cfg.inter // 32)
+    return tuple(t.cpu().numpy() for t in (w13, s13, w2, s2))
 
 
 def logits_f32(rows: int, experts: int, device, seed: int = 0) -> torch.Tensor:

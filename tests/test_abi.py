@@ -31,6 +31,7 @@ def _c_layout(struct, fields, tmp_path):
 
 
 @pytest.mark.parametrize("cls,cname", [(_lib.MonoMoeFp8Args, "MonoMoeFp8Args"),
+                                        (_lib.MonoMoeMxfp4Args, "MonoMoeMxfp4Args"),
                                         (_lib.MonoDeviceInfo, "MonoDeviceInfo")])
 def test_ctypes_mirrors_match_the_c_layout(cls, cname, tmp_path):
     fields = [f for f, _ in cls._fields_]
@@ -44,11 +45,17 @@ def test_null_args_are_refused_without_a_gpu():
     assert rc == _lib.MONO_E_ARG and "null" in _lib.last_error()
     args = _lib.MonoMoeFp8Args(rows=0, experts=256)
     assert _lib.lib().mono_moe_fp8_launch(ctypes.byref(args), None) == _lib.MONO_E_ARG
+    assert _lib.lib().mono_moe_mxfp4_launch(None, None) == _lib.MONO_E_ARG
+    mx = _lib.MonoMoeMxfp4Args(rows=17, experts=256)
+    assert _lib.lib().mono_moe_mxfp4_launch(ctypes.byref(mx), None) == _lib.MONO_E_ARG
+    assert "rows" in _lib.last_error()
 
 
 def test_scratch_bytes_only_for_built_geometries():
     assert _lib.lib().mono_moe_fp8_scratch_bytes(7168, 512, 256) > 0
     assert _lib.lib().mono_moe_fp8_scratch_bytes(7168, 384, 256) == 0
+    assert _lib.lib().mono_moe_mxfp4_scratch_bytes(3072, 384, 256) > 0
+    assert _lib.lib().mono_moe_mxfp4_scratch_bytes(3072, 512, 256) == 0
 
 
 def test_deadline_ticks_bounds():
@@ -99,3 +106,27 @@ def test_aiter16_shuffle_is_the_reference_index_map():
     assert torch.equal(layouts.unshuffle_16x16(layouts.shuffle_16x16(w)), w)
     e = torch.randint(0, 255, (3, 32, 64), dtype=torch.uint8)
     assert torch.equal(layouts.unshuffle_16x16(layouts.shuffle_16x16(e)), e)
+
+
+def test_e8m0_shuffle_is_the_reference_index_map():
+    """Scale (row, col) of the e8m0 shuffle sits at byte
+    ((((r32 * CP/8 + c8) * 4 + e) * 16 + b) * 2 + d) * 2 + a, row = 32 r32 + 16 a + b,
+    col = 8 c8 + 4 d + e (sgl_amd_mono/common/mx.py:40-44), with the columns padded to
+    a multiple of 8; unshuffle inverts it."""
+    import torch
+
+    from sgl_amd_mono_amd import layouts
+
+    for n, c in [(64, 12), (96, 96), (32, 8)]:
+        s = torch.randint(0, 256, (n, c), dtype=torch.uint8)
+        sh = layouts.shuffle_e8m0(s)
+        cp = layouts.e8m0_cols(c)
+        assert sh.shape == (n, cp)
+        flat = sh.reshape(-1)
+        for r in range(n):
+            for k in range(c):
+                r32, a, b = r // 32, (r // 16) % 2, r % 16
+                c8, d, e = k // 8, (k // 4) % 2, k % 4
+                pos = ((((r32 * (cp // 8) + c8) * 4 + e) * 16 + b) * 2 + d) * 2 + a
+                assert int(flat[pos]) == int(s[r, k])
+        assert torch.equal(layouts.unshuffle_e8m0(sh, c), s)

@@ -130,3 +130,84 @@ def test_config1_softmax_top2_block_against_dense_masked():
     want = (dense * mask[..., None]).sum(1)
     assert sorted(map(tuple, np.sort(ids, 1))) == sorted(map(tuple, np.sort(top.indices.numpy(), 1)))
     torch.testing.assert_close(y, want, rtol=1e-4, atol=1e-6)
+
+
+def _e2m1_bits(codes: torch.Tensor) -> torch.Tensor:
+    """E2M1 values from the bit fields (sign, 2-bit exponent, 1-bit mantissa), low
+    nibble first, computed independently of the oracle's table."""
+    nib = torch.stack([codes & 15, codes >> 4], -1).reshape(*codes.shape[:-1], -1).long()
+    s, e, m = (nib >> 3) & 1, (nib >> 1) & 3, nib & 1
+    mag = torch.where(e == 0, 0.5 * m, torch.exp2(e.double() - 1) * (1 + 0.5 * m))
+    return torch.where(s == 1, -mag, mag)
+
+
+def _mx_dequant(codes, scales):
+    c = torch.from_numpy(np.ascontiguousarray(codes))
+    sc = torch.from_numpy(np.ascontiguousarray(scales)).view(torch.float8_e8m0fnu).double()
+    return _e2m1_bits(c) * sc.repeat_interleave(32, -1)
+
+
+def _tiny_mx_layer(h=256, inter=128, e=4, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    u8 = dict(dtype=torch.uint8, generator=g)
+    w13 = torch.randint(0, 256, (e + 1, 2 * inter, h // 2), **u8).numpy()
+    s13 = torch.randint(119, 123, (e + 1, 2 * inter, h // 32), **u8).numpy()
+    w2 = torch.randint(0, 256, (e + 1, h, inter // 2), **u8).numpy()
+    s2 = torch.randint(119, 123, (e + 1, h, inter // 32), **u8).numpy()
+    return w13, s13, w2, s2
+
+
+def _with_shared(id_, fn):
+    saved, M.SHARED = M.SHARED, id_
+    try:
+        return fn()
+    finally:
+        M.SHARED = saved
+
+
+def test_moe_mxfp4_against_dense_masked_evaluation():
+    """The A16W4 block with its own routing against every expert evaluated densely from
+    bit-field dequantised weights (F.silu, bf16 mid) and masked by torch.topk routing."""
+    h, inter, e = 256, 128, 8
+    w13, s13, w2, s2 = _tiny_mx_layer(h, inter, e, seed=1)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(3, h, generator=g).to(torch.bfloat16)
+    logits = torch.randn(3, e, generator=g)
+    bias = torch.randn(e, generator=g) * 0.01
+    ref = _with_shared(e, lambda: M.moe_mxfp4(x, logits, bias, w13, s13, w2, s2, top_k=3))
+    xf = x.double()
+    dense = []
+    for i in range(e + 1):
+        hh = (xf @ _mx_dequant(w13[i], s13[i]).T).float()
+        mid = (tF.silu(hh[:, :inter]) * hh[:, inter:]).to(torch.bfloat16).double()
+        dense.append(mid @ _mx_dequant(w2[i], s2[i]).T)
+    dense = torch.stack(dense, 1)  # [R, E + 1, H]
+    sc = torch.sigmoid(logits)
+    top = torch.topk(sc + bias, 3, -1).indices
+    raw = sc.gather(1, top).double()
+    wts = raw / raw.sum(-1, keepdim=True) * 2.5
+    mask = torch.zeros(3, e + 1, dtype=torch.float64).scatter(1, top, wts)
+    mask[:, e] = 1.0
+    want = (dense * mask[..., None]).sum(1)
+    assert np.array_equal(np.sort(ref["ids"][:, 1:], 1), np.sort(top.numpy(), 1))
+    np.testing.assert_allclose(ref["y"].numpy(), want.numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_moe_mxfp4_power_of_two_scales_are_exact():
+    """E8M0 codes + 1 on every down scale, or on every up-row scale, doubles y exactly
+    (the bf16 mid of 2u is exactly twice that of u)."""
+    h, inter, e = 256, 128, 4
+    w13, s13, w2, s2 = _tiny_mx_layer(h, inter, e, seed=4)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, h, generator=g).to(torch.bfloat16)
+    ids = np.array([[e, 1], [e, 2]])
+    wts = np.array([[1.0, 0.75], [1.0, 1.25]], np.float32)
+    run = lambda a, b, c, d: _with_shared(e, lambda: M.moe_mxfp4(
+        x, torch.zeros(2, e), torch.zeros(e), a, b, c, d, routing=(ids, wts))["y"].numpy())
+    base = run(w13, s13, w2, s2)
+    s2b = s2 + 1
+    s13b = s13.copy()
+    s13b[:, inter:] += 1
+    assert np.abs(base).max() > 0
+    np.testing.assert_array_equal(run(w13, s13, w2, s2b), 2 * base)
+    np.testing.assert_array_equal(run(w13, s13b, w2, s2), 2 * base)
