@@ -26,44 +26,44 @@ struct RouteLds {
   int32_t nd;
 };
 
-// The top-k of one row, called by one whole wave. `score_of(i)` gives this lane's
-// i-th candidate score (expert lane + 64 i) and `bias` the matching biases.
+// The top-k of one row, called by one whole wave. Lane l holds the scores of experts
+// l + 64 i (i < 4) in `sc` and the matching biases in `bs`.
 // Order: radix key of f32(score + bias) descending, then lower expert id
-// (sgl_amd_mono/glm53/gfx950/kernel.py:1575-1629). Writes slots 1..8 of row t into
-// `rl` and sets the row's bit in rl.mask. Returns nothing; weights are
-// raw / (sum of the 8 raw, in pick order) * route_scale.
+// (sgl_amd_mono/glm53/gfx950/kernel.py:1575-1629). Each round takes the wave maximum of
+// the 32-bit keys (a DPP / permlane butterfly) and then the lowest id holding it: four
+// ballots, scanned from the lowest id block, and the first set lane (all scalar work).
+// The pick's key becomes 0, below every non-NaN key. Writes slots 1..8 of row t into
+// `rl` and sets the row's bit in rl.mask; weights are raw / (sum of the 8 raw, in pick
+// order) * route_scale.
 __device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], const float (&bs)[4],
                                  float route_scale, float* scores_out, int32_t* ids_out,
                                  float* weights_out) {
   const int l = lane_id();
-  uint64_t cand[4];
+  uint32_t key[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = l + 64 * i;
-    const uint32_t key = radix_key(sc[i] + bs[i]);
-    cand[i] = ((uint64_t)key << 32) | (uint32_t)(0xFFFF - e);
-  }
+  for (int i = 0; i < 4; ++i) key[i] = radix_key(sc[i] + bs[i]);
   float picked_raw[MOE_TOPK];
   int picked_id[MOE_TOPK];
 #pragma unroll
   for (int r = 0; r < MOE_TOPK; ++r) {
-    uint64_t mine = cand[0];
+    uint32_t m = key[0] > key[1] ? key[0] : key[1];
+    const uint32_t m2 = key[2] > key[3] ? key[2] : key[3];
+    m = wave_max_u32(m > m2 ? m : m2);
+    const uint64_t b0 = __ballot(key[0] == m), b1 = __ballot(key[1] == m);
+    const uint64_t b2 = __ballot(key[2] == m), b3 = __ballot(key[3] == m);
+    const int slot = b0 ? 0 : b1 ? 1 : b2 ? 2 : 3;
+    const uint64_t bb = b0 ? b0 : b1 ? b1 : b2 ? b2 : b3;
+    const int owner = __ffsll((long long)bb) - 1;
+    const int e = owner + 64 * slot;
+    float mine = sc[0];
 #pragma unroll
-    for (int i = 1; i < 4; ++i) mine = cand[i] > mine ? cand[i] : mine;
-    const uint64_t best = wave_max_u64(mine);
-    const int e = 0xFFFF - (int)(uint32_t)(best & 0xFFFFFFFFu);
-    // the owner lane of expert e knows its raw score
-    const int owner = e & 63, slot = e >> 6;
-    float raw = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i == slot) raw = sc[i];
-    raw = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(raw), owner));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (cand[i] == best) cand[i] = 0;  // 0 is below every live candidate
-    picked_raw[r] = raw;
+    for (int i = 1; i < 4; ++i)
+      if (i == slot) mine = sc[i];
+    picked_raw[r] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(mine), owner));
     picked_id[r] = e;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i == slot && l == owner) key[i] = 0;
   }
   float tot = 0.f;
 #pragma unroll

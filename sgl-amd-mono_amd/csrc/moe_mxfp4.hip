@@ -9,13 +9,13 @@
 //      task t runs on CTA t mod grid. Waves 0-7 take the gate rows, 8-15 the up rows,
 //      each wave a 384-K slice. A lane's 16 code bytes are one row's 32-group, which
 //      shares one E8M0 scale: v_cvt_scalef32_pk_bf16_fp4 dequantises them exactly to 32
-//      bf16 for four 16x16x32 bf16 MFMAs. Each wave keeps two tasks of weights in
-//      flight. Wave 0 reduces the task and stores mid = bf16(silu(g) * u) by slot (row,
-//      pick), then the task's ready word gets the launch tag. Only wave 0 stores, so
-//      only wave 0 ever waits for its loads to drain (and it refills after that wait).
+//      bf16 for four 16x16x32 bf16 MFMAs; the B operands (the rows) wait in LDS. Each
+//      wave keeps three tasks of weights in flight. Wave 0 reduces each task and stores
+//      mid = bf16(silu(g) * u) by slot (row, pick); only after the CTA's last task does
+//      it wait for those stores, then the CTA's done word gets the launch tag.
 //   2  down: task f = 16 output rows over every distinct expert, wave w taking experts
-//      u = w mod 16. Its first three experts' weights are in flight before the wait for
-//      every ready word; the R x 9 mid slot rows are then copied into LDS. Each
+//      u = w mod 16. Its first four experts' weights are in flight before the wait for
+//      every CTA's done word; the R x 9 mid slot rows are then copied into LDS. Each
 //      expert's partial is scaled by the row's route weight; a fixed-order reduction
 //      over the 16 waves and out = bf16(res + y).
 // The tag of a launch is the guard block's epoch + 1; the last CTA out advances it.
@@ -38,23 +38,23 @@ template <int H, int I>
 struct MoeMxGeom {
   static constexpr int WAVES = 16;
   static constexpr int THREADS = WAVES * WAVE;
-  static constexpr int QW = 8;          // waves of a K split (up/gate)
+  static constexpr int QK = 4;          // waves splitting K for one 16-row group (up/gate)
   static constexpr int NKS = H / 128;   // 128-K steps of the hidden dim
-  static constexpr int KSW = NKS / QW;  // steps of a wave's slice
-  static constexpr int NUG = I / 16;    // up/gate tasks per expert
+  static constexpr int KSW = NKS / QK;  // steps of a wave's K slice
+  static constexpr int NUG = I / 32;    // up/gate tasks per expert (32 gate + 32 up rows)
   static constexpr int NDS = I / 128;   // 128-K steps of the intermediate
   static constexpr int NDN = H / 16;    // down tasks
-  static constexpr int RING = 3;        // experts of down weights a wave keeps in flight
-  static constexpr int MROW = I * 2 + 16;  // LDS bytes of a mid slot row (16 off the banks)
-  static_assert(NKS % QW == 0, "hidden must split into 8 slices of 128-steps");
+  static constexpr int DW = WAVES - 1;  // down: waves that stream weights (the last one waits)
+  static constexpr int RING = 4;        // experts of down weights a wave keeps in flight
+  static_assert(NKS % QK == 0, "hidden must split into 4 slices of 128-steps");
   static_assert(I % 128 == 0, "intermediate must be whole 128-steps");
 
   // scratch layout (bytes)
   static constexpr size_t OFF_MID = 0;  // bf16 [R x 9 slots][I]
   static constexpr size_t SZ_MID = (size_t)MOE_MAXR * MOE_SLOTS * I * 2;
-  static constexpr size_t OFF_READY = (OFF_MID + SZ_MID + 255) & ~(size_t)255;
-  static constexpr size_t SZ_READY = (size_t)MOE_NDIST * NUG * 4;
-  static constexpr size_t BYTES = (OFF_READY + SZ_READY + 255) & ~(size_t)255;
+  static constexpr int MAX_GRID = 1024;
+  static constexpr size_t OFF_DONE = (OFF_MID + SZ_MID + 255) & ~(size_t)255;  // u32 per CTA
+  static constexpr size_t BYTES = (OFF_DONE + MAX_GRID * 4 + 255) & ~(size_t)255;
 };
 
 // Operand addressing of one MXFP4 weight matrix [N, K] (one expert): a lane's 16 code
@@ -140,67 +140,83 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   using G = MoeMxGeom<H, I>;
   using W13 = MxOperand<SHUF, H>;  // [2 I, H]
   using W2 = MxOperand<SHUF, I>;   // [H, I]
-  constexpr int KSW = G::KSW, NUG = G::NUG, NDS = G::NDS, QW = G::QW, RING = G::RING;
+  constexpr int KSW = G::KSW, NUG = G::NUG, NDS = G::NDS, QK = G::QK, RING = G::RING;
+  constexpr int THREADS = G::THREADS, DW = G::DW;
   const int tid = threadIdx.x, l = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t = l & 15, grp = l >> 4;  // MFMA column (row of the batch) and K group
-  const int half = w / QW, wq = w % QW;
+  // up/gate roles: gate or up half, 16-row group of the task's pair, K slice
+  const int half = w >> 3, rsub = (w >> 2) & 1, kq = w & 3;
   const int R = p.rows;
   const int nblk = gridDim.x, b = blockIdx.x;
 
   __shared__ RouteLds rl;
   __shared__ v4f red[2][G::WAVES][64];  // up/gate: by task parity; down: [0]
-  __shared__ __attribute__((aligned(16))) uint8_t mid_lds[MOE_MAXR * MOE_SLOTS * G::MROW];
+  // up/gate: the rows as MFMA B operands, [step][d][lane] (16 B: 8 bf16 of row lane % 16
+  // at K 128 step + 32 (lane / 16) + 8 d); down: the mid slot rows, bf16 [R x 9][I]
+  __shared__ __attribute__((aligned(16))) uint8_t mid_lds[MOE_MAXR * MOE_SLOTS * I * 2];
+  static_assert(G::NKS * 4 * 64 * 16 <= (int)sizeof(mid_lds), "B operand staging");
   __shared__ float wslot[MOE_MAXR * MOE_SLOTS];  // route weight of each (expert, row) slot
   __shared__ uint32_t head_s[4];
   __shared__ int ok_s;
 
   uint16_t* mid = reinterpret_cast<uint16_t*>(p.scratch + G::OFF_MID);
-  uint32_t* ready = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
+  uint32_t* done = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_DONE);
+  v4i* x_lds = reinterpret_cast<v4i*>(mid_lds);
 
   stamp(p.timeline, MONO_TL_START);
-  // B operands: x[t][128 s + 32 grp + 8 d ..] for the wave's steps s (0 past row R)
-  v4i xb[KSW][4];
+  // the loads everything else waits on, in the order they are needed: the routing
+  // waves' logits and biases, the guard words, the rows
+  float lg[4] = {0.f, 0.f, 0.f, 0.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
+  if (w < R) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lg[i] = p.logits[w * MOE_NEXP + l + 64 * i];
+      bs[i] = p.bias[l + 64 * i];
+    }
+  }
+  v4i head = {0, 0, 0, 0};
+  if (tid == 0) head = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
+  constexpr int XPT = G::NKS * 4 * 64 / THREADS;  // B-operand pieces per thread
+  static_assert(G::NKS * 4 * 64 % THREADS == 0, "B operand staging split");
+  v4i xv[XPT];
   {
     const __amdgpu_buffer_rsrc_t rx = rsrc(p.x, (uint32_t)R * H * 2);
-    const uint32_t vo = (uint32_t)(t * H + 32 * grp) * 2;
 #pragma unroll
-    for (int j = 0; j < KSW; ++j)
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        xb[j][d] = ld16s<CP_NONE>(rx, vo, (uint32_t)(((wq * KSW + j) * 128 + 8 * d) * 2));
+    for (int k = 0; k < XPT; ++k) {
+      const int i = tid + THREADS * k, ln = i & 63, sd = i >> 6;
+      xv[k] = ld16<CP_NONE>(
+          rx, (uint32_t)(((ln & 15) * H + 128 * (sd >> 2) + 32 * (ln >> 4) + 8 * (sd & 3)) * 2));
+    }
   }
-  if (tid == 0) {
-    const v4i h = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)h[i];
-  }
-  for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
+  for (int i = tid; i < MOE_NDIST; i += THREADS) rl.mask[i] = 0;
   if (tid == 0) ok_s = 1;
   __syncthreads();
-  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
-  Guard guard;
-  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
 
   // ---------------------------------------------------------------- stage 0: routing
   stamp(p.timeline, MONO_TL_STAGED);
   if (w < R) {
-    float sc[4], bs[4];
+    float sc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lg = p.logits[w * MOE_NEXP + l + 64 * i];
-      sc[i] = 1.0f / (1.0f + expf(-lg));
-      bs[i] = p.bias[l + 64 * i];
-    }
+    for (int i = 0; i < 4; ++i) sc[i] = 1.0f / (1.0f + expf(-lg[i]));
     const bool out0 = b == 0;
     route_row(rl, w, sc, bs, p.route_scale, out0 ? p.scores : nullptr, out0 ? p.ids : nullptr,
               out0 ? p.weights : nullptr);
   }
+#pragma unroll
+  for (int k = 0; k < XPT; ++k) x_lds[tid + THREADS * k] = xv[k];
+  if (tid == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)head[i];
+  }
   __syncthreads();
+  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
+  Guard guard;
+  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
   if (w == 0) build_distinct(rl, R);
   __syncthreads();
   const int nd = rl.nd;
-  for (int s = tid; s < R * MOE_SLOTS; s += G::THREADS) {
+  for (int s = tid; s < R * MOE_SLOTS; s += THREADS) {
     const int ut = rl.slot_ut[s];
     wslot[s] = route_weight(rl, ut & 255, rl.uexp[ut >> 8]);
   }
@@ -217,8 +233,8 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
       const int tk = live ? task : 0;
       const int u = tk / NUG, cc = tk % NUG;
       const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
-      const int rg = half * NUG + cc;
-      const int s = wq * KSW + j;
+      const int rg = half * (I / 16) + 2 * cc + rsub;
+      const int s = kq * KSW + j;
       const __amdgpu_buffer_rsrc_t rc =
           rsrc(p.w13 + (size_t)e * W13::code_bytes(2 * I), live ? W13::code_bytes(2 * I) : 0u);
       const __amdgpu_buffer_rsrc_t rs =
@@ -226,32 +242,43 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
       wv = ld16s<CP_NT>(rc, cv, W13::code_s(rg, s));
       code = ld1(rs, sv, W13::scale_s(rg, s));
     };
-    v4i wa[KSW], wb[KSW];
-    uint32_t ca[KSW], cb[KSW];
+    // two tasks of weights in flight per wave
+    v4i w0[KSW], w1[KSW];
+    uint32_t c0[KSW], c1[KSW];
 #pragma unroll
-    for (int j = 0; j < KSW; ++j) issue(b, j, wa[j], ca[j]);
+    for (int j = 0; j < KSW; ++j) issue(b, j, w0[j], c0[j]);
 #pragma unroll
-    for (int j = 0; j < KSW; ++j) issue(b + nblk, j, wb[j], cb[j]);
+    for (int j = 0; j < KSW; ++j) issue(b + nblk, j, w1[j], c1[j]);
 
-    auto run = [&](int task, int par, v4i (&wv)[KSW], uint32_t (&code)[KSW]) {
+    int k = 0;  // tasks this CTA ran (the parity of the reduction buffer)
+    auto run = [&](int task, v4i (&wv)[KSW], uint32_t (&code)[KSW]) {
       const int u = task / NUG, cc = task % NUG;
-      const int nt = task + 2 * nblk;  // the task this ring slot holds next
+      const int par = k & 1;
+      ++k;
+      // the B operands: the same LDS words every task, read through an opaque base so
+      // they are not hoisted out of the task loop (they would hold 96 VGPRs)
+      const int xo = opaque_v(kq * KSW * 256 + l);
       v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < KSW; ++j) {
-        acc = fp4_step(wv[j], code[j], xb[j], acc);
-        if (w != 0) issue(nt, j, wv[j], code[j]);
+        v4i B[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) B[d] = x_lds[xo + (j * 4 + d) * 64];
+        acc = fp4_step(wv[j], code[j], B, acc);
+        issue(task + 2 * nblk, j, wv[j], code[j]);
         __builtin_amdgcn_sched_barrier(0);
       }
       red[par][w][l] = acc;
       __syncthreads();
-      if (w == 0) {
-        // lane l: rows 4 (l / 16) + v of the task's 16, batch row l % 16
-        v4f gs = red[par][0][l], us = red[par][QW][l];
+      if (w < 2) {
+        // wave r finishes 16-row group r of the pair: lane l holds rows 4 (l / 16) + v,
+        // batch row l % 16; the gate and up partials of the four K slices summed in order
+        const int g0 = 4 * w, u0 = 8 + 4 * w;
+        v4f gs = red[par][g0][l], us = red[par][u0][l];
 #pragma unroll
-        for (int i = 1; i < QW; ++i) {
-          gs += red[par][i][l];
-          us += red[par][QW + i][l];
+        for (int i = 1; i < QK; ++i) {
+          gs += red[par][g0 + i][l];
+          us += red[par][u0 + i][l];
         }
         const uint32_t mask = rl.umask[u];
         if (t < R && ((mask >> t) & 1u)) {
@@ -259,19 +286,20 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) h[v] = bf16_bits(gs[v] / (1.0f + expf(-gs[v])) * us[v]);
           const int sl = slot_of(rl, u, mask, t);
-          st_dev64(reinterpret_cast<uint64_t*>(mid + (size_t)sl * I + cc * 16 + 4 * grp),
+          st_dev64(reinterpret_cast<uint64_t*>(mid + (size_t)sl * I + (2 * cc + w) * 16 + 4 * grp),
                    (uint64_t)(h[0] | (h[1] << 16)) | ((uint64_t)(h[2] | (h[3] << 16)) << 32));
         }
-        drain();  // the mid stores (and this wave's in-flight loads) completed
-#pragma unroll
-        for (int j = 0; j < KSW; ++j) issue(nt, j, wv[j], code[j]);
-        if (l == 0) st_dev(&ready[u * NUG + cc], tag);
       }
     };
     for (int task = b; task < ntask; task += 2 * nblk) {
-      run(task, 0, wa, ca);
-      if (task + nblk < ntask) run(task + nblk, 1, wb, cb);
+      run(task, w0, c0);
+      if (task + nblk < ntask) run(task + nblk, w1, c1);
     }
+    // waves 0 and 1 made every mid store of this CTA: once they completed, the CTA's
+    // done word takes the launch tag (the one wait for stores in the stage)
+    if (w < 2) drain();
+    __syncthreads();
+    if (tid == 0) st_dev(&done[b], tag);
   }
 
   // ---------------------------------------------------------------- stage 2: down
@@ -279,70 +307,77 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   bool ok = true;
   {
     const uint32_t cv = W2::code_v(l), sv = W2::scale_v(l);
-    auto issue = [&](int f, int u, int s, v4i& wv, uint32_t& code) {
+    // the NDS steps of expert u's 16-row group f (an expert past the end: no traffic)
+    auto issue = [&](int f, int u, v4i (&wv)[NDS], uint32_t (&code)[NDS]) {
       const bool live = u < nd;
       const int e = __builtin_amdgcn_readfirstlane(rl.uexp[live ? u : 0]);
       const __amdgpu_buffer_rsrc_t rc =
           rsrc(p.w2 + (size_t)e * W2::code_bytes(H), live ? W2::code_bytes(H) : 0u);
       const __amdgpu_buffer_rsrc_t rs =
           rsrc(p.s2 + (size_t)e * W2::scale_bytes(H), live ? W2::scale_bytes(H) : 0u);
-      wv = ld16s<CP_NT>(rc, cv, W2::code_s(f, s));
-      code = ld1(rs, sv, W2::scale_s(f, s));
+#pragma unroll
+      for (int s = 0; s < NDS; ++s) {
+        wv[s] = ld16s<CP_NT>(rc, cv, W2::code_s(f, s));
+        code[s] = ld1(rs, sv, W2::scale_s(f, s));
+      }
     };
     bool first = true;
     for (int f = b; f < G::NDN; f += nblk) {
+      // waves 0..DW-1 take experts u = w, w + DW, ...; their first RING experts' weights
+      // fly while the last wave, with no load of its own in flight (loads complete in
+      // order), polls the done words; then every wave copies mid rows into LDS
       v4i dw[RING][NDS];
       uint32_t dc[RING][NDS];
+      const int wu = w < DW ? w : MOE_NDIST;  // the last wave takes no expert
 #pragma unroll
-      for (int k = 0; k < RING; ++k)
-#pragma unroll
-        for (int s = 0; s < NDS; ++s) issue(f, w + G::WAVES * k, s, dw[k][s], dc[k][s]);
+      for (int q = 0; q < RING; ++q) issue(f, wu + DW * q, dw[q], dc[q]);
       if (first) {
         first = false;
-        // every up/gate task of this launch, then the mid slot rows into LDS
-        const int nflag = nd * NUG;
-        ok = wait_until(guard, MONO_SITE_MID, [&]() {
-          bool all = true;
-          for (int i = tid; i < nflag; i += G::THREADS) all &= ld_dev(&ready[i]) == tag;
-          return __all(all);
-        });
+        if (w == DW)
+          ok = wait_until(guard, MONO_SITE_MID, [&]() {
+            bool all = true;
+            for (int i = l; i < nblk; i += WAVE) all &= ld_dev(&done[i]) == tag;
+            return __all(all);
+          });
         ok = cta_all(ok, ok_s);
-        stamp(p.timeline, MONO_TL_MIDQ);
         if (ok) {
-          const __amdgpu_buffer_rsrc_t rm = rsrc(mid, (uint32_t)G::SZ_MID);
-          constexpr int CPR = I * 2 / 16;  // 16-byte pieces of a mid row
-          for (int i = tid; i < R * MOE_SLOTS * CPR; i += G::THREADS) {
-            const int s = i / CPR, c = i % CPR;
-            *reinterpret_cast<v4i*>(mid_lds + s * G::MROW + c * 16) =
-                ld16<CP_DEV>(rm, (uint32_t)(s * I * 2 + c * 16));
-          }
+          // every wave copies 1 KiB pieces straight into LDS (a wave's copy lands after
+          // its weight loads, which the compute waits for anyway)
+          const uint32_t nbytes = (uint32_t)R * MOE_SLOTS * I * 2;
+          const __amdgpu_buffer_rsrc_t rm = rsrc(mid, nbytes);
+          for (uint32_t off = (uint32_t)w * 1024; off < nbytes; off += G::WAVES * 1024)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rm, (__attribute__((address_space(3))) void*)(mid_lds + off), 16, l * 16 + off,
+                0, 0, CP_DEV);
+          drain();
         }
         __syncthreads();
+        stamp(p.timeline, MONO_TL_MIDQ);
       }
       if (!ok) break;
       v4f acc = {0.f, 0.f, 0.f, 0.f};
-      for (int k0 = 0; w + G::WAVES * k0 < nd; k0 += RING) {
+      for (int k0 = 0; wu + DW * k0 < nd; k0 += RING) {
 #pragma unroll
-        for (int k = 0; k < RING; ++k) {
-          const int u = w + G::WAVES * (k0 + k);
+        for (int q = 0; q < RING; ++q) {
+          const int u = wu + DW * (k0 + q);
           if (u < nd) {
             const int sl = slot_of(rl, u, rl.umask[u], t);
             const bool on = sl >= 0;
             const float wt = on ? wslot[sl] : 0.f;
-            const uint8_t* mrow = mid_lds + (on ? sl : 0) * G::MROW + 64 * grp;
+            const uint8_t* mrow = mid_lds + (on ? sl : 0) * I * 2 + 64 * grp;
             v4f d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NDS; ++s) {
               v4i B[4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
+              for (int dd = 0; dd < 4; ++dd) {
                 const v4i z = {0, 0, 0, 0};
-                B[q] = on ? *reinterpret_cast<const v4i*>(mrow + s * 256 + q * 16) : z;
+                B[dd] = on ? *reinterpret_cast<const v4i*>(mrow + s * 256 + dd * 16) : z;
               }
-              d = fp4_step(dw[k][s], dc[k][s], B, d);
-              issue(f, u + G::WAVES * RING, s, dw[k][s], dc[k][s]);
-              __builtin_amdgcn_sched_barrier(0);
+              d = fp4_step(dw[q][s], dc[q][s], B, d);
             }
+            issue(f, u + DW * RING, dw[q], dc[q]);
+            __builtin_amdgcn_sched_barrier(0);
             acc += d * wt;
           }
         }
@@ -352,7 +387,7 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
       if (w == 0) {
         v4f ys = red[0][0][l];
 #pragma unroll
-        for (int i = 1; i < G::WAVES; ++i) ys += red[0][i][l];
+        for (int i = 1; i < DW; ++i) ys += red[0][i][l];
         if (t < R) {
           const int col = f * 16 + 4 * grp;
           uint32_t h[4];
@@ -435,6 +470,8 @@ extern "C" int mono_moe_mxfp4_launch(const MonoMoeMxfp4Args* a, mono_stream_t st
   int grid = 0;
   int rc = monokernel_grid(&grid);
   if (rc) return rc;
+  if (grid > MoeMxGeom<3072, 384>::MAX_GRID)
+    return set_error(MONO_E_DEVICE, "mono_moe_mxfp4_launch: more CUs than done words");
   if (a->hidden == 3072 && a->inter == 384) {
     auto k = a->layout == MONO_LAYOUT_AITER16 ? moe_mxfp4_kernel<3072, 384, true>
                                               : moe_mxfp4_kernel<3072, 384, false>;

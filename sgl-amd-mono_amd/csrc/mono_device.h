@@ -166,25 +166,17 @@ __device__ inline float wave_sum(float v) { return red64(v, OpAdd()); }
 __device__ inline float wave_max(float v) { return red64(v, OpMax()); }
 __device__ inline float row16_max(float v) { return red16(v, OpMax()); }
 
-// maximum of a u64 over the wave
-__device__ inline uint64_t wave_max_u64(uint64_t v) {
-  auto mx = [](uint64_t a, uint64_t b) { return a > b ? a : b; };
-  auto step = [&](uint32_t lo, uint32_t hi) { return ((uint64_t)hi << 32) | lo; };
-  v = mx(v, step(dpp_u<DPP_XOR1>((uint32_t)v), dpp_u<DPP_XOR1>((uint32_t)(v >> 32))));
-  v = mx(v, step(dpp_u<DPP_XOR2>((uint32_t)v), dpp_u<DPP_XOR2>((uint32_t)(v >> 32))));
-  v = mx(v, step(dpp_u<DPP_HALF_MIRROR>((uint32_t)v), dpp_u<DPP_HALF_MIRROR>((uint32_t)(v >> 32))));
-  v = mx(v, step(dpp_u<DPP_MIRROR>((uint32_t)v), dpp_u<DPP_MIRROR>((uint32_t)(v >> 32))));
-  {
-    auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
-    auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
-    v = mx(step(lo[0], hi[0]), step(lo[1], hi[1]));
-  }
-  {
-    auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
-    auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
-    v = mx(step(lo[0], hi[0]), step(lo[1], hi[1]));
-  }
-  return v;
+// maximum of a u32 over the wave (every lane ends with it)
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  v = mx(v, dpp_u<DPP_XOR1>(v));
+  v = mx(v, dpp_u<DPP_XOR2>(v));
+  v = mx(v, dpp_u<DPP_HALF_MIRROR>(v));
+  v = mx(v, dpp_u<DPP_MIRROR>(v));
+  auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = mx(a[0], a[1]);
+  auto c = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return mx(c[0], c[1]);
 }
 
 // ------------------------------------------------------------------ number formats
