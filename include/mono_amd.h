@@ -47,6 +47,9 @@ typedef void* mono_stream_t;
 #define MONO_SITE_LOGITS 1   /* routing waits on the router's logits */
 #define MONO_SITE_MID 2      /* a mid quant task waits on up/gate tiles */
 #define MONO_SITE_MQ 3       /* an expert-down tile waits on a quantised mid block */
+#define MONO_SITE_SCORES 4   /* a row's top-k waits on its indexer scores */
+#define MONO_SITE_TOPK 5     /* a sparse-MLA split waits on its row's top-k */
+#define MONO_SITE_SPLIT 6    /* a merge waits on its row's splits */
 
 int mono_version(void);
 const char* mono_last_error(void);
@@ -176,6 +179,62 @@ typedef struct {
 
 size_t mono_moe_mxfp4_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts);
 int mono_moe_mxfp4_launch(const MonoMoeMxfp4Args* args, mono_stream_t stream);
+
+/* ------------------------------------------------------------------------------
+ * The attention phase as one persistent launch: FP4 indexer scores of every key a row
+ * sees, their exact top-2048 (ranked by the radix order of the f32 score, ties to the
+ * lower position, kept in ascending position order; every key when a row sees at
+ * most 2048), and sparse MLA decode of the absorbed queries over the selected tokens'
+ * FP8 cache rows, merged across splits into the latent output (before W_UV).
+ * Replaces the index-score, top-k, split and merge stages of the reference layer
+ * kernel: sgl_amd_mono/glm53/gfx950/kernel.py:2684-3000 (scores; FP4 form
+ * sgl_amd_mono/deepseek_v41/gfx950/indexer/score_fp4.py:254-296), :3002-3636 (exact
+ * top-k), :3638-3973 (split), :3975-4123 (merge, without W_UV).
+ * Layouts (SGLang's FP4 index plane, sgl_amd_mono/deepseek_v41/gfx950/indexer/
+ * score_fp4.py:11-14): plane [pages, 4 (32-dim chunk), 64 (slot), 16 B] E2M1, low
+ * nibble first; plane_scale [pages, 4, 64] E8M0, slot s's byte at (s % 16) * 4 + s / 16;
+ * iq [R, 64 heads, 64 B] E2M1; iqs [R, 4 (chunk), 16 (head % 16), 4 (head / 16)] E8M0.
+ * The score of key t: sum_h iw[h] relu(sum_c 2^(qe - 127) 2^(ke - 127) iq[h, c] . k[t, c]).
+ * KV: kv [slots, 576] E4M3 (latent 512, rope 64) times kv_scale[slot]; a key's slot is
+ * page_table[req_ids[row], pos / 64] * 64 + pos % 64. Timeline marks 1-5 of this launch:
+ * scores, top-k, splits, merge done, exit. */
+typedef struct {
+  int32_t rows;          /* R, 1..48: decode rows, row r at positions[r] of req_ids[r] */
+  int32_t heads;         /* 32 */
+  int32_t index_heads;   /* 64 */
+  int32_t topk;          /* 2048 */
+  int32_t page;          /* 64 */
+  int32_t ctx_max;       /* keys a row may see at most (positions clamp to it): 1..32768;
+                            the row stride of `scores` */
+  int32_t pt_stride;     /* page_table row stride (entries), >= ceil(ctx_max / 64) */
+  int32_t pt_rows;       /* page_table rows */
+  uint32_t plane_pages;  /* pages of plane / plane_scale */
+  uint32_t kv_slots;     /* rows of kv / kv_scale */
+  float sm_scale;        /* softmax scale, (nope + rope)^-0.5 times any YaRN factor */
+  const int64_t* positions;  /* i64 [R]: the row's position (keys 0..position); < 0: none */
+  const int32_t* req_ids;    /* i32 [R] */
+  const int32_t* page_table; /* i32 [pt_rows, pt_stride] */
+  const void* q;             /* bf16 [R, 32, 576]: absorbed latent query, then rope */
+  const uint8_t* iq;
+  const uint8_t* iqs;
+  const float* iw;           /* f32 [R, 64]: index head weights */
+  const uint8_t* plane;
+  const uint8_t* plane_scale;
+  const uint8_t* kv;
+  const float* kv_scale;     /* f32 [slots] */
+  void* out;                 /* bf16 [R, 32, 512] */
+  float* scores;             /* optional f32 [R, ctx_max]: the indexer scores */
+  int32_t* topk_pos;         /* optional i32 [R, 2048]: selected positions, -1 past count */
+  void* scratch;             /* runtime owned, mono_attn_scratch_bytes() */
+  int32_t* guard;
+  uint32_t* host_error;
+  int32_t fault_site;        /* test fault injection (MONO_SITE_SCORES/TOPK/SPLIT) */
+  int32_t fault_after;
+  uint64_t* timeline;
+} MonoAttnArgs;
+
+size_t mono_attn_scratch_bytes(int32_t rows_max);
+int mono_attn_launch(const MonoAttnArgs* args, mono_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -82,11 +82,14 @@ def e8m0_to_f32(codes) -> np.ndarray:
     return np.where(b == 255, np.nan, v).astype(np.float32)
 
 
+# byte -> (value of the low nibble, value of the high nibble)
+_E2M1_PAIRS = np.stack([E2M1[np.arange(256) & 15], E2M1[np.arange(256) >> 4]], axis=-1)
+
+
 def unpack_e2m1(packed) -> np.ndarray:
     """[..., K/2] uint8 (even index in the low nibble) -> [..., K] f32 values."""
     p = np.asarray(packed, dtype=np.uint8)
-    lo, hi = E2M1[p & 15], E2M1[p >> 4]
-    return np.stack([lo, hi], axis=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
+    return _E2M1_PAIRS[p].reshape(*p.shape[:-1], p.shape[-1] * 2)
 
 
 def dequant_mxfp4(packed, scales) -> np.ndarray:

@@ -42,7 +42,10 @@ TL_MARKS = ("start", "staged", "routed", "upgate", "midq", "down", "end")
 TL_COLS = 8
 
 # wait sites (the deadline error word holds 1 + site)
-SITES = {1: "logits", 2: "mid", 3: "mq"}
+SITES = {1: "logits", 2: "mid", 3: "mq", 4: "scores", 5: "topk", 6: "split"}
+SITE_MID, SITE_SCORES, SITE_TOPK, SITE_SPLIT = 2, 4, 5, 6
+# timeline marks of the attention launch (same columns)
+TL_ATTN_MARKS = ("start", "scores", "topk", "split", "merge", "exit", "end")
 
 
 class MonoDeviceInfo(ctypes.Structure):
@@ -114,6 +117,44 @@ class MonoMoeMxfp4Args(ctypes.Structure):
     ]
 
 
+class MonoAttnArgs(ctypes.Structure):
+    """Mirror of ``MonoAttnArgs`` in mono_amd.h (same order and types)."""
+
+    _fields_ = [
+        ("rows", c_int32),
+        ("heads", c_int32),
+        ("index_heads", c_int32),
+        ("topk", c_int32),
+        ("page", c_int32),
+        ("ctx_max", c_int32),
+        ("pt_stride", c_int32),
+        ("pt_rows", c_int32),
+        ("plane_pages", c_uint32),
+        ("kv_slots", c_uint32),
+        ("sm_scale", c_float),
+        ("positions", c_void_p),
+        ("req_ids", c_void_p),
+        ("page_table", c_void_p),
+        ("q", c_void_p),
+        ("iq", c_void_p),
+        ("iqs", c_void_p),
+        ("iw", c_void_p),
+        ("plane", c_void_p),
+        ("plane_scale", c_void_p),
+        ("kv", c_void_p),
+        ("kv_scale", c_void_p),
+        ("out", c_void_p),
+        ("scores", c_void_p),
+        ("topk_pos", c_void_p),
+        ("scratch", c_void_p),
+        ("guard", c_void_p),
+        ("host_error", c_void_p),
+        ("fault_site", c_int32),
+        ("fault_after", c_int32),
+        ("timeline", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mono_version": (c_int32, []),
@@ -125,6 +166,8 @@ SIGNATURES = {
     "mono_moe_fp8_launch": (c_int32, [ctypes.POINTER(MonoMoeFp8Args), c_void_p]),
     "mono_moe_mxfp4_scratch_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "mono_moe_mxfp4_launch": (c_int32, [ctypes.POINTER(MonoMoeMxfp4Args), c_void_p]),
+    "mono_attn_scratch_bytes": (c_size_t, [c_int32]),
+    "mono_attn_launch": (c_int32, [ctypes.POINTER(MonoAttnArgs), c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,669 @@
+// The attention phase of the DSA layer as one persistent gfx950 launch: the FP4
+// indexer's scores, their exact top-2048, and sparse MLA decode over the selected
+// tokens' FP8 cache rows.
+//
+// Stages, every CTA in order (task t of a stage runs on CTA (t + offset) mod grid):
+//   1  scores: task (row, 1024-token chunk), one 64-token page a wave. Per 16-token
+//      tile and 16-head group one scaled 16x16x128 MFMA with E2M1 operands and their
+//      E8M0 scales (query rows = heads, key columns = tokens, K = the 128 dims); relu,
+//      the head weights and the sum over heads stay in the lane, then two permlane
+//      swaps sum the lane groups. Scores go to scratch; the chunk's done word follows.
+//   2  top-k: task = row. Its scores as radix keys in LDS (128 KB); three histogram
+//      passes (12, 12, 8 bits) find the 2048th key T; the selection is every key above
+//      T plus the lowest positions holding T, written in ascending position order.
+//   3  split: task (row, 128-key split), all 32 heads. The split's tokens (through the
+//      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
+//      widened exactly), times the token's scale and the softmax scale; per head the
+//      split's max m and sum l; P, with the token's scale folded in, as bf16; O = P V on
+//      MFMAs, V read from the same rows. O, m and l go to scratch.
+//   4  merge: task (row, head): o = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s,
+//      rounded to bf16.
+// Every hand-off is a (word = launch tag) wait under the guard's deadline.
+//
+// Reference: FP4 scores sgl_amd_mono/deepseek_v41/gfx950/indexer/score_fp4.py:1-20,
+// 254-296 (plane layout, formula); exact top-k sgl_amd_mono/glm53/gfx950/kernel.py:
+// 3002-3636 (rule: glm53/check.py:94-117); sparse MLA split and merge kernel.py:
+// 3638-4123; softmax scale glm53/gfx950/config.py:180-181.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "mono_abi.h"
+#include "mono_device.h"
+
+namespace mono {
+
+constexpr int AT_HEADS = 32;     // attention heads of one GPU's TP=4 share
+constexpr int AT_IHEADS = 64;    // index heads
+constexpr int AT_KV = 576;       // cached row: latent 512 + rope 64
+constexpr int AT_LAT = 512;
+constexpr int AT_PAGE = 64;
+constexpr int AT_TOPK = 2048;
+constexpr int AT_MAXCTX = 32768;  // keys a row may see (the top-k's LDS image)
+constexpr int AT_CHUNK = 1024;    // tokens of a score task
+constexpr int AT_NCHUNK = AT_MAXCTX / AT_CHUNK;
+constexpr int AT_SPLIT = 128;     // keys of a split task
+constexpr int AT_NSPLIT = AT_TOPK / AT_SPLIT;
+constexpr int AT_MAXR = 48;
+constexpr int AT_THREADS = 1024;
+constexpr int AT_WAVES = AT_THREADS / WAVE;
+
+constexpr size_t at_align(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct AttnScratch {
+  static constexpr size_t SCORES = 0;  // f32 [MAXR][MAXCTX]
+  static constexpr size_t SCORE_DONE = at_align(SCORES + (size_t)AT_MAXR * AT_MAXCTX * 4);
+  static constexpr size_t TOPK = at_align(SCORE_DONE + (size_t)AT_MAXR * AT_NCHUNK * 4);
+  static constexpr size_t TOPK_DONE = at_align(TOPK + (size_t)AT_MAXR * AT_TOPK * 4);
+  static constexpr size_t ACC = at_align(TOPK_DONE + (size_t)AT_MAXR * 4);  // f32 [R][split][h][512]
+  static constexpr size_t ML = at_align(ACC + (size_t)AT_MAXR * AT_NSPLIT * AT_HEADS * AT_LAT * 4);
+  static constexpr size_t SPLIT_DONE = at_align(ML + (size_t)AT_MAXR * AT_NSPLIT * AT_HEADS * 8);
+  static constexpr size_t BYTES = at_align(SPLIT_DONE + (size_t)AT_MAXR * AT_NSPLIT * 4);
+};
+
+struct AttnParams {
+  int rows, ctx_max, pt_stride, pt_rows;
+  float sm_scale;
+  uint32_t plane_pages, kv_slots;
+  const int64_t* positions;
+  const int32_t* req_ids;
+  const int32_t* page_table;
+  const uint16_t* q;
+  const uint8_t* iq;
+  const uint8_t* iqs;
+  const float* iw;
+  const uint8_t* plane;
+  const uint8_t* plane_scale;
+  const uint8_t* kv;
+  const float* kv_scale;
+  uint16_t* out;
+  float* scores_out;
+  int32_t* topk_out;
+  uint8_t* scratch;
+  int32_t* guard;
+  uint32_t* host_err;
+  int fault_site, fault_after;
+  uint64_t* timeline;
+};
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// 16x16x128 E2M1 x E2M1 -> f32, each operand's E8M0 scale the byte OA / OB of its dword
+template <int OA, int OB>
+__device__ inline v4f mfma_fp4(v4i a, v4i b, int sa, int sb) {
+  const v8i A = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
+  const v8i B = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, z, 4, 4, OA, sa, OB, sb);
+}
+
+// 8 E4M3 (two dwords) -> 8 bf16 (exact)
+__device__ inline v8bf fp8x8_bf16(uint32_t lo, uint32_t hi) {
+  const v2bf a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+  const v2bf b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+  const v2bf c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+  const v2bf d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+  return v8bf{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ inline v4f mfma_bf16(v8bf a, v8bf b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// exclusive prefix sum over the CTA's 1024 threads; `wsum` is 16 ints of LDS
+__device__ inline int block_scan(int v, int* wsum, int& total) {
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int y = __shfl_up(x, o, WAVE);
+    if (l >= o) x += y;
+  }
+  if (l == WAVE - 1) wsum[w] = x;
+  __syncthreads();
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < AT_WAVES; ++i) {
+    const int s = wsum[i];
+    pre += i < w ? s : 0;
+    tot += s;
+  }
+  __syncthreads();
+  total = tot;
+  return pre + x - v;
+}
+
+// one radix pass over keys[0..n) whose bits above `shift + BITS` equal `prefix`: the
+// histogram of the next BITS bits, then the bin holding the kk-th largest such key and
+// how many of them lie in higher bins
+template <int BITS>
+__device__ inline void radix_pass(const uint32_t* keys, int n, int shift, uint32_t prefix,
+                                  bool any_prefix, int kk, uint32_t* hist, int* wsum,
+                                  int* res) {
+  constexpr int NB = 1 << BITS;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < NB; i += AT_THREADS) hist[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += AT_THREADS) {
+    const uint32_t k = keys[i];
+    const bool in = any_prefix || (k >> (shift + BITS)) == prefix;
+    if (in) atomicAdd(&hist[(k >> shift) & (NB - 1)], 1u);
+  }
+  __syncthreads();
+  // thread t owns bins [NB - G (t + 1), NB - G t): the scan runs from the top bin down
+  constexpr int G = NB >= AT_THREADS ? NB / AT_THREADS : 1;
+  const bool owns = tid * G < NB;
+  int s = 0;
+  if (owns)
+#pragma unroll
+    for (int g = 0; g < G; ++g) s += (int)hist[NB - 1 - (tid * G + g)];
+  int tot;
+  const int pre = block_scan(s, wsum, tot);
+  if (owns && pre < kk && kk <= pre + s) {
+    int cum = pre;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int bin = NB - 1 - (tid * G + g);
+      const int c = (int)hist[bin];
+      if (cum < kk && kk <= cum + c) {
+        res[0] = bin;
+        res[1] = cum;
+      }
+      cum += c;
+    }
+  }
+  __syncthreads();
+}
+
+__global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
+  using S = AttnScratch;
+  const int tid = threadIdx.x, l = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int R = p.rows;
+  const int nblk = gridDim.x, b = blockIdx.x;
+
+  // one LDS arena, carved per stage
+  __shared__ __attribute__((aligned(16))) uint8_t smem[150 * 1024];
+  __shared__ uint32_t head_s[4];
+  __shared__ int ok_s;
+  __shared__ int wsum[AT_WAVES];
+  __shared__ int res_s[2];
+
+  float* scores = reinterpret_cast<float*>(p.scratch + S::SCORES);
+  uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S::SCORE_DONE);
+  int32_t* topk = reinterpret_cast<int32_t*>(p.scratch + S::TOPK);
+  uint32_t* topk_done = reinterpret_cast<uint32_t*>(p.scratch + S::TOPK_DONE);
+  float* accs = reinterpret_cast<float*>(p.scratch + S::ACC);
+  float* mls = reinterpret_cast<float*>(p.scratch + S::ML);
+  uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S::SPLIT_DONE);
+
+  stamp(p.timeline, MONO_TL_START);
+  if (tid == 0) {
+    const v4i h = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)h[i];
+    ok_s = 1;
+  }
+  __syncthreads();
+  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
+  Guard guard;
+  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
+  bool ok = true;
+
+  // keys a row sees (its position + 1, within the launch's context bound)
+  auto row_n = [&](int r) -> int {
+    const int64_t pos = p.positions[r];
+    return (int)(pos < 0 ? 0 : (pos + 1 > p.ctx_max ? p.ctx_max : pos + 1));
+  };
+  // the page table through a bounded resource: an entry past it reads page 0
+  const __amdgpu_buffer_rsrc_t rpt =
+      rsrc(p.page_table, (uint32_t)p.pt_rows * (uint32_t)p.pt_stride * 4u);
+  auto page_of = [&](int r, int pg) -> int {
+    return ld4<CP_NONE>(rpt, ((uint32_t)p.req_ids[r] * (uint32_t)p.pt_stride + (uint32_t)pg) * 4u);
+  };
+  const __amdgpu_buffer_rsrc_t rplane = rsrc(p.plane, p.plane_pages * 4096u);
+  const __amdgpu_buffer_rsrc_t rpsc = rsrc(p.plane_scale, p.plane_pages * 256u);
+
+  // ---------------------------------------------------------------- 1: scores
+  for (int task = b; task < R * AT_NCHUNK; task += nblk) {
+    const int r = task / AT_NCHUNK, c = task % AT_NCHUNK;
+    const int n = row_n(r);
+    if (c * AT_CHUNK >= n) continue;
+    const int pg = c * (AT_CHUNK / AT_PAGE) + w;
+    if (pg * AT_PAGE < n) {
+      const int pid = __builtin_amdgcn_readfirstlane(page_of(r, pg));
+      // the row's query as A operands: head tile mi, lane l: head 16 mi + l % 16, dims
+      // 32 (l / 16) .. (16 bytes); its scales: the dword of lane l holds tile mi's byte mi
+      const __amdgpu_buffer_rsrc_t rq = rsrc(p.iq + (size_t)r * AT_IHEADS * 64, AT_IHEADS * 64);
+      v4i qa[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        qa[mi] = ld16<CP_NONE>(rq, (uint32_t)((16 * mi + (l & 15)) * 64 + 16 * (l >> 4)));
+      const int qs = ld4<CP_NONE>(rsrc(p.iqs + (size_t)r * 256, 256), (uint32_t)l * 4);
+      // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
+      v4f wv[4];
+      const __amdgpu_buffer_rsrc_t rw = rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        wv[mi] = __builtin_bit_cast(
+            v4f, ld16<CP_NONE>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
+      // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
+      // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword
+      v4i kb[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        kb[nt] = ld16<CP_NT>(rplane, (uint32_t)pid * 4096u +
+                                         (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
+      const int ks = ld4<CP_NT>(rpsc, (uint32_t)pid * 256u + (uint32_t)l * 4);
+      float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
+      auto tile = [&](auto nt_c) {
+        constexpr int NT = decltype(nt_c)::value;
+        float acc = 0.f;
+        auto head_tile = [&](auto mi_c) {
+          constexpr int MI = decltype(mi_c)::value;
+          const v4f d = mfma_fp4<MI, NT>(qa[MI], kb[NT], qs, ks);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = fmaf(fmaxf(d[e], 0.f), wv[MI][e], acc);
+        };
+        head_tile(std::integral_constant<int, 0>());
+        head_tile(std::integral_constant<int, 1>());
+        head_tile(std::integral_constant<int, 2>());
+        head_tile(std::integral_constant<int, 3>());
+        // sum the four lane groups (heads 4 (l / 16) ..): lane l keeps token l % 16
+        float a, bb;
+        swap16(acc, a, bb);
+        acc = a + bb;
+        swap32(acc, a, bb);
+        acc = a + bb;
+        if (l < 16) {
+          st_devf(dst + 16 * NT + l, acc);
+          const int tok = pg * AT_PAGE + 16 * NT + l;
+          if (p.scores_out && tok < n) p.scores_out[(size_t)r * p.ctx_max + tok] = acc;
+        }
+      };
+      tile(std::integral_constant<int, 0>());
+      tile(std::integral_constant<int, 1>());
+      tile(std::integral_constant<int, 2>());
+      tile(std::integral_constant<int, 3>());
+    }
+    drain();
+    __syncthreads();
+    if (tid == 0) st_dev(&score_done[r * AT_NCHUNK + c], tag);
+  }
+
+  // ---------------------------------------------------------------- 2: top-k
+  stamp(p.timeline, MONO_TL_STAGED);
+  for (int r = b; r < R; r += nblk) {
+    const int n = row_n(r);
+    int32_t* sel = topk + (size_t)r * AT_TOPK;
+    if (n <= AT_TOPK) {
+      // every key of the row, in position order
+      for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
+        if (i < n) st_dev(reinterpret_cast<uint32_t*>(sel + i), (uint32_t)i);
+        if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = i < n ? i : -1;
+      }
+    } else {
+      const int nch = (n + AT_CHUNK - 1) / AT_CHUNK;
+      if (w == 0)
+        ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
+          return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + l]) == tag);
+        });
+      ok = cta_all(ok, ok_s);
+      if (ok) {
+        uint32_t* keys = reinterpret_cast<uint32_t*>(smem);
+        uint32_t* hist = keys + AT_MAXCTX;
+        const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
+        for (int i = tid * 4; i < n; i += AT_THREADS * 4) {
+          const v4i v = ld16<CP_DEV>(rs, (uint32_t)i * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) keys[i + e] = radix_key(__int_as_float(v[e]));
+        }
+        __syncthreads();
+        const int k = AT_TOPK;
+        radix_pass<12>(keys, n, 20, 0, true, k, hist, wsum, res_s);
+        const uint32_t b1 = (uint32_t)res_s[0];
+        const int above1 = res_s[1];
+        radix_pass<12>(keys, n, 8, b1, false, k - above1, hist, wsum, res_s);
+        const uint32_t b2 = (uint32_t)res_s[0];
+        const int above2 = res_s[1];
+        radix_pass<8>(keys, n, 0, (b1 << 12) | b2, false, k - above1 - above2, hist, wsum,
+                      res_s);
+        const uint32_t T = (b1 << 20) | (b2 << 8) | (uint32_t)res_s[0];
+        const int need = k - above1 - above2 - res_s[1];  // keys equal to T to take
+        // thread t: positions [32 t, 32 t + 32), in order
+        constexpr int PER = AT_MAXCTX / AT_THREADS;
+        const int i0 = tid * PER;
+        int gt = 0, eq = 0;
+#pragma unroll 8
+        for (int j = 0; j < PER; ++j) {
+          const int i = i0 + j;
+          const uint32_t kv = i < n ? keys[i] : 0u;
+          gt += (i < n) & (kv > T);
+          eq += (i < n) & (kv == T);
+        }
+        int tot;
+        const int eq_before = block_scan(eq, wsum, tot);
+        int take = need - eq_before;
+        take = take < 0 ? 0 : (take > eq ? eq : take);
+        const int at = block_scan(gt + take, wsum, tot);
+        int o = at;
+        for (int j = 0; j < PER; ++j) {
+          const int i = i0 + j;
+          if (i >= n) break;
+          const uint32_t kv = keys[i];
+          bool pick = kv > T;
+          if (kv == T && take > 0) {
+            pick = true;
+            --take;
+          }
+          if (pick && o < AT_TOPK) {
+            st_dev(reinterpret_cast<uint32_t*>(sel + o), (uint32_t)i);
+            if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + o] = i;
+            ++o;
+          }
+        }
+      }
+    }
+    drain();
+    __syncthreads();
+    if (tid == 0 && ok) st_dev(&topk_done[r], tag);
+  }
+
+  // ---------------------------------------------------------------- 3: split
+  stamp(p.timeline, MONO_TL_ROUTED);
+  {
+    // LDS: K rows (E4M3, 576 + 16 bytes apart), q (bf16, 1152 + 16), S (f32), P (bf16),
+    // the split's slots and token scales
+    constexpr int KSTR = AT_KV + 16, QSTR = AT_KV * 2 + 16, SSTR = AT_SPLIT + 4,
+                  PSTR = AT_SPLIT * 2 + 16;
+    uint8_t* kbuf = smem;
+    uint8_t* qbuf = kbuf + AT_SPLIT * KSTR;
+    float* sbuf = reinterpret_cast<float*>(qbuf + AT_HEADS * QSTR);
+    uint8_t* pbuf = reinterpret_cast<uint8_t*>(sbuf + AT_HEADS * SSTR);
+    int32_t* slot_s = reinterpret_cast<int32_t*>(pbuf + AT_HEADS * PSTR);
+    float* ksc = reinterpret_cast<float*>(slot_s + AT_SPLIT);
+    static_assert(AT_SPLIT * KSTR + AT_HEADS * QSTR + AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
+                          AT_SPLIT * 8 <=
+                      150 * 1024,
+                  "split LDS");
+    const __amdgpu_buffer_rsrc_t rkv = rsrc(p.kv, p.kv_slots * (uint32_t)AT_KV);
+    const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, p.kv_slots * 4u);
+    const int nt = R * AT_NSPLIT;
+    for (int t0 = 0; t0 < nt; t0 += nblk) {
+      const int task = t0 + (b + nblk - (R % nblk)) % nblk;  // rows' top-k CTAs go last
+      if (task >= nt) continue;
+      const int r = task / AT_NSPLIT, sp = task % AT_NSPLIT;
+      const int n = row_n(r);
+      const int k = n < AT_TOPK ? n : AT_TOPK;
+      const int kcnt = k - sp * AT_SPLIT < AT_SPLIT ? k - sp * AT_SPLIT : AT_SPLIT;
+      if (kcnt <= 0) continue;
+      if (w == 0)
+        ok = wait_until(guard, MONO_SITE_TOPK,
+                        [&]() { return ld_dev(&topk_done[r]) == tag; });
+      ok = cta_all(ok, ok_s);
+      if (!ok) break;
+      // the split's tokens -> cache slots
+      if (tid < AT_SPLIT) {
+        int slot = -1;
+        if (tid < kcnt) {
+          const int pos = (int)ld_dev(reinterpret_cast<const uint32_t*>(
+              topk + (size_t)r * AT_TOPK + sp * AT_SPLIT + tid));
+          slot = page_of(r, pos >> 6) * AT_PAGE + (pos & 63);
+        }
+        slot_s[tid] = slot;
+        ksc[tid] = slot >= 0 ? __int_as_float(ld4<CP_NONE>(rks, (uint32_t)slot * 4)) : 0.f;
+      }
+      // q of the row, all heads: [32][576] bf16
+      const __amdgpu_buffer_rsrc_t rq = rsrc(p.q + (size_t)r * AT_HEADS * AT_KV, AT_HEADS * AT_KV * 2);
+      for (int i = tid; i < AT_HEADS * AT_KV / 8; i += AT_THREADS) {
+        const int h = i / (AT_KV / 8), c = i % (AT_KV / 8);
+        *reinterpret_cast<v4i*>(qbuf + h * QSTR + c * 16) = ld16<CP_NONE>(rq, (uint32_t)i * 16);
+      }
+      __syncthreads();
+      // gather the rows: 36 pieces of 16 bytes a row (a dead slot reads zeros)
+      for (int i = tid; i < AT_SPLIT * (AT_KV / 16); i += AT_THREADS) {
+        const int j = i / (AT_KV / 16), c = i % (AT_KV / 16);
+        const int slot = slot_s[j];
+        const uint32_t off = slot >= 0 ? (uint32_t)slot * AT_KV + c * 16 : 0x80000000u;
+        *reinterpret_cast<v4i*>(kbuf + j * KSTR + c * 16) = ld16<CP_NT>(rkv, off);
+      }
+      __syncthreads();
+      // S = q K^T: wave w takes heads 16 (w / 8) .. and keys 16 (w % 8) ..
+      {
+        const int h0 = 16 * (w >> 3), j0 = 16 * (w & 7);
+        v4f d = {0.f, 0.f, 0.f, 0.f};
+        const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4);
+        const uint8_t* kr = kbuf + (j0 + (l & 15)) * KSTR + 8 * (l >> 4);
+#pragma unroll 6
+        for (int ks = 0; ks < AT_KV / 32; ++ks) {
+          const v8bf a = *reinterpret_cast<const v8bf*>(qa + ks * 64);
+          const v2i kk = *reinterpret_cast<const v2i*>(kr + ks * 32);
+          d = mfma_bf16(a, fp8x8_bf16((uint32_t)kk[0], (uint32_t)kk[1]), d);
+        }
+        const float f = ksc[j0 + (l & 15)] * p.sm_scale;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sbuf[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e] * f;
+      }
+      __syncthreads();
+      // softmax of the split, per head: wave w takes heads 2w, 2w + 1; lane l keys l, l + 64
+      float* ml = mls + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * 2;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int h = 2 * w + hh;
+        const bool v0 = l < kcnt, v1 = l + 64 < kcnt;
+        const float s0 = v0 ? sbuf[h * SSTR + l] : -INFINITY;
+        const float s1 = v1 ? sbuf[h * SSTR + l + 64] : -INFINITY;
+        const float m = wave_max(fmaxf(s0, s1));
+        const float p0 = v0 ? expf(s0 - m) : 0.f, p1 = v1 ? expf(s1 - m) : 0.f;
+        const float lsum = wave_sum(p0 + p1);
+        // P with the token's scale folded in (V = E4M3 value x scale)
+        reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l] = (uint16_t)bf16_bits(p0 * ksc[l]);
+        reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l + 64] =
+            (uint16_t)bf16_bits(p1 * ksc[l + 64]);
+        if (l == 0) {
+          st_devf(ml + 2 * h, m);
+          st_devf(ml + 2 * h + 1, lsum);
+        }
+      }
+      __syncthreads();
+      // O = P V: wave w takes heads 16 (w / 8) .. and dims 64 (w % 8) ..; MFMA j4 covers
+      // dims d0 + 4 c + j4 (column c), so one dword of a row feeds four MFMAs
+      {
+        const int h0 = 16 * (w >> 3), d0 = 64 * (w & 7);
+        const int c = l & 15, g = l >> 4;
+        v4f o0 = {0.f, 0.f, 0.f, 0.f}, o1 = o0, o2 = o0, o3 = o0;
+        const uint8_t* pa = pbuf + (h0 + c) * PSTR + 16 * g;
+#pragma unroll
+        for (int kst = 0; kst < AT_SPLIT / 32; ++kst) {
+          const v8bf a = *reinterpret_cast<const v8bf*>(pa + kst * 64);
+          uint32_t dv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            dv[i] = *reinterpret_cast<const uint32_t*>(kbuf + (32 * kst + 8 * g + i) * KSTR + d0 +
+                                                       4 * c);
+          // byte j of keys (2i, 2i + 1): perm picks bytes j and j + 1 of both dwords
+          uint32_t pr[4][2];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pr[i][0] = __builtin_amdgcn_perm(dv[2 * i + 1], dv[2 * i], 0x05010400u);  // j 0, 1
+            pr[i][1] = __builtin_amdgcn_perm(dv[2 * i + 1], dv[2 * i], 0x07030602u);  // j 2, 3
+          }
+          auto gather = [&](auto hi_c, int which) {
+            constexpr bool HI = decltype(hi_c)::value;
+            const v2bf q0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[0][which], 1.0f, HI);
+            const v2bf q1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[1][which], 1.0f, HI);
+            const v2bf q2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[2][which], 1.0f, HI);
+            const v2bf q3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[3][which], 1.0f, HI);
+            return v8bf{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
+          };
+          const v8bf bj[4] = {gather(std::false_type(), 0), gather(std::true_type(), 0),
+                              gather(std::false_type(), 1), gather(std::true_type(), 1)};
+          o0 = mfma_bf16(a, bj[0], o0);
+          o1 = mfma_bf16(a, bj[1], o1);
+          o2 = mfma_bf16(a, bj[2], o2);
+          o3 = mfma_bf16(a, bj[3], o3);
+        }
+        float* acc = accs + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * AT_LAT;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int h = h0 + 4 * g + e;
+          const v4f v = {o0[e], o1[e], o2[e], o3[e]};
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(v4i, v), rsrc(acc, AT_HEADS * AT_LAT * 4),
+              (uint32_t)(h * AT_LAT + d0 + 4 * c) * 4, 0, CP_DEV);
+        }
+      }
+      drain();
+      __syncthreads();
+      if (tid == 0) st_dev(&split_done[r * AT_NSPLIT + sp], tag);
+    }
+  }
+
+  // ---------------------------------------------------------------- 4: merge
+  stamp(p.timeline, MONO_TL_UPGATE);
+  {
+    float* red = reinterpret_cast<float*>(smem);  // [NSPLIT][512]
+    __shared__ float wsp_s[AT_NSPLIT];
+    __shared__ float linv_s;
+    for (int task = b; task < R * AT_HEADS; task += nblk) {
+      if (!ok) break;
+      const int r = task / AT_HEADS, h = task % AT_HEADS;
+      const int n = row_n(r);
+      const int k = n < AT_TOPK ? n : AT_TOPK;
+      const int nsp = (k + AT_SPLIT - 1) / AT_SPLIT;
+      if (w == 0 && nsp > 0)
+        ok = wait_until(guard, MONO_SITE_SPLIT, [&]() {
+          return __all(l >= nsp || ld_dev(&split_done[r * AT_NSPLIT + l]) == tag);
+        });
+      ok = cta_all(ok, ok_s);
+      if (!ok) break;
+      if (w == 0) {
+        const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
+        const bool on = l < nsp;
+        const float m = on ? __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
+                                 ml + ((size_t)l * AT_HEADS + h) * 2)))
+                           : -INFINITY;
+        const float ls = on ? __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
+                                  ml + ((size_t)l * AT_HEADS + h) * 2 + 1)))
+                            : 0.f;
+        const float M = wave_max(m);
+        const float ws = on ? expf(m - M) : 0.f;
+        const float L = wave_sum(ws * ls);
+        if (l < AT_NSPLIT) wsp_s[l] = ws;
+        if (l == 0) linv_s = L > 0.f ? 1.0f / L : 0.f;
+      }
+      __syncthreads();
+      {
+        const int sp = tid >> 6, d8 = tid & 63;
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (sp < nsp) {
+          const __amdgpu_buffer_rsrc_t ra = rsrc(
+              accs + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS + h) * AT_LAT, AT_LAT * 4);
+          const v4i a0 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32);
+          const v4i a1 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32 + 16);
+          const float ws = wsp_s[sp];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = __int_as_float(a0[e]) * ws;
+            v[4 + e] = __int_as_float(a1[e]) * ws;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[sp * AT_LAT + 8 * d8 + e] = v[e];
+      }
+      __syncthreads();
+      if (tid < AT_LAT) {
+        float s = 0.f;
+        for (int sp = 0; sp < nsp; ++sp) s += red[sp * AT_LAT + tid];
+        p.out[((size_t)r * AT_HEADS + h) * AT_LAT + tid] = (uint16_t)bf16_bits(s * linv_s);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---------------------------------------------------------------- exit
+  stamp(p.timeline, MONO_TL_DOWN);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
+    drain();
+    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
+    if (old == (uint32_t)nblk - 1u) {
+      st_dev(gw + MONO_GUARD_EXIT, 0u);
+      st_dev(gw + MONO_GUARD_EPOCH, tag);
+    }
+  }
+  stamp(p.timeline, MONO_TL_END);
+}
+
+}  // namespace mono
+
+using namespace mono;
+
+extern "C" size_t mono_attn_scratch_bytes(int32_t rows_max) {
+  return (rows_max >= 1 && rows_max <= AT_MAXR) ? AttnScratch::BYTES : 0;
+}
+
+extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
+  if (!a) return set_error(MONO_E_ARG, "mono_attn_launch: null args");
+  if (a->rows < 1 || a->rows > AT_MAXR)
+    return set_error(MONO_E_ARG, "mono_attn_launch: rows must be 1..48");
+  if (a->heads != AT_HEADS || a->index_heads != AT_IHEADS || a->topk != AT_TOPK ||
+      a->page != AT_PAGE)
+    return set_error(MONO_E_ARG, "mono_attn_launch: built for 32 heads, 64 index heads, "
+                                 "top-2048 and 64-token pages");
+  if (a->ctx_max < 1 || a->ctx_max > AT_MAXCTX)
+    return set_error(MONO_E_ARG, "mono_attn_launch: ctx_max must be 1..32768");
+  if (a->pt_stride < (a->ctx_max + AT_PAGE - 1) / AT_PAGE || a->pt_rows < 1 ||
+      (uint64_t)a->pt_rows * a->pt_stride * 4 > 0x7FFFFFFFull)
+    return set_error(MONO_E_ARG, "mono_attn_launch: page table rows shorter than ctx_max");
+  if (a->plane_pages == 0 || a->plane_pages > (1u << 19) || a->kv_slots == 0 ||
+      (uint64_t)a->kv_slots * AT_KV > 0x7FFFFFFFull)
+    return set_error(MONO_E_ARG, "mono_attn_launch: plane_pages / kv_slots out of range");
+  if (!a->positions || !a->req_ids || !a->page_table || !a->q || !a->iq || !a->iqs || !a->iw ||
+      !a->plane || !a->plane_scale || !a->kv || !a->kv_scale || !a->out || !a->scratch ||
+      !a->guard)
+    return set_error(MONO_E_ARG, "mono_attn_launch: null tensor");
+  AttnParams p;
+  p.rows = a->rows;
+  p.ctx_max = a->ctx_max;
+  p.pt_stride = a->pt_stride;
+  p.pt_rows = a->pt_rows;
+  p.sm_scale = a->sm_scale;
+  p.plane_pages = a->plane_pages;
+  p.kv_slots = a->kv_slots;
+  p.positions = a->positions;
+  p.req_ids = a->req_ids;
+  p.page_table = a->page_table;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.iq = a->iq;
+  p.iqs = a->iqs;
+  p.iw = a->iw;
+  p.plane = a->plane;
+  p.plane_scale = a->plane_scale;
+  p.kv = a->kv;
+  p.kv_scale = a->kv_scale;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.scores_out = a->scores;
+  p.topk_out = a->topk_pos;
+  p.scratch = static_cast<uint8_t*>(a->scratch);
+  p.guard = a->guard;
+  p.host_err = nullptr;
+  if (a->host_error) {
+    void* dptr = nullptr;
+    if (hipHostGetDevicePointer(&dptr, a->host_error, 0) != hipSuccess || !dptr)
+      return set_error(MONO_E_ARG, "mono_attn_launch: host_error is not pinned host memory");
+    p.host_err = static_cast<uint32_t*>(dptr);
+  }
+  p.fault_site = a->fault_site;
+  p.fault_after = a->fault_after;
+  p.timeline = a->timeline;
+  int grid = 0;
+  int rc = monokernel_grid(&grid);
+  if (rc) return rc;
+  rc = check_coresident(attn_kernel, AT_THREADS, 0,
+                        "mono_attn_launch: one 1024-thread CTA per CU does not fit");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_kernel, dim3(grid), dim3(AT_THREADS), 0, (hipStream_t)stream, p);
+  return check_launch("mono_attn_launch");
+}

@@ -101,3 +101,42 @@ def rowmajor_mxfp4_expert(w: MoeMxfp4Weights, e: int, cfg: Mxfp4MoeConfig = MXFP
 def logits_f32(rows: int, experts: int, device, seed: int = 0) -> torch.Tensor:
     g = _gen(torch.device(device), seed, 200 + rows)
     return torch.randn(rows, experts, generator=g, device=device)
+
+
+def attention_inputs(rows: int, ctx: int, device, seed: int = 0, positions=None,
+                     extra_pages: int = 3):
+    """Config 3: each row its own request seeing ``ctx`` keys (position ctx - 1 unless
+    ``positions`` is given), its pages a random permutation of the plane (as
+    ``test/kernels/test_deepseek_v41_k2i.py:109-119``). Index plane: random E2M1 bytes,
+    E8M0 scales in [123, 129]; index query likewise; head weights 0.05 N(0, 1); q bf16
+    N(0, 1); KV rows E4M3 of N(0, 1) with per-token scales U(0.5, 1.5)."""
+    from .attn import AttnInputs
+
+    dev = torch.device(device)
+    ppr = -(-ctx // 64)
+    pages = rows * ppr + extra_pages
+    g = _gen(dev, seed, 21)
+    u8 = dict(dtype=torch.uint8, device=dev, generator=g)
+    plane = torch.randint(0, 256, (pages, 4, 64, 16), **u8)
+    plane_scale = torch.randint(123, 130, (pages, 4, 64), **u8)
+    perm = torch.randperm(pages, generator=g, device=dev).to(torch.int32)
+    page_table = perm[: rows * ppr].view(rows, ppr).contiguous()
+    iq = torch.randint(0, 256, (rows, 64, 64), **u8)
+    iqs = torch.randint(123, 130, (rows, 4, 16, 4), **u8)
+    gq = _gen(dev, seed, 22)
+    iw = torch.randn(rows, 64, generator=gq, device=dev) * 0.05
+    q = torch.randn(rows, 32, 576, generator=gq, device=dev).to(torch.bfloat16)
+    gk = _gen(dev, seed, 23)
+    kv = torch.empty(pages * 64, 576, dtype=torch.uint8, device=dev)
+    for i in range(0, pages * 64, 1 << 16):  # in pieces: no f32 copy of the whole cache
+        n = min(1 << 16, pages * 64 - i)
+        kv[i : i + n] = torch.randn(n, 576, generator=gk, device=dev).to(FP8).view(torch.uint8)
+    kv_scale = 0.5 + torch.rand(pages * 64, generator=gk, device=dev)
+    if positions is None:
+        positions = torch.full((rows,), ctx - 1, dtype=torch.int64, device=dev)
+    else:
+        positions = torch.as_tensor(positions, dtype=torch.int64, device=dev)
+    req_ids = torch.arange(rows, dtype=torch.int32, device=dev)
+    return AttnInputs(q=q, iq=iq, iqs=iqs, iw=iw, plane=plane, plane_scale=plane_scale, kv=kv,
+                      kv_scale=kv_scale, positions=positions, req_ids=req_ids,
+                      page_table=page_table)

@@ -32,6 +32,7 @@ def _c_layout(struct, fields, tmp_path):
 
 @pytest.mark.parametrize("cls,cname", [(_lib.MonoMoeFp8Args, "MonoMoeFp8Args"),
                                         (_lib.MonoMoeMxfp4Args, "MonoMoeMxfp4Args"),
+                                        (_lib.MonoAttnArgs, "MonoAttnArgs"),
                                         (_lib.MonoDeviceInfo, "MonoDeviceInfo")])
 def test_ctypes_mirrors_match_the_c_layout(cls, cname, tmp_path):
     fields = [f for f, _ in cls._fields_]
@@ -49,6 +50,9 @@ def test_null_args_are_refused_without_a_gpu():
     mx = _lib.MonoMoeMxfp4Args(rows=17, experts=256)
     assert _lib.lib().mono_moe_mxfp4_launch(ctypes.byref(mx), None) == _lib.MONO_E_ARG
     assert "rows" in _lib.last_error()
+    at = _lib.MonoAttnArgs(rows=8, heads=32, index_heads=64, topk=2048, page=64, ctx_max=40000)
+    assert _lib.lib().mono_attn_launch(ctypes.byref(at), None) == _lib.MONO_E_ARG
+    assert "ctx_max" in _lib.last_error()
 
 
 def test_scratch_bytes_only_for_built_geometries():
@@ -56,6 +60,7 @@ def test_scratch_bytes_only_for_built_geometries():
     assert _lib.lib().mono_moe_fp8_scratch_bytes(7168, 384, 256) == 0
     assert _lib.lib().mono_moe_mxfp4_scratch_bytes(3072, 384, 256) > 0
     assert _lib.lib().mono_moe_mxfp4_scratch_bytes(3072, 512, 256) == 0
+    assert _lib.lib().mono_attn_scratch_bytes(48) > 0 and _lib.lib().mono_attn_scratch_bytes(49) == 0
 
 
 def test_deadline_ticks_bounds():

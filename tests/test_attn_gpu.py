@@ -1,0 +1,138 @@
+"""The attention launch (config 3) against the CPU oracle on the same seeded inputs.
+
+Bars: indexer scores within 1e-5 of the row's largest (f32 against the oracle's f64,
+sampled columns on long rows, as test/kernels/test_deepseek_v41_k2i.py:262-274 does);
+the selection bit-exact against the exact top-2048 of the launch's own scores (radix
+order of the f32 bits, ties to the lower position, ascending), every key when a row sees
+at most 2048; the latent output within 2e-2 max-abs + 1e-2 relative and 1e-2 relative
+in norm of the oracle's f64 sparse MLA over the launch's selection."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as A
+from oracle.topk import topk_sort
+from sgl_amd_mono_amd.dsv32 import synthetic
+from sgl_amd_mono_amd.dsv32.attn import AttnOp
+
+pytestmark = pytest.mark.gpu
+TOPK = 2048
+
+
+def _run(op, inp):
+    r = inp.rows
+    scores = torch.full((r, op.ctx_max), float("nan"), device=inp.q.device)
+    topk = torch.full((r, TOPK), -7, dtype=torch.int32, device=inp.q.device)
+    out = op.launch(inp, scores=scores, topk=topk)
+    op.rt.check()
+    return out.float().cpu(), scores.cpu().numpy(), topk.cpu().numpy()
+
+
+def _check(op, inp, full_score_rows=1, sample=4096, seed=0):
+    out, scores, topk = _run(op, inp)
+    pos = inp.positions.cpu().numpy()
+    pt = inp.page_table.cpu().numpy()
+    plane, psc = inp.plane.cpu().numpy(), inp.plane_scale.cpu().numpy()
+    iq, iqs, iw = inp.iq.cpu().numpy(), inp.iqs.cpu().numpy(), inp.iw.cpu().numpy()
+    kv, ksc = inp.kv.cpu().numpy(), inp.kv_scale.cpu().numpy()
+    rng = np.random.default_rng(seed)
+    for r in range(inp.rows):
+        n = int(min(max(pos[r] + 1, 0), op.ctx_max))
+        pages = pt[int(inp.req_ids[r])]
+        if n == 0:
+            assert np.all(topk[r] == -1)
+            assert torch.all(out[r] == 0)
+            continue
+        cols = np.arange(n) if (r < full_score_rows or n <= sample) else np.sort(
+            rng.choice(n, sample, replace=False))
+        want = A.index_scores(iq[r], iqs[r], iw[r], plane, psc, pages, n, cols=cols)
+        got = scores[r, cols].astype(np.float64)
+        assert np.all(np.isfinite(got)), r
+        err = np.abs(got - want).max() / max(np.abs(want).max(), 1e-30)
+        assert err <= 1e-5, (r, err)
+        k = min(n, TOPK)
+        sel = topk[r, :k]
+        want_sel = np.arange(n, dtype=np.int32) if n <= TOPK else topk_sort(scores[r, :n], TOPK)
+        assert np.array_equal(sel, want_sel), (r, n)
+        assert np.all(topk[r, k:] == -1)
+        slots = pages[sel // 64].astype(np.int64) * 64 + sel % 64
+        o, _ = A.sparse_mla(inp.q[r].cpu(), kv, ksc, slots, op.sm_scale)
+        o = torch.from_numpy(o)
+        rel = float((out[r].double() - o).norm() / o.norm())
+        assert rel <= 1e-2, (r, rel)
+        assert torch.all((out[r].double() - o).abs() <= 2e-2 + 1e-2 * o.abs()), r
+    return out, scores, topk
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_attention_matches_oracle_at_32k(gpu, rows):
+    print(f"case attention rows={rows} ctx=32768", flush=True)
+    inp = synthetic.attention_inputs(rows, 32768, gpu, seed=rows)
+    op = AttnOp(gpu, max_rows=rows)
+    _check(op, inp, full_score_rows=1)
+
+
+def test_attention_short_and_ragged_rows(gpu):
+    """Rows seeing 101, 2048, 2049 and 3000 keys, and a pad row seeing none."""
+    print("case attention ragged rows", flush=True)
+    inp = synthetic.attention_inputs(5, 4096, gpu, seed=11,
+                                     positions=[100, 2047, 2048, 2999, -1])
+    op = AttnOp(gpu, max_rows=8, ctx_max=4096)
+    _check(op, inp, full_score_rows=5)
+
+
+def test_attention_48_rows(gpu):
+    print("case attention rows=48 ctx=8192", flush=True)
+    inp = synthetic.attention_inputs(48, 8192, gpu, seed=48)
+    op = AttnOp(gpu, max_rows=48, ctx_max=8192)
+    _check(op, inp, full_score_rows=0, sample=1024)
+
+
+def test_attention_deterministic_and_graph_replay(gpu):
+    print("case attention determinism + graph", flush=True)
+    inp = synthetic.attention_inputs(4, 32768, gpu, seed=5)
+    op = AttnOp(gpu, max_rows=4)
+    a = op.launch(inp).clone()
+    b = op.launch(inp).clone()
+    op.rt.check()
+    assert torch.equal(a, b)
+    out = torch.empty_like(a)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op.launch(inp, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        op.launch(inp, out=out)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, a), f"replay {i}"
+        op.launch(inp)
+        torch.cuda.synchronize()
+    op.rt.check()
+
+
+def test_attention_deadline_stops_and_reports(gpu):
+    """A split's wait for its row's top-k is forced to stall from the host: it times
+    out after 5 ms, every CTA exits, the host raises, and a reset launches cleanly."""
+    print("case attention fault injection site=topk", flush=True)
+    inp = synthetic.attention_inputs(2, 4096, gpu, seed=9)
+    op = AttnOp(gpu, max_rows=2, ctx_max=4096, deadline_s=0.005, fault=(5, 0))
+    op.launch(inp)
+    with pytest.raises(RuntimeError, match="topk"):
+        op.rt.check()
+    words = op.rt.guard.cpu().tolist()
+    assert words[3] == 6 and words[5] == 1
+    op.fault = (0, 0)
+    op.rt.reset()
+    op.rt.set_deadline(10.0)
+    clean = op.launch(inp).clone()
+    op.rt.check()
+    ref = AttnOp(gpu, max_rows=2, ctx_max=4096).launch(inp)
+    torch.cuda.synchronize()
+    assert torch.equal(clean, ref)
