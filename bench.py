@@ -41,9 +41,11 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4"),
+    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4", "attn"),
                    help="moe_fp8: BASELINE configs[1] (the metric's MoE phase); "
-                        "moe_mxfp4: configs[3], the MXFP4 A16W4 expert block")
+                        "moe_mxfp4: configs[3], the MXFP4 A16W4 expert block; "
+                        "attn: configs[2], FP4 indexer + top-2048 + sparse MLA")
+    p.add_argument("--ctx", type=int, default=32768, help="attn: keys each row sees")
     p.add_argument("--rows", type=int, default=8)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -267,6 +269,62 @@ def bench_moe_mxfp4(args):
     return us, steps, sum(bytes_per) / L, "bf16 x e2m1", config, f"moe_mxfp4_r{rows}", cpu
 
 
+def cpu_baseline_attn(inp, sm_scale, rows):
+    """The oracle's attention chain on the host for one row (bounded sample), scaled to
+    the launch's rows."""
+    import torch
+
+    from oracle import attn as A
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    r = 0
+    args = (inp.q[r].cpu(), inp.iq[r].cpu().numpy(), inp.iqs[r].cpu().numpy(),
+            inp.iw[r].cpu().numpy(), inp.plane.cpu().numpy(), inp.plane_scale.cpu().numpy(),
+            inp.page_table[r].cpu().numpy(), inp.kv.cpu().numpy(), inp.kv_scale.cpu().numpy(),
+            int(inp.positions[r]), 2048, sm_scale)
+    t0 = time.perf_counter()
+    A.attention_row(*args)
+    us = (time.perf_counter() - t0) * 1e6
+    return {"value": round(us * rows, 1), "unit": f"µs per attention phase ({rows} rows)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 of {rows} rows (f64 numpy/torch: scores of {int(inp.positions[r]) + 1} "
+                      f"keys, exact top-2048, sparse MLA), timed once and scaled x{rows}"}
+
+
+def bench_attn(args):
+    import torch
+
+    from sgl_amd_mono_amd.dsv32 import synthetic
+    from sgl_amd_mono_amd.dsv32.attn import AttnOp
+
+    dev = torch.device("cuda:0")
+    rows, L, ctx = args.rows, args.layers, args.ctx
+    print(f"bench: generating {L} layers of caches ({rows} rows x {ctx} keys)", file=sys.stderr,
+          flush=True)
+    inps = [synthetic.attention_inputs(rows, ctx, dev, seed=400 + i) for i in range(L)]
+    ops = [AttnOp(dev, max_rows=rows, ctx_max=ctx) for _ in range(L)]
+    outs = [torch.empty(rows, 32, 512, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    n = min(ctx, 1 << 30)
+    k = min(n, 2048)
+    # KV rows gathered (576 E4M3 + a 4-byte scale), index keys scanned (64 B + 4 scales),
+    # the queries in (absorbed q bf16, index q + scales + weights) and the latent out
+    bytes_per = rows * (k * 580 + n * 68 + 32 * 576 * 2 + 64 * 64 + 256 + 64 * 4 + 32 * 512 * 2)
+    us, wall, steps = time_graph(lambda i: ops[i].launch(inps[i], out=outs[i]), L, args.steps,
+                                 args.warmup)
+    for op in ops:
+        op.rt.check()
+    print(f"bench: {steps} launches, {us:.1f} us each (wall {wall * 1e3 / steps:.1f} ms/step)",
+          file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline_attn(inps[0], ops[0].sm_scale, rows)
+    config = {
+        "workload": "BASELINE configs[2]: sparse MLA decode, 32 heads, kv_lora 512 + rope 64, "
+                    "64-token paged E4M3 KV with per-token scales, FP4 indexer (64 heads x 128, "
+                    "E2M1 + E8M0) top-2048, one persistent launch",
+        "rows": rows, "context": ctx, "topk": k, "layers_rotated": L,
+    }
+    return us, steps, bytes_per, "fp4 idx / bf16 x e4m3 attn", config, f"attn_r{rows}", cpu
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -276,7 +334,7 @@ def main():
         print(f"bench.py measures one GPU: every GPU box here has one GPU, and the sharded "
               f"path (TP=4 exchanges) is not built; got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
-    run = bench_moe_fp8 if args.workload == "moe_fp8" else bench_moe_mxfp4
+    run = {"moe_fp8": bench_moe_fp8, "moe_mxfp4": bench_moe_mxfp4, "attn": bench_attn}[args.workload]
     us, steps, avg_bytes, dtype, config, prof, cpu = run(args)
     achieved = avg_bytes / (us * 1e-6) / 1e9  # GB/s
     line = {

@@ -8,9 +8,11 @@
 //      E8M0 scales (query rows = heads, key columns = tokens, K = the 128 dims); relu,
 //      the head weights and the sum over heads stay in the lane, then two permlane
 //      swaps sum the lane groups. Scores go to scratch; the chunk's done word follows.
-//   2  top-k: task = row. Its scores as radix keys in LDS (128 KB); three histogram
-//      passes (12, 12, 8 bits) find the 2048th key T; the selection is every key above
-//      T plus the lowest positions holding T, written in ascending position order.
+//   2  top-k: task = row (topk_lds.h): thread t holds the radix keys of positions
+//      32 t .. in registers; a sample narrows the range, histograms over the live range
+//      keep the bin of the 2048th key until its few candidates rank themselves; the
+//      selection (every element up to the threshold element of the order key
+//      descending, position ascending) is published as (position, tag) pairs.
 //   3  split: task (row, 128-key split), all 32 heads. The split's tokens (through the
 //      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
 //      widened exactly), times the token's scale and the softmax scale; per head the
@@ -30,6 +32,7 @@
 
 #include "mono_abi.h"
 #include "mono_device.h"
+#include "topk_lds.h"
 
 namespace mono {
 
@@ -38,24 +41,20 @@ constexpr int AT_IHEADS = 64;    // index heads
 constexpr int AT_KV = 576;       // cached row: latent 512 + rope 64
 constexpr int AT_LAT = 512;
 constexpr int AT_PAGE = 64;
-constexpr int AT_TOPK = 2048;
-constexpr int AT_MAXCTX = 32768;  // keys a row may see (the top-k's LDS image)
 constexpr int AT_CHUNK = 1024;    // tokens of a score task
 constexpr int AT_NCHUNK = AT_MAXCTX / AT_CHUNK;
 constexpr int AT_SPLIT = 128;     // keys of a split task
 constexpr int AT_NSPLIT = AT_TOPK / AT_SPLIT;
 constexpr int AT_MAXR = 48;
-constexpr int AT_THREADS = 1024;
-constexpr int AT_WAVES = AT_THREADS / WAVE;
 
 constexpr size_t at_align(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct AttnScratch {
   static constexpr size_t SCORES = 0;  // f32 [MAXR][MAXCTX]
   static constexpr size_t SCORE_DONE = at_align(SCORES + (size_t)AT_MAXR * AT_MAXCTX * 4);
+  // the selection as (position, tag) pairs [MAXR][TOPK]
   static constexpr size_t TOPK = at_align(SCORE_DONE + (size_t)AT_MAXR * AT_NCHUNK * 4);
-  static constexpr size_t TOPK_DONE = at_align(TOPK + (size_t)AT_MAXR * AT_TOPK * 4);
-  static constexpr size_t ACC = at_align(TOPK_DONE + (size_t)AT_MAXR * 4);  // f32 [R][split][h][512]
+  static constexpr size_t ACC = at_align(TOPK + (size_t)AT_MAXR * AT_TOPK * 8);  // f32 [R][split][h][512]
   static constexpr size_t ML = at_align(ACC + (size_t)AT_MAXR * AT_NSPLIT * AT_HEADS * AT_LAT * 4);
   static constexpr size_t SPLIT_DONE = at_align(ML + (size_t)AT_MAXR * AT_NSPLIT * AT_HEADS * 8);
   static constexpr size_t BYTES = at_align(SPLIT_DONE + (size_t)AT_MAXR * AT_NSPLIT * 4);
@@ -110,71 +109,6 @@ __device__ inline v4f mfma_bf16(v8bf a, v8bf b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// exclusive prefix sum over the CTA's 1024 threads; `wsum` is 16 ints of LDS
-__device__ inline int block_scan(int v, int* wsum, int& total) {
-  const int l = lane_id(), w = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const int y = __shfl_up(x, o, WAVE);
-    if (l >= o) x += y;
-  }
-  if (l == WAVE - 1) wsum[w] = x;
-  __syncthreads();
-  int pre = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < AT_WAVES; ++i) {
-    const int s = wsum[i];
-    pre += i < w ? s : 0;
-    tot += s;
-  }
-  __syncthreads();
-  total = tot;
-  return pre + x - v;
-}
-
-// one radix pass over keys[0..n) whose bits above `shift + BITS` equal `prefix`: the
-// histogram of the next BITS bits, then the bin holding the kk-th largest such key and
-// how many of them lie in higher bins
-template <int BITS>
-__device__ inline void radix_pass(const uint32_t* keys, int n, int shift, uint32_t prefix,
-                                  bool any_prefix, int kk, uint32_t* hist, int* wsum,
-                                  int* res) {
-  constexpr int NB = 1 << BITS;
-  const int tid = threadIdx.x;
-  for (int i = tid; i < NB; i += AT_THREADS) hist[i] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += AT_THREADS) {
-    const uint32_t k = keys[i];
-    const bool in = any_prefix || (k >> (shift + BITS)) == prefix;
-    if (in) atomicAdd(&hist[(k >> shift) & (NB - 1)], 1u);
-  }
-  __syncthreads();
-  // thread t owns bins [NB - G (t + 1), NB - G t): the scan runs from the top bin down
-  constexpr int G = NB >= AT_THREADS ? NB / AT_THREADS : 1;
-  const bool owns = tid * G < NB;
-  int s = 0;
-  if (owns)
-#pragma unroll
-    for (int g = 0; g < G; ++g) s += (int)hist[NB - 1 - (tid * G + g)];
-  int tot;
-  const int pre = block_scan(s, wsum, tot);
-  if (owns && pre < kk && kk <= pre + s) {
-    int cum = pre;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int bin = NB - 1 - (tid * G + g);
-      const int c = (int)hist[bin];
-      if (cum < kk && kk <= cum + c) {
-        res[0] = bin;
-        res[1] = cum;
-      }
-      cum += c;
-    }
-  }
-  __syncthreads();
-}
-
 __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   using S = AttnScratch;
   const int tid = threadIdx.x, l = tid & 63;
@@ -183,16 +117,17 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   const int nblk = gridDim.x, b = blockIdx.x;
 
   // one LDS arena, carved per stage
-  __shared__ __attribute__((aligned(16))) uint8_t smem[150 * 1024];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[TOPK_ARENA_WORDS * 4];
   __shared__ uint32_t head_s[4];
   __shared__ int ok_s;
-  __shared__ int wsum[AT_WAVES];
-  __shared__ int res_s[2];
+  __shared__ __attribute__((aligned(16))) int wsum[2 * AT_WAVES];
+  __shared__ int res_s[4];
+  __shared__ __attribute__((aligned(16))) uint32_t wsum_mm[4 * AT_WAVES];
+  __shared__ uint32_t thr_s[2];
 
   float* scores = reinterpret_cast<float*>(p.scratch + S::SCORES);
   uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S::SCORE_DONE);
-  int32_t* topk = reinterpret_cast<int32_t*>(p.scratch + S::TOPK);
-  uint32_t* topk_done = reinterpret_cast<uint32_t*>(p.scratch + S::TOPK_DONE);
+  uint64_t* topk = reinterpret_cast<uint64_t*>(p.scratch + S::TOPK);
   float* accs = reinterpret_cast<float*>(p.scratch + S::ACC);
   float* mls = reinterpret_cast<float*>(p.scratch + S::ML);
   uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S::SPLIT_DONE);
@@ -225,7 +160,11 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   const __amdgpu_buffer_rsrc_t rpsc = rsrc(p.plane_scale, p.plane_pages * 256u);
 
   // ---------------------------------------------------------------- 1: scores
+  // Each stage takes the thread index through an opaque copy: conditions on it are then
+  // computed inside the stage, not hoisted to the kernel's top where they would hold
+  // registers through every stage.
   for (int task = b; task < R * AT_NCHUNK; task += nblk) {
+    const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
     const int r = task / AT_NCHUNK, c = task % AT_NCHUNK;
     const int n = row_n(r);
     if (c * AT_CHUNK >= n) continue;
@@ -294,12 +233,13 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   // ---------------------------------------------------------------- 2: top-k
   stamp(p.timeline, MONO_TL_STAGED);
   for (int r = b; r < R; r += nblk) {
+    const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
     const int n = row_n(r);
-    int32_t* sel = topk + (size_t)r * AT_TOPK;
+    uint64_t* sel = topk + (size_t)r * AT_TOPK;
     if (n <= AT_TOPK) {
       // every key of the row, in position order
       for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
-        if (i < n) st_dev(reinterpret_cast<uint32_t*>(sel + i), (uint32_t)i);
+        if (i < n) st_dev64(sel + i, pair((uint32_t)i, tag));
         if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = i < n ? i : -1;
       }
     } else {
@@ -310,63 +250,16 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         });
       ok = cta_all(ok, ok_s);
       if (ok) {
-        uint32_t* keys = reinterpret_cast<uint32_t*>(smem);
-        uint32_t* hist = keys + AT_MAXCTX;
         const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
-        for (int i = tid * 4; i < n; i += AT_THREADS * 4) {
-          const v4i v = ld16<CP_DEV>(rs, (uint32_t)i * 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) keys[i + e] = radix_key(__int_as_float(v[e]));
-        }
-        __syncthreads();
-        const int k = AT_TOPK;
-        radix_pass<12>(keys, n, 20, 0, true, k, hist, wsum, res_s);
-        const uint32_t b1 = (uint32_t)res_s[0];
-        const int above1 = res_s[1];
-        radix_pass<12>(keys, n, 8, b1, false, k - above1, hist, wsum, res_s);
-        const uint32_t b2 = (uint32_t)res_s[0];
-        const int above2 = res_s[1];
-        radix_pass<8>(keys, n, 0, (b1 << 12) | b2, false, k - above1 - above2, hist, wsum,
-                      res_s);
-        const uint32_t T = (b1 << 20) | (b2 << 8) | (uint32_t)res_s[0];
-        const int need = k - above1 - above2 - res_s[1];  // keys equal to T to take
-        // thread t: positions [32 t, 32 t + 32), in order
-        constexpr int PER = AT_MAXCTX / AT_THREADS;
-        const int i0 = tid * PER;
-        int gt = 0, eq = 0;
-#pragma unroll 8
-        for (int j = 0; j < PER; ++j) {
-          const int i = i0 + j;
-          const uint32_t kv = i < n ? keys[i] : 0u;
-          gt += (i < n) & (kv > T);
-          eq += (i < n) & (kv == T);
-        }
-        int tot;
-        const int eq_before = block_scan(eq, wsum, tot);
-        int take = need - eq_before;
-        take = take < 0 ? 0 : (take > eq ? eq : take);
-        const int at = block_scan(gt + take, wsum, tot);
-        int o = at;
-        for (int j = 0; j < PER; ++j) {
-          const int i = i0 + j;
-          if (i >= n) break;
-          const uint32_t kv = keys[i];
-          bool pick = kv > T;
-          if (kv == T && take > 0) {
-            pick = true;
-            --take;
-          }
-          if (pick && o < AT_TOPK) {
-            st_dev(reinterpret_cast<uint32_t*>(sel + o), (uint32_t)i);
-            if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + o] = i;
-            ++o;
-          }
+        const int32_t* sel_l = topk_select(tid, rs, n, smem, wsum, wsum_mm, res_s, thr_s);
+        for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
+          const int v = sel_l[i];
+          st_dev64(sel + i, pair((uint32_t)v, tag));
+          if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = v;
         }
       }
     }
-    drain();
-    __syncthreads();
-    if (tid == 0 && ok) st_dev(&topk_done[r], tag);
+    __syncthreads();  // the LDS arena is reused by the next row
   }
 
   // ---------------------------------------------------------------- 3: split
@@ -384,12 +277,13 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     float* ksc = reinterpret_cast<float*>(slot_s + AT_SPLIT);
     static_assert(AT_SPLIT * KSTR + AT_HEADS * QSTR + AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
                           AT_SPLIT * 8 <=
-                      150 * 1024,
+                      (int)sizeof(smem),
                   "split LDS");
     const __amdgpu_buffer_rsrc_t rkv = rsrc(p.kv, p.kv_slots * (uint32_t)AT_KV);
     const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, p.kv_slots * 4u);
     const int nt = R * AT_NSPLIT;
     for (int t0 = 0; t0 < nt; t0 += nblk) {
+      const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
       const int task = t0 + (b + nblk - (R % nblk)) % nblk;  // rows' top-k CTAs go last
       if (task >= nt) continue;
       const int r = task / AT_NSPLIT, sp = task % AT_NSPLIT;
@@ -397,22 +291,24 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       const int k = n < AT_TOPK ? n : AT_TOPK;
       const int kcnt = k - sp * AT_SPLIT < AT_SPLIT ? k - sp * AT_SPLIT : AT_SPLIT;
       if (kcnt <= 0) continue;
-      if (w == 0)
-        ok = wait_until(guard, MONO_SITE_TOPK,
-                        [&]() { return ld_dev(&topk_done[r]) == tag; });
-      ok = cta_all(ok, ok_s);
-      if (!ok) break;
-      // the split's tokens -> cache slots
+      // the split's tokens, polled as (position, tag) pairs, -> cache slots
       if (tid < AT_SPLIT) {
+        uint64_t v = 0;
+        const uint64_t* src = topk + (size_t)r * AT_TOPK + sp * AT_SPLIT + tid;
+        ok = wait_until(guard, MONO_SITE_TOPK, [&]() {
+          v = tid < kcnt ? ld_dev64(src) : pair(0u, tag);
+          return __all((uint32_t)(v >> 32) == tag);
+        });
         int slot = -1;
-        if (tid < kcnt) {
-          const int pos = (int)ld_dev(reinterpret_cast<const uint32_t*>(
-              topk + (size_t)r * AT_TOPK + sp * AT_SPLIT + tid));
+        if (ok && tid < kcnt) {
+          const int pos = (int)(uint32_t)v;
           slot = page_of(r, pos >> 6) * AT_PAGE + (pos & 63);
         }
         slot_s[tid] = slot;
         ksc[tid] = slot >= 0 ? __int_as_float(ld4<CP_NONE>(rks, (uint32_t)slot * 4)) : 0.f;
       }
+      ok = cta_all(ok, ok_s);
+      if (!ok) break;
       // q of the row, all heads: [32][576] bf16
       const __amdgpu_buffer_rsrc_t rq = rsrc(p.q + (size_t)r * AT_HEADS * AT_KV, AT_HEADS * AT_KV * 2);
       for (int i = tid; i < AT_HEADS * AT_KV / 8; i += AT_THREADS) {
@@ -526,6 +422,7 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     __shared__ float wsp_s[AT_NSPLIT];
     __shared__ float linv_s;
     for (int task = b; task < R * AT_HEADS; task += nblk) {
+      const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
       if (!ok) break;
       const int r = task / AT_HEADS, h = task % AT_HEADS;
       const int n = row_n(r);

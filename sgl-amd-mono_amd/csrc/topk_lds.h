@@ -1,0 +1,290 @@
+// Exact top-k selection of one row in one CTA's LDS (the attention launch's stage 2).
+// Rule (sgl_amd_mono/glm53/gfx950/kernel.py:3002-3636; glm53/check.py:94-117): rank by
+// the radix order key of the f32 score bits, larger first, ties to the lower position;
+// the selection in ascending position order.
+#pragma once
+
+#include <type_traits>
+
+#include "mono_device.h"
+
+namespace mono {
+
+constexpr int AT_TOPK = 2048;
+constexpr int AT_MAXCTX = 32768;  // keys a row may see (the LDS image)
+constexpr int AT_THREADS = 1024;
+constexpr int AT_WAVES = AT_THREADS / WAVE;
+constexpr int CAND = 256;  // a threshold bin this small is ranked directly
+// LDS words topk_select needs: the padded key image, then the histogram
+constexpr int TOPK_ARENA_WORDS = AT_THREADS * 33 + 4096;
+
+// inclusive prefix sum over the wave: DPP row shifts scan each row of 16 lanes, then
+// the row totals (read from lanes 15, 31, 47) are added to the rows above them
+__device__ inline int wave_scan(int v) {
+  auto shr = [](int x, auto ctrl_c) {
+    constexpr int CTRL = decltype(ctrl_c)::value;
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, true);
+  };
+  v += shr(v, std::integral_constant<int, 0x111>());  // row_shr:1
+  v += shr(v, std::integral_constant<int, 0x112>());  // row_shr:2
+  v += shr(v, std::integral_constant<int, 0x114>());  // row_shr:4
+  v += shr(v, std::integral_constant<int, 0x118>());  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+            r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane_id() >> 4;
+  return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
+// exclusive prefix sum over the CTA's 1024 threads. `wsum` is 2 x 16 ints of LDS (16-byte
+// aligned) used alternately by successive calls (`phase` flips), so one barrier suffices:
+// a call's buffer is not rewritten until the call after next, behind the next barrier.
+__device__ inline int block_scan(int v, int* wsum, int& phase, int& total) {
+  const int l = lane_id(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int* buf = wsum + AT_WAVES * phase;
+  phase ^= 1;
+  const int x = wave_scan(v);
+  if (l == WAVE - 1) buf[w] = x;
+  __syncthreads();
+  const v4i* ws = reinterpret_cast<const v4i*>(buf);
+  const v4i a = ws[0], b = ws[1], c = ws[2], d = ws[3];
+  const int s[16] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3],
+                     c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < AT_WAVES; ++i) {
+    pre += i < w ? s[i] : 0;
+    tot += s[i];
+  }
+  total = tot;
+  return pre + x - v;
+}
+
+// (hist must be zero on entry; select_pass leaves it zero)
+template <int NK>
+__device__ inline void select_pass(int tid, const uint32_t (&key)[NK], uint32_t lo, uint32_t hi,
+                                   int shift, int kk, uint32_t* hist, int* wsum, int& phase,
+                                   int* res) {
+  constexpr int NB = 4096;
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    const uint32_t k = key[j];
+    if (k >= lo && k <= hi) atomicAdd(&hist[(k - lo) >> shift], 1u);
+  }
+  __syncthreads();
+  // thread t owns bins [NB - 4 (t + 1), NB - 4 t): the scan runs from the top bin down;
+  // the thread clears its bins once read (no other thread reads them)
+  constexpr int G = NB / AT_THREADS;
+  v4i* mine = reinterpret_cast<v4i*>(hist + NB - G * (tid + 1));
+  const v4i h4 = *mine;
+  *mine = v4i{0, 0, 0, 0};
+  const int s = h4[0] + h4[1] + h4[2] + h4[3];
+  int tot;
+  const int pre = block_scan(s, wsum, phase, tot);
+  if (tid == 0) res[3] = tot;
+  if (pre < kk && kk <= pre + s) {
+    int cum = pre;
+#pragma unroll
+    for (int g = G - 1; g >= 0; --g) {
+      const int c = h4[g];
+      if (cum < kk && kk <= cum + c) {
+        res[0] = NB - G * (tid + 1) + g;
+        res[1] = cum;
+        res[2] = c;
+      }
+      cum += c;
+    }
+  }
+  __syncthreads();
+}
+
+// minimum and maximum over the CTA (every thread gets them); `red` is 2 x 32 u32 of LDS,
+// 16-byte aligned, used alternately like block_scan's buffers (one barrier)
+__device__ inline void block_minmax(uint32_t& mn, uint32_t& mx, uint32_t* red, int& phase) {
+  const int l = lane_id(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint32_t* buf = red + 2 * AT_WAVES * phase;
+  phase ^= 1;
+  mx = wave_max_u32(mx);
+  mn = ~wave_max_u32(~mn);
+  if (l == 0) {
+    buf[w] = mn;
+    buf[AT_WAVES + w] = mx;
+  }
+  __syncthreads();
+  const v4i* rv = reinterpret_cast<const v4i*>(buf);
+  v4i r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = rv[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t a = (uint32_t)r[i][e], b = (uint32_t)r[4 + i][e];
+      mn = a < mn ? a : mn;
+      mx = b > mx ? b : mx;
+    }
+}
+
+// The exact top-TOPK of one row's n scores (TOPK < n <= 32768), in LDS: returns the
+// selected positions in ascending order (sel[0 .. TOPK)). Ranked by the radix key of
+// the f32 score, larger first, ties to the lower position. `rs` covers the n scores
+// (f32, device coherent loads); `arena` holds TOPK_ARENA_WORDS words. Every thread of the
+// CTA calls it. With `ts` non-null, thread 0 records the shader clock after each step.
+//
+// Thread t keeps the keys of positions 32 t .. 32 t + 31 in registers (loaded through a
+// padded LDS image, 33 words a thread, so both the coalesced writes and the per-thread
+// reads are conflict-free). A sample (every 32nd position) narrows the key range to one
+// holding about 1.5 TOPK keys; histogram passes over the live range (4096 bins) keep the
+// bin holding the TOPK-th key until it holds few keys (then they rank themselves) or one
+// key value (then its positions do). The threshold is an element (key, position) of the
+// order (key descending, position ascending); the selection is every element up to it.
+__device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n, uint8_t* arena,
+                                       int* wsum, uint32_t* wsum_mm, int* res_s, uint32_t* thr_s,
+                                       uint64_t* ts = nullptr) {
+  int phase = 0, mphase = 0;
+  auto mark = [&](int k) {
+    if (ts && tid == 0) ts[k] = __builtin_amdgcn_s_memtime();
+  };
+  mark(0);
+  uint32_t* kl = reinterpret_cast<uint32_t*>(arena);  // [1024][33] image
+  uint32_t* hist = kl + AT_THREADS * 33;               // [4096]
+  uint32_t* ck = hist;                                 // candidates, after the passes
+  int32_t* cp = reinterpret_cast<int32_t*>(hist + CAND);
+  int32_t* sel = reinterpret_cast<int32_t*>(hist + 2 * CAND);  // [TOPK + 64]
+  static_assert(2 * CAND + AT_TOPK + WAVE <= 4096, "candidates and the selection fit the histogram");
+  constexpr int NLD = AT_MAXCTX / 4 / AT_THREADS;
+  v4i raw[NLD];
+#pragma unroll
+  for (int q = 0; q < NLD; ++q) raw[q] = ld16<CP_DEV>(rs, (uint32_t)(4 * (tid + AT_THREADS * q)) * 4);
+  reinterpret_cast<v4i*>(hist)[tid] = v4i{0, 0, 0, 0};  // select_pass expects it zero
+  // a position past the row holds key 0, below every real key (a score keeps key >= 1:
+  // only the all-ones NaN would map to 0, and it ranks next to it)
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+  for (int q = 0; q < NLD; ++q) {
+    const int i = 4 * (tid + AT_THREADS * q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t k = radix_key(__int_as_float(raw[q][e]));
+      k = i + e < n ? (k > 1u ? k : 1u) : 0u;
+      kl[((i + e) >> 5) * 33 + ((i + e) & 31)] = k;
+      kmin = (k && k < kmin) ? k : kmin;
+      kmax = k > kmax ? k : kmax;
+    }
+  }
+  __syncthreads();
+  uint32_t key[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) key[j] = kl[33 * tid + j];
+  mark(1);
+  block_minmax(kmin, kmax, wsum_mm, mphase);
+  mark(2);
+  uint32_t lo = kmin, hi = kmax;
+  int kk = AT_TOPK, cnt = n, shift = 1;
+  // Sample the range first: position 32 t is thread t's sample. The bin of the sample
+  // ranked SR from the top bounds a range [cut, kmax] expected to hold about 1.5 TOPK
+  // keys. The first pass bins only that range; it counts the keys there, and if they
+  // are fewer than TOPK the pass is redone over the whole range.
+  uint32_t cut = kmin;
+  {
+    const int ns = (n + 31) / 32;
+    const int sr = (3 * AT_TOPK * ns + 2 * n - 1) / (2 * n);
+    if (sr >= 1 && sr <= ns) {
+      const uint32_t span = kmax - kmin;
+      const int bits = span ? 32 - __clz((int)span) : 0;
+      const int sh = bits > 12 ? bits - 12 : 0;
+      const uint32_t one[1] = {key[0]};
+      select_pass<1>(tid, one, kmin, kmax, sh, sr, hist, wsum, phase, res_s);
+      cut = kmin + ((uint32_t)res_s[0] << sh);
+    }
+  }
+  mark(3);
+#pragma unroll 1
+  for (int pass = 0; shift > 0 && cnt > CAND; ++pass) {
+    const uint32_t plo = pass == 0 ? cut : lo;
+    const uint32_t span = hi - plo;
+    const int bits = span ? 32 - __clz((int)span) : 0;
+    shift = bits > 12 ? bits - 12 : 0;
+    select_pass<32>(tid, key, plo, hi, shift, kk, hist, wsum, phase, res_s);
+    if (pass == 0 && res_s[3] < AT_TOPK) {  // the sampled range holds too few keys
+      shift = 1;
+      continue;
+    }
+    const uint32_t bin = (uint32_t)res_s[0];
+    kk -= res_s[1];
+    cnt = res_s[2];
+    const uint32_t nlo = plo + (bin << shift);
+    const uint64_t top = (uint64_t)nlo + ((1ull << shift) - 1ull);
+    hi = top < (uint64_t)hi ? (uint32_t)top : hi;
+    lo = nlo;
+  }
+  mark(4);
+  // the threshold element (Tkey, Tpos): the kk-th of the bin's keys in (key descending,
+  // position ascending) order
+  if (cnt <= CAND) {
+    // few candidates: gather them, and each finds its own rank among them
+    if (tid == 0) res_s[0] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      if (key[j] >= lo && key[j] <= hi) {
+        const int at = atomicAdd(&res_s[0], 1);
+        ck[at] = key[j];
+        cp[at] = 32 * tid + j;
+      }
+    __syncthreads();
+    if (tid < cnt) {
+      const uint32_t mk = ck[tid];
+      const int mp = cp[tid];
+      int rank = 0;
+      for (int m = 0; m < cnt; ++m) rank += (ck[m] > mk) | ((ck[m] == mk) & (cp[m] < mp));
+      if (rank == kk - 1) {
+        thr_s[0] = mk;
+        thr_s[1] = (uint32_t)mp;
+      }
+    }
+  } else {
+    // one key value shared by many positions: the kk-th of them in position order
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) c += key[j] == lo;
+    int tot;
+    const int before = block_scan(c, wsum, phase, tot);
+    if (before < kk && kk <= before + c) {
+      int seen = before;
+      for (int j = 0; j < 32; ++j) {
+        const bool e = key[j] == lo;
+        seen += e;
+        if (e && seen == kk) {
+          thr_s[0] = lo;
+          thr_s[1] = (uint32_t)(32 * tid + j);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  mark(5);
+  const uint32_t tk = thr_s[0];
+  const int tp = (int)thr_s[1];
+  int np = 0;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) np += (key[j] > tk) | ((key[j] == tk) & (32 * tid + j <= tp));
+  int tot;
+  const int o = block_scan(np, wsum, phase, tot);
+  // the picks at their ranks; a key not taken writes its lane's dummy slot past the
+  // selection (no store branches, and no two lanes of a wave on one address)
+  int pc = 0;
+  const int dummy = AT_TOPK + (tid & (WAVE - 1));
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const bool pick = (key[j] > tk) | ((key[j] == tk) & (32 * tid + j <= tp));
+    const int at = o + pc;
+    sel[pick && at < AT_TOPK ? at : dummy] = 32 * tid + j;
+    pc += pick;
+  }
+  mark(6);
+  __syncthreads();
+  mark(7);
+  return sel;
+}
+
+}  // namespace mono
