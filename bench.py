@@ -41,7 +41,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4", "attn"),
+    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4", "attn", "post"),
                    help="moe_fp8: BASELINE configs[1] (the metric's MoE phase); "
                         "moe_mxfp4: configs[3], the MXFP4 A16W4 expert block; "
                         "attn: configs[2], FP4 indexer + top-2048 + sparse MLA")
@@ -325,6 +325,58 @@ def bench_attn(args):
     return us, steps, bytes_per, "fp4 idx / bf16 x e4m3 attn", config, f"attn_r{rows}", cpu
 
 
+def cpu_baseline_post(o_lat, h, w):
+    """The oracle's W_UV + o_proj + residual on the host for the whole launch."""
+    import torch
+
+    from oracle import dense as D
+    from sgl_amd_mono_amd.dsv32 import synthetic
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    ws = synthetic.rowmajor_post(w)
+    t0 = time.perf_counter()
+    D.attn_out(o_lat.cpu(), h.cpu(), *ws)
+    us = (time.perf_counter() - t0) * 1e6
+    return {"value": round(us, 1), "unit": f"µs per attention output block ({o_lat.shape[0]} rows)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "the whole launch: f64 dequantisation of W_UV and W_o and the two GEMVs, "
+                      "timed once"}
+
+
+def bench_post(args):
+    import torch
+
+    from sgl_amd_mono_amd.dsv32 import synthetic
+    from sgl_amd_mono_amd.dsv32.post import PostOp
+
+    dev = torch.device("cuda:0")
+    rows, L = args.rows, args.layers
+    print(f"bench: generating {L} layers of W_UV + o_proj", file=sys.stderr, flush=True)
+    ws = [synthetic.post_weights(dev, seed=500 + i, layout=args.layout) for i in range(L)]
+    ops = [PostOp(w, dev, max_rows=rows) for w in ws]
+    g = torch.Generator(device=dev).manual_seed(5)
+    o_lat = torch.randn(rows, 32, 512, generator=g, device=dev).to(torch.bfloat16)
+    h = torch.randn(rows, 7168, generator=g, device=dev).to(torch.bfloat16)
+    outs = [torch.empty(rows, 7168, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    # E4M3 weights + f32 block scales, o_lat in, h in, a out
+    bytes_per = (32 * 128 * 512 + 7168 * 4096 + (32 * 4 + 56 * 32) * 4
+                 + rows * (32 * 512 * 2 + 7168 * 2 * 2))
+    us, wall, steps = time_graph(lambda i: ops[i].launch(o_lat, h, out=outs[i]), L, args.steps,
+                                 args.warmup)
+    for op in ops:
+        op.rt.check()
+    print(f"bench: {steps} launches, {us:.1f} us each (wall {wall * 1e3 / steps:.1f} ms/step)",
+          file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline_post(o_lat, h, ws[0])
+    config = {
+        "workload": "attention output block: W_UV per head (32 x [128, 512]) and o_proj "
+                    "([7168, 4096]), E4M3 + f32 128x128 block scales, bf16 activations, "
+                    "residual add, one persistent launch",
+        "rows": rows, "layout": args.layout, "layers_rotated": L,
+    }
+    return us, steps, bytes_per, "bf16 x e4m3", config, f"post_r{rows}", cpu
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -334,7 +386,8 @@ def main():
         print(f"bench.py measures one GPU: every GPU box here has one GPU, and the sharded "
               f"path (TP=4 exchanges) is not built; got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
-    run = {"moe_fp8": bench_moe_fp8, "moe_mxfp4": bench_moe_mxfp4, "attn": bench_attn}[args.workload]
+    run = {"moe_fp8": bench_moe_fp8, "moe_mxfp4": bench_moe_mxfp4, "attn": bench_attn,
+           "post": bench_post}[args.workload]
     us, steps, avg_bytes, dtype, config, prof, cpu = run(args)
     achieved = avg_bytes / (us * 1e-6) / 1e9  # GB/s
     line = {

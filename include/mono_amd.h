@@ -50,6 +50,7 @@ typedef void* mono_stream_t;
 #define MONO_SITE_SCORES 4   /* a row's top-k waits on its indexer scores */
 #define MONO_SITE_TOPK 5     /* a sparse-MLA split waits on its row's top-k */
 #define MONO_SITE_SPLIT 6    /* a merge waits on its row's splits */
+#define MONO_SITE_O 7        /* o_proj waits on the W_UV outputs */
 
 int mono_version(void);
 const char* mono_last_error(void);
@@ -235,6 +236,37 @@ typedef struct {
 
 size_t mono_attn_scratch_bytes(int32_t rows_max);
 int mono_attn_launch(const MonoAttnArgs* args, mono_stream_t stream);
+
+/* ------------------------------------------------------------------------------
+ * The attention output block as one persistent launch: the merged latent o_lat through
+ * W_UV per head (o, handed over in bf16), o_proj, and the residual add of the W == 1
+ * reduce: out = bf16(h + W_o o). FP8 E4M3 weights with f32 128 x 128 block scales, read
+ * in place (MONO_LAYOUT_*), widened exactly to bf16 against bf16 activations.
+ * Replaces sgl_amd_mono/glm53/gfx950/kernel.py:3975-4123 (W_UV after the merge),
+ * :4125-4197 (o_proj + residual) and the W == 1 peer_reduce branch :1665-1669. */
+typedef struct {
+  int32_t rows;          /* R, 1..16 */
+  int32_t heads;         /* 32 */
+  int32_t hidden;        /* 7168 */
+  int32_t layout;        /* MONO_LAYOUT_* of w_uv and w_o */
+  const void* o_lat;     /* bf16 [R, 32, 512]: the merged latent attention output */
+  const void* h;         /* bf16 [R, 7168]: the residual stream */
+  const uint8_t* w_uv;   /* E4M3 [32, 128, 512] */
+  const float* s_uv;     /* f32 [32, 1, 4] */
+  const uint8_t* w_o;    /* E4M3 [7168, 4096] */
+  const float* s_o;      /* f32 [56, 32] */
+  void* out;             /* bf16 [R, 7168]: h + o_proj(o) */
+  void* o;               /* optional bf16 [R, 4096]: W_UV's output (else kept in scratch) */
+  void* scratch;         /* runtime owned, mono_post_scratch_bytes() */
+  int32_t* guard;
+  uint32_t* host_error;
+  int32_t fault_site;    /* test fault injection (MONO_SITE_O) */
+  int32_t fault_after;
+  uint64_t* timeline;    /* marks 1: W_UV done, 2: o_proj done */
+} MonoPostArgs;
+
+size_t mono_post_scratch_bytes(void);
+int mono_post_launch(const MonoPostArgs* args, mono_stream_t stream);
 
 #ifdef __cplusplus
 }

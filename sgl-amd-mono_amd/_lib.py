@@ -42,8 +42,8 @@ TL_MARKS = ("start", "staged", "routed", "upgate", "midq", "down", "end")
 TL_COLS = 8
 
 # wait sites (the deadline error word holds 1 + site)
-SITES = {1: "logits", 2: "mid", 3: "mq", 4: "scores", 5: "topk", 6: "split"}
-SITE_MID, SITE_SCORES, SITE_TOPK, SITE_SPLIT = 2, 4, 5, 6
+SITES = {1: "logits", 2: "mid", 3: "mq", 4: "scores", 5: "topk", 6: "split", 7: "o"}
+SITE_MID, SITE_SCORES, SITE_TOPK, SITE_SPLIT, SITE_O = 2, 4, 5, 6, 7
 # timeline marks of the attention launch (same columns)
 TL_ATTN_MARKS = ("start", "scores", "topk", "split", "merge", "exit", "end")
 
@@ -155,6 +155,31 @@ class MonoAttnArgs(ctypes.Structure):
     ]
 
 
+class MonoPostArgs(ctypes.Structure):
+    """Mirror of ``MonoPostArgs`` in mono_amd.h (same order and types)."""
+
+    _fields_ = [
+        ("rows", c_int32),
+        ("heads", c_int32),
+        ("hidden", c_int32),
+        ("layout", c_int32),
+        ("o_lat", c_void_p),
+        ("h", c_void_p),
+        ("w_uv", c_void_p),
+        ("s_uv", c_void_p),
+        ("w_o", c_void_p),
+        ("s_o", c_void_p),
+        ("out", c_void_p),
+        ("o", c_void_p),
+        ("scratch", c_void_p),
+        ("guard", c_void_p),
+        ("host_error", c_void_p),
+        ("fault_site", c_int32),
+        ("fault_after", c_int32),
+        ("timeline", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mono_version": (c_int32, []),
@@ -168,6 +193,8 @@ SIGNATURES = {
     "mono_moe_mxfp4_launch": (c_int32, [ctypes.POINTER(MonoMoeMxfp4Args), c_void_p]),
     "mono_attn_scratch_bytes": (c_size_t, [c_int32]),
     "mono_attn_launch": (c_int32, [ctypes.POINTER(MonoAttnArgs), c_void_p]),
+    "mono_post_scratch_bytes": (c_size_t, []),
+    "mono_post_launch": (c_int32, [ctypes.POINTER(MonoPostArgs), c_void_p]),
 }
 
 _lock = threading.Lock()

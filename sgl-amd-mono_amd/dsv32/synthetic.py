@@ -15,6 +15,7 @@ import torch
 from .. import layouts
 from .config import DSV32, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
 from .moe import MoeFp8Weights, MoeMxfp4Weights
+from .post import PostWeights
 
 FP8 = torch.float8_e4m3fn
 
@@ -140,3 +141,32 @@ def attention_inputs(rows: int, ctx: int, device, seed: int = 0, positions=None,
     return AttnInputs(q=q, iq=iq, iqs=iqs, iw=iw, plane=plane, plane_scale=plane_scale, kv=kv,
                       kv_scale=kv_scale, positions=positions, req_ids=req_ids,
                       page_table=page_table)
+
+
+def post_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
+                 layout: str = layouts.ROWMAJOR) -> PostWeights:
+    """W_UV [32, 128, 512] and o_proj [7168, 4096]: ``randn`` cast to E4M3 with block
+    scales ~U(0.5, 2)/448 (as the expert weights); ``layout`` "aiter16" shuffles each
+    [N, K] matrix."""
+    dev = torch.device(device)
+    hh, v, c, hid = cfg.heads, cfg.v_dim, cfg.kv_lora, cfg.hidden
+    g = _gen(dev, seed, 40)
+    w_uv = torch.randn(hh, v, c, generator=g, device=dev).to(FP8)
+    w_o = torch.randn(hid, hh * v, generator=g, device=dev).to(FP8)
+    gs = _gen(dev, seed, 41)
+    s_uv = (0.5 + 1.5 * torch.rand(hh, v // 128, c // 128, generator=gs, device=dev)) / 448.0
+    s_o = (0.5 + 1.5 * torch.rand(hid // 128, hh * v // 128, generator=gs, device=dev)) / 448.0
+    if layout == layouts.AITER16:
+        for i in range(hh):
+            w_uv[i] = layouts.shuffle_16x16(w_uv[i].view(torch.uint8)).view(FP8)
+        w_o = layouts.shuffle_16x16(w_o.view(torch.uint8)).view(FP8)
+    return PostWeights(w_uv=w_uv, s_uv=s_uv, w_o=w_o, s_o=s_o, layout=layout)
+
+
+def rowmajor_post(w: PostWeights):
+    """(w_uv, s_uv, w_o, s_o) on the host as numpy, row-major (for the oracle)."""
+    w_uv, w_o = w.w_uv.view(torch.uint8), w.w_o.view(torch.uint8)
+    if w.layout == layouts.AITER16:
+        w_uv = torch.stack([layouts.unshuffle_16x16(x) for x in w_uv])
+        w_o = layouts.unshuffle_16x16(w_o)
+    return (w_uv.cpu().numpy(), w.s_uv.cpu().numpy(), w_o.cpu().numpy(), w.s_o.cpu().numpy())
