@@ -1,16 +1,20 @@
-// W8A16 GEMV tasks for the dense projections of the layer: y[r, n] = sum_k x[r, k]
+// W8A16 GEMV tiles for the dense projections of the layer: y[r, n] = sum_k x[r, k]
 // W[n, k] s[n / 128, k / 128] for up to 16 rows r (the MFMA columns), with W in E4M3
 // read in place (row-major, or AITER's (16, 16) shuffle) and widened exactly to bf16,
 // x in bf16, f32 accumulation (sgl_amd_mono/glm53/gfx950/kernel.py:823-875 unit_fp8x2,
 // :1061-1213 units and row reduction).
 //
-// A task is RG 16-row groups of one group g (per-head GEMVs are G independent groups);
-// its 16 waves are RG row groups x KS K-splits, each wave STEPS steps of 64 K. A lane's
-// 16 weight bytes are row l % 16, K k0 + 16 (l / 16) .. + 15 (in the shuffle, a 16-row x
-// 64-K tile is 1 KiB contiguous with lane l at 16 l); they feed two 16x16x32 bf16 MFMAs
-// whose B operands are x[l % 16][k0 + 16 (l / 16) + 8 m ..] (m = 0, 1). Each step's
-// partial is scaled by its block's f32 scale. The KS partials of a row group are summed
-// in a fixed order through LDS.
+// A tile is RG 16-row groups of one group g (per-head GEMVs are G independent groups);
+// KS x RG waves of the CTA take it, RG row groups x KS K-splits, each wave STEPS steps of
+// 64 K. A lane's 16 weight bytes are row l % 16, K k0 + 16 (l / 16) .. + 15 (in the
+// shuffle, a 16-row x 64-K tile is 1 KiB contiguous with lane l at 16 l); they feed two
+// 16x16x32 bf16 MFMAs whose B operands are x[l % 16][k0 + 16 (l / 16) + 8 m ..] (m = 0,
+// 1). Each step's partial is scaled by its block's f32 scale. The KS partials of a row
+// group are summed in a fixed order through LDS.
+//
+// The phases are separate so a launch can put a tile's weights in flight long before its
+// x exists (issue), load x once for several tiles of one group (load_x: x depends on the
+// wave's K range only), and reduce several tiles behind one barrier (dot, epilogue).
 #pragma once
 
 #include "mono_device.h"
@@ -46,92 +50,154 @@ struct GemvJob {
   int out_stride, out_gstride;
   const uint16_t* res;
   int res_stride;
+  // bf16 pairs are stored XOR out_xor (a hand-off whose zero words mean "not written
+  // yet" stores the complement); out_plain, if given, gets the plain pairs as well
+  uint32_t out_xor;
+  uint16_t* out_plain;
 };
 
-// Run every task of `j` this CTA owns (tasks b, b + nblk, ...). XCP: cache policy of the x
-// loads (CP_DEV when another CTA of this launch wrote x). `before_x` runs once, after the
-// first task's weight loads are issued and before its x loads: the place to wait for x.
-// Returns false if before_x reported a failure (the CTA then skips its tasks).
-template <int KS, int STEPS, int XCP, class BeforeX>
-__device__ inline bool gemv_tasks(const GemvJob& j, int R, int b, int nblk, int tid, v4f (*red)[64],
-                                  BeforeX before_x) {
-  constexpr int RG = 16 / KS;
-  static_assert(KS * RG == 16, "16 waves: KS K-splits x RG row groups");
-  const int l = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rg = w / KS, ks = w % KS;
-  const int t = l & 15, grp = l >> 4;
-  const int tiles = j.N / (16 * RG);
-  const int ntask = j.G * tiles;
-  const uint32_t wbytes = (uint32_t)j.N * (uint32_t)j.K;
-  const uint32_t vo = j.shuf ? (uint32_t)l * 16 : (uint32_t)(t * j.K + 16 * grp);
-  bool ok = true, first = true;
-  for (int task = b; task < ntask; task += nblk) {
-    const int g = task / tiles, tile = task % tiles;
-    const int rgg = tile * RG + rg;  // this wave's 16-row group within the group's N rows
-    const __amdgpu_buffer_rsrc_t rw = rsrc(j.w + (size_t)g * wbytes, wbytes);
-    v4i wv[STEPS];
+template <int KS, int RG, int STEPS>
+struct Gemv {
+  static_assert(KS * RG <= 16, "16 waves a CTA");
+  static constexpr int ROWS = 16 * RG;  // rows of a tile
+  int l, w, rg, ks, t, grp;
+  bool on;  // this wave takes part (w < KS * RG)
+
+  __device__ explicit Gemv(int tid) {
+    l = tid & 63;
+    w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    rg = w / KS;
+    ks = w % KS;
+    t = l & 15;
+    grp = l >> 4;
+    on = KS * RG == 16 || w < KS * RG;
+  }
+  __device__ int k0(int s) const { return (ks * STEPS + s) * 64; }
+
+  // put the wave's weight bytes of tile `tile` of group g in flight (a tile that is not
+  // `valid` reads zeros without memory traffic: no branch, so the loads that follow keep
+  // static wait counts)
+  // Both layouts put row group rgg at byte 16 rgg K; within it the shuffle's 64-K step
+  // is 1 KiB (lane l at 16 l) and the row-major one 64 B (lane at t K + 16 grp): one
+  // formula, so the unrolled loads carry no branch. Waves beyond KS x RG read zeros.
+  // The steps' block scales are read here too, as vector loads issued with the weights
+  // (they return in order with them): a scalar load at the dot would cost a round trip
+  // of its own after the data arrived, and a constant load may sink to its use.
+  __device__ void issue(const GemvJob& j, int g, int tile, v4i (&wv)[STEPS],
+                        float (&sc)[STEPS], bool valid = true) const {
+    const uint32_t wbytes = (uint32_t)j.N * (uint32_t)j.K;
+    const __amdgpu_buffer_rsrc_t rw =
+        rsrc(j.w + (size_t)g * wbytes, valid && on ? wbytes : 0u);
+    const int rgg = tile * RG + rg;
+    const uint32_t vo = j.shuf ? (uint32_t)l * 16 : (uint32_t)(t * j.K + 16 * grp);
+    const int sh = j.shuf ? 4 : 0;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+      wv[s] = ld16s<CP_NT>(rw, vo, (uint32_t)(rgg * 16 * j.K) + ((uint32_t)k0(s) << sh));
+    // (an absent tile reads zeros; with STEPS even, steps 2i and 2i + 1 share a block)
+    const int sbase = (g * (j.N / 128) + rgg / 8) * (j.K / 128);
+    const __amdgpu_buffer_rsrc_t rs =
+        rsrc(j.s, valid && on ? (uint32_t)(j.G * (j.N / 128) * (j.K / 128)) * 4u : 0u);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
-      const int k0 = (ks * STEPS + s) * 64;
-      const uint32_t so = j.shuf ? (uint32_t)(rgg * (j.K / 32) + k0 / 32) * 512u
-                                 : (uint32_t)(rgg * 16 * j.K + k0);
-      wv[s] = ld16s<CP_NT>(rw, vo, so);
+      if (STEPS % 2 == 0 && (s & 1))
+        sc[s] = sc[s - 1];
+      else
+        sc[s] = __int_as_float(ld4<CP_NONE>(rs, (uint32_t)(sbase + k0(s) / 128) * 4u));
     }
-    if (first) {
-      first = false;
-      ok = before_x();
-      if (!ok) break;
-    }
+  }
+
+  // the wave's x operands of group g (rows >= R read zeros); XCP: cache policy (CP_DEV
+  // when another CTA of this launch wrote x)
+  template <int XCP>
+  __device__ void load_x(const GemvJob& j, int g, int R, v4i (&xa)[STEPS][2],
+                         bool valid = true) const {
     const uint16_t* xg = j.x + (size_t)g * j.x_gstride;
     const __amdgpu_buffer_rsrc_t rx =
-        rsrc(xg, (uint32_t)((R - 1) * j.x_stride + j.K) * 2u);  // rows >= R read zeros
-    v4i xa[STEPS][2];
+        rsrc(xg, valid && on ? (uint32_t)((R - 1) * j.x_stride + j.K) * 2u : 0u);
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int k0 = (ks * STEPS + s) * 64;
+    for (int s = 0; s < STEPS; ++s)
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const uint32_t off = t < R ? (uint32_t)(t * j.x_stride + k0 + 16 * grp + 8 * m) * 2u
+        const uint32_t off = t < R ? (uint32_t)(t * j.x_stride + k0(s) + 16 * grp + 8 * m) * 2u
                                    : 0x80000000u;
         xa[s][m] = ld16<XCP>(rx, off);
       }
-    }
-    const int sbase = (g * (j.N / 128) + rgg / 8) * (j.K / 128);
+  }
+
+  // the wave's scaled partial of tile `tile`, into red[w] (a barrier must follow)
+  __device__ void dot(const v4i (&wv)[STEPS], const float (&sc)[STEPS],
+                      const v4i (&xa)[STEPS][2], v4f (*red)[64]) const {
+    if (!on) return;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
-      const int k0 = (ks * STEPS + s) * 64;
       v4f d = {0.f, 0.f, 0.f, 0.f};
       d = mfma_bf16(fp8x8_bf16((uint32_t)wv[s][0], (uint32_t)wv[s][1]),
                     __builtin_bit_cast(v8bf, xa[s][0]), d);
       d = mfma_bf16(fp8x8_bf16((uint32_t)wv[s][2], (uint32_t)wv[s][3]),
                     __builtin_bit_cast(v8bf, xa[s][1]), d);
-      acc += d * sld(j.s, sbase + k0 / 128);
+      acc += d * sc[s];
     }
     red[w][l] = acc;
-    __syncthreads();
-    // 256 threads a row group: row = e % 16 (adjacent threads, adjacent rows), token e / 16
-    if (tid < RG * 256) {
-      const int rge = tid >> 8, e = tid & 255;
-      const int row = e & 15, tok = e >> 4;
-      const int L = tok + 16 * (row >> 2), v = row & 3;
-      float y = 0.f;
+  }
+
+  // sum the KS partials of tile `tile` and store it: threads e in [0, RG * 256) of the
+  // CTA (whole waves), row = e % 16 (adjacent threads, adjacent rows), token e / 16 % 16
+  // (`hres`: the residual's bits for this thread's output, if the caller loaded it ahead;
+  // else j.res is read here)
+  __device__ static void epilogue(const GemvJob& j, int g, int tile, int R, int e,
+                                  v4f (*red)[64], int hres = -1) {
+    const int rge = e >> 8, row = e & 15, tok = (e >> 4) & 15;
+    const int L = tok + 16 * (row >> 2), v = row & 3;
+    float y = 0.f;
 #pragma unroll
-      for (int i = 0; i < KS; ++i) y += red[rge * KS + i][L][v];
-      const int n = (tile * RG + rge) * 16 + row;
-      if (j.out_f) {
-        if (tok < R) st_devf(j.out_f + (size_t)g * j.out_gstride + tok * j.out_stride + n, y);
-      } else {
-        if (j.res && tok < R) y += bf16_lo(j.res[tok * j.res_stride + g * j.N + n]);
-        const uint32_t h = bf16_bits(y);
-        const uint32_t hn = dpp_u<DPP_XOR1>(h);  // the next row's bits (same token)
-        if (tok < R && (row & 1) == 0)
-          st_dev(reinterpret_cast<uint32_t*>(j.out_bf + (size_t)g * j.out_gstride +
-                                             tok * j.out_stride + n),
-                 h | (hn << 16));
+    for (int i = 0; i < KS; ++i) y += red[rge * KS + i][L][v];
+    const int n = (tile * RG + rge) * 16 + row;
+    if (j.out_f) {
+      if (tok < R) st_devf(j.out_f + (size_t)g * j.out_gstride + tok * j.out_stride + n, y);
+    } else {
+      if (j.res && tok < R)
+        y += bf16_lo(hres >= 0 ? (uint32_t)hres : j.res[tok * j.res_stride + g * j.N + n]);
+      const uint32_t h = bf16_bits(y);
+      const uint32_t hn = dpp_u<DPP_XOR1>(h);  // the next row's bits (same token)
+      uint32_t pair = h | (hn << 16);
+      if (pair == 0xFFFFFFFFu) pair = 0xFFC0FFC0u;  // two NaNs; keeps ~pair nonzero
+      const size_t at = (size_t)g * j.out_gstride + tok * j.out_stride + n;
+      if (tok < R && (row & 1) == 0) {
+        st_dev(reinterpret_cast<uint32_t*>(j.out_bf + at), pair ^ j.out_xor);
+        if (j.out_plain) st_dev(reinterpret_cast<uint32_t*>(j.out_plain + at), pair);
       }
     }
+  }
+};
+
+// Run every tile of `j` this CTA owns (tasks b, b + nblk, ... over G x N / (16 RG)),
+// one at a time. `before_x` runs once, after the first task's weight loads are issued
+// and before its x loads: the place to wait for x. Returns false if before_x reported a
+// failure (the CTA then skips its tasks).
+template <int KS, int RG, int STEPS, int XCP, class BeforeX>
+__device__ inline bool gemv_tasks(const GemvJob& j, int R, int b, int nblk, int tid,
+                                  v4f (*red)[64], BeforeX before_x) {
+  const Gemv<KS, RG, STEPS> gv(tid);
+  const int tiles = j.N / Gemv<KS, RG, STEPS>::ROWS;
+  const int ntask = j.G * tiles;
+  bool ok = true, first = true;
+  for (int task = b; task < ntask; task += nblk) {
+    const int g = task / tiles, tile = task % tiles;
+    v4i wv[STEPS];
+    float sc[STEPS];
+    gv.issue(j, g, tile, wv, sc);
+    if (first) {
+      first = false;
+      ok = before_x();
+      if (!ok) break;
+    }
+    v4i xa[STEPS][2];
+    gv.template load_x<XCP>(j, g, R, xa);
+    gv.dot(wv, sc, xa, red);
+    __syncthreads();
+    if (tid < RG * 256) Gemv<KS, RG, STEPS>::epilogue(j, g, tile, R, tid, red);
     __syncthreads();
   }
   return ok;

@@ -37,6 +37,10 @@ template <int CP>
 __device__ inline v4i ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP);
 }
+template <int CP>
+__device__ inline void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, v4i v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, CP);
+}
 // per-lane offset `voff` (VGPR) + wave-uniform offset `soff` (SGPR)
 template <int CP>
 __device__ inline v4i ld16s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
