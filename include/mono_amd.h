@@ -51,6 +51,9 @@ typedef void* mono_stream_t;
 #define MONO_SITE_TOPK 5     /* a sparse-MLA split waits on its row's top-k */
 #define MONO_SITE_SPLIT 6    /* a merge waits on its row's splits */
 #define MONO_SITE_O 7        /* o_proj waits on the W_UV outputs */
+#define MONO_SITE_FRONT_A 8  /* a row task waits on the q_a | kv_a | index-key outputs */
+#define MONO_SITE_QAN 9      /* q_b / W_iq wait on the normalised q_a */
+#define MONO_SITE_QB 10      /* W_UK / the index query wait on q_b / W_iq outputs */
 
 int mono_version(void);
 const char* mono_last_error(void);
@@ -267,6 +270,63 @@ typedef struct {
 
 size_t mono_post_scratch_bytes(void);
 int mono_post_launch(const MonoPostArgs* args, mono_stream_t stream);
+
+/* ------------------------------------------------------------------------------
+ * The front of the layer as one persistent launch: from the layer input h to the
+ * attention launch's inputs (q, iq, iqs, iw), with the rows' KV and index-key cache
+ * writes. x = bf16(rmsnorm(h) g_in); q_a | kv_a, the index key and the head weights off
+ * x; q_an = bf16(rmsnorm(q_a) g_q); the KV row (kv_n = bf16(rmsnorm(kv_a[:512]) g_kv),
+ * k_pe = bf16(rope(kv_a[512:]))) as E4M3 with a power-of-two per-token scale at the
+ * row's slot; the index key (LayerNorm, RoPE on dims 0..63, FWHT-128, FP4 e2m1 + e8m0
+ * per 32) into the index plane at the slot; q_b over q_an (nope bf16, rope rotated),
+ * q_lat = bf16(W_UK q_nope); the index query (W_iq q_an, RoPE, FWHT, FP4); the head
+ * weights bf16(W_w x) 128^-1/2 64^-1/2. RoPE pairs are interleaved (x0 c - x1 s,
+ * x0 s + x1 c) with bf16 tables cos/sin [rope_rows, 32] indexed by position. A slot
+ * outside the caches (e.g. -1, a pad row) writes nothing.
+ * Replaces sgl_amd_mono/glm53/gfx950/kernel.py:1781-2443 (stages qkv_a, q_norm, cache,
+ * q_b, index_q, uk) and the FP4 index paths of
+ * sgl_amd_mono/deepseek_v4/gfx950/kernels/stages/indexer.py:143-151,311-338,340-408. */
+typedef struct {
+  int32_t rows;          /* R, 1..8 */
+  int32_t hidden;        /* 7168 */
+  int32_t heads;         /* 32 */
+  int32_t layout;        /* MONO_LAYOUT_* of the FP8 weights */
+  int32_t rope_rows;     /* rows of cos / sin */
+  uint32_t kv_slots;     /* rows of kv */
+  uint32_t plane_pages;  /* pages of the index plane */
+  float eps;             /* RMSNorm epsilon (1e-6 for DeepSeek) */
+  const void* h;         /* bf16 [R, 7168] */
+  const void* g_in;      /* bf16 [7168] input RMSNorm weight */
+  const void* g_q;       /* bf16 [1536] */
+  const void* g_kv;      /* bf16 [512] */
+  const uint8_t* w_qkv_a; const float* s_qkv_a;  /* E4M3 [2112, 7168] + f32 [17, 56] */
+  const uint8_t* w_k; const float* s_k;          /* E4M3 [128, 7168] + f32 [1, 56] */
+  const void* w_w;                               /* bf16 [64, 7168] */
+  const float* g_k; const float* b_k;            /* f32 [128] index-key LayerNorm */
+  const uint8_t* w_qb; const float* s_qb;        /* E4M3 [6144, 1536] + f32 [48, 12] */
+  const uint8_t* w_iq; const float* s_iq;        /* E4M3 [8192, 1536] + f32 [64, 12] */
+  const uint8_t* w_uk; const float* s_uk;        /* E4M3 [32, 512, 128] + f32 [32, 4, 1] */
+  const void* cos; const void* sin;              /* bf16 [rope_rows, 32] */
+  const int64_t* positions;  /* [R] */
+  const int64_t* slots;      /* [R] cache slot (page * 64 + offset), -1 = none */
+  uint8_t* kv;               /* E4M3 [kv_slots, 576] */
+  float* kv_scale;           /* f32 [kv_slots] */
+  uint8_t* plane;            /* [plane_pages, 4, 64, 16] */
+  uint8_t* plane_scale;      /* [plane_pages, 4, 64] */
+  void* q;                   /* out bf16 [R, 32, 576]: q_lat | q_pe */
+  uint8_t* iq;               /* out [R, 64, 64] E2M1 */
+  uint8_t* iqs;              /* out [R, 4, 16, 4] E8M0 */
+  float* iw;                 /* out f32 [R, 64] */
+  void* scratch;             /* runtime owned, mono_front_scratch_bytes() */
+  int32_t* guard;
+  uint32_t* host_error;
+  int32_t fault_site;        /* test fault injection (MONO_SITE_FRONT_A / QAN / QB) */
+  int32_t fault_after;
+  uint64_t* timeline;
+} MonoFrontArgs;
+
+size_t mono_front_scratch_bytes(void);
+int mono_front_launch(const MonoFrontArgs* args, mono_stream_t stream);
 
 #ifdef __cplusplus
 }

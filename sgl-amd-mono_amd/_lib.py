@@ -42,8 +42,10 @@ TL_MARKS = ("start", "staged", "routed", "upgate", "midq", "down", "end")
 TL_COLS = 8
 
 # wait sites (the deadline error word holds 1 + site)
-SITES = {1: "logits", 2: "mid", 3: "mq", 4: "scores", 5: "topk", 6: "split", 7: "o"}
+SITES = {1: "logits", 2: "mid", 3: "mq", 4: "scores", 5: "topk", 6: "split", 7: "o",
+         8: "front_a", 9: "q_an", 10: "q_b"}
 SITE_MID, SITE_SCORES, SITE_TOPK, SITE_SPLIT, SITE_O = 2, 4, 5, 6, 7
+SITE_FRONT_A, SITE_QAN, SITE_QB = 8, 9, 10
 # timeline marks of the attention launch (same columns)
 TL_ATTN_MARKS = ("start", "scores", "topk", "split", "merge", "exit", "end")
 
@@ -180,6 +182,56 @@ class MonoPostArgs(ctypes.Structure):
     ]
 
 
+class MonoFrontArgs(ctypes.Structure):
+    """Mirror of ``MonoFrontArgs`` in mono_amd.h (same order and types)."""
+
+    _fields_ = [
+        ("rows", c_int32),
+        ("hidden", c_int32),
+        ("heads", c_int32),
+        ("layout", c_int32),
+        ("rope_rows", c_int32),
+        ("kv_slots", c_uint32),
+        ("plane_pages", c_uint32),
+        ("eps", c_float),
+        ("h", c_void_p),
+        ("g_in", c_void_p),
+        ("g_q", c_void_p),
+        ("g_kv", c_void_p),
+        ("w_qkv_a", c_void_p),
+        ("s_qkv_a", c_void_p),
+        ("w_k", c_void_p),
+        ("s_k", c_void_p),
+        ("w_w", c_void_p),
+        ("g_k", c_void_p),
+        ("b_k", c_void_p),
+        ("w_qb", c_void_p),
+        ("s_qb", c_void_p),
+        ("w_iq", c_void_p),
+        ("s_iq", c_void_p),
+        ("w_uk", c_void_p),
+        ("s_uk", c_void_p),
+        ("cos", c_void_p),
+        ("sin", c_void_p),
+        ("positions", c_void_p),
+        ("slots", c_void_p),
+        ("kv", c_void_p),
+        ("kv_scale", c_void_p),
+        ("plane", c_void_p),
+        ("plane_scale", c_void_p),
+        ("q", c_void_p),
+        ("iq", c_void_p),
+        ("iqs", c_void_p),
+        ("iw", c_void_p),
+        ("scratch", c_void_p),
+        ("guard", c_void_p),
+        ("host_error", c_void_p),
+        ("fault_site", c_int32),
+        ("fault_after", c_int32),
+        ("timeline", c_void_p),
+    ]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mono_version": (c_int32, []),
@@ -195,6 +247,8 @@ SIGNATURES = {
     "mono_attn_launch": (c_int32, [ctypes.POINTER(MonoAttnArgs), c_void_p]),
     "mono_post_scratch_bytes": (c_size_t, []),
     "mono_post_launch": (c_int32, [ctypes.POINTER(MonoPostArgs), c_void_p]),
+    "mono_front_scratch_bytes": (c_size_t, []),
+    "mono_front_launch": (c_int32, [ctypes.POINTER(MonoFrontArgs), c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -91,6 +91,9 @@ __device__ inline uint32_t add_dev(uint32_t* p, uint32_t v) {
 }
 // wait until this wave's earlier memory operations (sc1 stores included) completed
 __device__ inline void drain() { __builtin_amdgcn_s_waitcnt(0); }
+// s_waitcnt immediate waiting for vmcnt <= n only (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // (value, tag) pair: one 8-byte store publishes a 32-bit word with its launch tag
 __device__ inline uint64_t pair(uint32_t v, uint32_t tag) {

@@ -16,6 +16,7 @@ from .. import layouts
 from .config import DSV32, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
 from .moe import MoeFp8Weights, MoeMxfp4Weights
 from .post import PostWeights
+from .front import FrontCaches, FrontWeights
 
 FP8 = torch.float8_e4m3fn
 
@@ -170,3 +171,72 @@ def rowmajor_post(w: PostWeights):
         w_uv = torch.stack([layouts.unshuffle_16x16(x) for x in w_uv])
         w_o = layouts.unshuffle_16x16(w_o)
     return (w_uv.cpu().numpy(), w.s_uv.cpu().numpy(), w_o.cpu().numpy(), w.s_o.cpu().numpy())
+
+
+def rope_tables(rows: int, device, dim: int = 64, base: float = 10000.0):
+    """bf16 cos / sin [rows, dim / 2] of position p and pair i: angle p base^(-2i / dim)."""
+    i = torch.arange(dim // 2, dtype=torch.float64)
+    ang = torch.arange(rows, dtype=torch.float64)[:, None] * base ** (-2.0 * i / dim)[None]
+    return (ang.cos().to(torch.bfloat16).to(device), ang.sin().to(torch.bfloat16).to(device))
+
+
+def front_weights(device, seed: int = 0, cfg: LayerConfig = DSV32, layout: str = layouts.ROWMAJOR,
+                  rope_rows: int = 32768) -> FrontWeights:
+    """The attention front of one layer: FP8 matrices ``randn`` cast to E4M3 with block
+    scales ~U(0.5, 2)/448, norm weights 1 + 0.1 N(0, 1) (``check_layer.py:67-68``), the
+    head weights bf16 N(0, 1) / sqrt(7168), the index-key LayerNorm bias 0.1 N(0, 1)."""
+    dev = torch.device(device)
+    H, QL, KL, PE = cfg.hidden, cfg.q_lora, cfg.kv_lora, cfg.rope_dim
+    qkv = QL + KL + PE
+    g = _gen(dev, seed, 60)
+    norm = lambda n: (1 + 0.1 * torch.randn(n, generator=g, device=dev)).to(torch.bfloat16)
+    g_in, g_q, g_kv = norm(H), norm(QL), norm(KL)
+    gw = _gen(dev, seed, 61)
+    fp8 = lambda *shape: torch.randn(*shape, generator=gw, device=dev).to(FP8)
+    w_qkv_a, w_k = fp8(qkv, H), fp8(cfg.index_dim, H)
+    w_qb = fp8(cfg.heads * cfg.qk_dim, QL)
+    w_iq = fp8(cfg.index_heads * cfg.index_dim, QL)
+    w_uk = fp8(cfg.heads, KL, cfg.nope_dim)
+    gs = _gen(dev, seed, 62)
+    sc = lambda *shape: (0.5 + 1.5 * torch.rand(*shape, generator=gs, device=dev)) / 448.0
+    cb = lambda n: (n + 127) // 128
+    s_qkv_a, s_k = sc(cb(qkv), H // 128), sc(1, H // 128)
+    s_qb, s_iq = sc(w_qb.shape[0] // 128, QL // 128), sc(w_iq.shape[0] // 128, QL // 128)
+    s_uk = sc(cfg.heads, KL // 128, 1)
+    gx = _gen(dev, seed, 63)
+    w_w = (torch.randn(cfg.index_heads, H, generator=gx, device=dev) / H ** 0.5).to(torch.bfloat16)
+    g_k = 1 + 0.1 * torch.randn(cfg.index_dim, generator=gx, device=dev)
+    b_k = 0.1 * torch.randn(cfg.index_dim, generator=gx, device=dev)
+    if layout == layouts.AITER16:
+        sh = lambda t: layouts.shuffle_16x16(t.view(torch.uint8)).view(FP8)
+        w_qkv_a, w_k, w_qb, w_iq = sh(w_qkv_a), sh(w_k), sh(w_qb), sh(w_iq)
+        w_uk = torch.stack([sh(w_uk[i]) for i in range(cfg.heads)])
+    cos, sin = rope_tables(rope_rows, dev, PE)
+    return FrontWeights(g_in=g_in, g_q=g_q, g_kv=g_kv, w_qkv_a=w_qkv_a, s_qkv_a=s_qkv_a, w_k=w_k,
+                        s_k=s_k, w_w=w_w, g_k=g_k, b_k=b_k, w_qb=w_qb, s_qb=s_qb, w_iq=w_iq,
+                        s_iq=s_iq, w_uk=w_uk, s_uk=s_uk, cos=cos, sin=sin, layout=layout)
+
+
+def rowmajor_front(w: FrontWeights) -> dict:
+    """The oracle's arguments (numpy, row-major) of ``oracle.front.front``."""
+    u8 = lambda t: t.view(torch.uint8)
+    un = (lambda t: layouts.unshuffle_16x16(u8(t))) if w.layout == layouts.AITER16 else u8
+    w_uk = torch.stack([un(w.w_uk[i]) for i in range(w.w_uk.shape[0])])
+    np_ = lambda t: t.cpu().numpy()
+    return dict(g_in=w.g_in.cpu(), g_q=w.g_q.cpu(), g_kv=w.g_kv.cpu(), w_qkv_a=np_(un(w.w_qkv_a)),
+                s_qkv_a=np_(w.s_qkv_a), w_k=np_(un(w.w_k)), s_k=np_(w.s_k), w_w=w.w_w.cpu(),
+                g_k=np_(w.g_k), b_k=np_(w.b_k), w_qb=np_(un(w.w_qb)), s_qb=np_(w.s_qb),
+                w_iq=np_(un(w.w_iq)), s_iq=np_(w.s_iq), w_uk=np_(w_uk), s_uk=np_(w.s_uk),
+                cos=w.cos.cpu(), sin=w.sin.cpu())
+
+
+def front_caches(device, slots: int, pages: int, seed: int = 0) -> FrontCaches:
+    """Caches with random prior contents (so untouched slots can be checked)."""
+    dev = torch.device(device)
+    g = _gen(dev, seed, 64)
+    kv = torch.randint(0, 256, (slots, 576), generator=g, device=dev, dtype=torch.uint8)
+    kv[(kv & 0x7F) == 0x7F] = 0  # no NaN codes
+    kv_scale = torch.rand(slots, generator=g, device=dev)
+    plane = torch.randint(0, 256, (pages, 4, 64, 16), generator=g, device=dev, dtype=torch.uint8)
+    plane_scale = torch.randint(120, 130, (pages, 4, 64), generator=g, device=dev, dtype=torch.uint8)
+    return FrontCaches(kv=kv, kv_scale=kv_scale, plane=plane, plane_scale=plane_scale)

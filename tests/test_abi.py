@@ -34,6 +34,7 @@ def _c_layout(struct, fields, tmp_path):
                                         (_lib.MonoMoeMxfp4Args, "MonoMoeMxfp4Args"),
                                         (_lib.MonoAttnArgs, "MonoAttnArgs"),
                                         (_lib.MonoPostArgs, "MonoPostArgs"),
+                                        (_lib.MonoFrontArgs, "MonoFrontArgs"),
                                         (_lib.MonoDeviceInfo, "MonoDeviceInfo")])
 def test_ctypes_mirrors_match_the_c_layout(cls, cname, tmp_path):
     fields = [f for f, _ in cls._fields_]
@@ -57,6 +58,9 @@ def test_null_args_are_refused_without_a_gpu():
     po = _lib.MonoPostArgs(rows=17, heads=32, hidden=7168)
     assert _lib.lib().mono_post_launch(ctypes.byref(po), None) == _lib.MONO_E_ARG
     assert "rows" in _lib.last_error()
+    fr = _lib.MonoFrontArgs(rows=9, hidden=7168, heads=32)
+    assert _lib.lib().mono_front_launch(ctypes.byref(fr), None) == _lib.MONO_E_ARG
+    assert "rows" in _lib.last_error()
     po = _lib.MonoPostArgs(rows=4, heads=16, hidden=7168)
     assert _lib.lib().mono_post_launch(ctypes.byref(po), None) == _lib.MONO_E_ARG
     assert "32 heads" in _lib.last_error()
@@ -69,6 +73,7 @@ def test_scratch_bytes_only_for_built_geometries():
     assert _lib.lib().mono_moe_mxfp4_scratch_bytes(3072, 512, 256) == 0
     assert _lib.lib().mono_attn_scratch_bytes(48) > 0 and _lib.lib().mono_attn_scratch_bytes(49) == 0
     assert _lib.lib().mono_post_scratch_bytes() >= 16 * 4096 * 2
+    assert _lib.lib().mono_front_scratch_bytes() > 0
 
 
 def test_deadline_ticks_bounds():
