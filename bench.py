@@ -41,7 +41,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4", "attn", "post"),
+    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4", "attn", "post", "layer"),
                    help="moe_fp8: BASELINE configs[1] (the metric's MoE phase); "
                         "moe_mxfp4: configs[3], the MXFP4 A16W4 expert block; "
                         "attn: configs[2], FP4 indexer + top-2048 + sparse MLA")
@@ -377,6 +377,150 @@ def bench_post(args):
     return us, steps, bytes_per, "bf16 x e4m3", config, f"post_r{rows}", cpu
 
 
+FRONT_W_BYTES = (2112 * 7168 + 17 * 56 * 4 + 128 * 7168 + 56 * 4 + 64 * 7168 * 2
+                 + 6144 * 1536 + 48 * 12 * 4 + 8192 * 1536 + 64 * 12 * 4 + 32 * 512 * 128
+                 + 32 * 4 * 4 + (7168 + 1536 + 512) * 2 + 128 * 4 * 2)
+POST_W_BYTES = 32 * 128 * 512 + 7168 * 4096 + (32 * 4 + 56 * 32) * 4
+
+
+def phase_bytes(rows, ctx, distinct):
+    """Algorithmic bytes of each phase of one layer (each needed byte counted once)."""
+    n, k = ctx, min(ctx, 2048)
+    front = (FRONT_W_BYTES + rows * (7168 * 2 + 580 + 68 + 32 * 576 * 2 + 64 * 64 + 256
+                                     + 64 * 4 + 64 * 2 * 2))
+    attn = rows * (k * 580 + n * 68 + 32 * 576 * 2 + 64 * 64 + 256 + 64 * 4 + 32 * 512 * 2)
+    post = POST_W_BYTES + rows * (32 * 512 * 2 + 7168 * 2 * 2)
+    moe = distinct * EXPERT_BYTES + ROUTER_BYTES + rows * 7168 * 2 * 2
+    return {"front": front, "attn": attn, "post": post, "moe": moe}
+
+
+def cpu_baseline_layer(h, w, caches, step, ids, rows):
+    """The oracle chain of one layer on the host for one row (front, attention over the
+    row's 32768 keys, output block, MoE over its 9 experts), scaled to the launch's rows."""
+    import numpy as np
+    import torch
+
+    from oracle import attn as A
+    from oracle import dense as D
+    from oracle import front as Fr
+    from oracle import moe as omoe
+    from sgl_amd_mono_amd.dsv32 import synthetic
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    fw = synthetic.rowmajor_front(w.front)
+    pw = synthetic.rowmajor_post(w.post)
+    experts = {int(e): synthetic.rowmajor_expert(w.moe, int(e)) for e in np.unique(ids[0])}
+    pos = int(step.positions[0])
+    pages = step.page_table[int(step.req_ids[0])].cpu().numpy()
+    plane, psc = caches.plane.cpu().numpy(), caches.plane_scale.cpu().numpy()
+    kv, ksc = caches.kv.cpu().numpy(), caches.kv_scale.cpu().numpy()
+    h0 = h[:1].cpu()
+    t0 = time.perf_counter()
+    f = Fr.front(h0, positions=np.array([pos]), **fw)
+    iq, iqs = Fr.iq_bytes(f["iq_codes"], f["iq_e8"])
+    att = A.attention_row(torch.from_numpy(f["q"][0]).float(), iq[0], iqs[0], f["iw"][0], plane,
+                          psc, pages, kv, ksc, pos, 2048, (128 + 64) ** -0.5)
+    o_lat = torch.from_numpy(D.bf16(att["o"])).reshape(1, 32, 512).to(torch.bfloat16)
+    a = D.attn_out(o_lat, h0, *pw)["a"]
+    omoe.moe_fp8(torch.from_numpy(a).to(torch.bfloat16), w.moe.g_post.cpu(), w.moe.w_r.cpu(),
+                 w.moe.bias.cpu(), None, None, None, None, experts=experts)
+    us = (time.perf_counter() - t0) * 1e6
+    return {"value": round(us * rows, 1), "unit": f"µs per decoder layer ({rows} rows)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 of {rows} rows through the oracle chain (front, FP4 scores of "
+                      f"{pos + 1} keys + exact top-2048 + sparse MLA, W_UV/o_proj, MoE over its "
+                      f"{len(experts)} experts), timed once and scaled x{rows}"}
+
+
+def bench_layer(args):
+    import numpy as np
+    import torch
+
+    from sgl_amd_mono_amd.dsv32 import synthetic
+    from sgl_amd_mono_amd.dsv32.attn import AttnInputs
+    from sgl_amd_mono_amd.dsv32.layer import LayerOp
+    from sgl_amd_mono_amd.dsv32.moe import MoeRouting
+
+    dev = torch.device("cuda:0")
+    rows, ctx = args.rows, args.ctx
+    L = args.layers
+    print(f"bench: generating {L} decoder layers ({rows} rows x {ctx} keys)", file=sys.stderr,
+          flush=True)
+    layers = []
+    for i in range(L):
+        layers.append(synthetic.layer(rows, ctx, dev, seed=1000 + i, layout=args.layout))
+        if (i + 1) % 8 == 0:
+            print(f"bench: {i + 1} layers", file=sys.stderr, flush=True)
+    ops = [LayerOp(w, dev, max_rows=rows, ctx_max=ctx) for w, _, _, _ in layers]
+    outs = [torch.empty(rows, 7168, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    # one eager pass, stage by stage: every phase's inputs for the per-phase timings, and
+    # the experts each layer's batch routes to
+    fr_out, att_in, olat, a_in, distinct, ids0 = [], [], [], [], [], None
+    for i, (op, (w, caches, step, h)) in enumerate(zip(ops, layers)):
+        f = op.front.launch(h, caches, step.positions, step.slots)
+        inp = AttnInputs(q=f.q, iq=f.iq, iqs=f.iqs, iw=f.iw, plane=caches.plane,
+                         plane_scale=caches.plane_scale, kv=caches.kv, kv_scale=caches.kv_scale,
+                         positions=step.positions, req_ids=step.req_ids, page_table=step.page_table)
+        o = op.attn.launch(inp).clone()
+        a = op.post.launch(o, h).clone()
+        rt = MoeRouting(torch.empty(rows, 256, device=dev),
+                        torch.empty(rows, 9, dtype=torch.int32, device=dev),
+                        torch.empty(rows, 9, device=dev))
+        op.moe.launch(a, routing=rt, out=outs[i])
+        op.check()
+        ids = rt.ids.cpu().numpy()
+        distinct.append(len(np.unique(ids)))
+        ids0 = ids if i == 0 else ids0
+        fr_out.append(f)
+        att_in.append(inp)
+        olat.append(o)
+        a_in.append(a)
+    per = [phase_bytes(rows, ctx, d) for d in distinct]
+    avg = {k: sum(p[k] for p in per) / L for k in per[0]}
+    total = sum(avg.values())
+    us, wall, steps = time_graph(
+        lambda i: ops[i].launch(layers[i][3], layers[i][1], layers[i][2], out=outs[i]), L,
+        args.steps, args.warmup)
+    for op in ops:
+        op.check()
+    print(f"bench: {steps} layers, {us:.1f} us each (wall {wall * 1e3 / steps:.1f} ms/layer), "
+          f"distinct experts {distinct}", file=sys.stderr, flush=True)
+    # each phase alone (its launches over the L layers in one graph)
+    phase_us = {
+        "front": time_graph(lambda i: ops[i].front.launch(layers[i][3], layers[i][1],
+                                                          layers[i][2].positions,
+                                                          layers[i][2].slots, out=fr_out[i]),
+                            L, args.steps, args.warmup)[0],
+        "attn": time_graph(lambda i: ops[i].attn.launch(att_in[i], out=olat[i]), L, args.steps,
+                           args.warmup)[0],
+        "post": time_graph(lambda i: ops[i].post.launch(olat[i], layers[i][3], out=a_in[i]), L,
+                           args.steps, args.warmup)[0],
+        "moe": time_graph(lambda i: ops[i].moe.launch(a_in[i], out=outs[i]), L, args.steps,
+                          args.warmup)[0],
+    }
+    for op in ops:
+        op.check()
+    phases = {k: {"us": round(v, 2), "bytes": int(avg[k]),
+                  "achieved_GBs": round(avg[k] / (v * 1e-6) / 1e9, 1)} for k, v in phase_us.items()}
+    print(f"bench: phases {phases}", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline_layer(layers[0][3], layers[0][0], layers[0][1],
+                                                      layers[0][2], ids0, rows)
+    config = {
+        "workload": "BASELINE configs[4]: full DeepSeek-V3.2 DSA decoder layer, one GPU's TP=4 "
+                    "share, 8 rows at position 32767 (context 32768): front (RMSNorm, q_a/kv_a, "
+                    "q_b, RoPE, W_UK, KV + FP4 index-key cache writes, FP4 index query), FP4 "
+                    "indexer + exact top-2048 + sparse MLA, W_UV + o_proj + residual, FP8 MoE "
+                    "(norm, router, top-8 + shared, residual): 4 persistent launches a layer",
+        "rows": rows, "context": ctx, "layers_rotated": L, "launches_per_layer": 4,
+        "weight_layout": args.layout, "distinct_experts": distinct, "phases": phases,
+        "bytes_per_layer": int(total), "layer_achieved_GBs": round(total / (us * 1e-6) / 1e9, 1),
+        "model_layers": 61, "us_per_token_step_61_layers": round(us * 61, 1),
+    }
+    # the roofline line is the dominant phase's (the MoE launch)
+    return (us, steps, avg["moe"], "fp8 / fp4 idx / bf16", config, "moe_fp8_r8", cpu,
+            phase_us["moe"])
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -387,9 +531,11 @@ def main():
               f"path (TP=4 exchanges) is not built; got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
     run = {"moe_fp8": bench_moe_fp8, "moe_mxfp4": bench_moe_mxfp4, "attn": bench_attn,
-           "post": bench_post}[args.workload]
-    us, steps, avg_bytes, dtype, config, prof, cpu = run(args)
-    achieved = avg_bytes / (us * 1e-6) / 1e9  # GB/s
+           "post": bench_post, "layer": bench_layer}[args.workload]
+    res = run(args)
+    us, steps, avg_bytes, dtype, config, prof, cpu = res[:7]
+    kernel_us = res[7] if len(res) > 7 else us  # the dominant kernel's launch time
+    achieved = avg_bytes / (kernel_us * 1e-6) / 1e9  # GB/s
     line = {
         "metric": METRIC,
         "value": round(us, 2),
@@ -404,7 +550,8 @@ def main():
         "dtype": dtype,
         "data": "synthetic",
         "config": config,
-        "rows_per_s": round(args.rows / (us * 1e-6), 1),
+        # rows a second through one launch, or (layer) through the 61 layers of the model
+        "rows_per_s": round(args.rows / (us * 1e-6 * (61 if args.workload == "layer" else 1)), 1),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -240,3 +240,23 @@ def front_caches(device, slots: int, pages: int, seed: int = 0) -> FrontCaches:
     plane = torch.randint(0, 256, (pages, 4, 64, 16), generator=g, device=dev, dtype=torch.uint8)
     plane_scale = torch.randint(120, 130, (pages, 4, 64), generator=g, device=dev, dtype=torch.uint8)
     return FrontCaches(kv=kv, kv_scale=kv_scale, plane=plane, plane_scale=plane_scale)
+
+
+def layer(rows: int, ctx: int, device, seed: int = 0, layout: str = layouts.AITER16):
+    """Config 5, one layer: its weights (front, output block, FP8 MoE), caches as config 3
+    (each row its own request at position ctx - 1 over shuffled pages), the step's
+    tables (each row's slot the page-table entry of its position) and the input rows h.
+    Returns (LayerWeights, FrontCaches, LayerStep, h)."""
+    from .layer import LayerStep, LayerWeights
+
+    dev = torch.device(device)
+    w = LayerWeights(front=front_weights(dev, seed, layout=layout, rope_rows=max(ctx, 1)),
+                     post=post_weights(dev, seed, layout=layout),
+                     moe=moe_fp8_weights(dev, seed, layout=layout))
+    a = attention_inputs(rows, ctx, dev, seed=seed)
+    caches = FrontCaches(kv=a.kv, kv_scale=a.kv_scale, plane=a.plane, plane_scale=a.plane_scale)
+    pos = a.positions
+    page = a.page_table.gather(1, (pos // 64).to(torch.int64)[:, None])[:, 0].to(torch.int64)
+    step = LayerStep(positions=pos, slots=page * 64 + pos % 64, req_ids=a.req_ids,
+                     page_table=a.page_table)
+    return w, caches, step, rows_bf16(rows, DSV32.hidden, dev, seed=seed)
