@@ -1,19 +1,28 @@
 """Benchmark of the MI355X DSA-layer hot path: one JSON line on stdout.
 
-Workload (N = 1): BASELINE.json configs[1], the FP8 routed MoE of one GPU's TP=4 share
-(hidden 7168, 256 experts top-8 + 1 shared, intermediate 512, E4M3 weights with 128x128
-f32 block scales) at 8 decode rows, as one persistent launch. A step is one launch
-over one batch of 8 rows, on one of ``--layers`` independently seeded layers in turn
-(about 2.8 GB of experts each, so the 256 MB MALL cannot serve the weights). Inputs are
-resident in HBM before the timed region; the timed region replays a HIP graph of one
-launch per layer, is bracketed by ``torch.cuda.synchronize()`` and is measured with HIP
-events on the replay stream.
+Workload (N = 1, the default ``--workload layer``): BASELINE.json configs[4], one GPU's
+TP=4 share of a DeepSeek-V3.2 DSA decoder layer at 8 decode rows, each row its own
+request at position 32767 (context 32768): the front (RMSNorm, q_a | kv_a, q_b, RoPE,
+W_UK, the KV and FP4 index-key cache writes, the FP4 index query), the attention phase
+(FP4 indexer scores, exact top-2048, sparse MLA), the output block (W_UV, o_proj,
+residual) and the FP8 MoE (RMSNorm, router, top-8 + shared experts, residual), as four
+persistent launches. A step is one layer over one batch; ``--layers`` independently
+seeded layers (about 3 GB each, 0.5 GB of it touched a step, so the 256 MB MALL cannot
+serve them) are rotated. Inputs are resident in HBM before the timed region; the timed
+region replays a HIP graph of the four launches of every layer, is bracketed by
+``torch.cuda.synchronize()`` and is measured with HIP events on the replay stream.
+``value`` is the average µs per layer.
 
-``roofline``: algorithmic bytes per launch = every distinct expert the batch actually
-routed to (shared included) x 11,012,736 B + the router 3,670,016 B + the rows in and
-out, over the average launch time, against 8 TB/s. ``cpu_baseline``: the CPU oracle
-(``oracle/moe.py``) on the same workload, one launch worth (8 rows, only the routed
-experts dequantised), on this host's cores.
+``roofline``: the dominant kernel's (the MoE launch's) algorithmic bytes per launch --
+every distinct expert the batch routed to (shared included) x 11,012,736 B + the router
+3,670,016 B + the rows in and out -- over its own average launch time (a graph of that
+launch alone over the same layers), against 8 TB/s; ``config.phases`` gives every
+phase's time and achieved bandwidth. ``cpu_baseline``: the CPU oracle chain
+(``oracle/front.py``, ``oracle/attn.py``, ``oracle/dense.py``, ``oracle/moe.py``) for one
+of the rows, scaled to the batch, on this host's cores.
+
+Other workloads (``--workload``): moe_fp8 (configs[1] alone), moe_mxfp4,
+attn, post (the output block alone).
 """
 
 from __future__ import annotations
@@ -41,10 +50,13 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="moe_fp8", choices=("moe_fp8", "moe_mxfp4", "attn", "post", "layer"),
-                   help="moe_fp8: BASELINE configs[1] (the metric's MoE phase); "
+    p.add_argument("--workload", default="layer",
+                   choices=("layer", "moe_fp8", "moe_mxfp4", "attn", "post"),
+                   help="layer: BASELINE configs[4], the full decoder layer (the metric); "
+                        "moe_fp8: configs[1], the FP8 MoE phase alone; "
                         "moe_mxfp4: configs[3], the MXFP4 A16W4 expert block; "
-                        "attn: configs[2], FP4 indexer + top-2048 + sparse MLA")
+                        "attn: configs[2], FP4 indexer + top-2048 + sparse MLA; "
+                        "post: W_UV + o_proj + residual")
     p.add_argument("--ctx", type=int, default=32768, help="attn: keys each row sees")
     p.add_argument("--rows", type=int, default=8)
     p.add_argument("--layers", type=int, default=4)
@@ -517,7 +529,7 @@ def bench_layer(args):
         "model_layers": 61, "us_per_token_step_61_layers": round(us * 61, 1),
     }
     # the roofline line is the dominant phase's (the MoE launch)
-    return (us, steps, avg["moe"], "fp8 / fp4 idx / bf16", config, "moe_fp8_r8", cpu,
+    return (us, steps, avg["moe"], "fp8 / fp4 idx / bf16", config, "layer_moe", cpu,
             phase_us["moe"])
 
 
