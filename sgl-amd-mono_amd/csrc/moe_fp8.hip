@@ -1,11 +1,17 @@
 // FP8 routed MoE as one persistent gfx950 launch (the FFN half of the DSA layer).
 //
 // Stages, every CTA in order (task t of a stage runs on CTA t mod grid):
-//   0  RMSNorm of the R rows (every CTA, from L2), per-128 E4M3 quant of its wave's
-//      K slice straight into MFMA B-operand registers, and the router logit of its
-//      expert(s), published as (value, tag) pairs.
-//   1  routing: each CTA polls the 256 x R logits and runs sigmoid + bias top-8
-//      itself (one wave a row), then compacts the distinct experts, shared first.
+//   0  the rows' RMSNorm factors (every CTA, from L2), then one task a CTA: a router
+//      tile (16 experts x 512 K of W_r x bf16(rmsnorm(a)) as a bf16 MFMA; 224 tiles,
+//      partial logits out), or a publisher (8 of the 56 128-K chunks: per-128 E4M3
+//      quant of every row straight into the MFMA B-operand image, scales out). The
+//      normalised rows are quantised once, not on every CTA.
+//   1  every CTA copies the published image into LDS (buffer -> LDS). Row r is routed
+//      by one CTA (NTASK0 + r mod grid): the 14 partials of its 256 logits summed in a
+//      fixed order, sigmoid + bias top-8, the 8 ids and weights out; every CTA reads
+//      the R routes and compacts the distinct experts, shared first. Every hand-off is
+//      complemented words in one of two scratch buffers (by the tag's parity), zero
+//      meaning "not written yet"; the launch clears the other.
 //   2  up/gate: task (u, c) = 16 gate + 16 up rows of distinct expert u over all of
 //      K, the 8 waves splitting K. W8A8 16x16x128 MFMA per 128-chunk, then the
 //      chunk's weight block scale x activation scale into the f32 accumulator.
@@ -48,9 +54,7 @@ struct MoeFp8Geom {
   static_assert(H % 128 == 0, "hidden must be whole 128-blocks");
 
   // scratch layout (bytes)
-  static constexpr size_t OFF_LOGIT = 0;
-  static constexpr size_t SZ_LOGIT = (size_t)MOE_MAXR * MOE_NEXP * 8;
-  static constexpr size_t OFF_MID = OFF_LOGIT + SZ_LOGIT;
+  static constexpr size_t OFF_MID = 0;
   static constexpr size_t SZ_MID = (size_t)MOE_NDIST * MOE_MAXR * I * 8;
   static constexpr size_t OFF_MQ = OFF_MID + SZ_MID;
   static constexpr size_t SZ_MQ = (size_t)MOE_NDIST * MOE_MAXR * I;
@@ -61,7 +65,26 @@ struct MoeFp8Geom {
   // work-queue counters (zero at launch entry; the last CTA out re-zeroes them)
   static constexpr size_t OFF_QUEUE = (OFF_READY + SZ_READY + 255) & ~(size_t)255;
   static constexpr int NQUEUE = 4;
-  static constexpr size_t BYTES = (OFF_QUEUE + NQUEUE * 4 + 255) & ~(size_t)255;
+  // stage 0 tasks: router tiles (16 experts x 512 K), then publishers (8 of the 128-K
+  // chunks each); the row routers (one a row) follow them
+  static constexpr int NKS = H / 512, NRT = MOE_NEXP / 16, NROUTER = NRT * NKS;
+  static constexpr int NPUB = NKC / 8, NTASK0 = NROUTER + NPUB;
+  static_assert(H % 1024 == 0 && NKC % 8 == 0, "hidden must be whole 1024-blocks");
+  // two parities of hand-offs (complemented words): the B image [NKC][2][64] x 16 B,
+  // its scales [NKC][16] f32, the partial logits [NKS][16 rows][256] f32, then the
+  // routes [NREP][16 rows][8 ids, 8 weights] in NREP copies 4 KB apart (CTA b reads
+  // copy b mod NREP: no line is polled by the whole grid)
+  static constexpr int NREP = 8;
+  static constexpr size_t REP_STRIDE = 4096;
+  static constexpr size_t SZ_XQ = (size_t)NKC * 2 * 64 * 16;
+  static constexpr size_t SZ_XS = (size_t)NKC * 16 * 4;
+  static constexpr size_t SZ_RP = (size_t)NKS * MOE_MAXR * MOE_NEXP * 4;
+  static constexpr size_t SZ_RT = NREP * REP_STRIDE;
+  static_assert(MOE_MAXR * 16 * 4 <= REP_STRIDE, "a route copy fits its stride");
+  static constexpr size_t OFF_XS = SZ_XQ, OFF_RP = OFF_XS + SZ_XS, OFF_RT = OFF_RP + SZ_RP;
+  static constexpr size_t SZ_HPAR = (OFF_RT + SZ_RT + 255) & ~(size_t)255;
+  static constexpr size_t OFF_H = (OFF_QUEUE + NQUEUE * 4 + 255) & ~(size_t)255;
+  static constexpr size_t BYTES = OFF_H + 2 * SZ_HPAR;
 };
 
 struct MoeFp8Params {
@@ -96,6 +119,8 @@ __device__ inline void bf16x8(v4i v, float* f) {
   }
 }
 
+typedef __bf16 v8bfm __attribute__((ext_vector_type(8)));
+
 __device__ inline v8i cat8(v4i a, v4i b) {
   return v8i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
@@ -121,12 +146,10 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   __shared__ float xs_lds[QW * KCW][16];  // activation block scale per (chunk, row)
   __shared__ v4f red[G::WAVES][64];
   __shared__ float red_small[2][2][16];
-  __shared__ v4i wr_lds[H / 8];  // this CTA's router row (bf16), staged like the norm weight
   __shared__ int next_s;
   __shared__ float rstd_s[MOE_MAXR];
   __shared__ int ok_s;
 
-  uint64_t* logit_pairs = reinterpret_cast<uint64_t*>(p.scratch + G::OFF_LOGIT);
   uint64_t* mid_pairs = reinterpret_cast<uint64_t*>(p.scratch + G::OFF_MID);
   uint8_t* mq = p.scratch + G::OFF_MQ;
   float* mcoef = reinterpret_cast<float*>(p.scratch + G::OFF_MCOEF);
@@ -147,22 +170,48 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
 #pragma unroll
     for (int q = 0; q < NQ0; ++q) av0[q] = ld16<CP_NONE>(rar, base + q * 1024);
   }
-  const __amdgpu_buffer_rsrc_t rg = rsrc(p.g_post, H * 2);
-  // the post-attention norm weight, the same for every row, into LDS (over the
-  // reduction buffer, idle until stage 2), ahead of the guard read so both overlap
+  // the post-attention norm weight, the same for every row, goes to LDS (over the
+  // reduction buffer, idle until stage 2); every load of the prologue is issued before
+  // the first is waited on, none under a branch (absent ones read through an empty
+  // range), so the one barrier below waits for a single round trip
   v4i* g_lds = reinterpret_cast<v4i*>(&red[0][0]);
   static_assert(H * 2 <= (int)sizeof(red), "norm weight staging");
-  for (int i = tid; i < H / 8; i += G::THREADS) g_lds[i] = ld16<CP_NONE>(rg, i * 16);
-  {
-    const bool has = b < MOE_NEXP;
-    const __amdgpu_buffer_rsrc_t rw0 =
-        rsrc(p.w_r + (size_t)(has ? b : 0) * H, has ? H * 2 : 0);
-    for (int i = tid; i < H / 8; i += G::THREADS) wr_lds[i] = ld16<CP_NT>(rw0, i * 16);
-  }
-  if (tid == 0) {
-    const v4i h = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
+  static_assert(H / 8 <= G::THREADS, "one norm-weight piece a thread");
+  const v4i gv = ld16<CP_NONE>(rsrc(p.g_post, H * 2), tid < H / 8 ? (uint32_t)tid * 16u : 0x80000000u);
+  // this CTA's stage-0 task (the first of them: a grid below NTASK0 loops, unprefetched):
+  // router tile
+  // tile (et, ks), wave w takes K [ks 512 + 32 w, + 32); lane l the A operand of expert
+  // 16 et + l % 16 at K + 8 (l / 16) and the B operand of row l % 16 there
+  auto router_loads = [&](int task, v4i& wa, v4i& xa) {
+    const bool on = task < G::NROUTER;
+    const int et = on ? task / G::NKS : 0, ks = on ? task % G::NKS : 0;
+    const int k = ks * 512 + 32 * w + 8 * grp;
+    wa = ld16<CP_NT>(rsrc(p.w_r, on ? MOE_NEXP * H * 2 : 0u),
+                     (uint32_t)((et * 16 + t) * H + k) * 2u);
+    xa = ld16<CP_NONE>(rsrc(p.a, on ? (uint32_t)R * H * 2 : 0u),
+                       t < R ? (uint32_t)(t * H + k) * 2u : 0x80000000u);
+  };
+  // publisher pt: thread tid the 8 values at 128 kc + 8 m of rows r and r + 8, with
+  // kc = 8 pt + tid / 128, r = (tid / 16) % 8, m = tid % 16
+  auto pub_loads = [&](int task, v4i (&pa)[2]) {
+    const int pt = task - G::NROUTER;
+    const bool on = task >= G::NROUTER && task < G::NTASK0;
+    const int kc = (on ? pt : 0) * 8 + (tid >> 7), r = (tid >> 4) & 7, m = tid & 15;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)h[i];
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = r + 8 * hh;
+      pa[hh] = ld16<CP_NONE>(rsrc(p.a, on ? (uint32_t)R * H * 2 : 0u),
+                             row < R ? (uint32_t)(row * H + kc * 128 + 8 * m) * 2u : 0x80000000u);
+    }
+  };
+  v4i wa0, xa0, pa0[2];
+  router_loads(b, wa0, xa0);
+  pub_loads(b, pa0);
+  const v4i hd = ld16<CP_DEV>(rsrc(p.guard, 16), tid == 0 ? 0u : 0x80000000u);
+  if (tid < H / 8) g_lds[tid] = gv;
+  if (tid == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)hd[i];
   }
   for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
   if (tid == 0) ok_s = 1;
@@ -171,93 +220,38 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   Guard guard;
   guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
   bool ok = true;
-
+  uint8_t* hcur = p.scratch + G::OFF_H + (tag & 1u) * G::SZ_HPAR;
+  uint8_t* hnxt = p.scratch + G::OFF_H + ((tag + 1u) & 1u) * G::SZ_HPAR;
+  uint32_t* hxq = reinterpret_cast<uint32_t*>(hcur);
+  uint32_t* hxs = reinterpret_cast<uint32_t*>(hcur + G::OFF_XS);
+  uint32_t* hrp = reinterpret_cast<uint32_t*>(hcur + G::OFF_RP);
+  uint32_t* hrt = reinterpret_cast<uint32_t*>(hcur + G::OFF_RT);
 
   // ---------------------------------------------------------------- stage 0
-  // Each row is owned by WPR waves (2 for R <= 8, else 1), each holding NQ 512-value
-  // slices of it: lane l holds the 8 values at q * 512 + l * 8. One round trip brings the
-  // row; the norm weight and this CTA's router row wait in LDS. The E4M3 codes go to
-  // xq_lds in the MFMA B-operand image of stage 2 (chunk kc = q * 4 + l / 16; K group
-  // (l % 16) / 4; byte (l % 4) * 8).
+  // the rows' rstd: two waves a row, one round trip (a second pass for rows 8-15)
   {
-    // the row values of pass `row0` (issued at the top of the kernel for the first)
-    auto rows_pass = [&](auto nq_tag, int row0, v4i* av) {
-      constexpr int NQ = decltype(nq_tag)::value;
-      constexpr int WPR = H / 512 / NQ;
-      const int r = row0 + w / WPR, ch = w % WPR;
-      const bool live = r < R;
+    auto ss_pass = [&](int row0, v4i* av) {
+      const int r = row0 + w / 2, ch = w % 2;
       float ss = 0.f;
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
+      for (int q = 0; q < NQ0; ++q) {
         float f[8];
         bf16x8(av[q], f);
 #pragma unroll
         for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
       }
       ss = wave_sum(ss);
-      if (l == 0 && r < 16) red_small[0][ch][r] = ss;
+      if (l == 0) red_small[0][ch][r] = ss;
       __syncthreads();
-      float tot = 0.f;
-      if (r < 16) {
-#pragma unroll
-        for (int c = 0; c < WPR; ++c) tot += red_small[0][c][r];
+      if (tid < 8) {
+        const int rr = row0 + tid;
+        const float tot = red_small[0][0][rr] + red_small[0][1][rr];
+        rstd_s[rr] = rr < R ? 1.0f / sqrtf(tot / (float)H + p.eps) : 0.f;
       }
-      const float rstd = live ? 1.0f / sqrtf(tot / (float)H + p.eps) : 0.f;
-      // widen the packed row again below rather than keep the 8 NQ f32 values of the
-      // sum of squares alive across the barrier
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(av[q]));
-      float rp = 0.f;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const int sl = ch * NQ + q;
-        float fa[8], fg[8], xn[8];
-        bf16x8(av[q], fa);
-        bf16x8(g_lds[sl * 64 + l], fg);
-        const v4i wv = wr_lds[sl * 64 + l];
-        float am = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          xn[i] = fa[i] * rstd * fg[i];
-          am = fmaxf(am, fabsf(xn[i]));
-        }
-        // router: the normalised row rounded to bf16 pairs, dotted with the bf16 weights
-#pragma unroll
-        for (int d = 0; d < 4; ++d) rp = dot2_bf16(xn[2 * d], xn[2 * d + 1], (uint32_t)wv[d], rp);
-        am = row16_max(am);
-        const bool nz = am > 0.f;
-        const float inv = nz ? FP8_MAX / am : 1.f;
-        const int kc = sl * 4 + (l >> 4);
-        if (live) {
-          v2i qq;
-          qq[0] = (int)pack_fp8x4(clamp_fp8(xn[0] * inv), clamp_fp8(xn[1] * inv),
-                                  clamp_fp8(xn[2] * inv), clamp_fp8(xn[3] * inv));
-          qq[1] = (int)pack_fp8x4(clamp_fp8(xn[4] * inv), clamp_fp8(xn[5] * inv),
-                                  clamp_fp8(xn[6] * inv), clamp_fp8(xn[7] * inv));
-          const int g4 = (l & 15) >> 2, h = (l & 3) >> 1;
-          char* dst = reinterpret_cast<char*>(xq_lds) +
-                      ((kc * 2 + h) * 64 + r + 16 * g4) * 16 + (l & 1) * 8;
-          *reinterpret_cast<v2i*>(dst) = qq;
-          if ((l & 15) == 0) xs_lds[kc][r] = nz ? am * INV_FP8_MAX : 1.f;
-        }
-        // one slice per scheduling region: the LDS operands are not hoisted ahead
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      rp = wave_sum(rp);
-      if (l == 0 && r < 16) red_small[1][ch][r] = rp;
       __syncthreads();
-      if (ch == 0 && l == 0 && live && b < MOE_NEXP) {
-        float lg = 0.f;
-#pragma unroll
-        for (int c = 0; c < WPR; ++c) lg += red_small[1][c][r];
-        st_dev64(&logit_pairs[r * MOE_NEXP + b], pair(__float_as_uint(lg), tag));
-      }
     };
-    static_assert(H % 1024 == 0, "hidden must split into two halves of 512-slices");
-    // two waves a row, eight rows a pass (the second pass only when R > 8)
-    rows_pass(std::integral_constant<int, NQ0>(), 0, av0);
+    ss_pass(0, av0);
     if (R > 8) {
-      __syncthreads();
       const int r = 8 + w / 2, ch = w % 2;
       const bool live = r < R;
       const __amdgpu_buffer_rsrc_t rar =
@@ -266,87 +260,235 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       v4i av1[NQ0];
 #pragma unroll
       for (int q = 0; q < NQ0; ++q) av1[q] = ld16<CP_NONE>(rar, base + q * 1024);
-      rows_pass(std::integral_constant<int, NQ0>(), 8, av1);
+      ss_pass(8, av1);
+    } else if (tid >= 8 && tid < 16) {
+      rstd_s[tid] = 0.f;
     }
-    const int ch = w / 8, wr = w % 8;
-    constexpr int NQ = H / 1024;
-    // rows past R: zero B operands, unit scales (stage 2 reads all 16 columns)
-    for (int i = tid; i < G::NKC * 16; i += G::THREADS) {
-      const int kc = i / 16, r = i % 16;
-      if (r >= R) {
-        xs_lds[kc][r] = 1.f;
+  }
+  // the task(s): router tiles publish partial logits, publishers the B image and scales
+  for (int task = b; task < G::NTASK0; task += nblk) {
+    v4i wa = wa0, xa = xa0, pa[2] = {pa0[0], pa0[1]};
+    if (task != b) {
+      router_loads(task, wa, xa);
+      pub_loads(task, pa);
+      // a previous router tile's reduction overwrote the norm weight (red overlays it)
+      __syncthreads();
+      if (tid < H / 8) g_lds[tid] = ld16<CP_NONE>(rsrc(p.g_post, H * 2), (uint32_t)tid * 16u);
+    }
+    __syncthreads();
+    if (task < G::NROUTER) {
+      const int et = task / G::NKS, ks = task % G::NKS;
+      const int k = ks * 512 + 32 * w + 8 * grp;
+      // B: bf16(a rstd g) of row t at K k .. k + 7 (rows past R: zeros)
+      const float rs = rstd_s[t];
+      float fa[8], fg[8];
+      bf16x8(xa, fa);
+      bf16x8(g_lds[k / 8], fg);
+      v4i xb;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+      for (int d = 0; d < 4; ++d)
+        xb[d] = (int)(bf16_bits(fa[2 * d] * rs * fg[2 * d]) |
+                      (bf16_bits(fa[2 * d + 1] * rs * fg[2 * d + 1]) << 16));
+      const v4f z = {0.f, 0.f, 0.f, 0.f};
+      const v4f dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(v8bfm, wa), __builtin_bit_cast(v8bfm, xb), z, 0, 0, 0);
+      __syncthreads();  // every wave read g_lds: red (which it overlays) is free
+      red[w][l] = dd;
+      __syncthreads();
+      if (tid < 256) {
+        const int i = tid & 15, r = tid >> 4;
+        const int L = r + 16 * (i >> 2), v = i & 3;
+        float sum = 0.f;
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) xq_lds[(kc * 2 + h) * 64 + r + 16 * g4] = v4i{0, 0, 0, 0};
+        for (int ww = 0; ww < G::WAVES; ++ww) sum += red[ww][L][v];
+        if (r < R) st_dev(&hrp[(ks * MOE_MAXR + r) * MOE_NEXP + et * 16 + i], enc_word(__float_as_uint(sum)));
       }
-    }
-    // a grid smaller than the expert count: this CTA's further router experts
-    for (int e = b + nblk; e < MOE_NEXP; e += nblk) {
-      for (int pass = 0; pass * 8 < R; ++pass) {
-        const int r = pass * 8 + wr;
-        const bool live = r < R;
-        const __amdgpu_buffer_rsrc_t rar =
-            rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
-        const __amdgpu_buffer_rsrc_t rwr = rsrc(p.w_r + (size_t)e * H, live ? H * 2 : 0);
-        const uint32_t base = (uint32_t)(ch * NQ * 512 + l * 8) * 2;
-        __syncthreads();
-        float ss = 0.f, rp = 0.f;
-        for (int q = 0; q < NQ; ++q) {
-          float f[8];
-          bf16x8(ld16<CP_NONE>(rar, base + q * 1024), f);
-          for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+    } else {
+      const int pt = task - G::NROUTER;
+      const int kc = pt * 8 + (tid >> 7), r = (tid >> 4) & 7, m = tid & 15;
+      const int g4 = m >> 2, hf = (m & 3) >> 1;
+      float fg[8];
+      bf16x8(g_lds[kc * 16 + m], fg);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int row = r + 8 * hh;
+        const float rs = rstd_s[row];
+        float fa[8], xn[8];
+        bf16x8(pa[hh], fa);
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          xn[i] = fa[i] * rs * fg[i];
+          am = fmaxf(am, fabsf(xn[i]));
         }
-        ss = wave_sum(ss);
-        if (l == 0) red_small[0][ch][wr] = ss;
-        __syncthreads();
-        const float rstd = live ? 1.0f / sqrtf((red_small[0][0][wr] + red_small[0][1][wr]) /
-                                               (float)H + p.eps)
-                                : 0.f;
-        for (int q = 0; q < NQ; ++q) {
-          float fa[8], fg[8], fw[8];
-          bf16x8(ld16<CP_NONE>(rar, base + q * 1024), fa);
-          bf16x8(g_lds[ch * NQ * 64 + q * 64 + l], fg);
-          bf16x8(ld16<CP_NT>(rwr, base + q * 1024), fw);
-          for (int i = 0; i < 8; ++i) rp += bf16_round(fa[i] * rstd * fg[i]) * fw[i];
-        }
-        rp = wave_sum(rp);
-        if (l == 0) red_small[1][ch][wr] = rp;
-        __syncthreads();
-        if (ch == 0 && l == 0 && live)
-          st_dev64(&logit_pairs[r * MOE_NEXP + e],
-                   pair(__float_as_uint(red_small[1][0][wr] + red_small[1][1][wr]), tag));
+        am = row16_max(am);
+        const bool nz = am > 0.f;
+        const float inv = nz ? FP8_MAX / am : 1.f;
+        const uint32_t q0 = pack_fp8x4(clamp_fp8(xn[0] * inv), clamp_fp8(xn[1] * inv),
+                                       clamp_fp8(xn[2] * inv), clamp_fp8(xn[3] * inv));
+        const uint32_t q1 = pack_fp8x4(clamp_fp8(xn[4] * inv), clamp_fp8(xn[5] * inv),
+                                       clamp_fp8(xn[6] * inv), clamp_fp8(xn[7] * inv));
+        // rows past R read zeros: zero codes, unit scale
+        const size_t at = ((size_t)(kc * 2 + hf) * 64 + row + 16 * g4) * 4 + (m & 1) * 2;
+        st_dev64(reinterpret_cast<uint64_t*>(hxq + at),
+                 (uint64_t)enc_word(q0) | ((uint64_t)enc_word(q1) << 32));
+        if (m == 0) st_dev(&hxs[kc * 16 + row], enc_word(__float_as_uint(nz ? am * INV_FP8_MAX : 1.f)));
       }
     }
   }
-  __syncthreads();
+  __syncthreads();  // g_lds (under red) is read by every task above
+  // clear this CTA's slice of the next launch's hand-off buffers (from the last wave:
+  // wave 0's polls below do not queue behind these stores)
+  {
+    constexpr uint32_t PB = (uint32_t)G::SZ_HPAR;
+    const uint32_t slice = (PB / 16 + nblk - 1) / nblk * 16;
+    const __amdgpu_buffer_rsrc_t rn = rsrc(hnxt, PB);
+    const int ct = G::THREADS - 1 - tid;
+    for (uint32_t i = (uint32_t)ct * 16u; i < slice; i += (uint32_t)G::THREADS * 16u)
+      st16<CP_DEV>(rn, b * slice + i, v4i{0, 0, 0, 0});
+  }
 
   // ---------------------------------------------------------------- stage 1
   stamp(p.timeline, MONO_TL_STAGED);
-  // one wave a row: poll the row's 256 logits, sigmoid, top-8
-  if (w < R) {
-    const int row = w;
-    uint64_t pr[4];
+  // The B image (buffer -> LDS, 1 KiB a wave instruction). Waves 1-15 first wait for
+  // the scale words of the chunks they copy (sc1 polls of 2 words a lane), then copy
+  // through L2: one CU of an XCD fetches a line, the others hit it. A line fetched
+  // before all of its words were written holds zeros, which the check below finds;
+  // the re-copy then reads device-coherent (sc1) data.
+  static_assert(G::SZ_XQ / 1024 == 2 * G::NKC, "two 1 KiB chunks a 128-K chunk");
+  const __amdgpu_buffer_rsrc_t rxq = rsrc(hxq, (uint32_t)G::SZ_XQ);
+  auto copy_image = [&](int w0, int nw, bool coherent) {
+    for (int c = w - w0; c < (int)(G::SZ_XQ / 1024); c += nw) {
+      auto* dst = (__attribute__((address_space(3))) void*)(reinterpret_cast<uint8_t*>(xq_lds) + c * 1024);
+      if (coherent)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rxq, dst, 16, (uint32_t)(c * 1024 + l * 16), 0, 0, CP_DEV);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rxq, dst, 16, (uint32_t)(c * 1024 + l * 16), 0, 0, CP_NONE);
+    }
+  };
+  if (w >= 1) {
+    constexpr int NCW = (int)(G::SZ_XQ / 1024) / (G::WAVES - 1) + 1;  // chunks a wave, at most
+    const __amdgpu_buffer_rsrc_t rxs = rsrc(hxs, (uint32_t)G::SZ_XS);
+    static_assert(NCW * 16 <= 2 * WAVE, "a wave's scale words fit two loads a lane");
+    // lane l: the scale word of chunk (w - 1) + 15 (l / 16 + 4 h), row l % 16
+    uint32_t sv[2];
     ok = wait_until(guard, MONO_SITE_LOGITS, [&]() {
-      bool all = true;
+      uint32_t v[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pr[i] = ld_dev64(&logit_pairs[row * MOE_NEXP + l + 64 * i]);
-        all &= (uint32_t)(pr[i] >> 32) == tag;
+      for (int h = 0; h < 2; ++h) {
+        const int c = (w - 1) + (G::WAVES - 1) * ((l >> 4) + 4 * h);
+        v[h] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+            rxs, c < 2 * G::NKC ? (uint32_t)(((c >> 1) * 16 + (l & 15)) * 4) : 0x80000000u, 0,
+            CP_DEV);
       }
-      return __all(all);
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t missing = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = (w - 1) + (G::WAVES - 1) * ((l >> 4) + 4 * h);
+        missing |= (uint32_t)(c < 2 * G::NKC) & (uint32_t)(v[h] == 0u);
+        sv[h] = v[h];
+      }
+      return !__any(missing);
     });
-    if (ok) {
-      float sc[4], bs[4];
+    copy_image(1, G::WAVES - 1, false);
+    // the scales polled above are final: both chunks of a 128-K chunk hold the same
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lg = __uint_as_float((uint32_t)pr[i]);
-        sc[i] = 1.0f / (1.0f + expf(-lg));
-        bs[i] = p.bias[l + 64 * i];
+    for (int h = 0; h < 2; ++h) {
+      const int c = (w - 1) + (G::WAVES - 1) * ((l >> 4) + 4 * h);
+      if (ok && c < 2 * G::NKC) xs_lds[c >> 1][l & 15] = __uint_as_float(~sv[h]);
+    }
+  }
+  // Row r is routed once, by wave 0 of CTA (NTASK0 + r) mod grid: its 256 logits (the
+  // 14 partials summed in a fixed order; a poll that finds an unwritten word is
+  // discarded whole), sigmoid, bias top-8; the 8 ids and weights go out as
+  // complemented words. Wave 0 of every CTA (which has no image copy queued ahead of
+  // its polls) then reads the R routes (4 words a lane) into its slot tables.
+  if (w == 0) {
+    const __amdgpu_buffer_rsrc_t rrp = rsrc(hrp, (uint32_t)G::SZ_RP);
+    for (int row = 0; row < R && ok; ++row) {
+      if ((G::NTASK0 + row) % nblk != b) continue;
+      float lg[4];
+      ok = wait_until(guard, MONO_SITE_LOGITS, [&]() {
+        // every load issued before the first is used: one round trip a poll
+        uint32_t v[G::NKS][4];
+#pragma unroll
+        for (int ks = 0; ks < G::NKS; ++ks)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            // lane offset in a VGPR, the rest a scalar offset: no per-load address
+            v[ks][i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                rrp, (uint32_t)l * 4u, (uint32_t)((ks * MOE_MAXR + row) * MOE_NEXP + 64 * i) * 4u,
+                CP_DEV);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t mn = 0xFFFFFFFFu;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lg[i] = __uint_as_float(~v[0][i]);
+#pragma unroll
+        for (int ks = 0; ks < G::NKS; ++ks)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            mn = min(mn, v[ks][i]);
+            if (ks) lg[i] += __uint_as_float(~v[ks][i]);
+          }
+        return __all(mn != 0u);
+      });
+      if (ok) {
+        float sc[4], bs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[i] = 1.0f / (1.0f + expf(-lg[i]));
+          bs[i] = p.bias[l + 64 * i];
+        }
+        route_row(rl, row, sc, bs, p.route_scale, p.scores, p.ids, p.weights);
+        // lanes l < 8 wrote slots 1 + l (LDS accesses of one wave complete in order)
+        __builtin_amdgcn_wave_barrier();
+        const int j = l & (MOE_TOPK - 1), c = l >> 3;
+        const uint32_t id = enc_word((uint32_t)rl.id[row][1 + j]);
+        const uint32_t wt = enc_word(__float_as_uint(rl.w[row][1 + j]));
+        static_assert(G::NREP * MOE_TOPK == WAVE, "a lane a (copy, slot)");
+        uint32_t* dst = hrt + c * (G::REP_STRIDE / 4) + row * 16;
+        st_dev(dst + j, id);
+        st_dev(dst + MOE_TOPK + j, wt);
       }
-      const bool out0 = b == 0;
-      route_row(rl, row, sc, bs, p.route_scale, out0 ? p.scores : nullptr,
-                out0 ? p.ids : nullptr, out0 ? p.weights : nullptr);
+    }
+    if (ok) {
+      const __amdgpu_buffer_rsrc_t rrt =
+          rsrc(hrt + (b % G::NREP) * (G::REP_STRIDE / 4), (uint32_t)G::REP_STRIDE);
+      uint32_t rv[4];
+      // 256 CTAs poll here for the slowest row's route: a longer sleep between polls
+      ok = wait_until<8>(guard, MONO_SITE_LOGITS, [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          rv[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rrt, (uint32_t)(l + 64 * i) * 4u,
+                                                                 0, CP_DEV);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t missing = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          missing |= (uint32_t)(((l + 64 * i) >> 4) < R) & (uint32_t)(rv[i] == 0u);
+        return !__any(missing);
+      });
+      if (ok) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int idx = l + 64 * i, tt = idx >> 4, j = idx & 15;
+          const uint32_t u = ~rv[i];
+          if (tt < R) {
+            if (j < MOE_TOPK) {
+              const int e = (int)min(u, (uint32_t)(MOE_NEXP - 1));
+              rl.id[tt][1 + j] = e;
+              atomicOr(&rl.mask[e], 1u << tt);
+            } else {
+              rl.w[tt][1 + j - MOE_TOPK] = __uint_as_float(u);
+            }
+          }
+        }
+        if (l < R) {
+          rl.id[l][0] = MOE_SHARED;
+          rl.w[l][0] = 1.f;
+        }
+      }
     }
   }
   if (!ok) ok_s = 0;
@@ -362,7 +504,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   // K slice is chunks [KCW wq, KCW (wq + 1)). Its ring holds one task's KCW chunks:
   // a slot is refilled with the next task's chunk as soon as its MFMA issued.
   {
-    const int ntask = ok ? nd * NUG : 0;
+    int ntask = ok ? nd * NUG : 0;
     v4i ring[KCW][2];
     // this lane's row and K group; the second 16 bytes of a lane's 32 sit 16 bytes on
     // (row major) or a 16-row half-tile on (shuffled); a 128-K chunk is CS bytes on
@@ -385,6 +527,12 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
     // refilled with the next task while this one runs. Tasks run the same arithmetic on
     // whichever CTA takes them, so results do not depend on the hand-out.
     int task = b;
+    // the counter grab goes ahead of the ring so its reply does not queue behind it:
+    // lane 0 of wave 0 only, the others out of range (a branch around it would make its
+    // reply wait before the ring issues)
+    const bool live0 = task < ntask;
+    const uint32_t grab = (uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
+        1, rsrc(queue, live0 ? 4u : 0u), tid == 0 ? 0u : 0x80000000u, 0, 0);
     {
       uint32_t so;
       const __amdgpu_buffer_rsrc_t r = task_src(task, so);
@@ -394,8 +542,53 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         ring[j][1] = ld16s<CP_NT>(r, vo + HO, so + j * CS);
       }
     }
-    if (tid == 0) next_s = task < ntask ? nblk + (int)add_dev(&queue[0], 1u) : ntask;
+    if (tid == 0) next_s = live0 ? nblk + (int)grab : ntask;
+    // The image, checked while the first task's weights are in flight: every word
+    // written (a line fetched early may hold zeros: copy it again, device-coherent). One
+    // pass checks and un-complements: a failed check re-copies all.
+    {
+      uint32_t* xw = reinterpret_cast<uint32_t*>(xq_lds);
+      bool got = ok_s != 0;  // set before the barrier above
+      int polls = 0;
+      uint64_t start = 0;
+      while (got) {
+        // the first pass waits for the image copy only (the 2 KCW ring loads issued after
+        // it stay in flight); a re-copy was issued after them
+        if (polls == 0)
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * KCW));
+        else
+          drain();
+        asm volatile("" ::: "memory");
+        __syncthreads();
+        int zero = 0;
+        static_assert(G::SZ_XQ / 4 % G::THREADS == 0, "whole passes over the image");
+#pragma unroll 7
+        for (int i = tid; i < (int)(G::SZ_XQ / 4); i += G::THREADS) {
+          const uint32_t v = xw[i];
+          zero |= v == 0u;
+          xw[i] = ~v;
+        }
+        if (!__syncthreads_or(zero)) break;
+        // bounded like every wait: the guard's deadline and abort flag
+        if ((++polls & 15) == 0) {
+          if (guard.aborted()) got = false;
+          const uint64_t now = wall_clock64();
+          if (start == 0) start = now;
+          if (got && now - start > guard.deadline * (guard.fault_site ? guard.slack : 1)) {
+            if (tid == 0) guard.fail(MONO_SITE_LOGITS);
+            got = false;
+          }
+        }
+        got = __syncthreads_or(got ? 0 : 1) == 0 && got;
+        if (got) copy_image(0, G::WAVES, true);
+      }
+      if (!got) ok_s = 0;
+    }
     __syncthreads();
+    if (ok_s == 0) {
+      ok = false;
+      ntask = 0;
+    }
     int next = next_s;
     while (task < ntask) {
       const int u = task / NUG, cc = task % NUG;

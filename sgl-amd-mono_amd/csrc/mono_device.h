@@ -95,6 +95,10 @@ __device__ inline void drain() { __builtin_amdgcn_s_waitcnt(0); }
 // 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// a complemented hand-off word: never zero once written (an all-ones word, a NaN in any
+// of the float formats carried, is stored as another NaN), so zero means "not written"
+__device__ inline uint32_t enc_word(uint32_t u) { return ~(u == 0xFFFFFFFFu ? 0xFFFFFFFEu : u); }
+
 // (value, tag) pair: one 8-byte store publishes a 32-bit word with its launch tag
 __device__ inline uint64_t pair(uint32_t v, uint32_t tag) {
   return (uint64_t)v | ((uint64_t)tag << 32);
@@ -305,10 +309,11 @@ __device__ inline bool cta_all(bool mine, int& ok_s) {
   return ok_s != 0;
 }
 
-// Poll `ready()` (wave-uniform result expected) until true. Every 64 polls: check the
-// abort flag and the deadline. Returns false if the launch is failing; the caller then
-// skips its remaining work so every wave still reaches the end of the kernel.
-template <class F>
+// Poll `ready()` (wave-uniform result expected) until true, sleeping SLEEP x 64 clocks
+// between polls. Every 64 polls: check the abort flag and the deadline. Returns false if
+// the launch is failing; the caller then skips its remaining work so every wave still
+// reaches the end of the kernel.
+template <int SLEEP = 1, class F>
 __device__ inline bool wait_until(Guard& g, int site, F ready) {
   const bool stalled = (site == g.fault_site);
   uint32_t polls = 0;
@@ -324,7 +329,7 @@ __device__ inline bool wait_until(Guard& g, int site, F ready) {
         return false;
       }
     }
-    __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_s_sleep(SLEEP);
   }
 }
 

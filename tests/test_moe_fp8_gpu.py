@@ -107,6 +107,21 @@ def test_moe_fp8_is_deterministic_and_writes_only_its_rows(layer, gpu):
     assert torch.all(full[8:] == 7.0), "wrote past its rows"
 
 
+def test_moe_fp8_back_to_back_launches_match_fresh_runtimes(layer, gpu):
+    """Launches on one runtime alternate between two scratch hand-off buffers, each
+    cleared by the launch before: with new inputs and row counts every launch, each
+    result equals that of a runtime that never launched (nothing stale is read)."""
+    print("case back-to-back rows=8,3,8,16,5", flush=True)
+    op = MoeFp8Op(layer, gpu, max_rows=16)
+    for i, rows in enumerate((8, 3, 8, 16, 5)):
+        a = synthetic.rows_bf16(rows, H, gpu, seed=300 + i)
+        got = op.launch(a).clone()
+        want = MoeFp8Op(layer, gpu, max_rows=16).launch(a)
+        torch.cuda.synchronize()
+        op.rt.check()
+        assert torch.equal(got, want), f"launch {i} rows={rows}"
+
+
 def test_moe_fp8_graph_replay_matches_eager(layer, gpu):
     print("case graph replay rows=4", flush=True)
     op = MoeFp8Op(layer, gpu, max_rows=16)
