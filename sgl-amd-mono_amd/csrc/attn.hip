@@ -266,19 +266,24 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   stamp(p.timeline, MONO_TL_ROUTED);
   {
     // LDS: K rows (E4M3, 576 + 16 bytes apart), q (bf16, 1152 + 16), S (f32), P (bf16),
-    // the split's slots and token scales
+    // the split's slots and token scales, the row's page-table entries
     constexpr int KSTR = AT_KV + 16, QSTR = AT_KV * 2 + 16, SSTR = AT_SPLIT + 4,
                   PSTR = AT_SPLIT * 2 + 16;
+    constexpr int NPG = AT_MAXCTX / AT_PAGE;
     uint8_t* kbuf = smem;
     uint8_t* qbuf = kbuf + AT_SPLIT * KSTR;
     float* sbuf = reinterpret_cast<float*>(qbuf + AT_HEADS * QSTR);
     uint8_t* pbuf = reinterpret_cast<uint8_t*>(sbuf + AT_HEADS * SSTR);
     int32_t* slot_s = reinterpret_cast<int32_t*>(pbuf + AT_HEADS * PSTR);
     float* ksc = reinterpret_cast<float*>(slot_s + AT_SPLIT);
+    int32_t* pt_s = reinterpret_cast<int32_t*>(ksc + AT_SPLIT);
     static_assert(AT_SPLIT * KSTR + AT_HEADS * QSTR + AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
-                          AT_SPLIT * 8 <=
+                          AT_SPLIT * 8 + NPG * 4 <=
                       (int)sizeof(smem),
                   "split LDS");
+    static_assert(NPG <= AT_THREADS, "a page-table entry a thread");
+    constexpr int QP = AT_HEADS * AT_KV / 8;  // 16-byte pieces of a row's q
+    constexpr int NQP = (QP + AT_THREADS - 1) / AT_THREADS;
     const __amdgpu_buffer_rsrc_t rkv = rsrc(p.kv, p.kv_slots * (uint32_t)AT_KV);
     const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, p.kv_slots * 4u);
     const int nt = R * AT_NSPLIT;
@@ -291,7 +296,21 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       const int k = n < AT_TOPK ? n : AT_TOPK;
       const int kcnt = k - sp * AT_SPLIT < AT_SPLIT ? k - sp * AT_SPLIT : AT_SPLIT;
       if (kcnt <= 0) continue;
-      // the split's tokens, polled as (position, tag) pairs, -> cache slots
+      // ahead of the wait (neither depends on the selection): the row's q, all heads
+      // ([32][576] bf16), and its page-table entries
+      const __amdgpu_buffer_rsrc_t rq = rsrc(p.q + (size_t)r * AT_HEADS * AT_KV, AT_HEADS * AT_KV * 2);
+      v4i qv[NQP];
+#pragma unroll
+      for (int i = 0; i < NQP; ++i) {
+        const int pc = tid + AT_THREADS * i;
+        qv[i] = ld16<CP_NONE>(rq, pc < QP ? (uint32_t)pc * 16u : 0x80000000u);
+      }
+      const int npg = (n + AT_PAGE - 1) / AT_PAGE;
+      const int pgv = ld4<CP_NONE>(
+          rpt, tid < npg ? ((uint32_t)p.req_ids[r] * (uint32_t)p.pt_stride + (uint32_t)tid) * 4u
+                         : 0x80000000u);
+      // the split's tokens, polled as (position, tag) pairs
+      int pos = -1;
       if (tid < AT_SPLIT) {
         uint64_t v = 0;
         const uint64_t* src = topk + (size_t)r * AT_TOPK + sp * AT_SPLIT + tid;
@@ -299,43 +318,65 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
           v = tid < kcnt ? ld_dev64(src) : pair(0u, tag);
           return __all((uint32_t)(v >> 32) == tag);
         });
-        int slot = -1;
-        if (ok && tid < kcnt) {
-          const int pos = (int)(uint32_t)v;
-          slot = page_of(r, pos >> 6) * AT_PAGE + (pos & 63);
-        }
-        slot_s[tid] = slot;
-        ksc[tid] = slot >= 0 ? __int_as_float(ld4<CP_NONE>(rks, (uint32_t)slot * 4)) : 0.f;
+        if (ok && tid < kcnt) pos = (int)(uint32_t)v;
       }
+#pragma unroll
+      for (int i = 0; i < NQP; ++i) {
+        const int pc = tid + AT_THREADS * i;
+        if (pc < QP)
+          *reinterpret_cast<v4i*>(qbuf + (pc / (AT_KV / 8)) * QSTR + (pc % (AT_KV / 8)) * 16) = qv[i];
+      }
+      if (tid < NPG) pt_s[tid] = pgv;
       ok = cta_all(ok, ok_s);
       if (!ok) break;
-      // q of the row, all heads: [32][576] bf16
-      const __amdgpu_buffer_rsrc_t rq = rsrc(p.q + (size_t)r * AT_HEADS * AT_KV, AT_HEADS * AT_KV * 2);
-      for (int i = tid; i < AT_HEADS * AT_KV / 8; i += AT_THREADS) {
-        const int h = i / (AT_KV / 8), c = i % (AT_KV / 8);
-        *reinterpret_cast<v4i*>(qbuf + h * QSTR + c * 16) = ld16<CP_NONE>(rq, (uint32_t)i * 16);
-      }
+      // position -> cache slot through the page table in LDS
+      if (tid < AT_SPLIT) slot_s[tid] = pos >= 0 ? pt_s[pos >> 6] * AT_PAGE + (pos & 63) : -1;
       __syncthreads();
-      // gather the rows: 36 pieces of 16 bytes a row (a dead slot reads zeros)
-      for (int i = tid; i < AT_SPLIT * (AT_KV / 16); i += AT_THREADS) {
-        const int j = i / (AT_KV / 16), c = i % (AT_KV / 16);
-        const int slot = slot_s[j];
-        const uint32_t off = slot >= 0 ? (uint32_t)slot * AT_KV + c * 16 : 0x80000000u;
-        *reinterpret_cast<v4i*>(kbuf + j * KSTR + c * 16) = ld16<CP_NT>(rkv, off);
+      // gather the rows: 36 pieces of 16 bytes a row (a dead slot reads zeros), and the
+      // token scales, in one round trip
+      {
+        constexpr int GP = AT_SPLIT * (AT_KV / 16);
+        constexpr int NGP = (GP + AT_THREADS - 1) / AT_THREADS;
+        const int slot = tid < AT_SPLIT ? slot_s[tid] : -1;
+        const float sc = __int_as_float(
+            ld4<CP_NONE>(rks, slot >= 0 ? (uint32_t)slot * 4u : 0x80000000u));
+        // every load issued before the first is stored (a load-store loop would wait
+        // one round trip an iteration)
+        v4i gv[NGP];
+#pragma unroll
+        for (int i = 0; i < NGP; ++i) {
+          const int idx = tid + AT_THREADS * i;
+          const int j = idx / (AT_KV / 16), c = idx % (AT_KV / 16);
+          const int sj = idx < GP ? slot_s[j] : -1;
+          gv[i] = ld16<CP_NT>(rkv, sj >= 0 ? (uint32_t)sj * AT_KV + c * 16 : 0x80000000u);
+        }
+#pragma unroll
+        for (int i = 0; i < NGP; ++i) {
+          const int idx = tid + AT_THREADS * i;
+          const int j = idx / (AT_KV / 16), c = idx % (AT_KV / 16);
+          if (idx < GP) *reinterpret_cast<v4i*>(kbuf + j * KSTR + c * 16) = gv[i];
+        }
+        if (tid < AT_SPLIT) ksc[tid] = slot >= 0 ? sc : 0.f;
       }
       __syncthreads();
       // S = q K^T: wave w takes heads 16 (w / 8) .. and keys 16 (w % 8) ..
       {
         const int h0 = 16 * (w >> 3), j0 = 16 * (w & 7);
-        v4f d = {0.f, 0.f, 0.f, 0.f};
+        // two accumulators (even and odd K steps): two MFMA chains in flight
+        v4f d = {0.f, 0.f, 0.f, 0.f}, d1 = d;
         const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4);
         const uint8_t* kr = kbuf + (j0 + (l & 15)) * KSTR + 8 * (l >> 4);
-#pragma unroll 6
-        for (int ks = 0; ks < AT_KV / 32; ++ks) {
-          const v8bf a = *reinterpret_cast<const v8bf*>(qa + ks * 64);
-          const v2i kk = *reinterpret_cast<const v2i*>(kr + ks * 32);
-          d = mfma_bf16(a, fp8x8_bf16((uint32_t)kk[0], (uint32_t)kk[1]), d);
+        static_assert(AT_KV / 32 % 2 == 0, "K steps in pairs");
+#pragma unroll 3
+        for (int ks = 0; ks < AT_KV / 32; ks += 2) {
+          const v8bf a0 = *reinterpret_cast<const v8bf*>(qa + ks * 64);
+          const v2i k0 = *reinterpret_cast<const v2i*>(kr + ks * 32);
+          const v8bf a1 = *reinterpret_cast<const v8bf*>(qa + ks * 64 + 64);
+          const v2i k1 = *reinterpret_cast<const v2i*>(kr + ks * 32 + 32);
+          d = mfma_bf16(a0, fp8x8_bf16((uint32_t)k0[0], (uint32_t)k0[1]), d);
+          d1 = mfma_bf16(a1, fp8x8_bf16((uint32_t)k1[0], (uint32_t)k1[1]), d1);
         }
+        d += d1;
         const float f = ksc[j0 + (l & 15)] * p.sm_scale;
 #pragma unroll
         for (int e = 0; e < 4; ++e) sbuf[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e] * f;
@@ -434,15 +475,23 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         });
       ok = cta_all(ok, ok_s);
       if (!ok) break;
+      // the split partials and their (m, l) in one round trip
+      const int sp = tid >> 6, d8 = tid & 63;
+      v4i a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+      {
+        const __amdgpu_buffer_rsrc_t ra = rsrc(
+            accs + ((size_t)(r * AT_NSPLIT + (sp < nsp ? sp : 0)) * AT_HEADS + h) * AT_LAT,
+            sp < nsp ? AT_LAT * 4 : 0);
+        a0 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32);
+        a1 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32 + 16);
+      }
       if (w == 0) {
         const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
         const bool on = l < nsp;
-        const float m = on ? __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
-                                 ml + ((size_t)l * AT_HEADS + h) * 2)))
-                           : -INFINITY;
-        const float ls = on ? __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
-                                  ml + ((size_t)l * AT_HEADS + h) * 2 + 1)))
-                            : 0.f;
+        const v2i mlv = ld8<CP_DEV>(rsrc(ml, on ? AT_NSPLIT * AT_HEADS * 8 : 0),
+                                    (uint32_t)((l * AT_HEADS + h) * 8));
+        const float m = on ? __int_as_float(mlv[0]) : -INFINITY;
+        const float ls = on ? __int_as_float(mlv[1]) : 0.f;
         const float M = wave_max(m);
         const float ws = on ? expf(m - M) : 0.f;
         const float L = wave_sum(ws * ls);
@@ -451,19 +500,12 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       }
       __syncthreads();
       {
-        const int sp = tid >> 6, d8 = tid & 63;
-        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (sp < nsp) {
-          const __amdgpu_buffer_rsrc_t ra = rsrc(
-              accs + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS + h) * AT_LAT, AT_LAT * 4);
-          const v4i a0 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32);
-          const v4i a1 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32 + 16);
-          const float ws = wsp_s[sp];
+        float v[8];
+        const float ws = sp < nsp ? wsp_s[sp] : 0.f;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = __int_as_float(a0[e]) * ws;
-            v[4 + e] = __int_as_float(a1[e]) * ws;
-          }
+        for (int e = 0; e < 4; ++e) {
+          v[e] = __int_as_float(a0[e]) * ws;
+          v[4 + e] = __int_as_float(a1[e]) * ws;
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) red[sp * AT_LAT + 8 * d8 + e] = v[e];

@@ -124,6 +124,109 @@ __device__ inline void block_minmax(uint32_t& mn, uint32_t& mx, uint32_t* red, i
     }
 }
 
+// The threshold and the selection from keys held in registers, NK a thread, thread
+// order then index order being position order (pos_of(j) gives the position of key[j]).
+// `cnt` keys lie in [lo, hi]; the first pass bins [plo0, hi] and, with `check0`, is
+// redone over [lo, hi] if that range holds fewer than TOPK keys. Histogram passes (4096
+// bins) keep the bin holding the TOPK-th key until it holds few keys (then they rank
+// themselves) or one key value (then its positions do). The threshold is an element
+// (key, position) of the order (key descending, position ascending); the selection,
+// every element up to it, goes to sel[0 .. TOPK) in ascending position order.
+template <int NK, class PosF>
+__device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_of, uint32_t lo,
+                                   uint32_t hi, int cnt, uint32_t plo0, bool check0,
+                                   uint32_t* hist, int* wsum, int& phase, int* res_s,
+                                   uint32_t* thr_s, int32_t* sel) {
+  uint32_t* ck = hist;                                  // candidates, after the passes
+  int32_t* cp = reinterpret_cast<int32_t*>(hist + CAND);
+  int kk = AT_TOPK, shift = 1;
+#pragma unroll 1
+  for (int pass = 0; shift > 0 && cnt > CAND; ++pass) {
+    const uint32_t plo = pass == 0 ? plo0 : lo;
+    const uint32_t span = hi - plo;
+    const int bits = span ? 32 - __clz((int)span) : 0;
+    shift = bits > 12 ? bits - 12 : 0;
+    select_pass<NK>(tid, key, plo, hi, shift, kk, hist, wsum, phase, res_s);
+    if (check0 && pass == 0 && res_s[3] < AT_TOPK) {  // the first range holds too few keys
+      shift = 1;
+      continue;
+    }
+    const uint32_t bin = (uint32_t)res_s[0];
+    kk -= res_s[1];
+    cnt = res_s[2];
+    const uint32_t nlo = plo + (bin << shift);
+    const uint64_t top = (uint64_t)nlo + ((1ull << shift) - 1ull);
+    hi = top < (uint64_t)hi ? (uint32_t)top : hi;
+    lo = nlo;
+  }
+  // the threshold element (Tkey, Tpos): the kk-th of the bin's keys in (key descending,
+  // position ascending) order
+  if (cnt <= CAND) {
+    // few candidates: gather them, and each finds its own rank among them (the barrier
+    // first: every wave has read the last pass's results before res_s[0] is reused)
+    __syncthreads();
+    if (tid == 0) res_s[0] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+      if (key[j] >= lo && key[j] <= hi) {
+        const int at = atomicAdd(&res_s[0], 1);
+        ck[at] = key[j];
+        cp[at] = pos_of(j);
+      }
+    __syncthreads();
+    if (tid < cnt) {
+      const uint32_t mk = ck[tid];
+      const int mp = cp[tid];
+      int rank = 0;
+      for (int m = 0; m < cnt; ++m) rank += (ck[m] > mk) | ((ck[m] == mk) & (cp[m] < mp));
+      if (rank == kk - 1) {
+        thr_s[0] = mk;
+        thr_s[1] = (uint32_t)mp;
+      }
+    }
+  } else {
+    // one key value shared by many positions: the kk-th of them in position order
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < NK; ++j) c += key[j] == lo;
+    int tot;
+    const int before = block_scan(c, wsum, phase, tot);
+    if (before < kk && kk <= before + c) {
+      int seen = before;
+      for (int j = 0; j < NK; ++j) {
+        const bool e = key[j] == lo;
+        seen += e;
+        if (e && seen == kk) {
+          thr_s[0] = lo;
+          thr_s[1] = (uint32_t)pos_of(j);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t tk = thr_s[0];
+  const int tp = (int)thr_s[1];
+  int np = 0;
+#pragma unroll
+  for (int j = 0; j < NK; ++j) np += (key[j] > tk) | ((key[j] == tk) & (pos_of(j) <= tp));
+  int tot;
+  const int o = block_scan(np, wsum, phase, tot);
+  // the picks at their ranks; a key not taken writes its lane's dummy slot past the
+  // selection (no store branches, and no two lanes of a wave on one address)
+  int pc = 0;
+  const int dummy = AT_TOPK + (tid & (WAVE - 1));
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    const int pj = pos_of(j);
+    const bool pick = (key[j] > tk) | ((key[j] == tk) & (pj <= tp));
+    const int at = o + pc;
+    sel[pick && at < AT_TOPK ? at : dummy] = pj;
+    pc += pick;
+  }
+  __syncthreads();
+}
+
 // The exact top-TOPK of one row's n scores (TOPK < n <= 32768), in LDS: returns the
 // selected positions in ascending order (sel[0 .. TOPK)). Ranked by the radix key of
 // the f32 score, larger first, ties to the lower position. `rs` covers the n scores
@@ -133,10 +236,7 @@ __device__ inline void block_minmax(uint32_t& mn, uint32_t& mx, uint32_t* red, i
 // Thread t keeps the keys of positions 32 t .. 32 t + 31 in registers (loaded through a
 // padded LDS image, 33 words a thread, so both the coalesced writes and the per-thread
 // reads are conflict-free). A sample (every 32nd position) narrows the key range to one
-// holding about 1.5 TOPK keys; histogram passes over the live range (4096 bins) keep the
-// bin holding the TOPK-th key until it holds few keys (then they rank themselves) or one
-// key value (then its positions do). The threshold is an element (key, position) of the
-// order (key descending, position ascending); the selection is every element up to it.
+// holding about 1.5 TOPK keys, where topk_refine's first pass starts.
 __device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n, uint8_t* arena,
                                        int* wsum, uint32_t* wsum_mm, int* res_s, uint32_t* thr_s,
                                        uint64_t* ts = nullptr) {
@@ -146,9 +246,7 @@ __device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n
   };
   mark(0);
   uint32_t* kl = reinterpret_cast<uint32_t*>(arena);  // [1024][33] image
-  uint32_t* hist = kl + AT_THREADS * 33;               // [4096]
-  uint32_t* ck = hist;                                 // candidates, after the passes
-  int32_t* cp = reinterpret_cast<int32_t*>(hist + CAND);
+  uint32_t* hist = kl + AT_THREADS * 33;               // [4096]; candidates after the passes
   int32_t* sel = reinterpret_cast<int32_t*>(hist + 2 * CAND);  // [TOPK + 64]
   static_assert(2 * CAND + AT_TOPK + WAVE <= 4096, "candidates and the selection fit the histogram");
   constexpr int NLD = AT_MAXCTX / 4 / AT_THREADS;
@@ -178,13 +276,11 @@ __device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n
   mark(1);
   block_minmax(kmin, kmax, wsum_mm, mphase);
   mark(2);
-  uint32_t lo = kmin, hi = kmax;
-  int kk = AT_TOPK, cnt = n, shift = 1;
   // Sample the range first: position 32 t is thread t's sample. The bin of the sample
   // ranked SR from the top bounds a range [cut, kmax] expected to hold about 1.5 TOPK
-  // keys. The first pass bins only that range; it counts the keys there, and if they
-  // are fewer than TOPK the pass is redone over the whole range.
+  // keys; if it holds fewer than TOPK the first pass is redone over the whole range.
   uint32_t cut = kmin;
+  bool sampled = false;
   {
     const int ns = (n + 31) / 32;
     const int sr = (3 * AT_TOPK * ns + 2 * n - 1) / (2 * n);
@@ -195,94 +291,12 @@ __device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n
       const uint32_t one[1] = {key[0]};
       select_pass<1>(tid, one, kmin, kmax, sh, sr, hist, wsum, phase, res_s);
       cut = kmin + ((uint32_t)res_s[0] << sh);
+      sampled = true;
     }
   }
   mark(3);
-#pragma unroll 1
-  for (int pass = 0; shift > 0 && cnt > CAND; ++pass) {
-    const uint32_t plo = pass == 0 ? cut : lo;
-    const uint32_t span = hi - plo;
-    const int bits = span ? 32 - __clz((int)span) : 0;
-    shift = bits > 12 ? bits - 12 : 0;
-    select_pass<32>(tid, key, plo, hi, shift, kk, hist, wsum, phase, res_s);
-    if (pass == 0 && res_s[3] < AT_TOPK) {  // the sampled range holds too few keys
-      shift = 1;
-      continue;
-    }
-    const uint32_t bin = (uint32_t)res_s[0];
-    kk -= res_s[1];
-    cnt = res_s[2];
-    const uint32_t nlo = plo + (bin << shift);
-    const uint64_t top = (uint64_t)nlo + ((1ull << shift) - 1ull);
-    hi = top < (uint64_t)hi ? (uint32_t)top : hi;
-    lo = nlo;
-  }
-  mark(4);
-  // the threshold element (Tkey, Tpos): the kk-th of the bin's keys in (key descending,
-  // position ascending) order
-  if (cnt <= CAND) {
-    // few candidates: gather them, and each finds its own rank among them
-    if (tid == 0) res_s[0] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 32; ++j)
-      if (key[j] >= lo && key[j] <= hi) {
-        const int at = atomicAdd(&res_s[0], 1);
-        ck[at] = key[j];
-        cp[at] = 32 * tid + j;
-      }
-    __syncthreads();
-    if (tid < cnt) {
-      const uint32_t mk = ck[tid];
-      const int mp = cp[tid];
-      int rank = 0;
-      for (int m = 0; m < cnt; ++m) rank += (ck[m] > mk) | ((ck[m] == mk) & (cp[m] < mp));
-      if (rank == kk - 1) {
-        thr_s[0] = mk;
-        thr_s[1] = (uint32_t)mp;
-      }
-    }
-  } else {
-    // one key value shared by many positions: the kk-th of them in position order
-    int c = 0;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) c += key[j] == lo;
-    int tot;
-    const int before = block_scan(c, wsum, phase, tot);
-    if (before < kk && kk <= before + c) {
-      int seen = before;
-      for (int j = 0; j < 32; ++j) {
-        const bool e = key[j] == lo;
-        seen += e;
-        if (e && seen == kk) {
-          thr_s[0] = lo;
-          thr_s[1] = (uint32_t)(32 * tid + j);
-        }
-      }
-    }
-  }
-  __syncthreads();
-  mark(5);
-  const uint32_t tk = thr_s[0];
-  const int tp = (int)thr_s[1];
-  int np = 0;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) np += (key[j] > tk) | ((key[j] == tk) & (32 * tid + j <= tp));
-  int tot;
-  const int o = block_scan(np, wsum, phase, tot);
-  // the picks at their ranks; a key not taken writes its lane's dummy slot past the
-  // selection (no store branches, and no two lanes of a wave on one address)
-  int pc = 0;
-  const int dummy = AT_TOPK + (tid & (WAVE - 1));
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const bool pick = (key[j] > tk) | ((key[j] == tk) & (32 * tid + j <= tp));
-    const int at = o + pc;
-    sel[pick && at < AT_TOPK ? at : dummy] = 32 * tid + j;
-    pc += pick;
-  }
-  mark(6);
-  __syncthreads();
+  topk_refine<32>(tid, key, [&](int j) { return 32 * tid + j; }, kmin, kmax, n, cut, sampled,
+                  hist, wsum, phase, res_s, thr_s, sel);
   mark(7);
   return sel;
 }

@@ -89,6 +89,59 @@ def test_attention_48_rows(gpu):
     _check(op, inp, full_score_rows=0, sample=1024)
 
 
+def _patterned(inp, ids, codes, scales):
+    """Every cached index key of slot-in-page s takes pattern ids[s]: E2M1 codes
+    codes[p] ([4, 16] bytes) and E8M0 scales scales[p] ([4]); the scores then take one
+    value a pattern, so the top-k meets ties."""
+    ids = torch.as_tensor(ids, device=inp.plane.device)
+    inp.plane[:] = codes.to(inp.plane.device)[ids].permute(1, 0, 2)[None]
+    sc = torch.empty(4, 64, dtype=torch.uint8, device=inp.plane.device)
+    s = torch.arange(64, device=sc.device)
+    sc[:, (s % 16) * 4 + s // 16] = scales.to(sc.device)[ids].T
+    inp.plane_scale[:] = sc[None]
+
+
+def test_attention_topk_all_scores_equal(gpu):
+    """Head weights 0: every score is 0, the selection the first 2048 positions (the
+    ranking by position alone)."""
+    print("case attention top-k all equal", flush=True)
+    inp = synthetic.attention_inputs(2, 32768, gpu, seed=21)
+    inp.iw.zero_()
+    op = AttnOp(gpu, max_rows=2)
+    _, _, topk = _check(op, inp, full_score_rows=0)
+    assert np.array_equal(topk[0], np.arange(TOPK))
+
+
+def test_attention_topk_twelve_score_values(gpu):
+    """Keys from 12 patterns: 12 score values, the threshold inside a run of ties."""
+    print("case attention top-k twelve values", flush=True)
+    inp = synthetic.attention_inputs(2, 32768, gpu, seed=22)
+    g = torch.Generator().manual_seed(22)
+    codes = torch.randint(0, 256, (12, 4, 16), dtype=torch.uint8, generator=g)
+    scales = torch.randint(124, 129, (12, 4), dtype=torch.uint8, generator=g)
+    _patterned(inp, [s % 12 for s in range(64)], codes, scales)
+    _check(AttnOp(gpu, max_rows=2), inp, full_score_rows=0)
+
+
+def test_attention_topk_sample_misled(gpu):
+    """The high keys sit exactly at the sampled positions (every 32nd): the sampled
+    range then holds 1024 keys, fewer than 2048, and the search widens to the whole row."""
+    print("case attention top-k sampled positions high", flush=True)
+    inp = synthetic.attention_inputs(2, 32768, gpu, seed=23)
+    inp.iq.fill_(0x22)  # every query code +1.0
+    inp.iqs.fill_(127)
+    inp.iw.abs_()
+    codes = torch.stack([torch.full((4, 16), 0x77, dtype=torch.uint8),   # +6.0
+                         torch.full((4, 16), 0x22, dtype=torch.uint8)])  # +1.0
+    scales = torch.full((2, 4), 127, dtype=torch.uint8)
+    _patterned(inp, [0 if s % 32 == 0 else 1 for s in range(64)], codes, scales)
+    _, scores, topk = _check(AttnOp(gpu, max_rows=2), inp, full_score_rows=0)
+    n = 32768
+    high = np.arange(0, n, 32)
+    want = np.sort(np.concatenate([high, np.setdiff1d(np.arange(n), high)[:TOPK - high.size]]))
+    assert np.array_equal(topk[0], want)
+
+
 def test_attention_deterministic_and_graph_replay(gpu):
     print("case attention determinism + graph", flush=True)
     inp = synthetic.attention_inputs(4, 32768, gpu, seed=5)
