@@ -597,9 +597,13 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       const float tok_on = ((mask >> t) & 1u) ? 1.f : 0.f;
       const int sbase = __builtin_amdgcn_readfirstlane(
           (e * (2 * I / 128) + (half * I + cc * 16) / 128) * (H / 128) + wq * KCW);
-      // the task after next (its value lands in LDS before the epilogue barrier)
-      int nn = ntask;
-      if (tid == 0 && next < ntask) nn = nblk + (int)add_dev(&queue[0], 1u);
+      // the task after next (its value lands in LDS before the epilogue barrier). Lane 0
+      // of wave 0 grabs it, the other lanes are out of range: with a branch around the
+      // atomic the compiler waits for its reply (and so for every load before it, the
+      // whole ring) right after the branch, before this task's MFMAs
+      const bool grab_on = next < ntask;
+      const uint32_t grabbed = (uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
+          1, rsrc(queue, grab_on ? 4u : 0u), tid == 0 ? 0u : 0x80000000u, 0, 0);
       uint32_t son;
       const __amdgpu_buffer_rsrc_t rn = task_src(next, son);
       // B operands and scales: the same LDS words every task, read through an opaque
@@ -620,7 +624,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         __builtin_amdgcn_sched_barrier(0);
       }
       red[w][l] = acc;
-      if (tid == 0) next_s = nn;
+      if (tid == 0) next_s = grab_on ? nblk + (int)grabbed : ntask;
       __syncthreads();
       const int after = next_s;
       if (tid < 256) {
