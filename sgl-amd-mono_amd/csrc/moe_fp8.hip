@@ -650,11 +650,20 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
 
   // ---------------------------------------------------------------- stage 3
   stamp(p.timeline, MONO_TL_UPGATE);
-  // mid quant: task (u, kb), one wave a row. Trip counts stay CTA-uniform (barriers
-  // per task); a failed wait only skips work.
+  // mid quant: task (u, kb), one wave a row, handed out in (u, kb) order from a
+  // device-wide counter: the CTAs that leave up/gate first quantise the experts whose
+  // tiles finished first, so the down stage can start on them. Trip counts stay
+  // CTA-uniform (barriers per task); a failed wait only skips work.
   {
     const int nq = ok ? nd * NKB : 0;
-    for (int q = b; q < nq; q += nblk) {
+    auto grab = [&]() {
+      if (tid == 0) next_s = nq ? (int)add_dev(&queue[1], 1u) : nq;
+      __syncthreads();
+      const int q = next_s;
+      __syncthreads();  // next_s is rewritten by the next grab
+      return q;
+    };
+    for (int q = grab(); q < nq; q = grab()) {
       const int u = q / NKB, kb = q % NKB;
       const int e = rl.uexp[u];
       const uint32_t mask = rl.umask[u];
@@ -696,10 +705,12 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   // ---------------------------------------------------------------- stage 4
   stamp(p.timeline, MONO_TL_MIDQ);
   // down: task f = output rows [32 f, 32 f + 32); waves 0-7 the first 16 rows, 8-15 the
-  // next 16; wave wq takes experts u = wq, wq + 8, ... One wait for every quantised mid
-  // block (the first weight tile already in flight), then the 9 R (expert, row) mid rows
-  // are copied into LDS over the dead activation operands, so the expert loop streams
-  // weights with no poll and no other global load.
+  // next 16; wave wq takes experts u = wq, wq + 8, ... in order. The (expert, row) mid
+  // rows are copied into LDS over the dead activation operands, so the expert loop
+  // streams weights with no poll and no other global load: first those of the experts
+  // already quantised when the CTA gets here (one pass over the ready words, the first
+  // weight tile already in flight), which it streams while the rest are quantised, then,
+  // after one wait, the others. Each wave still takes its experts in the same order.
   {
     const int ntask = ok ? G::NDN : 0;
     uint8_t* mql = reinterpret_cast<uint8_t*>(xq_lds);  // [9 R slots][I] E4M3
@@ -726,38 +737,59 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         buf[kb][1] = ld16s<CP_NT>(r, vo, so + kb * CS + HO);
       }
     }
-    // every quantised mid block of this launch
-    if (ntask) {
-      const int i = w * 64 + l;
-      ok = wait_until(guard, MONO_SITE_MQ, [&]() {
-        const uint32_t rv = i < nd * NKB ? ld_dev(&ready[i]) : tag;
-        return __all(rv == tag);
-      });
-    }
-    ok = cta_all(ok, ok_s);
-    if (ok && ntask) {
-      // mid rows + coefficients into LDS: 32 lanes of 16 B a slot row
+    // mid rows + coefficients of slots [s0, s1) into LDS (slots are in expert order):
+    // the rows by buffer -> LDS copies (2 rows of 512 B a wave instruction, no
+    // registers), the coefficients one a thread; then every wave drains (the copies
+    // land behind its weight tile in flight, which its next MFMA waits for anyway)
+    const int nsl = R * MOE_SLOTS;
+    static_assert(I == 512, "a wave's 1 KiB copy is two mid rows");
+    auto copy_slots = [&](int s0, int s1) {
       const __amdgpu_buffer_rsrc_t rmq = rsrc(mq, (uint32_t)G::SZ_MQ);
-      const int nsl = R * MOE_SLOTS;
-      constexpr int CPR = I / 16;  // 16-byte pieces of a mid row
-      for (int i = tid; i < nsl * CPR; i += G::THREADS) {
-        const int s = i / CPR, c = i % CPR;
-        const int ut = rl.slot_ut[s];
-        const uint32_t src_off = (uint32_t)(((ut >> 8) * MOE_MAXR + (ut & 255)) * I + c * 16);
-        *reinterpret_cast<v4i*>(mql + s * I + c * 16) = ld16<CP_DEV>(rmq, src_off);
+      const __amdgpu_buffer_rsrc_t rmc = rsrc(mcoef, (uint32_t)G::SZ_MCOEF);
+      for (int c = w; 2 * c < s1 - s0; c += G::WAVES) {
+        const int sl = s0 + 2 * c + (l >> 5);
+        if (sl < s1) {  // an odd count: the last copy's upper half-wave writes nothing
+          const int ut = rl.slot_ut[sl];
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rmq, (__attribute__((address_space(3))) void*)(mql + (s0 + 2 * c) * I), 16,
+              (uint32_t)(((ut >> 8) * MOE_MAXR + (ut & 255)) * I + (l & 31) * 16), 0, 0, CP_DEV);
+        }
       }
-      for (int i = tid; i < nsl * NKB; i += G::THREADS) {
-        const int s = i / NKB, kb = i % NKB;
-        const int ut = rl.slot_ut[s];
-        mcl[i] = __uint_as_float(ld_dev(reinterpret_cast<const uint32_t*>(
-            &mcoef[((size_t)(ut >> 8) * MOE_MAXR + (ut & 255)) * NKB + kb])));
-      }
+      static_assert(MOE_MAXR * MOE_SLOTS * NKB <= G::THREADS, "a coefficient a thread");
+      const int nc = (s1 - s0) * NKB;
+      const int sc_ = s0 + (tid < nc ? tid / NKB : 0), kc = tid % NKB;
+      const int utc = rl.slot_ut[sc_];
+      const uint32_t cw = (uint32_t)ld4<CP_DEV>(
+          rmc, tid < nc ? (uint32_t)((((utc >> 8) * MOE_MAXR + (utc & 255)) * NKB + kc) * 4)
+                        : 0x80000000u);
+      if (tid < nc) mcl[s0 * NKB + tid] = __uint_as_float(cw);
+      drain();
+      asm volatile("" ::: "memory");  // the LDS reads after the barrier stay after it
+    };
+    // the leading experts already quantised: one pass over the ready words
+    __shared__ int n1_s;
+    if (tid == 0) n1_s = nd;
+    __syncthreads();
+    if (ntask) {
+      const int i = tid;
+      static_assert(MOE_NDIST * NKB <= 2 * G::THREADS, "two ready words a thread");
+      const uint32_t r0 = ld4<CP_DEV>(rsrc(ready, (uint32_t)(nd * NKB) * 4u), (uint32_t)i * 4u);
+      const uint32_t r1 = ld4<CP_DEV>(rsrc(ready, (uint32_t)(nd * NKB) * 4u),
+                                      (uint32_t)(i + G::THREADS) * 4u);
+      if (i < nd * NKB && r0 != tag) atomicMin(&n1_s, i / NKB);
+      if (i + G::THREADS < nd * NKB && r1 != tag) atomicMin(&n1_s, (i + G::THREADS) / NKB);
     }
     __syncthreads();
+    const int n1 = ntask ? n1_s : nd;
+    const int s_split = n1 < nd ? rl.uslot[n1] : nsl;
+    if (ok && ntask) copy_slots(0, s_split);
+    __syncthreads();
+    bool rest = n1 < nd;  // the experts from n1 on are still to be copied
     for (int f = b; f < (ok ? ntask : 0); f += nblk) {
       const int rg0 = f * G::DNT + 16 * half;
       v4f acc = {0.f, 0.f, 0.f, 0.f};
-      for (int u = wq; u < nd; u += QW) {
+      int u = wq;
+      auto step = [&]() {
         int fn = f, un = u + QW;
         if (un >= nd) {
           fn = f + nblk;
@@ -784,6 +816,23 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
           acc += d * (sld(p.s2, s2b + kb) * cf);
           __builtin_amdgcn_sched_barrier(0);
         }
+        u += QW;
+      };
+      while (u < (rest ? n1 : nd)) step();
+      if (rest) {
+        // the other experts: every wave waits for their ready words (its polls return
+        // behind its weight tiles in flight), then their mid rows into LDS
+        rest = false;
+        const int i = w * 64 + l;
+        ok = wait_until(guard, MONO_SITE_MQ, [&]() {
+          const uint32_t rv = i < nd * NKB && i >= n1 * NKB ? ld_dev(&ready[i]) : tag;
+          return __all(rv == tag);
+        });
+        ok = cta_all(ok, ok_s);
+        if (ok) copy_slots(s_split, nsl);
+        __syncthreads();
+        if (!ok) break;
+        while (u < nd) step();
       }
       // fixed-order reduction over each half's 8 waves, then the residual add
       red[w][l] = acc;
