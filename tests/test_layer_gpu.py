@@ -1,0 +1,131 @@
+"""The four launches of one decoder layer chained on one stream (config 5), every phase
+checked against the CPU oracle on the inputs that phase received from the one before.
+
+Bars as the per-phase tests: q and the output block within 2e-2 max-abs + 1e-2 relative
+and 1e-2 relative in norm of the oracle's f64; indexer scores within 1e-5 of the row's
+largest; the selection bit-exact against the exact top-2048 of the launch's own scores;
+the router's top-8 bit-exact against the oracle's over the launch's own scores; the
+MoE's y and the layer output to the same bf16 bars."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn as A
+from oracle import dense as D
+from oracle import front as Fr
+from oracle import moe as M
+from oracle.topk import topk_sort
+from sgl_amd_mono_amd.dsv32 import synthetic
+from sgl_amd_mono_amd.dsv32.attn import AttnInputs
+from sgl_amd_mono_amd.dsv32.layer import LayerOp, LayerStep
+from sgl_amd_mono_amd.dsv32.moe import MoeRouting
+
+pytestmark = pytest.mark.gpu
+TOPK = 2048
+
+
+def _close(got, want, what):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel <= 1e-2, (what, rel)
+    bad = np.abs(got - want) > 2e-2 + 1e-2 * np.abs(want)
+    assert not bad.any(), (what, int(bad.sum()), np.argwhere(bad)[:4])
+
+
+def _ragged(step: LayerStep, positions) -> LayerStep:
+    """The same requests at other positions: each row's slot is its page-table entry."""
+    pos = torch.as_tensor(positions, dtype=torch.int64, device=step.positions.device)
+    page = step.page_table.gather(1, (pos // 64)[:, None])[:, 0].to(torch.int64)
+    return LayerStep(positions=pos, slots=page * 64 + pos % 64, req_ids=step.req_ids,
+                     page_table=step.page_table)
+
+
+def test_layer_eight_rows_ragged_contexts(gpu):
+    """8 rows seeing 8192, 5001, 2049, 2048, 101, 7001, 3000 and 1 keys."""
+    print("case layer rows=8 ctx<=8192 ragged", flush=True)
+    rows, ctx = 8, 8192
+    w, caches, step, h = synthetic.layer(rows, ctx, gpu, seed=3)
+    step = _ragged(step, [8191, 5000, 2048, 2047, 100, 7000, 2999, 0])
+    op = LayerOp(w, gpu, max_rows=rows, ctx_max=ctx)
+    f = op.front.launch(h, caches, step.positions, step.slots)
+    inp = AttnInputs(q=f.q, iq=f.iq, iqs=f.iqs, iw=f.iw, plane=caches.plane,
+                     plane_scale=caches.plane_scale, kv=caches.kv, kv_scale=caches.kv_scale,
+                     positions=step.positions, req_ids=step.req_ids, page_table=step.page_table)
+    scores = torch.full((rows, ctx), float("nan"), device=gpu)
+    topk = torch.full((rows, TOPK), -7, dtype=torch.int32, device=gpu)
+    o_lat = op.attn.launch(inp, scores=scores, topk=topk)
+    a = op.post.launch(o_lat, h)
+    y = torch.empty(rows, 7168, dtype=torch.float32, device=gpu)
+    rt = MoeRouting(torch.empty(rows, 256, device=gpu), torch.empty(rows, 9, dtype=torch.int32,
+                    device=gpu), torch.empty(rows, 9, device=gpu))
+    out = op.moe.launch(a, y=y, routing=rt)
+    op.check()
+
+    pos = step.positions.cpu().numpy()
+    fr = Fr.front(h.cpu(), positions=pos, **synthetic.rowmajor_front(w.front))
+    _close(f.q.float().cpu(), fr["q"], "front q")
+
+    sc, tk = scores.cpu().numpy(), topk.cpu().numpy()
+    iq, iqs, iw = f.iq.cpu().numpy(), f.iqs.cpu().numpy(), f.iw.cpu().numpy()
+    plane, psc = caches.plane.cpu().numpy(), caches.plane_scale.cpu().numpy()
+    kv, ksc = caches.kv.cpu().numpy(), caches.kv_scale.cpu().numpy()
+    pt = step.page_table.cpu().numpy()
+    rng = np.random.default_rng(3)
+    for r in range(rows):
+        n = int(pos[r]) + 1
+        pages = pt[r]
+        cols = np.arange(n) if n <= 3000 else np.sort(rng.choice(n, 3000, replace=False))
+        want = A.index_scores(iq[r], iqs[r], iw[r], plane, psc, pages, n, cols=cols)
+        err = np.abs(sc[r, cols] - want).max() / max(np.abs(want).max(), 1e-30)
+        assert err <= 1e-5, (r, err)
+        k = min(n, TOPK)
+        want_sel = np.arange(n, dtype=np.int32) if n <= TOPK else topk_sort(sc[r, :n], TOPK)
+        assert np.array_equal(tk[r, :k], want_sel), (r, n)
+        assert np.all(tk[r, k:] == -1), r
+        slots = pages[tk[r, :k] // 64].astype(np.int64) * 64 + tk[r, :k] % 64
+        o, _ = A.sparse_mla(f.q[r].cpu(), kv, ksc, slots, op.attn.sm_scale)
+        _close(o_lat[r].float().cpu(), o, f"o_lat row {r}")
+
+    pr = D.attn_out(o_lat.cpu(), h.cpu(), *synthetic.rowmajor_post(w.post))
+    _close(a.float().cpu(), pr["a"], "post a")
+
+    ids = rt.ids.cpu().numpy()
+    sel8, _ = M.route_topk(rt.scores.cpu(), w.moe.bias.cpu())
+    assert np.array_equal(np.sort(ids[:, 1:], 1), np.sort(sel8, 1)), "router top-8"
+    experts = {int(e): synthetic.rowmajor_expert(w.moe, int(e)) for e in np.unique(ids)}
+    ref = M.moe_fp8(a.cpu(), w.moe.g_post.cpu(), w.moe.w_r.cpu(), w.moe.bias.cpu(), None, None,
+                    None, None, experts=experts, routing=(ids, rt.weights.cpu().numpy()))
+    _close(y.cpu(), ref["y"], "moe y")
+    _close(out.float().cpu(), ref["out"], "layer out")
+
+
+def test_layer_graph_replay_matches_eager(gpu):
+    """The layer captured in one graph: three replays, with eager layers between them,
+    each bit-equal to the eager result."""
+    print("case layer graph replay rows=8 ctx=4096", flush=True)
+    rows = 8
+    w, caches, step, h = synthetic.layer(rows, 4096, gpu, seed=4)
+    op = LayerOp(w, gpu, max_rows=rows, ctx_max=4096)
+    want = op.launch(h, caches, step).clone()
+    again = op.launch(h, caches, step).clone()
+    op.check()
+    assert torch.equal(want, again)
+    out = torch.empty_like(want)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op.launch(h, caches, step, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        op.launch(h, caches, step, out=out)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        op.launch(h, caches, step)
+        torch.cuda.synchronize()
+    op.check()
