@@ -316,11 +316,7 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
           if (xk) {
             const v4i hw = *reinterpret_cast<const v4i*>(&xs[t * FR_XS + 8 * ck]);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float a = bf16_lo((uint32_t)hw[q]), c = bf16_hi((uint32_t)hw[q]);
-              s = fmaf(a, a, s);
-              s = fmaf(c, c, s);
-            }
+            for (int q = 0; q < 4; ++q) s = dot2_bf16_sq((uint32_t)hw[q], s);
           }
           ss[t] = wave_sum(s);
         }
@@ -335,6 +331,12 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
           rs_s[tid] = __builtin_amdgcn_rsqf(s * (1.0f / FR_H) + p.eps);
         }
         __syncthreads();
+        float gf[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          gf[2 * q] = bf16_lo((uint32_t)gv[q]);
+          gf[2 * q + 1] = bf16_hi((uint32_t)gv[q]);
+        }
 #pragma unroll
         for (int t = 0; t < FR_XG; ++t) {
           const float rs = rs_s[t];
@@ -344,10 +346,8 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
             v4i o;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const uint32_t hq = (uint32_t)hw[q], gq = (uint32_t)gv[q];
-              const uint32_t lo = bf16_bits(bf16_lo(hq) * rs * bf16_lo(gq));
-              const uint32_t hi = bf16_bits(bf16_hi(hq) * rs * bf16_hi(gq));
-              o[q] = (int)(lo | (hi << 16));
+              const uint32_t hq = (uint32_t)hw[q];
+              o[q] = (int)bf16x2_bits(bf16_lo(hq) * rs * gf[2 * q], bf16_hi(hq) * rs * gf[2 * q + 1]);
             }
             *px = o;
           }

@@ -213,6 +213,17 @@ __device__ inline v2f fp8x2_hi(uint32_t w) { return __builtin_amdgcn_cvt_pk_f32_
 __device__ inline float clamp_fp8(float v) { return __builtin_amdgcn_fmed3f(v, -FP8_MAX, FP8_MAX); }
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+// two f32 -> two bf16 (lo in bits 0-15), round to nearest even: one v_cvt_pk_bf16_f32,
+// equal to bf16_bits on every non-NaN input (denormals included)
+__device__ inline uint32_t bf16x2_bits(float lo, float hi) {
+  const v2f f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));
+}
+// acc + w.lo^2 + w.hi^2 for a bf16 pair w, by v_dot2c_f32_bf16
+__device__ inline float dot2_bf16_sq(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, w), __builtin_bit_cast(v2bf, w),
+                                        acc, false);
+}
 // acc + bf16(a) * w.lo + bf16(b) * w.hi, with a, b rounded to bf16 (nearest even) by
 // v_cvt_pk_bf16_f32 and the products summed by v_dot2c_f32_bf16
 __device__ inline float dot2_bf16(float a, float b, uint32_t w, float acc) {
