@@ -287,8 +287,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       v4i xb;
 #pragma unroll
       for (int d = 0; d < 4; ++d)
-        xb[d] = (int)(bf16_bits(fa[2 * d] * rs * fg[2 * d]) |
-                      (bf16_bits(fa[2 * d + 1] * rs * fg[2 * d + 1]) << 16));
+        xb[d] = (int)bf16x2_bits(fa[2 * d] * rs * fg[2 * d], fa[2 * d + 1] * rs * fg[2 * d + 1]);
       const v4f z = {0.f, 0.f, 0.f, 0.f};
       const v4f dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           __builtin_bit_cast(v8bfm, wa), __builtin_bit_cast(v8bfm, xb), z, 0, 0, 0);

@@ -4,7 +4,8 @@
 //         reference rounds o to bf16 before o_proj, kernel.py:4080-4123): 256 tiles of 16
 //         rows, one a CTA, issued before anything else so they lead every CU's queue.
 //   o_proj a[r][n] = bf16(h[r][n] + sum_k W_o[n][k] o[r][k]): 448 tiles of 16 rows, two
-//         at a time a CTA, their weights and h in flight from the launch's start.
+//         at a time a CTA: the first tile's weights and h in flight from the launch's
+//         start, the second's from the moment W_UV's outputs are stored.
 // The hand-off of o needs no flag, drain or poll: W_UV stores the complement of each bf16
 // pair into one of two scratch buffers (by the launch tag's parity), and clears the other
 // for the next launch; a zero word is "not written yet". o_proj's x loads are its wait:
@@ -112,9 +113,12 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
   const int etok = (tid >> 4) & 15, erow = tid & 15;     // o_proj epilogue coordinates
 
   // ---------------------------------------------------------------- prefetch
-  // W_UV tile b (waves 0-7), then o_proj tiles b and b + nblk (all waves), then h. The
-  // barrier between them puts every W_UV load of the CU ahead of every o_proj load: the
-  // CU's vector memory path returns data in issue order, across its waves too.
+  // W_UV tile b (waves 0-7), then o_proj tile b (all waves) and h; o_proj tile b + nblk
+  // only once W_UV's outputs are stored. The barrier puts every W_UV load of the CU ahead
+  // of every o_proj load: the CU's vector memory path serves its waves' requests in
+  // issue order, stores included, and drains a prefetch at the CU's share of HBM
+  // bandwidth (~23 KB/us), so a store issued behind both tiles (128 KB) would wait ~4 us
+  // and hold back the o hand-off; one tile keeps HBM busy through W_UV.
   const bool uv0 = b < PO_UV_TILES;
   v4i wu[1], xu[1][2];
   float su[1];
@@ -125,7 +129,6 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
   v4i w0[4], w1[4];
   float s0[4], s1[4];
   go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
-  go.issue(jo, 0, a1, w1, s1, a1 < PO_TILES);
   auto load_h = [&](int t0, int t1) -> int {
     const int t = tid < 256 ? t0 : t1;
     const bool v = etok < R && tid < 512 && t < PO_TILES;
@@ -138,6 +141,11 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
   // tile b from the prefetch (no loads in this branch: the wait for wu / xu stays exact)
   if (uv0) {
     gu.dot(wu, su, xu, red + 32);
+    // The W_UV loads retire here on every wave: the waves outside the tile skip the dot,
+    // and on their path the compiler would otherwise wait at later register writes for
+    // loads behind them too (the o_proj prefetch). 7 loads follow them: an o_proj tile's
+    // 4 weight and 2 scale loads, and h.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(7));
     __syncthreads();
     if (tid < UV_STORE) GemvUV::epilogue(ju, b / UV_TPR, b % UV_TPR, R, tid, red + 32);
     __syncthreads();
@@ -151,6 +159,7 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
     if (tid < UV_STORE) GemvUV::epilogue(ju, u / UV_TPR, u % UV_TPR, R, tid, red + 32);
     __syncthreads();
   }
+  go.issue(jo, 0, a1, w1, s1, a1 < PO_TILES);
   // clear this CTA's slice of the next launch's hand-off buffer
   {
     constexpr uint32_t OB = (uint32_t)PostScratch::OBUF;
