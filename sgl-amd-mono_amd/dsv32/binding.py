@@ -1,0 +1,212 @@
+"""A loaded SGLang DeepSeek-V3.2 layer bound to the launches' weight and cache structs.
+
+The reference binds GLM-5.3 layers the same way (``sgl_amd_mono/glm53/gfx950/weights.py:
+94-310``, caches ``sgl_amd_mono/glm53/spec.py:431-465``; the FP4 index pages of
+``sgl_amd_mono/deepseek_v4/gfx950/runner.py:336-346``). Every FP8 projection is read in
+place (its ``weight`` and ``weight_scale_inv``), and so are the norms, the indexer's head
+weights and the MoE. Four kinds of tensor are copied once, because the launches read
+another format, and each copy is logged in ``copies`` under (what, layer, name):
+
+* W_UK / W_UV: SGLang's per-tensor FP8 ``w_kc`` [heads, 128, 512] / ``w_vc`` [heads,
+  512, 128] transposed to the launches' [head][out][in] rows, with the scalar ``w_scale``
+  as every block scale (``weights.py:145-184``);
+* the index key LayerNorm weight and bias in f32 (``weights.py:187-210``);
+* the RoPE table: SGLang's f32 ``cos_sin_cache`` [positions, 64] (cos | sin) as the
+  bf16 [positions, 32] pair the front reads.
+
+Mismatches raise ``ValueError`` naming the tensor, before anything launches; a cache
+that does not have the launches' layout raises ``RuntimeError`` (``spec.py:446-461``).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import layouts
+from .config import DSV32, LayerConfig
+from .front import FrontCaches, FrontWeights
+from .layer import LayerWeights
+from .moe import FP8, MoeFp8Weights
+from .post import PostWeights
+
+
+def _layout(linear) -> str:
+    """AITER's (16, 16) shuffle when SGLang marked the weight pre-shuffled."""
+    shuffled = getattr(linear, "aiter_bpreshuffled", False) or getattr(
+        linear.weight, "is_shuffled", False)
+    return layouts.AITER16 if shuffled else layouts.ROWMAJOR
+
+
+def _linear(name: str, linear, rows: int, cols: int):
+    """(weight, weight_scale_inv, layout) of an FP8 block-scaled projection, in place."""
+    w = linear.weight
+    s = getattr(linear, "weight_scale_inv", None)
+    if w.dtype != FP8 or tuple(w.shape) != (rows, cols):
+        raise ValueError(f"{name}: needs E4M3 [{rows}, {cols}], got {w.dtype} {tuple(w.shape)}")
+    want = ((rows + 127) // 128, cols // 128)
+    if s is None or s.dtype != torch.float32 or tuple(s.shape) != want:
+        got = None if s is None else f"{s.dtype} {tuple(s.shape)}"
+        raise ValueError(f"{name}: needs 128 x 128 block scales f32 {list(want)}, got {got}")
+    return w, s, _layout(linear)
+
+
+def _same(name: str, t: torch.Tensor, shape: tuple, dtype) -> torch.Tensor:
+    if t.dtype != dtype or tuple(t.shape) != shape:
+        raise ValueError(f"{name}: needs {dtype} {list(shape)}, got {t.dtype} {tuple(t.shape)}")
+    return t
+
+
+def _one_layout(parts: dict) -> str:
+    """The launches take one layout for all FP8 projections of a struct."""
+    kinds = set(parts.values())
+    if len(kinds) != 1:
+        raise ValueError(f"mixed FP8 layouts {parts}: the launches read one layout a layer")
+    return kinds.pop()
+
+
+def _shuffled(t: torch.Tensor, layout: str) -> torch.Tensor:
+    """An [N, K] E4M3 copy in ``layout`` (the copies follow the in-place projections)."""
+    if layout == layouts.AITER16:
+        return layouts.shuffle_16x16(t.view(torch.uint8)).view(FP8)
+    return t.contiguous()
+
+
+def absorbed(attn, idx: int, copies: dict, layout: str, cfg: LayerConfig = DSV32):
+    """W_UK [heads, 512, 128] and W_UV [heads, 128, 512] (E4M3, ``layout`` per head) with
+    their block scales, from ``w_kc`` / ``w_vc`` and the scalar ``w_scale``."""
+    w_kc, w_vc, w_scale = attn.w_kc, attn.w_vc, getattr(attn, "w_scale", None)
+    hh, nope, c, v = cfg.heads, cfg.nope_dim, cfg.kv_lora, cfg.v_dim
+    if w_kc.dtype != FP8 or w_scale is None or w_scale.numel() != 1:
+        raise ValueError(
+            f"w_kc / w_vc: needs per-tensor E4M3 with a scalar w_scale, got {w_kc.dtype} and "
+            f"{None if w_scale is None else tuple(w_scale.shape)}")
+    _same("w_kc", w_kc, (hh, nope, c), FP8)
+    _same("w_vc", w_vc, (hh, c, v), FP8)
+    scale = float(w_scale.float().reshape(()).item())
+    uk = w_kc.transpose(1, 2).contiguous()  # [h][c][nope]: latent rows over the nope dims
+    uv = w_vc.transpose(1, 2).contiguous()  # [h][v][c]: value rows over the latent
+    w_uk = torch.stack([_shuffled(uk[h], layout) for h in range(hh)])
+    w_uv = torch.stack([_shuffled(uv[h], layout) for h in range(hh)])
+    f32 = dict(dtype=torch.float32, device=w_kc.device)
+    s_uk = torch.full((hh, c // 128, (nope + 127) // 128), scale, **f32)
+    s_uv = torch.full((hh, v // 128, c // 128), scale, **f32)
+    for name, t in (("w_uk", w_uk), ("s_uk", s_uk), ("w_uv", w_uv), ("s_uv", s_uv)):
+        copies["W_UK / W_UV packed", idx, name] = t
+    return w_uk, s_uk, w_uv, s_uv
+
+
+def rope_table(rotary, idx: int, copies: dict):
+    """bf16 cos / sin [positions, 32] from SGLang's f32 ``cos_sin_cache`` [positions, 64]
+    (cos in the first half, sin in the second)."""
+    cache = getattr(rotary, "cos_sin_cache", None)
+    if cache is None or cache.dim() != 2 or cache.shape[1] != DSV32.rope_dim:
+        got = None if cache is None else tuple(cache.shape)
+        raise ValueError(f"rotary_emb.cos_sin_cache: needs [positions, {DSV32.rope_dim}], got {got}")
+    half = DSV32.rope_dim // 2
+    cos = cache[:, :half].to(torch.bfloat16).contiguous()
+    sin = cache[:, half:].to(torch.bfloat16).contiguous()
+    copies["RoPE table bf16", idx, "cos"] = cos
+    copies["RoPE table bf16", idx, "sin"] = sin
+    return cos, sin
+
+
+def front_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> FrontWeights:
+    """The attention front of a loaded layer (``self_attn`` with its indexer)."""
+    attn = layer.self_attn
+    ind = getattr(attn, "indexer", None)
+    if ind is None:
+        raise ValueError("self_attn.indexer: the front is built for DSA layers with an indexer")
+    H, QL, KL, PE = cfg.hidden, cfg.q_lora, cfg.kv_lora, cfg.rope_dim
+    w_qkv_a, s_qkv_a, l_a = _linear("fused_qkv_a_proj_with_mqa", attn.fused_qkv_a_proj_with_mqa,
+                                    QL + KL + PE, H)
+    w_qb, s_qb, l_b = _linear("q_b_proj", attn.q_b_proj, cfg.heads * cfg.qk_dim, QL)
+    w_k, s_k, l_k = _linear("indexer.wk", ind.wk, cfg.index_dim, H)
+    w_iq, s_iq, l_q = _linear("indexer.wq_b", ind.wq_b, cfg.index_heads * cfg.index_dim, QL)
+    layout = _one_layout({"fused_qkv_a_proj_with_mqa": l_a, "q_b_proj": l_b, "indexer.wk": l_k,
+                          "indexer.wq_b": l_q})
+    bf16 = torch.bfloat16
+    g_in = _same("input_layernorm", layer.input_layernorm.weight, (H,), bf16)
+    g_q = _same("q_a_layernorm", attn.q_a_layernorm.weight, (QL,), bf16)
+    g_kv = _same("kv_a_layernorm", attn.kv_a_layernorm.weight, (KL,), bf16)
+    w_w = _same("indexer.weights_proj", ind.weights_proj.weight, (cfg.index_heads, H), bf16)
+    g_k = _same("indexer.k_norm", ind.k_norm.weight, (cfg.index_dim,), ind.k_norm.weight.dtype)
+    g_k = g_k.detach().float().contiguous()
+    b_k = ind.k_norm.bias.detach().float().contiguous()
+    copies["indexer k LayerNorm f32", idx, "weight"] = g_k
+    copies["indexer k LayerNorm f32", idx, "bias"] = b_k
+    w_uk, s_uk, _, _ = absorbed(attn, idx, copies, layout, cfg)
+    cos, sin = rope_table(attn.rotary_emb, idx, copies)
+    return FrontWeights(g_in=g_in, g_q=g_q, g_kv=g_kv, w_qkv_a=w_qkv_a, s_qkv_a=s_qkv_a,
+                        w_k=w_k, s_k=s_k, w_w=w_w, g_k=g_k, b_k=b_k, w_qb=w_qb, s_qb=s_qb,
+                        w_iq=w_iq, s_iq=s_iq, w_uk=w_uk, s_uk=s_uk, cos=cos, sin=sin,
+                        layout=layout)
+
+
+def post_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> PostWeights:
+    """The attention output block: ``o_proj`` in place, W_UV packed in its layout."""
+    attn = layer.self_attn
+    w_o, s_o, layout = _linear("o_proj", attn.o_proj, cfg.hidden, cfg.heads * cfg.v_dim)
+    _, _, w_uv, s_uv = absorbed(attn, idx, copies, layout, cfg)
+    return PostWeights(w_uv=w_uv, s_uv=s_uv, w_o=w_o, s_o=s_o, layout=layout)
+
+
+def moe_weights(layer) -> MoeFp8Weights:
+    """The FFN half: the fused experts (the shared expert last), router and norm, in place."""
+    mlp, ex = layer.mlp, layer.mlp.experts
+    return MoeFp8Weights(
+        g_post=layer.post_attention_layernorm.weight,
+        w_r=mlp.gate.weight,
+        bias=mlp.gate.e_score_correction_bias,
+        w13=ex.w13_weight, s13=ex.w13_weight_scale_inv,
+        w2=ex.w2_weight, s2=ex.w2_weight_scale_inv,
+        layout=layouts.AITER16 if getattr(ex.w13_weight, "is_shuffled", False)
+        else layouts.ROWMAJOR,
+    )
+
+
+def layer_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> LayerWeights:
+    """Every weight of a covered layer's four launches."""
+    return LayerWeights(front=front_weights(layer, idx, copies, cfg),
+                        post=post_weights(layer, idx, copies, cfg), moe=moe_weights(layer))
+
+
+def layer_disable_reason(layer, idx: int, cfg: LayerConfig = DSV32) -> Optional[str]:
+    """Why a layer's attention half cannot be bound (None: it can); nothing is kept."""
+    try:
+        layer_weights(layer, idx, {}, cfg)
+    except (ValueError, AttributeError) as e:
+        return f"layer {idx}: {e}"
+    return None
+
+
+def caches(pool, idx: int, kv_scale: torch.Tensor, cfg: LayerConfig = DSV32) -> FrontCaches:
+    """A layer's caches from SGLang's KV pool, in place: the MLA rows E4M3 [slots, 1, 576]
+    (``get_key_buffer``) and the FP4 index pages [pages, 1, 4, 64, 16] with their E8M0
+    scales [pages, 1, 4, 64] (``get_index_k_fp4_payload_buffer`` / ``_scale_buffer``).
+    ``kv_scale`` f32 [slots] is the launches' per-token scale of a row (the caller's: 1
+    for a row written unscaled)."""
+    kv = pool.get_key_buffer(idx)
+    pay = pool.get_index_k_fp4_payload_buffer(idx)
+    sc = pool.get_index_k_fp4_scale_buffer(idx)
+    row = cfg.kv_row
+    if kv.element_size() != 1 or kv.shape[-1] != row or not kv.is_contiguous():
+        raise RuntimeError(f"layer {idx}: MLA cache {kv.dtype} {tuple(kv.shape)}; needs "
+                           f"contiguous E4M3 [slots, 1, {row}]")
+    slots = kv.numel() // row
+    if kv_scale.dtype != torch.float32 or tuple(kv_scale.shape) != (slots,):
+        raise RuntimeError(f"layer {idx}: KV scales {kv_scale.dtype} {tuple(kv_scale.shape)}; "
+                           f"needs f32 [{slots}]")
+    if (pay.dtype != torch.uint8 or tuple(pay.shape[1:]) != (1, 4, cfg.page, 16)
+            or not pay.is_contiguous()):
+        raise RuntimeError(f"layer {idx}: FP4 index pages {pay.dtype} {tuple(pay.shape)}; "
+                           f"needs contiguous uint8 [pages, 1, 4, {cfg.page}, 16]")
+    if (sc.dtype != torch.uint8 or tuple(sc.shape) != (pay.shape[0], 1, 4, cfg.page)
+            or not sc.is_contiguous()):
+        raise RuntimeError(f"layer {idx}: FP4 index scales {sc.dtype} {tuple(sc.shape)}; "
+                           f"needs contiguous uint8 [{pay.shape[0]}, 1, 4, {cfg.page}]")
+    pages = pay.shape[0]
+    return FrontCaches(kv=kv.view(torch.uint8).view(slots, row), kv_scale=kv_scale,
+                       plane=pay.view(pages, 4, cfg.page, 16),
+                       plane_scale=sc.view(pages, 4, cfg.page))

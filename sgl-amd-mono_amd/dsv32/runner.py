@@ -110,3 +110,14 @@ def take_topk(st: Dsv32Step, topk_indices: torch.Tensor, rows: int) -> None:
     count = (st.indptr[1 : S + 1] - st.indptr[:S]).to(torch.int64).unsqueeze(1)
     dst = torch.where(cols < count, start + cols, torch.full_like(cols, W * TOPK))
     st.topk.scatter_(0, dst.reshape(-1), topk_indices[:S].reshape(-1).to(torch.int32))
+
+
+def page_table(req_to_token: torch.Tensor, req_pool_indices: torch.Tensor, rows: int,
+               context: int, page: int = DSV32.page) -> torch.Tensor:
+    """The rows' page tables i32 [rows, pages] from SGLang's ``req_to_token`` (a request's
+    KV slot at every position; pages of ``page`` slots): a page id is the slot of the
+    page's first position divided by ``page``. Row s is request s of the step (the
+    launches' request ids)."""
+    pages = -(-context // page)
+    first = req_to_token[req_pool_indices[:rows].to(torch.int64)][:, : pages * page : page]
+    return (first.to(torch.int64) // page).to(torch.int32).contiguous()

@@ -8,10 +8,12 @@ SGLang calls for a routed step. The forward decides by the graph key alone
 (``plan.key.rows`` against the widths built), so every rank and every graph replay makes
 the same choice; a wider step runs the model's own forward.
 
-Each covered MoE layer runs its FFN half as one persistent launch (``MoeFp8Op``): the
-post-attention RMSNorm, router, top-8 + shared expert, W8A8 experts and the residual
-add, reading SGLang's loaded weights in place (no copy is made of the experts, the
-router or the norm). The attention half still runs SGLang's module.
+A covered layer whose attention half binds (``binding.layer_disable_reason`` is None)
+runs as the four launches of ``LayerOp``: front, attention, output block and MoE, over
+SGLang's weights in place (the few copies logged by ``binding``) and its KV / FP4
+index pages in place. Any other covered layer runs its FFN half as one persistent launch
+(``MoeFp8Op``: post-attention RMSNorm, router, top-8 + shared expert, W8A8 experts and
+the residual add, experts, router and norm read in place) after SGLang's attention.
 
 One GPU's TP=4 share is what the kernels compute; the two TP exchanges of the layer are
 not built, so ``build`` refuses a TP size above 1 with that reason rather than serve
@@ -44,7 +46,7 @@ except ModuleNotFoundError:  # SGLang before sgl-project/sglang#45389
     )
 
 from .config import DSV32, MAX_ROWS
-from .runner import alloc_step, fill_step
+from .runner import alloc_step, fill_step, page_table
 
 # one build takes any row count up to 16 (the kernels read the count at run time)
 WIDTHS = tuple(range(1, MAX_ROWS + 1))
@@ -121,10 +123,21 @@ def _model_disable_reasons(model, hf_config, copies) -> list:
 
 
 class _Layer:
-    """A covered layer: its SGLang module and its launch."""
+    """A covered layer: its SGLang module and its launch (``LayerOp`` for the whole
+    layer, or ``MoeFp8Op`` for its FFN half, ``full`` saying which)."""
 
-    def __init__(self, i: int, module, op):
-        self.i, self.module, self.op = i, module, op
+    def __init__(self, i: int, module, op, full: bool = False, kv_scale=None):
+        self.i, self.module, self.op, self.full = i, module, op, full
+        self.kv_scale = kv_scale  # f32 [slots]: the per-token scales of the layer's KV rows
+        self.caches = None
+
+
+def plan_layers(model, hf_config) -> dict:
+    """Layer -> None (the whole layer binds) or the reason its attention half does not
+    (it then runs its FFN half only)."""
+    from .binding import layer_disable_reason
+
+    return {i: layer_disable_reason(model.model.layers[i], i) for i in covered_layers(hf_config)}
 
 
 class _Built:
@@ -153,24 +166,59 @@ class _Built:
         if "step" not in plan.state:
             S = plan.key.rows
             st = self.steps[_width(S)]
+            pt = None
+            if any(L.full for L in self.layers.values()):
+                pt = page_table(forward_batch.req_to_token_pool.req_to_token,
+                                forward_batch.req_pool_indices, S, self.max_position + 1)
             plan.state["step"] = fill_step(st, positions, forward_batch.out_cache_loc, S,
-                                           self.max_position)
+                                           self.max_position, page_table=pt)
         return plan.state["step"]
 
     def _backbone(self, plan, input_ids, positions, forward_batch, input_embeds):
-        """The embedding and dense layers on SGLang's path; each covered layer's
-        attention half on its module, its FFN half as one launch."""
+        """The embedding and dense layers on SGLang's path; a fully bound layer as its
+        four launches; any other covered layer's attention half on its module and its
+        FFN half as one launch."""
         m = self.lm.model
         hidden = m.embed_tokens(input_ids) if input_embeds is None else input_embeds
-        self.step(plan, positions, forward_batch)
+        st = self.step(plan, positions, forward_batch)
         for i, layer in enumerate(m.layers):
             L = self.layers.get(i)
             if L is None:
                 hidden = layer(positions, hidden, forward_batch)
-                continue
-            a = layer.attention_half(positions, hidden, forward_batch)
-            hidden = L.op.launch(a.contiguous())
+            elif L.full:
+                hidden = L.op.launch(hidden.contiguous(), self._caches(L, forward_batch),
+                                     self._layer_step(st, forward_batch, plan.key.rows))
+            else:
+                a = layer.attention_half(positions, hidden, forward_batch)
+                hidden = L.op.launch(a.contiguous())
         return m.norm(hidden)
+
+    @staticmethod
+    def _caches(L, forward_batch):
+        """The layer's caches in SGLang's pool, bound once (rebound if the pool moved)."""
+        from .binding import caches
+
+        pool = forward_batch.token_to_kv_pool
+        if getattr(pool, "page_size", 64) != 64:
+            raise RuntimeError(f"KV pool page size {pool.page_size}: the launches' pages hold 64")
+        kv = pool.get_key_buffer(L.i)
+        if L.caches is None or L.caches.kv.data_ptr() != kv.data_ptr():
+            if L.kv_scale is None or L.kv_scale.numel() * kv.shape[-1] != kv.numel():
+                L.kv_scale = torch.ones(kv.numel() // kv.shape[-1], dtype=torch.float32,
+                                        device=kv.device)
+            L.caches = caches(pool, L.i, L.kv_scale)
+        return L.caches
+
+    @staticmethod
+    def _layer_step(st, forward_batch, rows: int):
+        """The launches' row tables from the step's: a row's page table is its request's
+        slots at every 64th position, as page ids."""
+        from .layer import LayerStep
+
+        if st.page_table.shape[0] < rows:
+            raise RuntimeError("the step has no page table: fill_step(page_table=...) first")
+        return LayerStep(positions=st.positions[:rows], slots=st.slots[:rows],
+                         req_ids=st.req_ids[:rows], page_table=st.page_table)
 
 
 def _build(model, hf_config, ctx):
@@ -178,30 +226,40 @@ def _build(model, hf_config, ctx):
     from sglang.srt.runtime_context import get_parallel
 
     from ..guard import watchdog_deadline
-    from .moe import MoeFp8Op, MoeFp8Weights
+    from .attn import MAX_CTX
+    from .binding import layer_weights, moe_weights
+    from .front import FRONT_MAX_ROWS
+    from .layer import LayerOp
+    from .moe import MoeFp8Op
 
     p = get_parallel()
     if p.tp_size > 1:
         raise ValueError(
             f"the DSA monokernel computes one GPU's TP share, but its TP exchanges are "
             f"not built: TP {p.tp_size} would serve unreduced partials")
+    deadline = watchdog_deadline(getattr(ctx, "deadline_s", 120.0) * 2)
+    context_len = getattr(ctx, "context_len", 163840)
+    copies = getattr(ctx, "copies", None)
+    copies = {} if copies is None else copies
     layers = {}
-    for i in covered_layers(hf_config):
+    plans = plan_layers(model, hf_config)
+    if context_len > MAX_CTX:  # the attention launch's score rows end at MAX_CTX keys
+        plans = {i: f"context {context_len} > {MAX_CTX}" for i in plans}
+    for i, why in plans.items():
         mod = model.model.layers[i]
-        ex = mod.mlp.experts
-        w = MoeFp8Weights(
-            g_post=mod.post_attention_layernorm.weight,
-            w_r=mod.mlp.gate.weight,
-            bias=mod.mlp.gate.e_score_correction_bias,
-            w13=ex.w13_weight, s13=ex.w13_weight_scale_inv,
-            w2=ex.w2_weight, s2=ex.w2_weight_scale_inv,
-            layout="aiter16" if getattr(ex.w13_weight, "is_shuffled", False) else "rowmajor",
-        )
-        op = MoeFp8Op(w, w.w13.device, max_rows=MAX_ROWS,
-                      deadline_s=watchdog_deadline(getattr(ctx, "deadline_s", 120.0) * 2))
-        layers[i] = _Layer(i, mod, op)
+        if why is None:
+            w = layer_weights(mod, i, copies)
+            op = LayerOp(w, w.moe.w13.device, max_rows=FRONT_MAX_ROWS, ctx_max=context_len,
+                         deadline_s=deadline)
+            layers[i] = _Layer(i, mod, op, full=True)
+        else:
+            w = moe_weights(mod)
+            op = MoeFp8Op(w, w.w13.device, max_rows=MAX_ROWS, deadline_s=deadline)
+            layers[i] = _Layer(i, mod, op)
     device = next(iter(layers.values())).op.device
-    return _Built(model, layers, device, context_len=getattr(ctx, "context_len", 163840))
+    full = any(L.full for L in layers.values())
+    return _Built(model, layers, device, context_len=context_len,
+                  max_rows=FRONT_MAX_ROWS if full else MAX_ROWS)
 
 
 SPEC = MonoSpec(

@@ -1,0 +1,160 @@
+"""Binding a loaded SGLang layer (modules with SGLang's attribute names, on the CPU) to the
+launches' structs: projections read in place, the logged copies equal to the launches'
+own formats, refusals naming the tensor, and the cache checks."""
+
+from types import SimpleNamespace as NS
+
+import pytest
+import torch
+
+from sgl_amd_mono_amd import layouts
+from sgl_amd_mono_amd.dsv32 import binding, synthetic
+from sgl_amd_mono_amd.dsv32.config import DSV32
+from sgl_amd_mono_amd.dsv32.moe import FP8
+
+SCALE = 0.0078125  # the scalar w_scale of w_kc / w_vc
+
+
+def _rowmajor(t, layout):
+    return layouts.unshuffle_16x16(t.view(torch.uint8)).view(FP8) if layout == layouts.AITER16 else t
+
+
+def _lin(w, s, layout):
+    lin = NS(weight=w, weight_scale_inv=s)
+    if layout == layouts.AITER16:
+        lin.aiter_bpreshuffled = True
+    return lin
+
+
+def _layer(layout):
+    """A DeepSeek-V3.2 layer as SGLang loads it, built from the synthetic launch weights
+    (W_UK / W_UV at one scalar scale, so the copies can be compared bit for bit)."""
+    fw = synthetic.front_weights("cpu", seed=3, layout=layout, rope_rows=64)
+    pw = synthetic.post_weights("cpu", seed=3, layout=layout)
+    hh = DSV32.heads
+    uk = torch.stack([_rowmajor(fw.w_uk[h], layout) for h in range(hh)])  # [h][512][128]
+    uv = torch.stack([_rowmajor(pw.w_uv[h], layout) for h in range(hh)])  # [h][128][512]
+    half = DSV32.rope_dim // 2
+    cache = torch.cat([fw.cos.float(), fw.sin.float()], 1)
+    attn = NS(
+        fused_qkv_a_proj_with_mqa=_lin(fw.w_qkv_a, fw.s_qkv_a, layout),
+        q_b_proj=_lin(fw.w_qb, fw.s_qb, layout),
+        o_proj=_lin(pw.w_o, pw.s_o, layout),
+        q_a_layernorm=NS(weight=fw.g_q), kv_a_layernorm=NS(weight=fw.g_kv),
+        w_kc=uk.transpose(1, 2).contiguous(), w_vc=uv.transpose(1, 2).contiguous(),
+        w_scale=torch.tensor(SCALE),
+        rotary_emb=NS(cos_sin_cache=cache),
+        indexer=NS(wk=_lin(fw.w_k, fw.s_k, layout), wq_b=_lin(fw.w_iq, fw.s_iq, layout),
+                   weights_proj=NS(weight=fw.w_w),
+                   k_norm=NS(weight=fw.g_k.to(torch.bfloat16), bias=fw.b_k.to(torch.bfloat16))),
+    )
+    assert half == fw.cos.shape[1]
+    return NS(self_attn=attn, input_layernorm=NS(weight=fw.g_in)), fw, pw
+
+
+@pytest.mark.parametrize("layout", [layouts.ROWMAJOR, layouts.AITER16])
+def test_the_front_and_output_block_bind_in_place(layout):
+    layer, fw, pw = _layer(layout)
+    copies = {}
+    f = binding.front_weights(layer, 5, copies)
+    p = binding.post_weights(layer, 5, copies)
+    assert f.layout == p.layout == layout
+    for name in ("w_qkv_a", "s_qkv_a", "w_qb", "s_qb", "w_k", "s_k", "w_iq", "s_iq", "w_w",
+                 "g_in", "g_q", "g_kv"):
+        assert getattr(f, name) is getattr(fw, name), name  # the loaded tensor itself
+    assert p.w_o is pw.w_o and p.s_o is pw.s_o
+    # the copies: W_UK / W_UV in the launches' layout with the scalar scale
+    assert torch.equal(f.w_uk.view(torch.uint8), fw.w_uk.view(torch.uint8))
+    assert torch.equal(p.w_uv.view(torch.uint8), pw.w_uv.view(torch.uint8))
+    assert torch.all(f.s_uk == SCALE) and f.s_uk.shape == fw.s_uk.shape
+    assert torch.all(p.s_uv == SCALE) and p.s_uv.shape == pw.s_uv.shape
+    assert torch.equal(f.cos, fw.cos) and torch.equal(f.sin, fw.sin)
+    assert f.g_k.dtype == torch.float32 and f.b_k.dtype == torch.float32
+    f.validate(DSV32, torch.device("cpu"))
+    p.validate(DSV32, torch.device("cpu"))
+    logged = {(k[0], k[2]) for k in copies}
+    assert logged == {("W_UK / W_UV packed", n) for n in ("w_uk", "s_uk", "w_uv", "s_uv")} | {
+        ("indexer k LayerNorm f32", "weight"), ("indexer k LayerNorm f32", "bias"),
+        ("RoPE table bf16", "cos"), ("RoPE table bf16", "sin")}
+    assert all(k[1] == 5 for k in copies)
+
+
+def test_refusals_name_the_tensor():
+    layer, fw, _ = _layer(layouts.ROWMAJOR)
+    assert binding.layer_disable_reason(NS(self_attn=layer.self_attn, input_layernorm=layer.input_layernorm,
+                                           post_attention_layernorm=None, mlp=None), 4) is not None
+    bad = NS(**vars(layer.self_attn))
+    bad.q_b_proj = NS(weight=fw.w_qb.to(torch.bfloat16), weight_scale_inv=fw.s_qb)
+    with pytest.raises(ValueError, match="q_b_proj"):
+        binding.front_weights(NS(self_attn=bad, input_layernorm=layer.input_layernorm), 4, {})
+    mixed = NS(**vars(layer.self_attn))
+    mixed.q_b_proj = _lin(fw.w_qb, fw.s_qb, layouts.AITER16)
+    with pytest.raises(ValueError, match="mixed FP8 layouts"):
+        binding.front_weights(NS(self_attn=mixed, input_layernorm=layer.input_layernorm), 4, {})
+    blocky = NS(**vars(layer.self_attn))
+    blocky.w_scale = torch.ones(4)
+    with pytest.raises(ValueError, match="scalar w_scale"):
+        binding.post_weights(NS(self_attn=blocky), 4, {})
+    no_index = NS(**vars(layer.self_attn))
+    no_index.indexer = None
+    with pytest.raises(ValueError, match="indexer"):
+        binding.front_weights(NS(self_attn=no_index, input_layernorm=layer.input_layernorm), 4, {})
+
+
+def _pool(slots=256, pages=4):
+    kv = torch.zeros(slots, 1, DSV32.kv_row, dtype=FP8)
+    pay = torch.zeros(pages, 1, 4, 64, 16, dtype=torch.uint8)
+    sc = torch.zeros(pages, 1, 4, 64, dtype=torch.uint8)
+    return NS(get_key_buffer=lambda i: kv, get_index_k_fp4_payload_buffer=lambda i: pay,
+              get_index_k_fp4_scale_buffer=lambda i: sc), kv, pay, sc
+
+
+def test_caches_bind_in_place_and_refuse_other_layouts():
+    pool, kv, pay, sc = _pool()
+    c = binding.caches(pool, 7, torch.ones(256))
+    assert c.kv.data_ptr() == kv.data_ptr() and c.kv.shape == (256, 576) and c.kv.dtype == torch.uint8
+    assert c.plane.data_ptr() == pay.data_ptr() and c.plane.shape == (4, 4, 64, 16)
+    assert c.plane_scale.data_ptr() == sc.data_ptr() and c.plane_scale.shape == (4, 4, 64)
+    with pytest.raises(RuntimeError, match="KV scales"):
+        binding.caches(pool, 7, torch.ones(255))
+    wide = NS(**vars(pool))
+    wide.get_key_buffer = lambda i: torch.zeros(256, 1, 656, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="MLA cache"):
+        binding.caches(wide, 7, torch.ones(256))
+    paged = NS(**vars(pool))
+    paged.get_index_k_fp4_payload_buffer = lambda i: torch.zeros(4, 1, 64, 132, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="FP4 index pages"):
+        binding.caches(paged, 7, torch.ones(256))
+
+
+def test_page_tables_come_from_req_to_token():
+    from sgl_amd_mono_amd.dsv32.runner import page_table
+
+    g = torch.Generator().manual_seed(1)
+    perm = torch.randperm(12, generator=g)
+    req_to_token = torch.zeros(5, 4 * 64, dtype=torch.int32)
+    for r in range(3):  # request r holds pages perm[4 r .. 4 r + 3], 64 slots each
+        req_to_token[r] = (perm[4 * r : 4 * r + 4, None] * 64 + torch.arange(64)).reshape(-1)
+    pt = page_table(req_to_token, torch.tensor([2, 0]), 2, 200)
+    assert pt.dtype == torch.int32 and pt.shape == (2, 4)
+    assert torch.equal(pt[0], perm[8:12].to(torch.int32)) and torch.equal(pt[1], perm[0:4].to(torch.int32))
+
+
+def test_every_covered_layer_is_planned_with_its_reason():
+    from tests import fake_sglang
+
+    fake_sglang.install()
+    from sgl_amd_mono_amd.dsv32 import spec
+
+    layer, _, _ = _layer(layouts.ROWMAJOR)
+    ok = NS(self_attn=layer.self_attn, input_layernorm=layer.input_layernorm,
+            post_attention_layernorm=NS(weight=torch.ones(DSV32.hidden, dtype=torch.bfloat16)),
+            mlp=NS(gate=NS(weight=None, e_score_correction_bias=None),
+                   experts=NS(w13_weight=torch.zeros(1, dtype=FP8), w13_weight_scale_inv=None,
+                              w2_weight=None, w2_weight_scale_inv=None)))
+    dense_attn = NS(**vars(layer.self_attn))
+    dense_attn.indexer = None
+    other = NS(**{**vars(ok), "self_attn": dense_attn})
+    model = NS(model=NS(layers=[None, ok, other]))
+    plans = spec.plan_layers(model, NS(first_k_dense_replace=1, num_hidden_layers=3))
+    assert plans[1] is None and "indexer" in plans[2] and 0 not in plans

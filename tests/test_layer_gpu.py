@@ -129,3 +129,50 @@ def test_layer_graph_replay_matches_eager(gpu):
         op.launch(h, caches, step)
         torch.cuda.synchronize()
     op.check()
+
+
+def test_layer_bound_from_sglang_modules_matches_the_direct_launch(gpu):
+    """A layer as SGLang loads it (its module attribute names, W_UK / W_UV as per-tensor
+    w_kc / w_vc, the RoPE table as f32 cos_sin_cache) bound by ``binding``: the launches
+    give the same bits as launches over the structs built directly."""
+    from types import SimpleNamespace as NS
+
+    from sgl_amd_mono_amd import layouts
+    from sgl_amd_mono_amd.dsv32 import binding
+    from sgl_amd_mono_amd.dsv32.moe import FP8
+
+    print("case layer bound from SGLang modules", flush=True)
+    rows, ctx, scale = 4, 2048, 0.0078125
+    w, caches, step, h = synthetic.layer(rows, ctx, gpu, seed=6)
+    w.front.s_uk.fill_(scale)
+    w.post.s_uv.fill_(scale)
+    un = lambda t: layouts.unshuffle_16x16(t.view(torch.uint8)).view(FP8)
+    uk = torch.stack([un(x) for x in w.front.w_uk])
+    uv = torch.stack([un(x) for x in w.post.w_uv])
+    lin = lambda wt, s: NS(weight=wt, weight_scale_inv=s, aiter_bpreshuffled=True)
+    f, po, m = w.front, w.post, w.moe
+    m.w13.is_shuffled = True
+    attn = NS(fused_qkv_a_proj_with_mqa=lin(f.w_qkv_a, f.s_qkv_a), q_b_proj=lin(f.w_qb, f.s_qb),
+              o_proj=lin(po.w_o, po.s_o), q_a_layernorm=NS(weight=f.g_q),
+              kv_a_layernorm=NS(weight=f.g_kv), w_kc=uk.transpose(1, 2).contiguous(),
+              w_vc=uv.transpose(1, 2).contiguous(), w_scale=torch.tensor(scale, device=gpu),
+              rotary_emb=NS(cos_sin_cache=torch.cat([f.cos.float(), f.sin.float()], 1)),
+              indexer=NS(wk=lin(f.w_k, f.s_k), wq_b=lin(f.w_iq, f.s_iq),
+                         weights_proj=NS(weight=f.w_w),
+                         k_norm=NS(weight=f.g_k.clone(), bias=f.b_k.clone())))
+    module = NS(self_attn=attn, input_layernorm=NS(weight=f.g_in),
+                post_attention_layernorm=NS(weight=m.g_post),
+                mlp=NS(gate=NS(weight=m.w_r, e_score_correction_bias=m.bias),
+                       experts=NS(w13_weight=m.w13, w13_weight_scale_inv=m.s13,
+                                  w2_weight=m.w2, w2_weight_scale_inv=m.s2)))
+    copies = {}
+    bound = binding.layer_weights(module, 9, copies)
+    assert bound.front.w_qkv_a is f.w_qkv_a and bound.moe.w13 is m.w13 and len(copies) == 8
+    kv0, plane0 = caches.kv.clone(), caches.plane.clone()
+    want = LayerOp(w, gpu, max_rows=rows, ctx_max=ctx).launch(h, caches, step).clone()
+    caches.kv.copy_(kv0)
+    caches.plane.copy_(plane0)
+    op = LayerOp(bound, gpu, max_rows=rows, ctx_max=ctx)
+    got = op.launch(h, caches, step)
+    op.check()
+    assert torch.equal(got, want)
