@@ -407,6 +407,10 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
     const __amdgpu_buffer_rsrc_t rrp = rsrc(hrp, (uint32_t)G::SZ_RP);
     for (int row = 0; row < R && ok; ++row) {
       if ((G::NTASK0 + row) % nblk != b) continue;
+      // the biases ahead of the poll: loaded after it, they would add a round trip
+      float bs[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bs[i] = p.bias[l + 64 * i];
       float lg[4];
       ok = wait_until(guard, MONO_SITE_LOGITS, [&]() {
         // every load issued before the first is used: one round trip a poll
@@ -433,12 +437,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         return __all(mn != 0u);
       });
       if (ok) {
-        float sc[4], bs[4];
+        float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[i] = 1.0f / (1.0f + expf(-lg[i]));
-          bs[i] = p.bias[l + 64 * i];
-        }
+        for (int i = 0; i < 4; ++i) sc[i] = 1.0f / (1.0f + expf(-lg[i]));
         route_row(rl, row, sc, bs, p.route_scale, p.scores, p.ids, p.weights);
         // lanes l < 8 wrote slots 1 + l (LDS accesses of one wave complete in order)
         __builtin_amdgcn_wave_barrier();
