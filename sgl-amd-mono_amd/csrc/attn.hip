@@ -122,8 +122,7 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   __shared__ int ok_s;
   __shared__ __attribute__((aligned(16))) int wsum[2 * AT_WAVES];
   __shared__ int res_s[4];
-  __shared__ __attribute__((aligned(16))) uint32_t wsum_mm[4 * AT_WAVES];
-  __shared__ uint32_t thr_s[2];
+  __shared__ uint32_t mm_s[2];
 
   float* scores = reinterpret_cast<float*>(p.scratch + S::SCORES);
   uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S::SCORE_DONE);
@@ -248,10 +247,14 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
           return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + l]) == tag);
         });
+      if (tid == 0) {  // topk_select's minimum / maximum words, set before the barrier
+        mm_s[0] = 0xFFFFFFFFu;
+        mm_s[1] = 0u;
+      }
       ok = cta_all(ok, ok_s);
       if (ok) {
         const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
-        const int32_t* sel_l = topk_select(tid, rs, n, smem, wsum, wsum_mm, res_s, thr_s);
+        const int32_t* sel_l = topk_select(tid, rs, n, smem, wsum, mm_s, res_s);
         for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
           const int v = sel_l[i];
           st_dev64(sel + i, pair((uint32_t)v, tag));

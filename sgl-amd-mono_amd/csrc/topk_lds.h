@@ -97,48 +97,27 @@ __device__ inline void select_pass(int tid, const uint32_t (&key)[NK], uint32_t 
   __syncthreads();
 }
 
-// minimum and maximum over the CTA (every thread gets them); `red` is 2 x 32 u32 of LDS,
-// 16-byte aligned, used alternately like block_scan's buffers (one barrier)
-__device__ inline void block_minmax(uint32_t& mn, uint32_t& mx, uint32_t* red, int& phase) {
-  const int l = lane_id(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint32_t* buf = red + 2 * AT_WAVES * phase;
-  phase ^= 1;
-  mx = wave_max_u32(mx);
-  mn = ~wave_max_u32(~mn);
-  if (l == 0) {
-    buf[w] = mn;
-    buf[AT_WAVES + w] = mx;
-  }
-  __syncthreads();
-  const v4i* rv = reinterpret_cast<const v4i*>(buf);
-  v4i r[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = rv[i];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t a = (uint32_t)r[i][e], b = (uint32_t)r[4 + i][e];
-      mn = a < mn ? a : mn;
-      mx = b > mx ? b : mx;
-    }
-}
-
-// The threshold and the selection from keys held in registers, NK a thread, thread
-// order then index order being position order (pos_of(j) gives the position of key[j]).
-// `cnt` keys lie in [lo, hi]; the first pass bins [plo0, hi] and, with `check0`, is
-// redone over [lo, hi] if that range holds fewer than TOPK keys. Histogram passes (4096
-// bins) keep the bin holding the TOPK-th key until it holds few keys (then they rank
-// themselves) or one key value (then its positions do). The threshold is an element
-// (key, position) of the order (key descending, position ascending); the selection,
-// every element up to it, goes to sel[0 .. TOPK) in ascending position order.
+// The selection from keys held in registers, NK (<= 32) a thread, thread order then index
+// order being position order (pos_of(j) gives the position of key[j]). `cnt` keys lie in
+// [lo, hi]; the first pass bins [plo0, hi] and, with `check0`, is redone over [lo, hi] if
+// that range holds fewer than TOPK keys. Histogram passes (4096 bins) keep the bin holding
+// the TOPK-th key until it holds few keys or one key value. The selection is every key
+// above that bin plus the first kk of the bin's keys in (key descending, position
+// ascending) order: few candidates rank themselves, one shared value takes its first kk
+// positions. A thread's picks are a 32-bit mask; the scan of the pick counts places them,
+// in ascending position order, at sel[0 .. TOPK). `hist` (4096 words, zero on entry) holds
+// the passes' bins, then the candidates and the masks of the candidates' owners.
 template <int NK, class PosF>
 __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_of, uint32_t lo,
                                    uint32_t hi, int cnt, uint32_t plo0, bool check0,
                                    uint32_t* hist, int* wsum, int& phase, int* res_s,
-                                   uint32_t* thr_s, int32_t* sel) {
-  uint32_t* ck = hist;                                  // candidates, after the passes
-  int32_t* cp = reinterpret_cast<int32_t*>(hist + CAND);
+                                   int32_t* sel) {
+  static_assert(NK <= 32, "a thread's picks fit one 32-bit mask");
+  uint32_t* ck = hist;                                       // candidates, after the passes
+  int32_t* cp = reinterpret_cast<int32_t*>(hist + CAND);     // their positions
+  uint32_t* co = hist + 2 * CAND;                            // their (thread, index)
+  uint32_t* pmask = hist + 3 * CAND;                         // [AT_THREADS] picked candidates
+  static_assert(3 * CAND + AT_THREADS <= 4096, "candidates and masks fit the histogram");
   int kk = AT_TOPK, shift = 1;
 #pragma unroll 1
   for (int pass = 0; shift > 0 && cnt > CAND; ++pass) {
@@ -159,71 +138,59 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
     hi = top < (uint64_t)hi ? (uint32_t)top : hi;
     lo = nlo;
   }
-  // the threshold element (Tkey, Tpos): the kk-th of the bin's keys in (key descending,
-  // position ascending) order
+  // every wave has read the last pass's results before res_s[0] is reused; the passes left
+  // the histogram (masks included) zero
+  __syncthreads();
+  if (tid == 0) res_s[0] = 0;
+  __syncthreads();
+  uint32_t pick = 0;  // bit j: key[j] is selected
   if (cnt <= CAND) {
-    // few candidates: gather them, and each finds its own rank among them (the barrier
-    // first: every wave has read the last pass's results before res_s[0] is reused)
-    __syncthreads();
-    if (tid == 0) res_s[0] = 0;
-    __syncthreads();
+    // keys above the bin, and the bin's candidates gathered in one pass
 #pragma unroll
-    for (int j = 0; j < NK; ++j)
+    for (int j = 0; j < NK; ++j) {
+      pick |= (uint32_t)(key[j] > hi) << j;
       if (key[j] >= lo && key[j] <= hi) {
         const int at = atomicAdd(&res_s[0], 1);
         ck[at] = key[j];
         cp[at] = pos_of(j);
+        co[at] = ((uint32_t)tid << 5) | (uint32_t)j;
       }
+    }
     __syncthreads();
+    // each candidate finds its rank among them; the first kk are picked
     if (tid < cnt) {
       const uint32_t mk = ck[tid];
       const int mp = cp[tid];
       int rank = 0;
       for (int m = 0; m < cnt; ++m) rank += (ck[m] > mk) | ((ck[m] == mk) & (cp[m] < mp));
-      if (rank == kk - 1) {
-        thr_s[0] = mk;
-        thr_s[1] = (uint32_t)mp;
+      if (rank < kk) {
+        const uint32_t o = co[tid];
+        atomicOr(&pmask[o >> 5], 1u << (o & 31u));
       }
     }
   } else {
-    // one key value shared by many positions: the kk-th of them in position order
+    // one key value (lo == hi) shared by many positions: the first kk of them
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < NK; ++j) c += key[j] == lo;
+    for (int j = 0; j < NK; ++j) {
+      pick |= (uint32_t)(key[j] > hi) << j;
+      c += key[j] == lo;
+    }
     int tot;
-    const int before = block_scan(c, wsum, phase, tot);
-    if (before < kk && kk <= before + c) {
-      int seen = before;
-      for (int j = 0; j < NK; ++j) {
-        const bool e = key[j] == lo;
-        seen += e;
-        if (e && seen == kk) {
-          thr_s[0] = lo;
-          thr_s[1] = (uint32_t)pos_of(j);
-        }
-      }
+    int seen = block_scan(c, wsum, phase, tot);
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+      const bool e = key[j] == lo;
+      pick |= (uint32_t)(e && seen < kk) << j;
+      seen += e;
     }
   }
   __syncthreads();
-  const uint32_t tk = thr_s[0];
-  const int tp = (int)thr_s[1];
-  int np = 0;
-#pragma unroll
-  for (int j = 0; j < NK; ++j) np += (key[j] > tk) | ((key[j] == tk) & (pos_of(j) <= tp));
+  pick |= pmask[tid];
   int tot;
-  const int o = block_scan(np, wsum, phase, tot);
-  // the picks at their ranks; a key not taken writes its lane's dummy slot past the
-  // selection (no store branches, and no two lanes of a wave on one address)
-  int pc = 0;
-  const int dummy = AT_TOPK + (tid & (WAVE - 1));
-#pragma unroll
-  for (int j = 0; j < NK; ++j) {
-    const int pj = pos_of(j);
-    const bool pick = (key[j] > tk) | ((key[j] == tk) & (pj <= tp));
-    const int at = o + pc;
-    sel[pick && at < AT_TOPK ? at : dummy] = pj;
-    pc += pick;
-  }
+  int at = block_scan(__popc(pick), wsum, phase, tot);
+  // the picks in position order: only the set bits are visited
+  for (uint32_t m = pick; m; m &= m - 1u) sel[at++] = pos_of(__builtin_ctz(m));
   __syncthreads();
 }
 
@@ -238,17 +205,18 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
 // reads are conflict-free). A sample (every 32nd position) narrows the key range to one
 // holding about 1.5 TOPK keys, where topk_refine's first pass starts.
 __device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n, uint8_t* arena,
-                                       int* wsum, uint32_t* wsum_mm, int* res_s, uint32_t* thr_s,
+                                       int* wsum, uint32_t* mm, int* res_s,
                                        uint64_t* ts = nullptr) {
-  int phase = 0, mphase = 0;
+  int phase = 0;
   auto mark = [&](int k) {
     if (ts && tid == 0) ts[k] = __builtin_amdgcn_s_memtime();
   };
   mark(0);
   uint32_t* kl = reinterpret_cast<uint32_t*>(arena);  // [1024][33] image
   uint32_t* hist = kl + AT_THREADS * 33;               // [4096]; candidates after the passes
-  int32_t* sel = reinterpret_cast<int32_t*>(hist + 2 * CAND);  // [TOPK + 64]
-  static_assert(2 * CAND + AT_TOPK + WAVE <= 4096, "candidates and the selection fit the histogram");
+  // [TOPK], past the candidates and masks of topk_refine (dead when it is written)
+  int32_t* sel = reinterpret_cast<int32_t*>(hist + 3 * CAND + AT_THREADS);
+  static_assert(3 * CAND + AT_THREADS + AT_TOPK <= 4096, "the selection fits the histogram");
   constexpr int NLD = AT_MAXCTX / 4 / AT_THREADS;
   v4i raw[NLD];
 #pragma unroll
@@ -269,12 +237,21 @@ __device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n
       kmax = k > kmax ? k : kmax;
     }
   }
+  // the CTA's minimum and maximum key: a wave reduction, then one LDS atomic a wave into
+  // mm[0], mm[1] (set to ~0 and 0 by the caller before its last barrier)
+  kmax = wave_max_u32(kmax);
+  kmin = ~wave_max_u32(~kmin);
+  if ((tid & (WAVE - 1)) == 0) {
+    atomicMin(&mm[0], kmin);
+    atomicMax(&mm[1], kmax);
+  }
   __syncthreads();
   uint32_t key[32];
 #pragma unroll
   for (int j = 0; j < 32; ++j) key[j] = kl[33 * tid + j];
+  kmin = mm[0];
+  kmax = mm[1];
   mark(1);
-  block_minmax(kmin, kmax, wsum_mm, mphase);
   mark(2);
   // Sample the range first: position 32 t is thread t's sample. The bin of the sample
   // ranked SR from the top bounds a range [cut, kmax] expected to hold about 1.5 TOPK
@@ -296,7 +273,7 @@ __device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n
   }
   mark(3);
   topk_refine<32>(tid, key, [&](int j) { return 32 * tid + j; }, kmin, kmax, n, cut, sampled,
-                  hist, wsum, phase, res_s, thr_s, sel);
+                  hist, wsum, phase, res_s, sel);
   mark(7);
   return sel;
 }
