@@ -13,7 +13,7 @@
 //      keep the bin of the 2048th key until its few candidates rank themselves; the
 //      selection (every element up to the threshold element of the order key
 //      descending, position ascending) is published as (position, tag) pairs.
-//   3  split: task (row, 128-key split), all 32 heads. The split's tokens (through the
+//   3  split: task (row, 64-key split), all 32 heads. The split's tokens (through the
 //      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
 //      widened exactly), times the token's scale and the softmax scale; per head the
 //      split's max m and sum l; P, with the token's scale folded in, as bf16; O = P V on
@@ -43,7 +43,7 @@ constexpr int AT_LAT = 512;
 constexpr int AT_PAGE = 64;
 constexpr int AT_CHUNK = 1024;    // tokens of a score task
 constexpr int AT_NCHUNK = AT_MAXCTX / AT_CHUNK;
-constexpr int AT_SPLIT = 128;     // keys of a split task
+constexpr int AT_SPLIT = 64;      // keys of a split task
 constexpr int AT_NSPLIT = AT_TOPK / AT_SPLIT;
 constexpr int AT_MAXR = 48;
 
@@ -270,17 +270,18 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   {
     // LDS: K rows (E4M3, 576 + 16 bytes apart), q (bf16, 1152 + 16), S (f32), P (bf16),
     // the split's slots and token scales, the row's page-table entries
+    static_assert(AT_SPLIT == 64, "QK: 4 key tiles x 2 head tiles x 2 K chains; softmax: a key a lane");
     constexpr int KSTR = AT_KV + 16, QSTR = AT_KV * 2 + 16, SSTR = AT_SPLIT + 4,
                   PSTR = AT_SPLIT * 2 + 16;
     constexpr int NPG = AT_MAXCTX / AT_PAGE;
     uint8_t* kbuf = smem;
     uint8_t* qbuf = kbuf + AT_SPLIT * KSTR;
     float* sbuf = reinterpret_cast<float*>(qbuf + AT_HEADS * QSTR);
-    uint8_t* pbuf = reinterpret_cast<uint8_t*>(sbuf + AT_HEADS * SSTR);
+    uint8_t* pbuf = reinterpret_cast<uint8_t*>(sbuf + 2 * AT_HEADS * SSTR);  // S: two K chains
     int32_t* slot_s = reinterpret_cast<int32_t*>(pbuf + AT_HEADS * PSTR);
     float* ksc = reinterpret_cast<float*>(slot_s + AT_SPLIT);
     int32_t* pt_s = reinterpret_cast<int32_t*>(ksc + AT_SPLIT);
-    static_assert(AT_SPLIT * KSTR + AT_HEADS * QSTR + AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
+    static_assert(AT_SPLIT * KSTR + AT_HEADS * QSTR + 2 * AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
                           AT_SPLIT * 8 + NPG * 4 <=
                       (int)sizeof(smem),
                   "split LDS");
@@ -362,44 +363,38 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         if (tid < AT_SPLIT) ksc[tid] = slot >= 0 ? sc : 0.f;
       }
       __syncthreads();
-      // S = q K^T: wave w takes heads 16 (w / 8) .. and keys 16 (w % 8) ..
+      // S = q K^T: wave w takes heads 16 (w / 8) .., keys 16 (w % 4) .. and the even (w / 4
+      // even) or odd K steps: two MFMA chains a tile, summed (even + odd) by the softmax
       {
-        const int h0 = 16 * (w >> 3), j0 = 16 * (w & 7);
-        // two accumulators (even and odd K steps): two MFMA chains in flight
-        v4f d = {0.f, 0.f, 0.f, 0.f}, d1 = d;
-        const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4);
-        const uint8_t* kr = kbuf + (j0 + (l & 15)) * KSTR + 8 * (l >> 4);
+        const int h0 = 16 * (w >> 3), j0 = 16 * (w & 3), odd = (w >> 2) & 1;
+        v4f d = {0.f, 0.f, 0.f, 0.f};
+        const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4) + odd * 64;
+        const uint8_t* kr = kbuf + (j0 + (l & 15)) * KSTR + 8 * (l >> 4) + odd * 32;
         static_assert(AT_KV / 32 % 2 == 0, "K steps in pairs");
 #pragma unroll 3
         for (int ks = 0; ks < AT_KV / 32; ks += 2) {
           const v8bf a0 = *reinterpret_cast<const v8bf*>(qa + ks * 64);
           const v2i k0 = *reinterpret_cast<const v2i*>(kr + ks * 32);
-          const v8bf a1 = *reinterpret_cast<const v8bf*>(qa + ks * 64 + 64);
-          const v2i k1 = *reinterpret_cast<const v2i*>(kr + ks * 32 + 32);
           d = mfma_bf16(a0, fp8x8_bf16((uint32_t)k0[0], (uint32_t)k0[1]), d);
-          d1 = mfma_bf16(a1, fp8x8_bf16((uint32_t)k1[0], (uint32_t)k1[1]), d1);
         }
-        d += d1;
-        const float f = ksc[j0 + (l & 15)] * p.sm_scale;
+        float* sb = sbuf + odd * AT_HEADS * SSTR;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sbuf[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e] * f;
+        for (int e = 0; e < 4; ++e) sb[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e];
       }
       __syncthreads();
-      // softmax of the split, per head: wave w takes heads 2w, 2w + 1; lane l keys l, l + 64
+      // softmax of the split, per head: wave w takes heads 2w, 2w + 1; lane l key l
       float* ml = mls + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * 2;
+      const float f0 = ksc[l] * p.sm_scale;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int h = 2 * w + hh;
-        const bool v0 = l < kcnt, v1 = l + 64 < kcnt;
-        const float s0 = v0 ? sbuf[h * SSTR + l] : -INFINITY;
-        const float s1 = v1 ? sbuf[h * SSTR + l + 64] : -INFINITY;
-        const float m = wave_max(fmaxf(s0, s1));
-        const float p0 = v0 ? expf(s0 - m) : 0.f, p1 = v1 ? expf(s1 - m) : 0.f;
-        const float lsum = wave_sum(p0 + p1);
+        const bool v0 = l < kcnt;
+        const float s0 = v0 ? (sbuf[h * SSTR + l] + sbuf[(AT_HEADS + h) * SSTR + l]) * f0 : -INFINITY;
+        const float m = wave_max(s0);
+        const float p0 = v0 ? expf(s0 - m) : 0.f;
+        const float lsum = wave_sum(p0);
         // P with the token's scale folded in (V = E4M3 value x scale)
         reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l] = (uint16_t)bf16_bits(p0 * ksc[l]);
-        reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l + 64] =
-            (uint16_t)bf16_bits(p1 * ksc[l + 64]);
         if (l == 0) {
           st_devf(ml + 2 * h, m);
           st_devf(ml + 2 * h + 1, lsum);
@@ -478,15 +473,17 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         });
       ok = cta_all(ok, ok_s);
       if (!ok) break;
-      // the split partials and their (m, l) in one round trip
-      const int sp = tid >> 6, d8 = tid & 63;
-      v4i a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+      // the split partials and their (m, l) in one round trip: 32 threads a split, 16
+      // values a thread
+      static_assert(AT_NSPLIT * 32 == AT_THREADS && AT_LAT == 32 * 16, "merge thread map");
+      const int sp = tid >> 5, d16 = tid & 31;
+      v4i a[4];
       {
         const __amdgpu_buffer_rsrc_t ra = rsrc(
             accs + ((size_t)(r * AT_NSPLIT + (sp < nsp ? sp : 0)) * AT_HEADS + h) * AT_LAT,
             sp < nsp ? AT_LAT * 4 : 0);
-        a0 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32);
-        a1 = ld16<CP_DEV>(ra, (uint32_t)d8 * 32 + 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = ld16<CP_DEV>(ra, (uint32_t)d16 * 64 + 16 * i);
       }
       if (w == 0) {
         const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
@@ -503,15 +500,12 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       }
       __syncthreads();
       {
-        float v[8];
         const float ws = sp < nsp ? wsp_s[sp] : 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = __int_as_float(a0[e]) * ws;
-          v[4 + e] = __int_as_float(a1[e]) * ws;
+        for (int i = 0; i < 4; ++i) {
+          const v4f v = __builtin_bit_cast(v4f, a[i]) * ws;
+          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + 16 * d16 + 4 * i]) = v;
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) red[sp * AT_LAT + 8 * d8 + e] = v[e];
       }
       __syncthreads();
       if (tid < AT_LAT) {
