@@ -29,12 +29,14 @@ struct RouteLds {
 // The top-k of one row, called by one whole wave. Lane l holds the scores of experts
 // l + 64 i (i < 4) in `sc` and the matching biases in `bs`.
 // Order: radix key of f32(score + bias) descending, then lower expert id
-// (sgl_amd_mono/glm53/gfx950/kernel.py:1575-1629). Each round takes the wave maximum of
-// the 32-bit keys (a DPP / permlane butterfly) and then the lowest id holding it: four
-// ballots, scanned from the lowest id block, and the first set lane (all scalar work).
-// The pick's key becomes 0, below every non-NaN key. Writes slots 1..8 of row t into
-// `rl` and sets the row's bit in rl.mask; weights are raw / (sum of the 8 raw, in pick
-// order) * route_scale.
+// (sgl_amd_mono/glm53/gfx950/kernel.py:1575-1629). Each lane keeps its best key (the
+// lowest slot among equal keys, i.e. its lowest id), that key's slot and raw score. A
+// round takes the wave maximum of the lanes' best keys (a DPP / permlane butterfly), then
+// the lowest id holding it: ids are slot-major (l + 64 i), so the first of four ballots
+// (one a slot) that is non-empty, and its first lane. Only the picking lane rescans its
+// four keys (the pick's key becomes 0, below every non-NaN key). Writes slots 1..8 of row
+// t into `rl` and sets the row's bit in rl.mask; weights are raw / (sum of the 8 raw, in
+// pick order) * route_scale.
 __device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], const float (&bs)[4],
                                  float route_scale, float* scores_out, int32_t* ids_out,
                                  float* weights_out) {
@@ -42,28 +44,41 @@ __device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], cons
   uint32_t key[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) key[i] = radix_key(sc[i] + bs[i]);
+  uint32_t best;
+  int bi;
+  float braw;
+  auto rescan = [&]() {
+    best = key[0];
+    bi = 0;
+    braw = sc[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+      if (key[i] > best) {  // strict: equal keys keep the lower slot (the lower id)
+        best = key[i];
+        bi = i;
+        braw = sc[i];
+      }
+  };
+  rescan();
   float picked_raw[MOE_TOPK];
   int picked_id[MOE_TOPK];
 #pragma unroll
   for (int r = 0; r < MOE_TOPK; ++r) {
-    uint32_t m = key[0] > key[1] ? key[0] : key[1];
-    const uint32_t m2 = key[2] > key[3] ? key[2] : key[3];
-    m = wave_max_u32(m > m2 ? m : m2);
-    const uint64_t b0 = __ballot(key[0] == m), b1 = __ballot(key[1] == m);
-    const uint64_t b2 = __ballot(key[2] == m), b3 = __ballot(key[3] == m);
+    const uint32_t m = wave_max_u32(best);
+    const bool top = best == m;
+    const uint64_t b0 = __ballot(top && bi == 0), b1 = __ballot(top && bi == 1);
+    const uint64_t b2 = __ballot(top && bi == 2), b3 = __ballot(top && bi == 3);
     const int slot = b0 ? 0 : b1 ? 1 : b2 ? 2 : 3;
     const uint64_t bb = b0 ? b0 : b1 ? b1 : b2 ? b2 : b3;
     const int owner = __ffsll((long long)bb) - 1;
-    const int e = owner + 64 * slot;
-    float mine = sc[0];
+    picked_raw[r] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(braw), owner));
+    picked_id[r] = owner + 64 * slot;
+    if (l == owner) {
 #pragma unroll
-    for (int i = 1; i < 4; ++i)
-      if (i == slot) mine = sc[i];
-    picked_raw[r] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(mine), owner));
-    picked_id[r] = e;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i == slot && l == owner) key[i] = 0;
+      for (int i = 0; i < 4; ++i)
+        if (i == slot) key[i] = 0;
+      rescan();
+    }
   }
   float tot = 0.f;
 #pragma unroll

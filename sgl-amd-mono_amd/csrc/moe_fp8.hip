@@ -522,17 +522,15 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
                 : (uint32_t)(row0 * H + wq * KCW * 128);
       return rsrc(p.w13 + (size_t)e * (2 * I) * H, live ? 2u * I * H : 0u);
     };
-    // Task hand-out: CTA b starts on task b; later tasks come from a device-wide
-    // counter in order (nblk, nblk + 1, ...), grabbed one task ahead so the ring can be
-    // refilled with the next task while this one runs. Tasks run the same arithmetic on
-    // whichever CTA takes them, so results do not depend on the hand-out.
+    // Task hand-out: CTA b runs tasks b and b + nblk first; later tasks come from a
+    // device-wide counter in order (2 nblk, 2 nblk + 1, ...), each grabbed one task ahead
+    // so the ring can be refilled with the next task while this one runs. The first grab
+    // is issued inside the first task: every CTA's grab hits the one counter at about the
+    // same moment and the replies return one after another over microseconds, which a
+    // grab ahead of the first ring would add to the first task's wait (the wave's loads
+    // retire in order). Tasks run the same arithmetic on whichever CTA takes them, so
+    // results do not depend on the hand-out.
     int task = b;
-    // the counter grab goes ahead of the ring so its reply does not queue behind it:
-    // lane 0 of wave 0 only, the others out of range (a branch around it would make its
-    // reply wait before the ring issues)
-    const bool live0 = task < ntask;
-    const uint32_t grab = (uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
-        1, rsrc(queue, live0 ? 4u : 0u), tid == 0 ? 0u : 0x80000000u, 0, 0);
     {
       uint32_t so;
       const __amdgpu_buffer_rsrc_t r = task_src(task, so);
@@ -542,24 +540,16 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         ring[j][1] = ld16s<CP_NT>(r, vo + HO, so + j * CS);
       }
     }
-    if (tid == 0) next_s = live0 ? nblk + (int)grab : ntask;
     // The image, checked while the first task's weights are in flight: every word
     // written (a line fetched early may hold zeros: copy it again, device-coherent). One
-    // pass checks and un-complements: a failed check re-copies all.
+    // pass checks and un-complements: a failed check re-copies all. The first pass waits
+    // for the image copy only (the 2 KCW ring loads issued after it stay in flight) and
+    // sits outside the retry loop: an LDS access reached from a re-copy issued behind the
+    // ring would make the compiler wait for every load, the whole ring, before it.
     {
       uint32_t* xw = reinterpret_cast<uint32_t*>(xq_lds);
-      bool got = ok_s != 0;  // set before the barrier above
-      int polls = 0;
-      uint64_t start = 0;
-      while (got) {
-        // the first pass waits for the image copy only (the 2 KCW ring loads issued after
-        // it stay in flight); a re-copy was issued after them
-        if (polls == 0)
-          __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * KCW));
-        else
-          drain();
-        asm volatile("" ::: "memory");
-        __syncthreads();
+      bool got = ok_s != 0;  // set before the barrier above (CTA-uniform)
+      auto check = [&]() {
         int zero = 0;
         static_assert(G::SZ_XQ / 4 % G::THREADS == 0, "whole passes over the image");
 #pragma unroll 7
@@ -568,7 +558,15 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
           zero |= v == 0u;
           xw[i] = ~v;
         }
-        if (!__syncthreads_or(zero)) break;
+        return __syncthreads_or(zero) != 0;
+      };
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * KCW));
+      asm volatile("" ::: "memory");
+      __syncthreads();
+      bool bad = got && check();
+      int polls = 0;
+      uint64_t start = 0;
+      while (bad) {
         // bounded like every wait: the guard's deadline and abort flag
         if ((++polls & 15) == 0) {
           if (guard.aborted()) got = false;
@@ -580,7 +578,12 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
           }
         }
         got = __syncthreads_or(got ? 0 : 1) == 0 && got;
-        if (got) copy_image(0, G::WAVES, true);
+        if (!got) break;
+        copy_image(0, G::WAVES, true);
+        drain();
+        asm volatile("" ::: "memory");
+        __syncthreads();
+        bad = check();
       }
       if (!got) ok_s = 0;
     }
@@ -589,7 +592,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       ok = false;
       ntask = 0;
     }
-    int next = next_s;
+    int next = b + nblk < ntask ? b + nblk : ntask;
     while (task < ntask) {
       const int u = task / NUG, cc = task % NUG;
       const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
@@ -624,7 +627,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         __builtin_amdgcn_sched_barrier(0);
       }
       red[w][l] = acc;
-      if (tid == 0) next_s = grab_on ? nblk + (int)grabbed : ntask;
+      if (tid == 0) next_s = grab_on ? 2 * nblk + (int)grabbed : ntask;
       __syncthreads();
       const int after = next_s;
       if (tid < 256) {
