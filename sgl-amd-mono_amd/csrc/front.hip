@@ -5,15 +5,18 @@
 //       140 FP8 16-row tiles over the whole K, the head weights (W_w [64, 7168] bf16) as
 //       28 tasks of 16 rows x 1024 K (partials summed in a fixed order by their reader)
 //       (sgl_amd_mono/glm53/gfx950/kernel.py:1781-1970, stage_x_rmsnorm :1367-1402);
-//   A'  four tasks a row on the last 4R CTAs: q_an = bf16(rmsnorm(q_a) g_q) (:1978-2003);
-//       the KV row, kv_n = bf16(rmsnorm(kv_a[:512]) g_kv) and k_pe = bf16(rope(kv_a[512:]))
+//   A'  tasks (row, kind) on the last 4R CTAs, which hold no B or C tile when the rest
+//       of the grid can hold them all: the KV row, kv_n = bf16(rmsnorm(kv_a[:512]) g_kv)
+//       and k_pe = bf16(rope(kv_a[512:]))
 //       as E4M3 with a power-of-two per-token scale (:2005-2101); the index key,
 //       LayerNorm, RoPE on dims 0..63, FWHT-128, FP4 (e2m1 + e8m0 per 32) into SGLang's
 //       index plane (:2103-2180, deepseek_v4 indexer.py:143-151); the head weights,
 //       bf16(w) 128^-1/2 64^-1/2 (indexer.py:400-406);
-//   B   q_b (W_qb [6144, 1536]) and the index query (W_iq [8192, 1536]) over q_an: 448
-//       tiles of 32 rows; q_b's nope rows go on in bf16, its rope rows are rotated in
-//       the epilogue (adjacent rows in adjacent lanes) into q[.., 512:] (:2183-2353);
+//   B   q_an = bf16(rmsnorm(q_a) g_q) (:1978-2003), built in LDS by every B CTA from
+//       A's q_a (no hand-off through A'), then q_b (W_qb [6144, 1536]) and the index
+//       query (W_iq [8192, 1536]) over it: 448 tiles of 32 rows; q_b's nope rows go on in
+//       bf16, its rope rows are rotated in the epilogue (adjacent rows in adjacent lanes,
+//       factors read from the cos / sin tables) into q[.., 512:] (:2183-2353);
 //   B'  the index query, RoPE, FWHT-128, FP4 per head (one wave a head, lane l holding
 //       dims 2l, 2l + 1) (indexer.py:311-338);
 //   C   the absorbed query q_lat = bf16(W_UK q_nope), 4 tiles of 128 latent rows a head
@@ -59,11 +62,9 @@ struct FrontScratch {
   // one parity's hand-off buffers (complemented words)
   static constexpr size_t HA = 0;                                           // f32 [16][2240]
   static constexpr size_t HW = HA + (size_t)FR_MAXR * FR_HA * 4;            // f32 [7][16][64]
-  static constexpr size_t HQ = HW + (size_t)FR_WCH * FR_MAXR * FR_IH * 4;   // bf16 [16][1536]
-  static constexpr size_t HN = HQ + (size_t)FR_MAXR * FR_QL * 2;            // bf16 [16][32][128]
+  static constexpr size_t HN = HW + (size_t)FR_WCH * FR_MAXR * FR_IH * 4;   // bf16 [16][32][128]
   static constexpr size_t HI = HN + (size_t)FR_MAXR * FR_HEADS * FR_NOPE * 2;  // bf16 [16][8192]
-  static constexpr size_t RP = HI + (size_t)FR_MAXR * FR_IQ * 2;            // f32 [16][64]
-  static constexpr size_t PARITY = (RP + (size_t)FR_MAXR * 64 * 4 + 255) & ~(size_t)255;
+  static constexpr size_t PARITY = (HI + (size_t)FR_MAXR * FR_IQ * 2 + 255) & ~(size_t)255;
   static constexpr size_t BYTES = 2 * PARITY;
 };
 
@@ -202,16 +203,26 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
   // the hand-off buffers of this launch
   auto rHA = [&]() { return rsrc(cur + FrontScratch::HA, FR_MAXR * FR_HA * 4); };
   auto rHW = [&]() { return rsrc(cur + FrontScratch::HW, FR_WCH * FR_MAXR * FR_IH * 4); };
-  auto rHQ = [&]() { return rsrc(cur + FrontScratch::HQ, FR_MAXR * FR_QL * 2); };
   auto rHN = [&]() { return rsrc(cur + FrontScratch::HN, FR_MAXR * FR_HEADS * FR_NOPE * 2); };
   auto rHI = [&]() { return rsrc(cur + FrontScratch::HI, FR_MAXR * FR_IQ * 2); };
-  auto rRP = [&]() { return rsrc(cur + FrontScratch::RP, FR_MAXR * 64 * 4); };
+  // the RoPE factors of row r's position, pair j, from the bf16 tables (as A' kind 1)
+  auto rope_at = [&](int r, int j, float& cs, float& sn) {
+    const int64_t pos = p.positions[r];
+    const uint32_t po = pos >= 0 && pos < p.rope_rows ? (uint32_t)(pos * 32 + j) * 2u : 0x80000000u;
+    cs = bf16_lo((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc(p.cos, (uint32_t)p.rope_rows * 64u), po, 0, 0));
+    sn = bf16_lo((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc(p.sin, (uint32_t)p.rope_rows * 64u), po, 0, 0));
+  };
   const int nap = 4 * R;            // A' tasks: the last nap CTAs
   const bool is_a = b < FR_ATASKS;
   const bool is_ap = b >= G - nap;
 
   // ---------------------------------------------------------------- B / C jobs
-  const int jb0 = b, jb1 = b + G;
+  // B and C tiles go to the CTAs without an A' task when those hold them all (two B
+  // tiles each): a tile placed behind an A' task (index key, KV row) would wait for it,
+  // and B', C and the end of the launch for the tile
+  const int nbc = 2 * (G - nap) >= FR_BT ? G - nap : G;
+  const bool bc = b < nbc;
+  const int jb0 = bc ? b : FR_BT, jb1 = bc ? b + nbc : FR_BT;
   auto bjob = [&](int j) {
     GemvJob jb{};
     const bool qb = j < FR_QBT;
@@ -226,7 +237,7 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
   };
   const GemvJob jB0 = bjob(jb0), jB1 = bjob(jb1);
   const int tb0 = jb0 < FR_QBT ? jb0 : jb0 - FR_QBT, tb1 = jb1 < FR_QBT ? jb1 : jb1 - FR_QBT;
-  const int cidx = G - 1 - b;  // this CTA's W_UK tile (if < 128)
+  const int cidx = bc ? nbc - 1 - b : -1;  // this CTA's W_UK tile (if 0 .. 127)
   GemvJob jC{};
   jC.w = p.w_uk;
   jC.s = p.s_uk;
@@ -410,39 +421,9 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
         const int u = b - (G - nap), r = u >> 2, kind = u & 3;
         bool ok = true;
         if (kind == 0) {
-          // q_an = bf16(rmsnorm(q_a) g_q) -> HQ
-          const bool on = tid < FR_QL / 4;
-          v4i v;
-          ok = wait_until(guard, MONO_SITE_FRONT_A, [&]() {
-            v = ld16<CP_DEV>(rHA(), on ? (uint32_t)(r * FR_HA + 4 * tid) * 4u : 0x80000000u);
-            const uint32_t mn = min(min((uint32_t)v[0], (uint32_t)v[1]),
-                                    min((uint32_t)v[2], (uint32_t)v[3]));
-            return __all(!on || mn != 0u);
-          });
-          ok = cta_all(ok, ok_s);
-          if (ok) {
-            float a[4], s = 0.f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              a[q] = on ? dec_f((uint32_t)v[q]) : 0.f;
-              s = fmaf(a[q], a[q], s);
-            }
-            const float rs = __builtin_amdgcn_rsqf(block_red(s, sred, false) * (1.0f / FR_QL) + p.eps);
-            if (on) {
-              const v2i gq = ld8<CP_NONE>(rsrc(p.g_q, FR_QL * 2), (uint32_t)(4 * tid) * 2u);
-              uint32_t pr[2];
-#pragma unroll
-              for (int j = 0; j < 2; ++j) {
-                const uint32_t gw = (uint32_t)gq[j];
-                pr[j] = bf16_bits(a[2 * j] * rs * bf16_lo(gw)) |
-                        (bf16_bits(a[2 * j + 1] * rs * bf16_hi(gw)) << 16);
-              }
-              st_dev64(reinterpret_cast<uint64_t*>(cur + FrontScratch::HQ) + (r * FR_QL + 4 * tid) / 4,
-                       (uint64_t)enc_pair(pr[0]) | ((uint64_t)enc_pair(pr[1]) << 32));
-            }
-          }
+          // q_an is built by every stage-B CTA from q_a: nothing to do
         } else if (kind == 1) {
-          // the KV row -> cache (E4M3 + power-of-two scale), and the row's RoPE factors
+          // the KV row -> cache (E4M3 + power-of-two scale)
           const int64_t pos = sld(p.positions, r), slot = sld(p.slots, r);
           const bool on = tid < FR_KVA / 2;       // pair i = tid
           const bool pe = tid >= FR_KVL / 2 && on;
@@ -459,11 +440,6 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
           });
           ok = cta_all(ok, ok_s);
           if (ok) {
-            if (tid < 32) {  // publish the RoPE factors of row r
-              uint32_t* rp = reinterpret_cast<uint32_t*>(cur + FrontScratch::RP) + r * 64;
-              st_dev(rp + tid, enc_f(cs));
-              st_dev(rp + 32 + tid, enc_f(sn));
-            }
             const float a = on ? dec_f((uint32_t)v[0]) : 0.f, c = on ? dec_f((uint32_t)v[1]) : 0.f;
             const float ss = block_red(pe || !on ? 0.f : fmaf(a, a, c * c), sred, false);
             const float rs = __builtin_amdgcn_rsqf(ss * (1.0f / FR_KVL) + p.eps);
@@ -573,7 +549,7 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
 
   // ---------------------------------------------------------------- B: q_b, W_iq
   bool okb = true;
-  {
+  if (jb0 < FR_BT) {
     const int tid = opaque_v((int)threadIdx.x);
     const int l = tid & 63, w = tid >> 6;
     const GemvB gb(tid);
@@ -584,29 +560,65 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
     const int en = ((ej < FR_QBT ? ej : ej - FR_QBT) * 2 + rge) * 16 + erow;
     const bool epe = ej < FR_QBT && en % FR_QHD >= FR_NOPE && etok < R && ej < FR_BT;
     const int epair = (en % FR_QHD - FR_NOPE) >> 1;
-    v4i xa[3][2];
-    uint32_t rcw = 0, rsw = 0;
+    // the epilogue's RoPE factors (row etok, pair epair) from the bf16 tables
+    float ecs = 0.f, esn = 0.f;
+    if (epe) rope_at(etok, epair, ecs, esn);
+    // q_an = bf16(rmsnorm(q_a) g_q) of every row, built by this CTA: thread tid holds 12
+    // q_a values of row tid / 128 (A's f32 outputs, complemented words: the loads are the
+    // wait), the row's sum of squares over its two waves in a fixed order, then the
+    // products into LDS (stage A's x buffer), where the MFMA operands are read from
+    constexpr int QNS = FR_QL + 8;  // LDS row stride of q_an (bf16)
+    static_assert(FR_MAXR * QNS <= FR_XG * FR_XS, "q_an fits the x buffer");
+    const int qr = tid >> 7, qc = (tid & 127) * 12;
+    const bool qon = qr < R;
+    const __amdgpu_buffer_rsrc_t rg = rsrc(p.g_q, FR_QL * 2);
+    const v4i g0 = ld16<CP_NONE>(rg, (uint32_t)qc * 2u);
+    const v2i g1 = ld8<CP_NONE>(rg, (uint32_t)qc * 2u + 16u);
+    v4i qv[3];
     okb = wait_until(guard, MONO_SITE_QAN, [&]() {
       uint32_t mn = 0xFFFFFFFFu;
 #pragma unroll
-      for (int s = 0; s < 3; ++s)
+      for (int i = 0; i < 3; ++i) {
+        qv[i] = ld16<CP_DEV>(rHA(), qon ? (uint32_t)(qr * FR_HA + qc + 4 * i) * 4u : 0x80000000u);
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const uint32_t off = t < R ? (uint32_t)(t * FR_QL + gb.k0(s) + 16 * grp + 8 * m) * 2u : 0x80000000u;
-          xa[s][m] = ld16<CP_DEV>(rHQ(), off);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) mn = min(mn, (uint32_t)xa[s][m][q]);
-        }
-      rcw = (uint32_t)ld4<CP_DEV>(rRP(), epe ? (uint32_t)(etok * 64 + epair) * 4u : 0x80000000u);
-      rsw = (uint32_t)ld4<CP_DEV>(rRP(), epe ? (uint32_t)(etok * 64 + 32 + epair) * 4u : 0x80000000u);
-      return __all((t >= R || mn != 0u) && (!epe || min(rcw, rsw) != 0u));
+        for (int q = 0; q < 4; ++q) mn = min(mn, (uint32_t)qv[i][q]);
+      }
+      return __all(!qon || mn != 0u);
     });
     okb = cta_all(okb, ok_s);
+    v4i xa[3][2];
     if (okb) {
+      float a[12], s = 0.f;
 #pragma unroll
-      for (int s = 0; s < 3; ++s)
+      for (int i = 0; i < 12; ++i) {
+        a[i] = qon ? dec_f((uint32_t)qv[i / 4][i % 4]) : 0.f;
+        s = fmaf(a[i], a[i], s);
+      }
+      s = wave_sum(s);
+      if (l == 0) sred[w] = s;
+      __syncthreads();
+      const float rs = __builtin_amdgcn_rsqf((sred[2 * qr] + sred[2 * qr + 1]) * (1.0f / FR_QL) + p.eps);
+      if (qon) {
+        const uint32_t gw[6] = {(uint32_t)g0[0], (uint32_t)g0[1], (uint32_t)g0[2], (uint32_t)g0[3],
+                                (uint32_t)g1[0], (uint32_t)g1[1]};
+        uint32_t pr[6];
 #pragma unroll
-        for (int m = 0; m < 2; ++m) xa[s][m] = ~xa[s][m];
+        for (int j = 0; j < 6; ++j)
+          pr[j] = bf16_bits(a[2 * j] * rs * bf16_lo(gw[j])) |
+                  (bf16_bits(a[2 * j + 1] * rs * bf16_hi(gw[j])) << 16);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(&xs[qr * QNS + qc]);
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+          *reinterpret_cast<v2i*>(dst + 2 * j) = v2i{(int)pr[2 * j], (int)pr[2 * j + 1]};
+      }
+      __syncthreads();
+      const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+      for (int s2 = 0; s2 < 3; ++s2)
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          xa[s2][m] = t < R ? *reinterpret_cast<const v4i*>(&xs[t * QNS + gb.k0(s2) + 16 * grp + 8 * m])
+                            : zero;
       const bool two = jb1 < FR_BT;
       if (jb0 < FR_BT) gb.dot(wb0, sb0, xa, red);
       if (two) gb.dot(wb1, sb1, xa, red + 16);
@@ -621,7 +633,7 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
         const bool qb = ej < FR_QBT;
         const int head = en / FR_QHD, d = en % FR_QHD;
         if (qb && d >= FR_NOPE) {
-          const float cs = dec_f(rcw), sn = dec_f(rsw);
+          const float cs = ecs, sn = esn;
           const float yp = dpp_f<DPP_XOR1>(y);  // the pair's other row
           y = (erow & 1) == 0 ? y * cs - yp * sn : yp * sn + y * cs;
         }
@@ -649,20 +661,19 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
     const int tid = opaque_v((int)threadIdx.x);
     const int l = tid & 63, w = tid >> 6;
     const int r = b >> 2, hi = (b & 3) * 16 + w;
-    uint32_t xw = 0, rcw = 0, rsw = 0;
+    uint32_t xw = 0;
     const bool rp = l < FR_PE / 2;
+    float cs = 0.f, sn = 0.f;
+    rope_at(r, l & 31, cs, sn);
     bool ok = wait_until(guard, MONO_SITE_QB, [&]() {
       xw = (uint32_t)ld4<CP_DEV>(rHI(), (uint32_t)((r * FR_IH + hi) * 64 + l) * 4u);
-      rcw = (uint32_t)ld4<CP_DEV>(rRP(), (uint32_t)(r * 64 + (l & 31)) * 4u);
-      rsw = (uint32_t)ld4<CP_DEV>(rRP(), (uint32_t)(r * 64 + 32 + (l & 31)) * 4u);
-      return __all(xw != 0u && min(rcw, rsw) != 0u);
+      return __all(xw != 0u);
     });
     ok = cta_all(ok, ok_s);
     if (ok) {
       const uint32_t pr = ~xw;
       float v0 = bf16_lo(pr), v1 = bf16_hi(pr);
       if (rp) {
-        const float cs = dec_f(rcw), sn = dec_f(rsw);
         const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
         v0 = r0;
         v1 = r1;
@@ -803,9 +814,10 @@ extern "C" int mono_front_launch(const MonoFrontArgs* a, mono_stream_t stream) {
   int grid = 0;
   int rc = monokernel_grid(&grid);
   if (rc) return rc;
-  // every stage-A task, every row task and every W_UK tile on a CTA of its own
-  if (grid > FR_MAX_GRID || grid < FR_ATASKS + 4 * a->rows || grid < FR_CT)
-    return set_error(MONO_E_DEVICE, "mono_front_launch: needs 232..1024 CUs");
+  // every stage-A task, every row task and every W_UK tile on a CTA of its own, and at
+  // most two B tiles a CTA
+  if (grid > FR_MAX_GRID || grid < FR_ATASKS + 4 * a->rows || grid < FR_CT || 2 * grid < FR_BT)
+    return set_error(MONO_E_DEVICE, "mono_front_launch: needs 224..1024 CUs (and 168 + 4 rows)");
   rc = check_coresident(front_kernel, 1024, 0,
                         "mono_front_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;
