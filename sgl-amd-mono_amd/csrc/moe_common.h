@@ -129,8 +129,8 @@ __device__ inline int wave_prefix(int v, int& total) {
 }
 
 // Compact rl.mask into the distinct list (one whole wave): u = 0 the shared expert,
-// then routed ids ascending; then the (expert, row) slots.
-__device__ inline void build_distinct(RouteLds& rl, int rows) {
+// then routed ids ascending, with each one's row mask. The up/gate stage needs only this.
+__device__ inline void build_experts(RouteLds& rl, int rows) {
   const int l = lane_id();
   uint32_t m[4];
   int cnt = 0;
@@ -141,31 +141,59 @@ __device__ inline void build_distinct(RouteLds& rl, int rows) {
   }
   int nroute = 0;
   int pos = 1 + wave_prefix<3>(cnt, nroute);
-  const int nd = 1 + nroute;
-  const uint32_t shared_mask = rows >= 32 ? 0xFFFFFFFFu : ((1u << rows) - 1u);
-  // (expert, row) slots, experts in u order: slot base of each of this lane's experts
-  int c2 = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) c2 += __popc(m[i]);
-  int nslot = 0;
-  int s = __popc(shared_mask) + wave_prefix<7>(c2, nslot);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (m[i]) {
       rl.uexp[pos] = 4 * l + i;
       rl.umask[pos] = m[i];
-      rl.uslot[pos] = s;
-      for (uint32_t mm = m[i]; mm; mm &= mm - 1) rl.slot_ut[s++] = (pos << 8) | (__ffs(mm) - 1);
       ++pos;
     }
   if (l == 0) {
-    rl.nd = nd;
+    rl.nd = 1 + nroute;
     rl.uexp[0] = MOE_SHARED;
-    rl.umask[0] = shared_mask;
+    rl.umask[0] = rows >= 32 ? 0xFFFFFFFFu : ((1u << rows) - 1u);
+  }
+}
+
+// The (expert, row) slots of the distinct list built by build_experts (one whole wave;
+// the list visible to it): uslot[u], the first slot of u (its rows in order), and
+// slot_ut, slot -> (u << 8) | row. The mid quant and down stages need these.
+__device__ inline void build_slots(RouteLds& rl, int rows) {
+  const int l = lane_id();
+  const int nd = rl.nd;
+  const uint32_t shared_mask = rows >= 32 ? 0xFFFFFFFFu : ((1u << rows) - 1u);
+  // lane l takes distinct experts u = 1 + 4 l .. 1 + 4 l + 3 (routed ones, in u order)
+  uint32_t m[4];
+  int c2 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = 1 + 4 * l + i;
+    m[i] = u < nd ? rl.umask[u] : 0u;
+    c2 += __popc(m[i]);
+  }
+  int nslot = 0;
+  int s = __popc(shared_mask) + wave_prefix<7>(c2, nslot);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = 1 + 4 * l + i;
+    if (u < nd) {
+      rl.uslot[u] = s;
+      for (uint32_t mm = m[i]; mm; mm &= mm - 1) rl.slot_ut[s++] = (u << 8) | (__ffs(mm) - 1);
+    }
+  }
+  if (l == 0) {
     rl.uslot[0] = 0;
     int s0 = 0;
     for (uint32_t mm = shared_mask; mm; mm &= mm - 1) rl.slot_ut[s0++] = __ffs(mm) - 1;
   }
+}
+
+// both, in order (the lists of build_experts written before build_slots reads them: one
+// wave's LDS accesses complete in order)
+__device__ inline void build_distinct(RouteLds& rl, int rows) {
+  build_experts(rl, rows);
+  __builtin_amdgcn_wave_barrier();
+  build_slots(rl, rows);
 }
 
 // the slot of (u, row t), or -1 when row t is not routed to u

@@ -493,7 +493,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   }
   if (!ok) ok_s = 0;
   __syncthreads();
-  if (w == 0) build_distinct(rl, R);
+  if (w == 0) build_experts(rl, R);  // the slot tables follow the first ring's loads
   __syncthreads();
   ok = ok_s != 0;
   const int nd = rl.nd;
@@ -540,6 +540,9 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         ring[j][1] = ld16s<CP_NT>(r, vo + HO, so + j * CS);
       }
     }
+    // the (expert, row) slot tables, needed from the mid quant on: built while the first
+    // ring is in flight (the image check's barrier publishes them)
+    if (w == 0) build_slots(rl, R);
     // The image, checked while the first task's weights are in flight: every word
     // written (a line fetched early may hold zeros: copy it again, device-coherent). One
     // pass checks and un-complements: a failed check re-copies all. The first pass waits
