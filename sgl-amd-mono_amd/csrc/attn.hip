@@ -13,7 +13,8 @@
 //      keep the bin of the 2048th key until its few candidates rank themselves; the
 //      selection (every element up to the threshold element of the order key
 //      descending, position ascending) is published as (position, tag) pairs.
-//   3  split: task (row, 64-key split), all 32 heads. The split's tokens (through the
+//   3  split: task (row, SPLIT-key split), all 32 heads (SPLIT 64 when the rows' 32
+//      splits each fill the grid once, else 128). The split's tokens (through the
 //      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
 //      widened exactly), times the token's scale and the softmax scale; per head the
 //      split's max m and sum l; P, with the token's scale folded in, as bf16; O = P V on
@@ -43,8 +44,9 @@ constexpr int AT_LAT = 512;
 constexpr int AT_PAGE = 64;
 constexpr int AT_CHUNK = 1024;    // tokens of a score task
 constexpr int AT_NCHUNK = AT_MAXCTX / AT_CHUNK;
-constexpr int AT_SPLIT = 64;      // keys of a split task
-constexpr int AT_NSPLIT = AT_TOPK / AT_SPLIT;
+// keys of a split task: 64 when the rows' splits (32 a row) fill the grid once, else 128
+// (16 a row); scratch is laid out for the most splits a row
+constexpr int AT_NSPLIT = AT_TOPK / 64;
 constexpr int AT_MAXR = 48;
 
 constexpr size_t at_align(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -109,8 +111,11 @@ __device__ inline v4f mfma_bf16(v8bf a, v8bf b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+template <int SPLIT>
 __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   using S = AttnScratch;
+  static_assert(SPLIT == 64 || SPLIT == 128, "64- or 128-key splits");
+  constexpr int NSP = AT_TOPK / SPLIT;  // splits a row
   const int tid = threadIdx.x, l = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R = p.rows;
@@ -270,19 +275,19 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   {
     // LDS: K rows (E4M3, 576 + 16 bytes apart), q (bf16, 1152 + 16), S (f32), P (bf16),
     // the split's slots and token scales, the row's page-table entries
-    static_assert(AT_SPLIT == 64, "QK: 4 key tiles x 2 head tiles x 2 K chains; softmax: a key a lane");
-    constexpr int KSTR = AT_KV + 16, QSTR = AT_KV * 2 + 16, SSTR = AT_SPLIT + 4,
-                  PSTR = AT_SPLIT * 2 + 16;
+    constexpr int KSTR = AT_KV + 16, QSTR = AT_KV * 2 + 16, SSTR = SPLIT + 4,
+                  PSTR = SPLIT * 2 + 16;
+    constexpr int NSB = SPLIT == 64 ? 2 : 1;  // S buffers: the two K chains (64), or summed
     constexpr int NPG = AT_MAXCTX / AT_PAGE;
     uint8_t* kbuf = smem;
-    uint8_t* qbuf = kbuf + AT_SPLIT * KSTR;
+    uint8_t* qbuf = kbuf + SPLIT * KSTR;
     float* sbuf = reinterpret_cast<float*>(qbuf + AT_HEADS * QSTR);
-    uint8_t* pbuf = reinterpret_cast<uint8_t*>(sbuf + 2 * AT_HEADS * SSTR);  // S: two K chains
+    uint8_t* pbuf = reinterpret_cast<uint8_t*>(sbuf + NSB * AT_HEADS * SSTR);
     int32_t* slot_s = reinterpret_cast<int32_t*>(pbuf + AT_HEADS * PSTR);
-    float* ksc = reinterpret_cast<float*>(slot_s + AT_SPLIT);
-    int32_t* pt_s = reinterpret_cast<int32_t*>(ksc + AT_SPLIT);
-    static_assert(AT_SPLIT * KSTR + AT_HEADS * QSTR + 2 * AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
-                          AT_SPLIT * 8 + NPG * 4 <=
+    float* ksc = reinterpret_cast<float*>(slot_s + SPLIT);
+    int32_t* pt_s = reinterpret_cast<int32_t*>(ksc + SPLIT);
+    static_assert(SPLIT * KSTR + AT_HEADS * QSTR + NSB * AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
+                          SPLIT * 8 + NPG * 4 <=
                       (int)sizeof(smem),
                   "split LDS");
     static_assert(NPG <= AT_THREADS, "a page-table entry a thread");
@@ -290,15 +295,15 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     constexpr int NQP = (QP + AT_THREADS - 1) / AT_THREADS;
     const __amdgpu_buffer_rsrc_t rkv = rsrc(p.kv, p.kv_slots * (uint32_t)AT_KV);
     const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, p.kv_slots * 4u);
-    const int nt = R * AT_NSPLIT;
+    const int nt = R * NSP;
     for (int t0 = 0; t0 < nt; t0 += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
       const int task = t0 + (b + nblk - (R % nblk)) % nblk;  // rows' top-k CTAs go last
       if (task >= nt) continue;
-      const int r = task / AT_NSPLIT, sp = task % AT_NSPLIT;
+      const int r = task / NSP, sp = task % NSP;
       const int n = row_n(r);
       const int k = n < AT_TOPK ? n : AT_TOPK;
-      const int kcnt = k - sp * AT_SPLIT < AT_SPLIT ? k - sp * AT_SPLIT : AT_SPLIT;
+      const int kcnt = k - sp * SPLIT < SPLIT ? k - sp * SPLIT : SPLIT;
       if (kcnt <= 0) continue;
       // ahead of the wait (neither depends on the selection): the row's q, all heads
       // ([32][576] bf16), and its page-table entries
@@ -315,9 +320,9 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
                          : 0x80000000u);
       // the split's tokens, polled as (position, tag) pairs
       int pos = -1;
-      if (tid < AT_SPLIT) {
+      if (tid < SPLIT) {
         uint64_t v = 0;
-        const uint64_t* src = topk + (size_t)r * AT_TOPK + sp * AT_SPLIT + tid;
+        const uint64_t* src = topk + (size_t)r * AT_TOPK + sp * SPLIT + tid;
         ok = wait_until(guard, MONO_SITE_TOPK, [&]() {
           v = tid < kcnt ? ld_dev64(src) : pair(0u, tag);
           return __all((uint32_t)(v >> 32) == tag);
@@ -334,14 +339,14 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       ok = cta_all(ok, ok_s);
       if (!ok) break;
       // position -> cache slot through the page table in LDS
-      if (tid < AT_SPLIT) slot_s[tid] = pos >= 0 ? pt_s[pos >> 6] * AT_PAGE + (pos & 63) : -1;
+      if (tid < SPLIT) slot_s[tid] = pos >= 0 ? pt_s[pos >> 6] * AT_PAGE + (pos & 63) : -1;
       __syncthreads();
       // gather the rows: 36 pieces of 16 bytes a row (a dead slot reads zeros), and the
       // token scales, in one round trip
       {
-        constexpr int GP = AT_SPLIT * (AT_KV / 16);
+        constexpr int GP = SPLIT * (AT_KV / 16);
         constexpr int NGP = (GP + AT_THREADS - 1) / AT_THREADS;
-        const int slot = tid < AT_SPLIT ? slot_s[tid] : -1;
+        const int slot = tid < SPLIT ? slot_s[tid] : -1;
         const float sc = __int_as_float(
             ld4<CP_NONE>(rks, slot >= 0 ? (uint32_t)slot * 4u : 0x80000000u));
         // every load issued before the first is stored (a load-store loop would wait
@@ -360,12 +365,12 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
           const int j = idx / (AT_KV / 16), c = idx % (AT_KV / 16);
           if (idx < GP) *reinterpret_cast<v4i*>(kbuf + j * KSTR + c * 16) = gv[i];
         }
-        if (tid < AT_SPLIT) ksc[tid] = slot >= 0 ? sc : 0.f;
+        if (tid < SPLIT) ksc[tid] = slot >= 0 ? sc : 0.f;
       }
       __syncthreads();
       // S = q K^T: wave w takes heads 16 (w / 8) .., keys 16 (w % 4) .. and the even (w / 4
       // even) or odd K steps: two MFMA chains a tile, summed (even + odd) by the softmax
-      {
+      if constexpr (SPLIT == 64) {
         const int h0 = 16 * (w >> 3), j0 = 16 * (w & 3), odd = (w >> 2) & 1;
         v4f d = {0.f, 0.f, 0.f, 0.f};
         const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4) + odd * 64;
@@ -380,21 +385,50 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         float* sb = sbuf + odd * AT_HEADS * SSTR;
 #pragma unroll
         for (int e = 0; e < 4; ++e) sb[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e];
+      } else {
+        // wave w takes heads 16 (w / 8) .. and keys 16 (w % 8) ..; two accumulators (even
+        // and odd K steps): two MFMA chains in flight, summed, then scaled
+        const int h0 = 16 * (w >> 3), j0 = 16 * (w & 7);
+        v4f d = {0.f, 0.f, 0.f, 0.f}, d1 = d;
+        const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4);
+        const uint8_t* kr = kbuf + (j0 + (l & 15)) * KSTR + 8 * (l >> 4);
+#pragma unroll 3
+        for (int ks = 0; ks < AT_KV / 32; ks += 2) {
+          const v8bf a0 = *reinterpret_cast<const v8bf*>(qa + ks * 64);
+          const v2i k0 = *reinterpret_cast<const v2i*>(kr + ks * 32);
+          const v8bf a1 = *reinterpret_cast<const v8bf*>(qa + ks * 64 + 64);
+          const v2i k1 = *reinterpret_cast<const v2i*>(kr + ks * 32 + 32);
+          d = mfma_bf16(a0, fp8x8_bf16((uint32_t)k0[0], (uint32_t)k0[1]), d);
+          d1 = mfma_bf16(a1, fp8x8_bf16((uint32_t)k1[0], (uint32_t)k1[1]), d1);
+        }
+        d += d1;
+        const float f = ksc[j0 + (l & 15)] * p.sm_scale;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sbuf[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e] * f;
       }
       __syncthreads();
-      // softmax of the split, per head: wave w takes heads 2w, 2w + 1; lane l key l
+      // softmax of the split, per head: wave w takes heads 2w, 2w + 1; lane l keys l (and
+      // l + 64 in a 128-key split)
       float* ml = mls + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * 2;
       const float f0 = ksc[l] * p.sm_scale;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int h = 2 * w + hh;
-        const bool v0 = l < kcnt;
-        const float s0 = v0 ? (sbuf[h * SSTR + l] + sbuf[(AT_HEADS + h) * SSTR + l]) * f0 : -INFINITY;
-        const float m = wave_max(s0);
-        const float p0 = v0 ? expf(s0 - m) : 0.f;
-        const float lsum = wave_sum(p0);
+        const bool v0 = l < kcnt, v1 = SPLIT == 128 && l + 64 < kcnt;
+        float s0, s1 = -INFINITY;
+        if constexpr (SPLIT == 64) {
+          s0 = v0 ? (sbuf[h * SSTR + l] + sbuf[(AT_HEADS + h) * SSTR + l]) * f0 : -INFINITY;
+        } else {
+          s0 = v0 ? sbuf[h * SSTR + l] : -INFINITY;
+          s1 = v1 ? sbuf[h * SSTR + l + 64] : -INFINITY;
+        }
+        const float m = wave_max(fmaxf(s0, s1));
+        const float p0 = v0 ? expf(s0 - m) : 0.f, p1 = v1 ? expf(s1 - m) : 0.f;
+        const float lsum = wave_sum(p0 + p1);
         // P with the token's scale folded in (V = E4M3 value x scale)
         reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l] = (uint16_t)bf16_bits(p0 * ksc[l]);
+        if constexpr (SPLIT == 128)
+          reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l + 64] = (uint16_t)bf16_bits(p1 * ksc[l + 64]);
         if (l == 0) {
           st_devf(ml + 2 * h, m);
           st_devf(ml + 2 * h + 1, lsum);
@@ -409,7 +443,7 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         v4f o0 = {0.f, 0.f, 0.f, 0.f}, o1 = o0, o2 = o0, o3 = o0;
         const uint8_t* pa = pbuf + (h0 + c) * PSTR + 16 * g;
 #pragma unroll
-        for (int kst = 0; kst < AT_SPLIT / 32; ++kst) {
+        for (int kst = 0; kst < SPLIT / 32; ++kst) {
           const v8bf a = *reinterpret_cast<const v8bf*>(pa + kst * 64);
           uint32_t dv[8];
 #pragma unroll
@@ -466,24 +500,25 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       const int r = task / AT_HEADS, h = task % AT_HEADS;
       const int n = row_n(r);
       const int k = n < AT_TOPK ? n : AT_TOPK;
-      const int nsp = (k + AT_SPLIT - 1) / AT_SPLIT;
+      const int nsp = (k + SPLIT - 1) / SPLIT;
       if (w == 0 && nsp > 0)
         ok = wait_until(guard, MONO_SITE_SPLIT, [&]() {
           return __all(l >= nsp || ld_dev(&split_done[r * AT_NSPLIT + l]) == tag);
         });
       ok = cta_all(ok, ok_s);
       if (!ok) break;
-      // the split partials and their (m, l) in one round trip: 32 threads a split, 16
+      // the split partials and their (m, l) in one round trip: TPS threads a split, VPT
       // values a thread
-      static_assert(AT_NSPLIT * 32 == AT_THREADS && AT_LAT == 32 * 16, "merge thread map");
-      const int sp = tid >> 5, d16 = tid & 31;
-      v4i a[4];
+      constexpr int TPS = AT_THREADS / NSP, VPT = AT_LAT / TPS;
+      static_assert(VPT % 4 == 0, "merge thread map");
+      const int sp = tid / TPS, dv = tid % TPS;
+      v4i a[VPT / 4];
       {
         const __amdgpu_buffer_rsrc_t ra = rsrc(
             accs + ((size_t)(r * AT_NSPLIT + (sp < nsp ? sp : 0)) * AT_HEADS + h) * AT_LAT,
             sp < nsp ? AT_LAT * 4 : 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = ld16<CP_DEV>(ra, (uint32_t)d16 * 64 + 16 * i);
+        for (int i = 0; i < VPT / 4; ++i) a[i] = ld16<CP_DEV>(ra, (uint32_t)(dv * VPT * 4 + 16 * i));
       }
       if (w == 0) {
         const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
@@ -502,9 +537,9 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       {
         const float ws = sp < nsp ? wsp_s[sp] : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < VPT / 4; ++i) {
           const v4f v = __builtin_bit_cast(v4f, a[i]) * ws;
-          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + 16 * d16 + 4 * i]) = v;
+          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + VPT * dv + 4 * i]) = v;
         }
       }
       __syncthreads();
@@ -597,9 +632,11 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
   int grid = 0;
   int rc = monokernel_grid(&grid);
   if (rc) return rc;
-  rc = check_coresident(attn_kernel, AT_THREADS, 0,
+  // 64-key splits when the rows' 32 splits each take one CTA, else 128-key splits
+  auto kern = p.rows * (AT_TOPK / 64) <= grid ? attn_kernel<64> : attn_kernel<128>;
+  rc = check_coresident(kern, AT_THREADS, 0,
                         "mono_attn_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_kernel, dim3(grid), dim3(AT_THREADS), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(AT_THREADS), 0, (hipStream_t)stream, p);
   return check_launch("mono_attn_launch");
 }

@@ -204,9 +204,12 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
 // padded LDS image, 33 words a thread, so both the coalesced writes and the per-thread
 // reads are conflict-free). A sample (every 32nd position) narrows the key range to one
 // holding about 1.5 TOPK keys, where topk_refine's first pass starts.
-__device__ inline int32_t* topk_select(int tid, __amdgpu_buffer_rsrc_t rs, int n, uint8_t* arena,
-                                       int* wsum, uint32_t* mm, int* res_s,
-                                       uint64_t* ts = nullptr) {
+// Always inlined: called from more than one kernel, it would otherwise become a real call
+// (registers saved through scratch around it, no scheduling across it), which measured
+// ~4 us slower a row.
+__device__ __attribute__((always_inline)) inline int32_t* topk_select(
+    int tid, __amdgpu_buffer_rsrc_t rs, int n, uint8_t* arena, int* wsum, uint32_t* mm,
+    int* res_s, uint64_t* ts = nullptr) {
   int phase = 0;
   auto mark = [&](int k) {
     if (ts && tid == 0) ts[k] = __builtin_amdgcn_s_memtime();
