@@ -213,13 +213,9 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
   Guard guard;
   guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
-  if (w == 0) build_distinct(rl, R);
+  if (w == 0) build_experts(rl, R);  // the slot tables follow the first weight loads
   __syncthreads();
   const int nd = rl.nd;
-  for (int s = tid; s < R * MOE_SLOTS; s += THREADS) {
-    const int ut = rl.slot_ut[s];
-    wslot[s] = route_weight(rl, ut & 255, rl.uexp[ut >> 8]);
-  }
 
   // ---------------------------------------------------------------- stage 1: up/gate
   stamp(p.timeline, MONO_TL_ROUTED);
@@ -249,6 +245,16 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
     for (int j = 0; j < KSW; ++j) issue(b, j, w0[j], c0[j]);
 #pragma unroll
     for (int j = 0; j < KSW; ++j) issue(b + nblk, j, w1[j], c1[j]);
+
+    // the (expert, row) slot tables and each slot's route weight, built while the first
+    // two tasks' weights are in flight
+    if (w == 0) build_slots(rl, R);
+    __syncthreads();
+    for (int s = tid; s < R * MOE_SLOTS; s += THREADS) {
+      const int ut = rl.slot_ut[s];
+      wslot[s] = route_weight(rl, ut & 255, rl.uexp[ut >> 8]);
+    }
+    __syncthreads();
 
     int k = 0;  // tasks this CTA ran (the parity of the reduction buffer)
     auto run = [&](int task, v4i (&wv)[KSW], uint32_t (&code)[KSW]) {
