@@ -18,8 +18,9 @@ every distinct expert the batch routed to (shared included) x 11,012,736 B + the
 3,670,016 B + the rows in and out -- over its own average launch time (a graph of that
 launch alone over the same layers), against 8 TB/s; ``config.phases`` gives every
 phase's time and achieved bandwidth. ``cpu_baseline``: the CPU oracle chain
-(``oracle/front.py``, ``oracle/attn.py``, ``oracle/dense.py``, ``oracle/moe.py``) for one
-of the rows, scaled to the batch, on this host's cores.
+(``oracle/front.py``, ``oracle/attn.py``, ``oracle/dense.py``, ``oracle/moe.py``) for the
+whole layer at all rows on this host's cores (the box's thread share), one warm-up then
+the median of five runs, with the core count and CPU model.
 
 Other workloads (``--workload``): moe_fp8 (configs[1] alone), moe_mxfp4,
 attn, post (the output block alone).
@@ -93,6 +94,48 @@ def traffic_from_profiles(name: str):
     return None
 
 
+def cpu_threads() -> int:
+    """Host threads for the CPU leg: the box's share (OMP_NUM_THREADS), else every core."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's, from /proc/cpuinfo)."""
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.lower().startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_timed(fn, runs: int = 5):
+    """One warm-up call, then the median of ``runs`` timed calls (perf_counter), as the
+    CPU-baseline plan asks. Returns (median s, every run's s)."""
+    import statistics
+
+    import torch
+
+    torch.set_num_threads(cpu_threads())
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def cpu_record(value_us: float, unit: str, sample: str, times) -> dict:
+    import torch
+
+    return {"value": round(value_us, 1), "unit": unit, "cores": torch.get_num_threads(),
+            "kind": "port", "sample": sample, "cpu_count": os.cpu_count(),
+            "cpu_model": cpu_model(), "runs_s": [round(t, 3) for t in times]}
+
+
 def cpu_baseline_mxfp4(x_cpu, logits_cpu, w, ids, rows):
     """The oracle's MXFP4 block on the host, one launch worth (bounded sample)."""
     import numpy as np
@@ -101,19 +144,14 @@ def cpu_baseline_mxfp4(x_cpu, logits_cpu, w, ids, rows):
     from oracle import moe as omoe
     from sgl_amd_mono_amd.dsv32 import synthetic
 
-    torch.set_num_threads(os.cpu_count() or 1)
     experts = {int(e): synthetic.rowmajor_mxfp4_expert(w, int(e)) for e in np.unique(ids)}
     parts = [{e: v[k] for e, v in experts.items()} for k in range(4)]
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        omoe.moe_mxfp4(x_cpu, logits_cpu, w.bias.cpu(), *parts, residual=x_cpu)
-        times.append(time.perf_counter() - t0)
-    us = min(times) * 1e6
-    return {"value": round(us, 1), "unit": f"µs per MXFP4 MoE block ({rows} rows)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"1 MXFP4 block of {rows} rows over its {len(experts)} routed experts, "
-                      f"best of {len(times)}; oracle/moe.py f64 GEMVs on dequantised E2M1"}
+    med, times = cpu_timed(lambda: omoe.moe_mxfp4(x_cpu, logits_cpu, w.bias.cpu(), *parts,
+                                                  residual=x_cpu))
+    return cpu_record(med * 1e6, f"µs per MXFP4 MoE block ({rows} rows)",
+                      f"the whole block: {rows} rows over their {len(experts)} routed experts "
+                      f"(oracle/moe.py, f64 GEMVs on dequantised E2M1), one warm-up then the "
+                      f"median of {len(times)} runs", times)
 
 
 def cpu_baseline(a_cpu, w, ids, rows):
@@ -123,23 +161,15 @@ def cpu_baseline(a_cpu, w, ids, rows):
 
     from oracle import moe as omoe
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    experts = {}
     from sgl_amd_mono_amd.dsv32 import synthetic
 
-    for e in np.unique(ids):
-        experts[int(e)] = synthetic.rowmajor_expert(w, int(e))
+    experts = {int(e): synthetic.rowmajor_expert(w, int(e)) for e in np.unique(ids)}
     args = (a_cpu, w.g_post.cpu(), w.w_r.cpu(), w.bias.cpu(), None, None, None, None)
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        omoe.moe_fp8(*args, experts=experts)
-        times.append(time.perf_counter() - t0)
-    us = min(times) * 1e6
-    return {"value": round(us, 1), "unit": "µs per layer (MoE block, 8 rows)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"1 MoE block of {rows} rows over its {len(experts)} routed experts, "
-                      f"best of {len(times)}; oracle/moe.py f64 GEMVs on dequantised E4M3"}
+    med, times = cpu_timed(lambda: omoe.moe_fp8(*args, experts=experts))
+    return cpu_record(med * 1e6, f"µs per MoE block ({rows} rows)",
+                      f"the whole block: {rows} rows over their {len(experts)} routed experts "
+                      f"(oracle/moe.py, f64 GEMVs on dequantised E4M3), one warm-up then the "
+                      f"median of {len(times)} runs", times)
 
 
 def time_graph(launch, L: int, steps: int, warmup: int):
@@ -282,25 +312,21 @@ def bench_moe_mxfp4(args):
 
 
 def cpu_baseline_attn(inp, sm_scale, rows):
-    """The oracle's attention chain on the host for one row (bounded sample), scaled to
-    the launch's rows."""
-    import torch
-
+    """The oracle's attention chain on the host for every row of the launch."""
     from oracle import attn as A
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    r = 0
-    args = (inp.q[r].cpu(), inp.iq[r].cpu().numpy(), inp.iqs[r].cpu().numpy(),
-            inp.iw[r].cpu().numpy(), inp.plane.cpu().numpy(), inp.plane_scale.cpu().numpy(),
-            inp.page_table[r].cpu().numpy(), inp.kv.cpu().numpy(), inp.kv_scale.cpu().numpy(),
-            int(inp.positions[r]), 2048, sm_scale)
-    t0 = time.perf_counter()
-    A.attention_row(*args)
-    us = (time.perf_counter() - t0) * 1e6
-    return {"value": round(us * rows, 1), "unit": f"µs per attention phase ({rows} rows)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"1 of {rows} rows (f64 numpy/torch: scores of {int(inp.positions[r]) + 1} "
-                      f"keys, exact top-2048, sparse MLA), timed once and scaled x{rows}"}
+    plane, psc = inp.plane.cpu().numpy(), inp.plane_scale.cpu().numpy()
+    kv = inp.kv.cpu().numpy()
+    ksc = None if inp.kv_scale is None else inp.kv_scale.cpu().numpy()
+    per_row = [(inp.q[r].cpu(), inp.iq[r].cpu().numpy(), inp.iqs[r].cpu().numpy(),
+                inp.iw[r].cpu().numpy(), plane, psc,
+                inp.page_table[int(inp.req_ids[r])].cpu().numpy(), kv, ksc,
+                int(inp.positions[r]), 2048, sm_scale) for r in range(rows)]
+    med, times = cpu_timed(lambda: [A.attention_row(*a) for a in per_row])
+    return cpu_record(med * 1e6, f"µs per attention phase ({rows} rows)",
+                      f"all {rows} rows (f64 numpy/torch: scores of "
+                      f"{int(inp.positions[0]) + 1} keys, exact top-2048, sparse MLA), one "
+                      f"warm-up then the median of {len(times)} runs", times)
 
 
 def bench_attn(args):
@@ -344,15 +370,12 @@ def cpu_baseline_post(o_lat, h, w):
     from oracle import dense as D
     from sgl_amd_mono_amd.dsv32 import synthetic
 
-    torch.set_num_threads(os.cpu_count() or 1)
     ws = synthetic.rowmajor_post(w)
-    t0 = time.perf_counter()
-    D.attn_out(o_lat.cpu(), h.cpu(), *ws)
-    us = (time.perf_counter() - t0) * 1e6
-    return {"value": round(us, 1), "unit": f"µs per attention output block ({o_lat.shape[0]} rows)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": "the whole launch: f64 dequantisation of W_UV and W_o and the two GEMVs, "
-                      "timed once"}
+    o_c, h_c = o_lat.cpu(), h.cpu()
+    med, times = cpu_timed(lambda: D.attn_out(o_c, h_c, *ws))
+    return cpu_record(med * 1e6, f"µs per attention output block ({o_lat.shape[0]} rows)",
+                      "the whole launch: f64 dequantisation of W_UV and W_o and the two GEMVs, "
+                      f"one warm-up then the median of {len(times)} runs", times)
 
 
 def bench_post(args):
@@ -406,42 +429,52 @@ def phase_bytes(rows, ctx, distinct):
     return {"front": front, "attn": attn, "post": post, "moe": moe}
 
 
-def cpu_baseline_layer(h, w, caches, step, ids, rows):
-    """The oracle chain of one layer on the host for one row (front, attention over the
-    row's 32768 keys, output block, MoE over its 9 experts), scaled to the launch's rows."""
+def cpu_baseline_layer(h, w, caches, step, rows):
+    """The oracle chain of one layer on the host for all of its rows: the front, each
+    row's attention over its keys, the output block and the MoE over the experts the
+    rows route to (dequantised on the fly, as the CPU-baseline plan asks)."""
     import numpy as np
     import torch
 
     from oracle import attn as A
     from oracle import dense as D
     from oracle import front as Fr
-    from oracle import moe as omoe
+    from oracle import moe as M
     from sgl_amd_mono_amd.dsv32 import synthetic
 
-    torch.set_num_threads(os.cpu_count() or 1)
     fw = synthetic.rowmajor_front(w.front)
     pw = synthetic.rowmajor_post(w.post)
-    experts = {int(e): synthetic.rowmajor_expert(w.moe, int(e)) for e in np.unique(ids[0])}
-    pos = int(step.positions[0])
-    pages = step.page_table[int(step.req_ids[0])].cpu().numpy()
+    pos = step.positions.cpu().numpy()
+    pt = step.page_table.cpu().numpy()
+    rid = step.req_ids.cpu().numpy()
     plane, psc = caches.plane.cpu().numpy(), caches.plane_scale.cpu().numpy()
-    kv, ksc = caches.kv.cpu().numpy(), caches.kv_scale.cpu().numpy()
-    h0 = h[:1].cpu()
-    t0 = time.perf_counter()
-    f = Fr.front(h0, positions=np.array([pos]), **fw)
-    iq, iqs = Fr.iq_bytes(f["iq_codes"], f["iq_e8"])
-    att = A.attention_row(torch.from_numpy(f["q"][0]).float(), iq[0], iqs[0], f["iw"][0], plane,
-                          psc, pages, kv, ksc, pos, 2048, (128 + 64) ** -0.5)
-    o_lat = torch.from_numpy(D.bf16(att["o"])).reshape(1, 32, 512).to(torch.bfloat16)
-    a = D.attn_out(o_lat, h0, *pw)["a"]
-    omoe.moe_fp8(torch.from_numpy(a).to(torch.bfloat16), w.moe.g_post.cpu(), w.moe.w_r.cpu(),
-                 w.moe.bias.cpu(), None, None, None, None, experts=experts)
-    us = (time.perf_counter() - t0) * 1e6
-    return {"value": round(us * rows, 1), "unit": f"µs per decoder layer ({rows} rows)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"1 of {rows} rows through the oracle chain (front, FP4 scores of "
-                      f"{pos + 1} keys + exact top-2048 + sparse MLA, W_UV/o_proj, MoE over its "
-                      f"{len(experts)} experts), timed once and scaled x{rows}"}
+    kv = caches.kv.cpu().numpy()
+    ksc = None if caches.kv_scale is None else caches.kv_scale.cpu().numpy()
+    hc = h.cpu()
+    g_post, w_r, bias = w.moe.g_post.cpu(), w.moe.w_r.cpu(), w.moe.bias.cpu()
+    seen = {}
+
+    def layer():
+        f = Fr.front(hc, positions=pos, kv_scaled=ksc is not None, **fw)
+        iq, iqs = Fr.iq_bytes(f["iq_codes"], f["iq_e8"])
+        o = np.stack([A.attention_row(torch.from_numpy(f["q"][r]).float(), iq[r], iqs[r],
+                                      f["iw"][r], plane, psc, pt[rid[r]], kv, ksc, int(pos[r]),
+                                      2048, (128 + 64) ** -0.5)["o"] for r in range(rows)])
+        o_lat = torch.from_numpy(D.bf16(o)).to(torch.bfloat16)
+        a = torch.from_numpy(D.attn_out(o_lat, hc, *pw)["a"]).to(torch.bfloat16)
+        ids, _ = M.route_topk(M.sigmoid(M.router_logits(M.rmsnorm(a, g_post), w_r)), bias)
+        experts = {e: synthetic.rowmajor_expert(w.moe, e)
+                   for e in sorted({int(e) for e in ids.ravel()} | {M.SHARED})}
+        seen["experts"] = len(experts)
+        M.moe_fp8(a, g_post, w_r, bias, None, None, None, None, experts=experts)
+
+    med, times = cpu_timed(layer)
+    return cpu_record(med * 1e6, f"µs per decoder layer ({rows} rows)",
+                      f"the whole layer for all {rows} rows through the oracle chain (front, "
+                      f"FP4 scores of {int(pos[0]) + 1} keys + exact top-2048 + sparse MLA a "
+                      f"row, W_UV/o_proj, router + MoE over the {seen['experts']} experts the "
+                      f"rows route to, dequantised on the fly), one warm-up then the median of "
+                      f"{len(times)} runs", times)
 
 
 def bench_layer(args):
@@ -516,7 +549,7 @@ def bench_layer(args):
                   "achieved_GBs": round(avg[k] / (v * 1e-6) / 1e9, 1)} for k, v in phase_us.items()}
     print(f"bench: phases {phases}", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline_layer(layers[0][3], layers[0][0], layers[0][1],
-                                                      layers[0][2], ids0, rows)
+                                                      layers[0][2], rows)
     config = {
         "workload": "BASELINE configs[4]: full DeepSeek-V3.2 DSA decoder layer, one GPU's TP=4 "
                     "share, 8 rows at position 32767 (context 32768): front (RMSNorm, q_a/kv_a, "

@@ -199,11 +199,14 @@ int mono_moe_mxfp4_launch(const MonoMoeMxfp4Args* args, mono_stream_t stream);
  * nibble first; plane_scale [pages, 4, 64] E8M0, slot s's byte at (s % 16) * 4 + s / 16;
  * iq [R, 64 heads, 64 B] E2M1; iqs [R, 4 (chunk), 16 (head % 16), 4 (head / 16)] E8M0.
  * The score of key t: sum_h iw[h] relu(sum_c 2^(qe - 127) 2^(ke - 127) iq[h, c] . k[t, c]).
- * KV: kv [slots, 576] E4M3 (latent 512, rope 64) times kv_scale[slot]; a key's slot is
+ * KV: kv [slots, 576] E4M3 (latent 512, rope 64) times kv_scale[slot] (1 without
+ * kv_scale: SGLang's raw E4M3 rows); a key's slot is
  * page_table[req_ids[row], pos / 64] * 64 + pos % 64. Timeline marks 1-5 of this launch:
  * scores, top-k, splits, merge done, exit. */
 typedef struct {
-  int32_t rows;          /* R, 1..48: decode rows, row r at positions[r] of req_ids[r] */
+  int32_t rows;          /* R, 1..rows_max: decode rows, row r at positions[r] of req_ids[r] */
+  int32_t rows_max;      /* 1..48: the rows the scratch was sized for (mono_attn_scratch_bytes);
+                            every launch on one scratch passes the same value */
   int32_t heads;         /* 32 */
   int32_t index_heads;   /* 64 */
   int32_t topk;          /* 2048 */
@@ -225,7 +228,8 @@ typedef struct {
   const uint8_t* plane;
   const uint8_t* plane_scale;
   const uint8_t* kv;
-  const float* kv_scale;     /* f32 [slots] */
+  const float* kv_scale;     /* optional f32 [slots]: per-token scales (null: every row is
+                                raw E4M3 at scale 1, the layout of SGLang's FP8 MLA pool) */
   void* out;                 /* bf16 [R, 32, 512] */
   float* scores;             /* optional f32 [R, ctx_max]: the indexer scores */
   int32_t* topk_pos;         /* optional i32 [R, 2048]: selected positions, -1 past count */
@@ -276,11 +280,14 @@ int mono_post_launch(const MonoPostArgs* args, mono_stream_t stream);
  * attention launch's inputs (q, iq, iqs, iw), with the rows' KV and index-key cache
  * writes. x = bf16(rmsnorm(h) g_in); q_a | kv_a, the index key and the head weights off
  * x; q_an = bf16(rmsnorm(q_a) g_q); the KV row (kv_n = bf16(rmsnorm(kv_a[:512]) g_kv),
- * k_pe = bf16(rope(kv_a[512:]))) as E4M3 with a power-of-two per-token scale at the
- * row's slot; the index key (LayerNorm, RoPE on dims 0..63, FWHT-128, FP4 e2m1 + e8m0
+ * k_pe = bf16(rope(kv_a[512:]))) as E4M3 at the row's slot, with a power-of-two
+ * per-token scale or, without kv_scale, raw at scale 1; the index key (LayerNorm, RoPE on dims 0..63, FWHT-128, FP4 e2m1 + e8m0
  * per 32) into the index plane at the slot; q_b over q_an (nope bf16, rope rotated),
  * q_lat = bf16(W_UK q_nope); the index query (W_iq q_an, RoPE, FWHT, FP4); the head
- * weights bf16(W_w x) 128^-1/2 64^-1/2. RoPE pairs are interleaved (x0 c - x1 s,
+ * weights bf16(W_w x) 128^-1/2 64^-1/2. The index key and query are rounded to bf16 at
+ * the points of the reference's FP4 indexer (after the key's LayerNorm, after RoPE and
+ * after the FWHT: sgl_amd_mono/deepseek_v4/gfx950/kernels/stages/indexer.py:242-254,
+ * 330-335). RoPE pairs are interleaved (x0 c - x1 s,
  * x0 s + x1 c) with bf16 tables cos/sin [rope_rows, 32] indexed by position. A slot
  * outside the caches (e.g. -1, a pad row) writes nothing.
  * Replaces sgl_amd_mono/glm53/gfx950/kernel.py:1781-2443 (stages qkv_a, q_norm, cache,
@@ -310,7 +317,9 @@ typedef struct {
   const int64_t* positions;  /* [R] */
   const int64_t* slots;      /* [R] cache slot (page * 64 + offset), -1 = none */
   uint8_t* kv;               /* E4M3 [kv_slots, 576] */
-  float* kv_scale;           /* f32 [kv_slots] */
+  float* kv_scale;           /* optional f32 [kv_slots]: written with a power-of-two per-token
+                                scale; null: raw E4M3 at scale 1 (SGLang's pool layout),
+                                values saturating at +-448 */
   uint8_t* plane;            /* [plane_pages, 4, 64, 16] */
   uint8_t* plane_scale;      /* [plane_pages, 4, 64] */
   void* q;                   /* out bf16 [R, 32, 576]: q_lat | q_pe */
@@ -323,6 +332,10 @@ typedef struct {
   int32_t fault_site;        /* test fault injection (MONO_SITE_FRONT_A / QAN / QB) */
   int32_t fault_after;
   uint64_t* timeline;
+  float* ik_raw;             /* optional out f32 [R, 128]: the index key W_k x, before its
+                                LayerNorm */
+  void* iq_raw;              /* optional out bf16 [R, 64, 128]: the index query W_iq q_an,
+                                before its RoPE */
 } MonoFrontArgs;
 
 size_t mono_front_scratch_bytes(void);

@@ -10,13 +10,15 @@ Modules:
 
 * ``formats``  number formats: E4M3, E8M0, E2M1, per-128 FP8 activation quant,
   the radix order key.
+* ``front``    RMSNorm, LayerNorm, RoPE, FWHT-128, the FP4 and FP8 quantisers, and the
+  front of the layer: projections, KV row, index key and query chains, absorbed query.
+* ``attn``     the FP4 indexer scores, the chain's exact top-k, sparse MLA decode.
+* ``dense``    the W8A16 block-scaled GEMV and the output block (W_UV, o_proj, residual).
 * ``moe``      RMSNorm, router, sigmoid top-8 routing, FP8 W8A8 and MXFP4 A16W4
   expert SwiGLU, the bf16 softmax top-2 plumbing block.
-* ``attention`` RoPE, FWHT-128, the FP4 indexer scores, exact top-k, sparse MLA
-  decode with absorbed W_UK / W_UV.
-* ``layer``    the whole layer, chained from the above.
-* ``topk.c``   the exact top-k selection and the router top-k in plain C (built
-  into ``liboracle_topk.so`` by ``oracle/Makefile``), used at full sizes.
+* ``topk``     the exact top-k selection: a sort-based restatement and the radix
+  select in plain C (``topk.c``, built into ``liboracle_topk.so`` by ``oracle/Makefile``)
+  used at full sizes.
 
 Every function cites the reference file:line it follows. How each is pinned (by a
 library routine, a closed form, brute force, or the reference's test formulas) is

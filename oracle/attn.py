@@ -74,9 +74,12 @@ def index_scores(q_fp4, q_scale, w, payload, kscale, pages, n, cols=None):
 
 
 def kv_rows(kv, kv_scale, slots):
-    """f64 [k, 576]: the cached rows at ``slots`` (E4M3 times the token's scale)."""
+    """f64 [k, 576]: the cached rows at ``slots`` (E4M3 times the token's scale; raw E4M3
+    at scale 1 when ``kv_scale`` is None, the layout of SGLang's FP8 MLA pool)."""
     slots = np.asarray(slots, dtype=np.int64)
     v = F.e4m3_to_f32(np.asarray(kv)[slots]).astype(np.float64)
+    if kv_scale is None:
+        return v
     return v * np.asarray(kv_scale, dtype=np.float64)[slots][:, None]
 
 

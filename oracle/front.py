@@ -10,18 +10,27 @@ Reference stages (``sgl_amd_mono/glm53/gfx950/kernel.py``):
 * q_an = bf16(rmsnorm(q_a) * g_q) (:1978-2003);
 * the KV row (:2005-2101): kv_n = bf16(rmsnorm(kv_a[:512]) * g_kv); k_pe = bf16(rope(kv_a
   [512:])) with interleaved pairs (x0 c - x1 s, x0 s + x1 c) at the row's position. The
-  cache takes E4M3 with one f32 scale per token (this build's north-star format): scale
-  = 2^ceil(log2(max(amax, 1e-4) / 448)) over the 576 values, as the reference's index
-  cache quantiser (:2138-2150), codes = E4M3(value / scale) round to nearest even;
-* the index key (:2103-2180): k_n = (k - mean) rstd g + b (LayerNorm, eps 1e-6), RoPE on
-  dims 0..63, the orthonormal Sylvester FWHT-128 (``fwht128`` :556-566), then FP4 as the
-  V4 indexer's ``fp4_block`` (``deepseek_v4/gfx950/kernels/stages/indexer.py:143-151``):
-  per 32 values scale = pow2_ceil(max(amax, 6 * 2^-126) / 6) (``ops.py:153-158``), codes =
-  E2M1(v / scale) round to nearest even, written into SGLang's FP4 index plane;
+  cache takes E4M3 either with one f32 scale per token (the north star's synthetic
+  format): scale = 2^ceil(log2(max(amax, 1e-4) / 448)) over the 576 values, as the
+  reference's index cache quantiser (:2138-2150), codes = E4M3(value / scale) round to
+  nearest even; or raw at scale 1 (SGLang's FP8 MLA pool, the GLM cache write
+  :2044-2062), ``kv_quant(row, scaled=False)``;
+* the index key (``index_key``): k_n = bf16((k - mean) rstd g + b) (the LayerNorm of
+  :2103-2131, eps 1e-6), bf16(RoPE) on dims 0..63, the orthonormal Sylvester FWHT-128
+  (``fwht128`` :556-566) rounded to bf16, then FP4 as the V4 indexer's ``fp4_block``
+  (``deepseek_v4/gfx950/kernels/stages/indexer.py:143-151``): per 32 values scale =
+  pow2_ceil(max(amax, 6 * 2^-126) / 6) (``ops.py:153-158``), codes = E2M1(v / scale)
+  round to nearest even, written into SGLang's FP4 index plane. The bf16 rounding points
+  are those of the reference's FP4 key path (``indexer.py:242-254``: the normalised key,
+  the rotated half and the Hadamard output are each ``bf16_round``-ed before
+  ``fp4_block``);
 * q = W_qb q_an (:2183-2260): the nope part bf16, the rope part rotated then bf16; the
   absorbed query q_lat = bf16(W_UK q_nope) per head (:2355-2443);
-* the index query: bf16(W_iq q_an) (:2262-2353), RoPE on dims 0..63, FWHT-128, FP4 per
-  32 (the V4 query path ``indexer.py:311-338``);
+* the index query (``index_query``): iq_raw = bf16(W_iq q_an) (:2262-2353), bf16(RoPE) on
+  dims 0..63, FWHT-128 rounded to bf16, FP4 per 32: the V4 query path
+  (``indexer.py:311-338``), whose rotated half is ``bf16_round``-ed before the Hadamard
+  transform and whose Hadamard output is ``bf16_round``-ed before ``fp4_block``
+  (:330-335);
 * the head weights: bf16(w) * 128^-0.5 * 64^-0.5 (``indexer.py:400-406``).
 
 The f32 / f64 arithmetic here is exact or correctly rounded; the launch uses f32 with
@@ -31,8 +40,10 @@ the value sits at a rounding boundary (the tests allow for exactly that).
 Pinned by ``tests/test_oracle_front.py``: rmsnorm and layer_norm against torch's; RoPE as
 a complex multiplication (and its inverse); the FWHT against scipy's Hadamard matrix
 (and as an involution); the FP4 and FP8 quantisers against brute-force nearest-value
-search with ties to even and the pow2 scale against frexp; the GEMVs are
-``oracle/dense.py`` (pinned there).
+search with ties to even and the pow2 scale against frexp; the index key and query
+chains' bf16 rounding points by constructed inputs whose FP4 codes flip when a rounding
+is dropped (one- or two-hot pre-transform vectors, whose Hadamard outputs are closed
+forms); the GEMVs are ``oracle/dense.py`` (pinned there).
 """
 
 from __future__ import annotations
@@ -144,16 +155,21 @@ def fp8_codes(v) -> np.ndarray:
     return F.f32_to_e4m3(np.asarray(v, np.float64))
 
 
-def kv_quant(row):
-    """A cache row [576] (bf16 values) -> (E4M3 codes [576], f32 scale)."""
+def kv_quant(row, scaled: bool = True):
+    """A cache row [576] (bf16 values) -> (E4M3 codes [576], f32 scale). Scaled: the
+    power-of-two per-token scale of the index-cache quantiser (``kernel.py:2138-2150``);
+    unscaled: raw E4M3 at scale 1 saturating at +-448 (the GLM cache write,
+    ``kernel.py:2050-2062``: the bf16 values cast to E4M3)."""
     row = np.asarray(row, np.float64)
+    if not scaled:
+        return fp8_codes(np.clip(row, -448.0, 448.0)), np.float32(1.0)
     amax = np.abs(row).max()
     sc = pow2_ceil(max(amax, 1e-4) / 448.0)
     return fp8_codes(row / sc), np.float32(sc)
 
 
 def front(h, g_in, g_q, g_kv, w_qkv_a, s_qkv_a, w_k, s_k, w_w, g_k, b_k, w_qb, s_qb,
-          w_iq, s_iq, w_uk, s_uk, cos, sin, positions, eps=1e-6):
+          w_iq, s_iq, w_uk, s_uk, cos, sin, positions, eps=1e-6, kv_scaled=True):
     """One step's front for rows h [R, 7168] (bf16 values) at ``positions``; row-major
     weights (numpy E4M3 codes, f32 scales; w_w bf16 values); cos/sin [pos, 32].
 
@@ -177,26 +193,64 @@ def front(h, g_in, g_q, g_kv, w_qkv_a, s_qkv_a, w_k, s_k, w_w, g_k, b_k, w_qb, s
     kv_n = bf16(rmsnorm(kv_a[:, :KV_LORA], f32(g_kv), eps))
     k_pe = bf16(rope(kv_a[:, KV_LORA:], c, s))
     kv_rows = np.concatenate([kv_n, k_pe], -1)
-    kq = [kv_quant(r) for r in kv_rows]
-    ik = fwht128(np.concatenate(
-        [rope(layernorm(k, f32(g_k), f32(b_k))[:, :ROPE], c, s),
-         layernorm(k, f32(g_k), f32(b_k))[:, ROPE:]], -1))
-    ik_codes, ik_e8, _ = fp4_block(ik)
-    qb = D.w8a16_gemv(q_an, w_qb, s_qb).reshape(R, HEADS, NOPE + ROPE)
+    kq = [kv_quant(r, kv_scaled) for r in kv_rows]
+    ikd = index_key(k, f32(g_k), f32(b_k), c, s)
+    qb =D.w8a16_gemv(q_an, w_qb, s_qb).reshape(R, HEADS, NOPE + ROPE)
     q_nope = bf16(qb[..., :NOPE])
     q_pe = bf16(rope(qb[..., NOPE:], c[:, None], s[:, None]))
     q_lat = np.stack([bf16(D.w8a16_gemv(q_nope[:, hh], w_uk[hh], s_uk[hh]))
                       for hh in range(HEADS)], 1)
     q = np.concatenate([q_lat, q_pe], -1)
     iq_raw = bf16(D.w8a16_gemv(q_an, w_iq, s_iq)).reshape(R, IHEADS, IDIM)
-    iq_pre = fwht128(np.concatenate(
-        [rope(iq_raw[..., :ROPE], c[:, None], s[:, None]), iq_raw[..., ROPE:]], -1))
-    iq_codes, iq_e8, _ = fp4_block(iq_pre)
+    iqd = index_query(iq_raw, c, s)
     iw = (bf16(w) * (IDIM ** -0.5 * IHEADS ** -0.5)).astype(np.float32)
     return dict(x=x, q_a=q_a, kv_a=kv_a, k=k, w=w, q_an=q_an, kv_rows=kv_rows,
                 kv_codes=np.stack([a for a, _ in kq]), kv_scale=np.array([b for _, b in kq]),
-                ik=ik, ik_codes=ik_codes, ik_e8=ik_e8, q=q, iq_raw=iq_raw, iq_pre=iq_pre,
-                iq_codes=iq_codes, iq_e8=iq_e8, iw=iw)
+                ik=ikd["pre"], ik_codes=ikd["codes"], ik_e8=ikd["e8"], q=q, iq_raw=iq_raw,
+                iq_pre=iqd["pre"], iq_codes=iqd["codes"], iq_e8=iqd["e8"], iw=iw)
+
+
+def _rope_lead(v, cos, sin):
+    """bf16(RoPE) of the first ROPE dims (interleaved pairs); the other dims unchanged."""
+    return np.concatenate([bf16(rope(v[..., :ROPE], cos, sin)), v[..., ROPE:]], -1)
+
+
+def index_key(k, g_k, b_k, cos, sin):
+    """The index-key chain of rows k [R, 128] (the W_k outputs) with the rows' RoPE
+    factors cos / sin [R, 32]: n = bf16(LayerNorm(k) g + b) (``kernel.py:2118-2131``),
+    r = bf16(RoPE(n[:64])) | n[64:], t = FWHT-128(r), pre = bf16(t), then FP4 of pre: the
+    rounding points of ``deepseek_v4/gfx950/kernels/stages/indexer.py:242-254``
+    (``bf16_round`` after the norm, after the rotation and after the Hadamard transform,
+    then ``fp4_block``).
+
+    Returns dict(norm, rot, fwht (f64, before its rounding), pre, codes u8 [R, 128],
+    e8 u8 [R, 4])."""
+    n = bf16(layernorm(k, g_k, b_k))
+    r = _rope_lead(n, cos, sin)
+    t = fwht128(r)
+    pre = bf16(t)
+    codes, e8, _ = fp4_block(pre)
+    return dict(norm=n, rot=r, fwht=t, pre=pre, codes=codes, e8=e8)
+
+
+def index_query(iq_raw, cos, sin):
+    """The index-query chain of iq_raw [R, 64, 128] (bf16 values of W_iq q_an) with the
+    rows' RoPE factors cos / sin [R, 32]: r = bf16(RoPE(iq_raw[..., :64])) | iq_raw[...,
+    64:], t = FWHT-128(r), pre = bf16(t), then FP4 per 32 of pre: the rounding points of
+    ``deepseek_v4/gfx950/kernels/stages/indexer.py:330-335`` (the rotated half
+    ``bf16_round``-ed before ``had_pair``, the Hadamard output ``bf16_round``-ed before
+    ``fp4_block``).
+
+    Returns dict(rot, fwht (f64, before its rounding), pre, codes u8 [R, 64, 128],
+    e8 u8 [R, 64, 4])."""
+    iq_raw = np.asarray(iq_raw, np.float64)
+    c = np.asarray(cos, np.float64)[:, None]
+    s = np.asarray(sin, np.float64)[:, None]
+    r = _rope_lead(iq_raw, c, s)
+    t = fwht128(r)
+    pre = bf16(t)
+    codes, e8, _ = fp4_block(pre)
+    return dict(rot=r, fwht=t, pre=pre, codes=codes, e8=e8)
 
 
 def iq_bytes(codes, e8):

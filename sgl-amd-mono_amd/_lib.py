@@ -124,6 +124,7 @@ class MonoAttnArgs(ctypes.Structure):
 
     _fields_ = [
         ("rows", c_int32),
+        ("rows_max", c_int32),
         ("heads", c_int32),
         ("index_heads", c_int32),
         ("topk", c_int32),
@@ -229,6 +230,8 @@ class MonoFrontArgs(ctypes.Structure):
         ("fault_site", c_int32),
         ("fault_after", c_int32),
         ("timeline", c_void_p),
+        ("ik_raw", c_void_p),
+        ("iq_raw", c_void_p),
     ]
 
 

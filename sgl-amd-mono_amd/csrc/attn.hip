@@ -51,19 +51,30 @@ constexpr int AT_MAXR = 48;
 
 constexpr size_t at_align(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// scratch of a runtime sized for `rm` rows (every launch on it passes the same rm, so a
+// word keeps its meaning from launch to launch and a stale tag can never match)
 struct AttnScratch {
-  static constexpr size_t SCORES = 0;  // f32 [MAXR][MAXCTX]
-  static constexpr size_t SCORE_DONE = at_align(SCORES + (size_t)AT_MAXR * AT_MAXCTX * 4);
-  // the selection as (position, tag) pairs [MAXR][TOPK]
-  static constexpr size_t TOPK = at_align(SCORE_DONE + (size_t)AT_MAXR * AT_NCHUNK * 4);
-  static constexpr size_t ACC = at_align(TOPK + (size_t)AT_MAXR * AT_TOPK * 8);  // f32 [R][split][h][512]
-  static constexpr size_t ML = at_align(ACC + (size_t)AT_MAXR * AT_NSPLIT * AT_HEADS * AT_LAT * 4);
-  static constexpr size_t SPLIT_DONE = at_align(ML + (size_t)AT_MAXR * AT_NSPLIT * AT_HEADS * 8);
-  static constexpr size_t BYTES = at_align(SPLIT_DONE + (size_t)AT_MAXR * AT_NSPLIT * 4);
+  size_t scores;      // f32 [rm][MAXCTX]
+  size_t score_done;  // u32 [rm][NCHUNK]
+  size_t topk;        // the selection as (position, tag) pairs [rm][TOPK]
+  size_t acc;         // f32 [rm][split][h][512]
+  size_t ml;          // f32 [rm][split][h][2]
+  size_t split_done;  // u32 [rm][split]
+  size_t bytes;
+  __host__ __device__ explicit AttnScratch(int rm) {
+    const size_t r = (size_t)rm;
+    scores = 0;
+    score_done = at_align(scores + r * AT_MAXCTX * 4);
+    topk = at_align(score_done + r * AT_NCHUNK * 4);
+    acc = at_align(topk + r * AT_TOPK * 8);
+    ml = at_align(acc + r * AT_NSPLIT * AT_HEADS * AT_LAT * 4);
+    split_done = at_align(ml + r * AT_NSPLIT * AT_HEADS * 8);
+    bytes = at_align(split_done + r * AT_NSPLIT * 4);
+  }
 };
 
 struct AttnParams {
-  int rows, ctx_max, pt_stride, pt_rows;
+  int rows, rows_max, ctx_max, pt_stride, pt_rows;
   float sm_scale;
   uint32_t plane_pages, kv_slots;
   const int64_t* positions;
@@ -113,7 +124,7 @@ __device__ inline v4f mfma_bf16(v8bf a, v8bf b, v4f c) {
 
 template <int SPLIT>
 __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
-  using S = AttnScratch;
+  const AttnScratch S(p.rows_max);
   static_assert(SPLIT == 64 || SPLIT == 128, "64- or 128-key splits");
   constexpr int NSP = AT_TOPK / SPLIT;  // splits a row
   const int tid = threadIdx.x, l = tid & 63;
@@ -129,12 +140,12 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   __shared__ int res_s[4];
   __shared__ uint32_t mm_s[2];
 
-  float* scores = reinterpret_cast<float*>(p.scratch + S::SCORES);
-  uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S::SCORE_DONE);
-  uint64_t* topk = reinterpret_cast<uint64_t*>(p.scratch + S::TOPK);
-  float* accs = reinterpret_cast<float*>(p.scratch + S::ACC);
-  float* mls = reinterpret_cast<float*>(p.scratch + S::ML);
-  uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S::SPLIT_DONE);
+  float* scores = reinterpret_cast<float*>(p.scratch + S.scores);
+  uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S.score_done);
+  uint64_t* topk = reinterpret_cast<uint64_t*>(p.scratch + S.topk);
+  float* accs = reinterpret_cast<float*>(p.scratch + S.acc);
+  float* mls = reinterpret_cast<float*>(p.scratch + S.ml);
+  uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S.split_done);
 
   stamp(p.timeline, MONO_TL_START);
   if (tid == 0) {
@@ -294,7 +305,9 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     constexpr int QP = AT_HEADS * AT_KV / 8;  // 16-byte pieces of a row's q
     constexpr int NQP = (QP + AT_THREADS - 1) / AT_THREADS;
     const __amdgpu_buffer_rsrc_t rkv = rsrc(p.kv, p.kv_slots * (uint32_t)AT_KV);
-    const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, p.kv_slots * 4u);
+    // without per-token scales every row is raw E4M3 (scale 1)
+    const bool scaled = p.kv_scale != nullptr;
+    const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, scaled ? p.kv_slots * 4u : 0u);
     const int nt = R * NSP;
     for (int t0 = 0; t0 < nt; t0 += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
@@ -365,7 +378,7 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
           const int j = idx / (AT_KV / 16), c = idx % (AT_KV / 16);
           if (idx < GP) *reinterpret_cast<v4i*>(kbuf + j * KSTR + c * 16) = gv[i];
         }
-        if (tid < SPLIT) ksc[tid] = slot >= 0 ? sc : 0.f;
+        if (tid < SPLIT) ksc[tid] = slot >= 0 ? (scaled ? sc : 1.0f) : 0.f;
       }
       __syncthreads();
       // S = q K^T: wave w takes heads 16 (w / 8) .., keys 16 (w % 4) .. and the even (w / 4
@@ -572,13 +585,13 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
 using namespace mono;
 
 extern "C" size_t mono_attn_scratch_bytes(int32_t rows_max) {
-  return (rows_max >= 1 && rows_max <= AT_MAXR) ? AttnScratch::BYTES : 0;
+  return (rows_max >= 1 && rows_max <= AT_MAXR) ? AttnScratch(rows_max).bytes : 0;
 }
 
 extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
   if (!a) return set_error(MONO_E_ARG, "mono_attn_launch: null args");
-  if (a->rows < 1 || a->rows > AT_MAXR)
-    return set_error(MONO_E_ARG, "mono_attn_launch: rows must be 1..48");
+  if (a->rows_max < 1 || a->rows_max > AT_MAXR || a->rows < 1 || a->rows > a->rows_max)
+    return set_error(MONO_E_ARG, "mono_attn_launch: rows must be 1..rows_max, rows_max 1..48");
   if (a->heads != AT_HEADS || a->index_heads != AT_IHEADS || a->topk != AT_TOPK ||
       a->page != AT_PAGE)
     return set_error(MONO_E_ARG, "mono_attn_launch: built for 32 heads, 64 index heads, "
@@ -592,11 +605,11 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
       (uint64_t)a->kv_slots * AT_KV > 0x7FFFFFFFull)
     return set_error(MONO_E_ARG, "mono_attn_launch: plane_pages / kv_slots out of range");
   if (!a->positions || !a->req_ids || !a->page_table || !a->q || !a->iq || !a->iqs || !a->iw ||
-      !a->plane || !a->plane_scale || !a->kv || !a->kv_scale || !a->out || !a->scratch ||
-      !a->guard)
+      !a->plane || !a->plane_scale || !a->kv || !a->out || !a->scratch || !a->guard)
     return set_error(MONO_E_ARG, "mono_attn_launch: null tensor");
   AttnParams p;
   p.rows = a->rows;
+  p.rows_max = a->rows_max;
   p.ctx_max = a->ctx_max;
   p.pt_stride = a->pt_stride;
   p.pt_rows = a->pt_rows;

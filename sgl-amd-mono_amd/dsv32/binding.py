@@ -173,7 +173,7 @@ def layer_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> La
 
 
 def layer_disable_reason(layer, idx: int, cfg: LayerConfig = DSV32) -> Optional[str]:
-    """Why a layer's attention half cannot be bound (None: it can); nothing is kept."""
+    """Why a covered layer cannot be bound in place (None: it can); nothing is kept."""
     try:
         layer_weights(layer, idx, {}, cfg)
     except (ValueError, AttributeError) as e:
@@ -181,12 +181,14 @@ def layer_disable_reason(layer, idx: int, cfg: LayerConfig = DSV32) -> Optional[
     return None
 
 
-def caches(pool, idx: int, kv_scale: torch.Tensor, cfg: LayerConfig = DSV32) -> FrontCaches:
+def caches(pool, idx: int, cfg: LayerConfig = DSV32) -> FrontCaches:
     """A layer's caches from SGLang's KV pool, in place: the MLA rows E4M3 [slots, 1, 576]
     (``get_key_buffer``) and the FP4 index pages [pages, 1, 4, 64, 16] with their E8M0
     scales [pages, 1, 4, 64] (``get_index_k_fp4_payload_buffer`` / ``_scale_buffer``).
-    ``kv_scale`` f32 [slots] is the launches' per-token scale of a row (the caller's: 1
-    for a row written unscaled)."""
+    The pool's MLA rows are raw E4M3 at scale 1 (SGLang's HIP DSA layout, as the
+    reference binds it: ``glm53/spec.py:451-461``), so the launches write and read them
+    with no per-token scale: a row SGLang wrote and a row the front wrote read the same
+    way, whichever path serves the next step."""
     kv = pool.get_key_buffer(idx)
     pay = pool.get_index_k_fp4_payload_buffer(idx)
     sc = pool.get_index_k_fp4_scale_buffer(idx)
@@ -195,9 +197,6 @@ def caches(pool, idx: int, kv_scale: torch.Tensor, cfg: LayerConfig = DSV32) -> 
         raise RuntimeError(f"layer {idx}: MLA cache {kv.dtype} {tuple(kv.shape)}; needs "
                            f"contiguous E4M3 [slots, 1, {row}]")
     slots = kv.numel() // row
-    if kv_scale.dtype != torch.float32 or tuple(kv_scale.shape) != (slots,):
-        raise RuntimeError(f"layer {idx}: KV scales {kv_scale.dtype} {tuple(kv_scale.shape)}; "
-                           f"needs f32 [{slots}]")
     if (pay.dtype != torch.uint8 or tuple(pay.shape[1:]) != (1, 4, cfg.page, 16)
             or not pay.is_contiguous()):
         raise RuntimeError(f"layer {idx}: FP4 index pages {pay.dtype} {tuple(pay.shape)}; "
@@ -207,6 +206,6 @@ def caches(pool, idx: int, kv_scale: torch.Tensor, cfg: LayerConfig = DSV32) -> 
         raise RuntimeError(f"layer {idx}: FP4 index scales {sc.dtype} {tuple(sc.shape)}; "
                            f"needs contiguous uint8 [{pay.shape[0]}, 1, 4, {cfg.page}]")
     pages = pay.shape[0]
-    return FrontCaches(kv=kv.view(torch.uint8).view(slots, row), kv_scale=kv_scale,
+    return FrontCaches(kv=kv.view(torch.uint8).view(slots, row), kv_scale=None,
                        plane=pay.view(pages, 4, cfg.page, 16),
                        plane_scale=sc.view(pages, 4, cfg.page))

@@ -21,7 +21,7 @@ from typing import Optional
 import torch
 
 from .. import _lib, layouts
-from ..runtime import MonoRuntime
+from ..runtime import MonoRuntime, shared_or_new
 from .config import DSV32, LayerConfig
 from .moe import FP8, _need
 
@@ -93,10 +93,11 @@ class FrontWeights:
 @dataclass
 class FrontCaches:
     """The layer's caches the front writes: kv E4M3 (uint8) [slots, 576] + kv_scale f32
-    [slots]; the FP4 index plane [pages, 4, 64, 16] + its scales [pages, 4, 64]."""
+    [slots] (None: raw E4M3 rows at scale 1, SGLang's FP8 MLA pool layout); the FP4 index
+    plane [pages, 4, 64, 16] + its scales [pages, 4, 64]."""
 
     kv: torch.Tensor
-    kv_scale: torch.Tensor
+    kv_scale: Optional[torch.Tensor]
     plane: torch.Tensor
     plane_scale: torch.Tensor
 
@@ -113,13 +114,15 @@ class FrontOp:
     """The front launch on one device for up to ``max_rows`` rows."""
 
     def __init__(self, weights: FrontWeights, device, cfg: LayerConfig = DSV32,
-                 max_rows: int = 8, deadline_s: float = 10.0, fault=(0, 0)):
+                 max_rows: int = 8, deadline_s: float = 10.0, fault=(0, 0),
+                 rt: Optional[MonoRuntime] = None):
         self.cfg, self.device = cfg, torch.device(device)
         if not 1 <= max_rows <= FRONT_MAX_ROWS:
             raise ValueError(f"max_rows must be 1..{FRONT_MAX_ROWS}")
         weights.validate(cfg, self.device)
         self.w = weights
-        self.rt = MonoRuntime(_lib.lib().mono_front_scratch_bytes(), self.device, deadline_s)
+        self.rt = shared_or_new(rt, _lib.lib().mono_front_scratch_bytes(), self.device,
+                                deadline_s)
         self.max_rows, self.fault = max_rows, fault
         d = self.device
         self.outs = [FrontOut(
@@ -132,7 +135,10 @@ class FrontOp:
 
     def launch(self, h: torch.Tensor, caches: FrontCaches, positions: torch.Tensor,
                slots: torch.Tensor, out: Optional[FrontOut] = None, stream=None,
-               timeline: Optional[torch.Tensor] = None) -> FrontOut:
+               timeline: Optional[torch.Tensor] = None, ik_raw: Optional[torch.Tensor] = None,
+               iq_raw: Optional[torch.Tensor] = None) -> FrontOut:
+        """One launch; ``ik_raw`` f32 [R, 128] / ``iq_raw`` bf16 [R, 64, 128], if given,
+        receive the index key's and query's projections before their LayerNorm / RoPE."""
         cfg, dev, w = self.cfg, self.device, self.w
         r = h.shape[0] if h.dim() == 2 else -1
         if not 1 <= r <= self.max_rows:
@@ -142,7 +148,8 @@ class FrontOp:
         _need(slots, "slots", torch.int64, (r,), dev)
         kv = caches.kv if caches.kv.dtype == U8 else caches.kv.view(U8)
         _need(kv, "kv", U8, (kv.shape[0], cfg.kv_row), dev)
-        _need(caches.kv_scale, "kv_scale", torch.float32, (kv.shape[0],), dev)
+        if caches.kv_scale is not None:
+            _need(caches.kv_scale, "kv_scale", torch.float32, (kv.shape[0],), dev)
         pages = caches.plane.shape[0]
         _need(caches.plane, "plane", U8, (pages, 4, cfg.page, 16), dev)
         _need(caches.plane_scale, "plane_scale", U8, (pages, 4, cfg.page), dev)
@@ -156,6 +163,10 @@ class FrontOp:
         _need(out.iw, "iw", torch.float32, (r, cfg.index_heads), dev)
         if timeline is not None:
             _need(timeline, "timeline", torch.int64, (self.rt.grid, _lib.TL_COLS), dev)
+        if ik_raw is not None:
+            _need(ik_raw, "ik_raw", torch.float32, (r, cfg.index_dim), dev)
+        if iq_raw is not None:
+            _need(iq_raw, "iq_raw", BF16, (r, cfg.index_heads, cfg.index_dim), dev)
         self.rt.before_launch()
         ptr = lambda t: t.data_ptr() if t is not None else None
         args = _lib.MonoFrontArgs(
@@ -168,12 +179,13 @@ class FrontOp:
             w_qb=w.w_qb.data_ptr(), s_qb=w.s_qb.data_ptr(), w_iq=w.w_iq.data_ptr(),
             s_iq=w.s_iq.data_ptr(), w_uk=w.w_uk.data_ptr(), s_uk=w.s_uk.data_ptr(),
             cos=w.cos.data_ptr(), sin=w.sin.data_ptr(), positions=positions.data_ptr(),
-            slots=slots.data_ptr(), kv=kv.data_ptr(), kv_scale=caches.kv_scale.data_ptr(),
+            slots=slots.data_ptr(), kv=kv.data_ptr(), kv_scale=ptr(caches.kv_scale),
             plane=caches.plane.data_ptr(), plane_scale=caches.plane_scale.data_ptr(),
             q=out.q.data_ptr(), iq=out.iq.data_ptr(), iqs=out.iqs.data_ptr(), iw=out.iw.data_ptr(),
             scratch=self.rt.scratch.data_ptr(), guard=self.rt.guard.data_ptr(),
             host_error=self.rt.host_error.data_ptr(), fault_site=int(self.fault[0]),
-            fault_after=int(self.fault[1]), timeline=ptr(timeline))
+            fault_after=int(self.fault[1]), timeline=ptr(timeline), ik_raw=ptr(ik_raw),
+            iq_raw=ptr(iq_raw))
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().mono_front_launch(ctypes.byref(args), _lib.stream_handle(stream)),
                        "mono_front_launch")

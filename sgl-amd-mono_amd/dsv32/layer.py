@@ -19,6 +19,8 @@ from typing import Optional
 
 import torch
 
+from .. import _lib
+from ..runtime import MonoRuntime
 from .attn import AttnInputs, AttnOp
 from .config import DSV32, LayerConfig
 from .front import FrontCaches, FrontOp, FrontWeights
@@ -44,20 +46,48 @@ class LayerStep:
     page_table: torch.Tensor
 
 
-class LayerOp:
-    """The four launches of one layer on one device for up to ``max_rows`` rows."""
+class LayerRuntimes:
+    """The scratch and guard blocks of the four launch kinds, shareable by every layer
+    on a device (the layers' launches are ordered on one stream, and each launch's tag
+    comes from its runtime's epoch, so one set serves all of them)."""
 
-    def __init__(self, weights: LayerWeights, device, cfg: LayerConfig = DSV32,
-                 max_rows: int = 8, ctx_max: int = 32768, deadline_s: float = 10.0):
-        self.cfg, self.device = cfg, torch.device(device)
-        self.front = FrontOp(weights.front, device, cfg, max_rows, deadline_s)
-        self.attn = AttnOp(device, cfg, max_rows, ctx_max, deadline_s=deadline_s)
-        self.post = PostOp(weights.post, device, cfg, max_rows, deadline_s)
-        self.moe = MoeFp8Op(weights.moe, device, cfg, max_rows=max_rows, deadline_s=deadline_s)
+    def __init__(self, device, cfg: LayerConfig = DSV32, max_rows: int = 8,
+                 ctx_max: int = 32768, deadline_s: float = 10.0):
+        lib = _lib.lib()
+        self.device = torch.device(device)
+        self.max_rows, self.ctx_max = max_rows, ctx_max
+        self.front = MonoRuntime(lib.mono_front_scratch_bytes(), self.device, deadline_s)
+        self.attn = MonoRuntime(lib.mono_attn_scratch_bytes(max_rows), self.device, deadline_s)
+        self.post = MonoRuntime(lib.mono_post_scratch_bytes(), self.device, deadline_s)
+        self.moe = MonoRuntime(lib.mono_moe_fp8_scratch_bytes(cfg.hidden, cfg.inter, cfg.experts),
+                               self.device, deadline_s)
+
+    def all(self):
+        return (self.front, self.attn, self.post, self.moe)
+
+
+class LayerOp:
+    """The four launches of one layer for up to ``max_rows`` rows, on a device (with
+    runtimes of its own) or on shared ``LayerRuntimes``."""
+
+    def __init__(self, weights: LayerWeights, device_or_rts, cfg: LayerConfig = DSV32,
+                 max_rows: int = 8, ctx_max: int = 32768, deadline_s: float = 10.0,
+                 sm_scale: Optional[float] = None):
+        rts = device_or_rts
+        if not isinstance(rts, LayerRuntimes):
+            rts = LayerRuntimes(rts, cfg, max_rows, ctx_max, deadline_s)
+        device, max_rows, ctx_max = rts.device, rts.max_rows, rts.ctx_max
+        self.cfg, self.device, self.rts = cfg, device, rts
+        self.front = FrontOp(weights.front, device, cfg, max_rows, deadline_s, rt=rts.front)
+        self.attn = AttnOp(device, cfg, max_rows, ctx_max, sm_scale=sm_scale,
+                           deadline_s=deadline_s, rt=rts.attn)
+        self.post = PostOp(weights.post, device, cfg, max_rows, deadline_s, rt=rts.post)
+        self.moe = MoeFp8Op(weights.moe, device, cfg, max_rows=max_rows, deadline_s=deadline_s,
+                            rt=rts.moe)
         self.max_rows = max_rows
 
     def runtimes(self):
-        return (self.front.rt, self.attn.rt, self.post.rt, self.moe.rt)
+        return self.rts.all()
 
     def check(self) -> None:
         for rt in self.runtimes():

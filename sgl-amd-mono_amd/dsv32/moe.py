@@ -20,7 +20,7 @@ from typing import Optional
 import torch
 
 from .. import _lib, layouts
-from ..runtime import MonoRuntime
+from ..runtime import MonoRuntime, shared_or_new
 from .config import DSV32, MAX_ROWS, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
 
 FP8 = torch.float8_e4m3fn
@@ -85,7 +85,8 @@ class MoeFp8Op:
     """The FP8 routed-MoE launch on one device for up to ``max_rows`` rows."""
 
     def __init__(self, weights: MoeFp8Weights, device, cfg: LayerConfig = DSV32,
-                 max_rows: int = MAX_ROWS, deadline_s: float = 10.0, fault=(0, 0)):
+                 max_rows: int = MAX_ROWS, deadline_s: float = 10.0, fault=(0, 0),
+                 rt: Optional[MonoRuntime] = None):
         self.cfg, self.device = cfg, torch.device(device)
         if not 1 <= max_rows <= MAX_ROWS:
             raise ValueError(f"max_rows must be 1..{MAX_ROWS}")
@@ -94,7 +95,7 @@ class MoeFp8Op:
         nbytes = _lib.lib().mono_moe_fp8_scratch_bytes(cfg.hidden, cfg.inter, cfg.experts)
         if nbytes == 0:
             raise ValueError(f"no FP8 MoE kernel for hidden {cfg.hidden}, inter {cfg.inter}")
-        self.rt = MonoRuntime(nbytes, self.device, deadline_s)
+        self.rt = shared_or_new(rt, nbytes, self.device, deadline_s)
         self.max_rows = max_rows
         self.fault = fault
         # two parity outputs: a launch never writes the tensor the previous one returned

@@ -18,7 +18,7 @@ from typing import Optional
 import torch
 
 from .. import _lib, layouts
-from ..runtime import MonoRuntime
+from ..runtime import MonoRuntime, shared_or_new
 from .config import DSV32, LayerConfig
 from .moe import FP8, _need
 
@@ -53,13 +53,15 @@ class PostOp:
     """The attention output launch on one device for up to ``max_rows`` rows."""
 
     def __init__(self, weights: PostWeights, device, cfg: LayerConfig = DSV32,
-                 max_rows: int = 8, deadline_s: float = 10.0, fault=(0, 0)):
+                 max_rows: int = 8, deadline_s: float = 10.0, fault=(0, 0),
+                 rt: Optional[MonoRuntime] = None):
         self.cfg, self.device = cfg, torch.device(device)
         if not 1 <= max_rows <= POST_MAX_ROWS:
             raise ValueError(f"max_rows must be 1..{POST_MAX_ROWS}")
         weights.validate(cfg, self.device)
         self.w = weights
-        self.rt = MonoRuntime(_lib.lib().mono_post_scratch_bytes(), self.device, deadline_s)
+        self.rt = shared_or_new(rt, _lib.lib().mono_post_scratch_bytes(), self.device,
+                                deadline_s)
         self.max_rows, self.fault = max_rows, fault
         self.outs = [torch.empty(max_rows, cfg.hidden, dtype=torch.bfloat16, device=self.device)
                      for _ in range(2)]

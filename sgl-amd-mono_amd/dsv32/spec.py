@@ -2,27 +2,28 @@
 
 The plugin surface of ``sgl_amd_mono/glm53/spec.py:584-616``: a ``MonoSpec`` registered
 under backend ``amd`` for the architecture, with device limits, requirements, numerics
-bounds, config and model refusal reasons, and ``build(model, hf_config, ctx)``
-returning an object whose ``forward(plan, input_ids, positions, forward_batch, ...)``
-SGLang calls for a routed step. The forward decides by the graph key alone
-(``plan.key.rows`` against the widths built), so every rank and every graph replay makes
-the same choice; a wider step runs the model's own forward.
+bounds, config and model refusal reasons (lists of reasons, never exceptions), and
+``build(model, hf_config, ctx)`` returning an object whose ``forward(plan, input_ids,
+positions, forward_batch, ...)`` SGLang calls for a routed step. The forward decides by
+the graph key alone (``plan.key.rows`` against the widths built), so every rank and every
+graph replay makes the same choice; a wider step runs the model's own forward.
 
-A covered layer whose attention half binds (``binding.layer_disable_reason`` is None)
-runs as the four launches of ``LayerOp``: front, attention, output block and MoE, over
-SGLang's weights in place (the few copies logged by ``binding``) and its KV / FP4
-index pages in place. Any other covered layer runs its FFN half as one persistent launch
-(``MoeFp8Op``: post-attention RMSNorm, router, top-8 + shared expert, W8A8 experts and
-the residual add, experts, router and norm read in place) after SGLang's attention.
+Every covered layer (the MoE layers) runs as the layer launch over SGLang's weights in
+place (the few copies logged by ``binding``) and its KV / FP4 index pages in place. The
+dense layers before them run on SGLang's path; the residual stream crosses between the
+two through SGLang's layer-boundary API, as the reference's backbone does
+(``glm53/spec.py:319-352``, ``:354-417``): the first covered layer folds the pending
+residual add of the layer before it into its input, the last marks its output as a
+written stream for the final norm.
 
-One GPU's TP=4 share is what the kernels compute; the two TP exchanges of the layer are
-not built, so ``build`` refuses a TP size above 1 with that reason rather than serve
-unreduced partial sums.
+The kernels carry one GPU's TP=4 share of a layer (32 heads, expert intermediate 512)
+and the two TP exchanges are not built, so the spec serves a model whose shapes at TP 1
+are that share, and refuses any other with the reason.
 """
 
 from __future__ import annotations
 
-import os
+import math
 
 import torch
 
@@ -45,39 +46,52 @@ except ModuleNotFoundError:  # SGLang before sgl-project/sglang#45389
         Requirements,
     )
 
-from .config import DSV32, MAX_ROWS
-from .runner import alloc_step, fill_step, page_table
+from .config import DSV32
+from .runner import StepRows, page_table
 
-# one build takes any row count up to 16 (the kernels read the count at run time)
-WIDTHS = tuple(range(1, MAX_ROWS + 1))
-TP_SIZES = (1, 4)
+MAX_ROWS = 8  # the front builds x of at most 8 rows in LDS
+WIDTHS = tuple(range(1, MAX_ROWS + 1))  # one build serves every row count up to 8
+TP_SIZES = (1,)
 BLOCKS = 256  # one CTA per MI355X CU
+PAGE_SIZE = DSV32.page
+MAX_CONTEXT = 32768  # keys a row's exact top-k ranks in one CTA's LDS
 
 # the bounds a check-mode step is held to (the north star's parity bar)
 NUMERICS = Numerics(
     NumericsKind.TOLERANCE,
     {
-        "moe.out.max_abs": 2e-2,
-        "moe.out.rel": 1e-2,
+        "layer.out.max_abs": 2e-2,
+        "layer.out.rel": 1e-2,
         "router.ids.mismatch": 0.0,
         "indexer.topk.mismatch": 0.0,
     },
 )
 
+# the shapes, routing and rotary layout the kernels build in (a layer's share at TP 1)
 HF_CONFIG = dict(
     hidden_size=DSV32.hidden,
-    n_routed_experts=DSV32.experts,
-    num_experts_per_tok=DSV32.top_k,
-    n_shared_experts=1,
+    num_attention_heads=DSV32.heads,
     q_lora_rank=DSV32.q_lora,
     kv_lora_rank=DSV32.kv_lora,
     qk_rope_head_dim=DSV32.rope_dim,
     qk_nope_head_dim=DSV32.nope_dim,
     v_head_dim=DSV32.v_dim,
+    n_routed_experts=DSV32.experts,
+    num_experts_per_tok=DSV32.top_k,
+    n_shared_experts=1,
+    moe_intermediate_size=DSV32.inter,
     routed_scaling_factor=DSV32.route_scale,
     scoring_func="sigmoid",
     topk_method="noaux_tc",
+    n_group=1,
+    topk_group=1,
+    norm_topk_prob=True,
+    hidden_act="silu",
     rms_norm_eps=DSV32.rms_eps,
+    index_n_heads=DSV32.index_heads,
+    index_head_dim=DSV32.index_dim,
+    index_topk=DSV32.index_topk,
+    indexer_rope_interleave=True,
 )
 
 
@@ -91,64 +105,99 @@ def covered_layers(hf_config) -> list:
     return list(range(first, hf_config.num_hidden_layers))
 
 
+def _rope(hf_config) -> dict:
+    return dict(getattr(hf_config, "rope_parameters", None)
+                or getattr(hf_config, "rope_scaling", None) or {})
+
+
+def softmax_scale(hf_config) -> float:
+    """(nope + rope)^-1/2, times YaRN's mscale^2 when the rotary embedding is YaRN (the
+    scale SGLang's MLA attention applies: 0.1 mscale_all_dim ln(factor) + 1 per factor
+    above 1); the launch's scale is a plain argument, so it follows the model."""
+    scale = (DSV32.nope_dim + DSV32.rope_dim) ** -0.5
+    rope = _rope(hf_config)
+    if rope.get("rope_type", rope.get("type", "default")) == "yarn":
+        factor = float(rope.get("factor", 1.0))
+        m_all = float(rope.get("mscale_all_dim", 0.0) or 0.0)
+        if factor > 1.0 and m_all:
+            m = 0.1 * m_all * math.log(factor) + 1.0
+            scale *= m * m
+    return scale
+
+
+def _same(have, want) -> bool:
+    if isinstance(want, float):
+        return have is not None and abs(float(have) - want) <= 1e-9 * max(1.0, abs(want))
+    return have == want
+
+
 def _config_disable_reasons(cfg, hf_config) -> list:
     """Why this spec cannot serve a model config (an empty list: it can)."""
-    reasons = []
-    for key, want in HF_CONFIG.items():
-        have = getattr(hf_config, key, None)
-        if have is None or (isinstance(want, float) and abs(float(have) - want) > 1e-9) or (
-            not isinstance(want, float) and have != want
-        ):
-            reasons.append(f"{key} is {have!r}, the kernels are built for {want!r}")
-    q = getattr(hf_config, "quantization_config", None) or {}
-    if q.get("quant_method") != "fp8" or list(q.get("weight_block_size", [])) != [128, 128]:
-        reasons.append("the experts must be FP8 with 128 x 128 block scales")
-    if getattr(cfg, "speculative_algorithm", None) not in (None,):
+    reasons = [f"needs {key} = {want!r}, got {getattr(hf_config, key, None)!r}"
+               for key, want in HF_CONFIG.items() if not _same(getattr(hf_config, key, None), want)]
+    if getattr(hf_config, "rope_interleave", True) is not True:
+        reasons.append("the MLA rotary embedding must rotate interleaved pairs "
+                       "(rope_interleave = True)")
+    rope_type = (lambda r: r.get("rope_type", r.get("type", "default")))(_rope(hf_config))
+    if rope_type not in ("default", "yarn"):
+        reasons.append(f"RoPE {rope_type!r}: the launches read SGLang's cos / sin table "
+                       "and scale the softmax for default or YaRN RoPE only")
+    if getattr(hf_config, "moe_layer_freq", 1) != 1:
+        reasons.append("needs every layer after the dense ones to be MoE")
+    tp = int(getattr(cfg, "tp_size", 1) or 1)
+    if tp not in TP_SIZES:
+        reasons.append(f"TP {tp}: the launches compute one GPU's share and the TP "
+                       "exchanges are not built")
+    page = getattr(cfg, "page_size", None)
+    if page not in (None, PAGE_SIZE):
+        reasons.append(f"--page-size {page}: the DSA caches need {PAGE_SIZE}")
+    context = getattr(cfg, "context_length", None) or getattr(
+        hf_config, "max_position_embeddings", None)
+    if context is not None and int(context) > MAX_CONTEXT:
+        reasons.append(f"context {context}: the exact top-k ranks at most {MAX_CONTEXT} "
+                       "keys a row (--context-length to serve within it)")
+    if getattr(cfg, "speculative_algorithm", None) is not None:
         reasons.append("speculative verify rows are not built: plain decode rows only")
+    q = getattr(hf_config, "quantization_config", None) or {}
+    if q.get("quant_method") != "fp8" or list(q.get("weight_block_size") or ()) != [128, 128]:
+        reasons.append("needs the FP8 checkpoint with 128 x 128 block scales, got "
+                       f"{q.get('quant_method')!r} {q.get('weight_block_size')!r}")
     return reasons
 
 
 def _model_disable_reasons(model, hf_config, copies) -> list:
     """Why the loaded model cannot be read in place (an empty list: it can)."""
+    from .binding import layer_disable_reason
+
     reasons = []
     for i in covered_layers(hf_config):
-        mlp = model.model.layers[i].mlp
-        experts = getattr(mlp, "experts", None)
-        if experts is None:
-            reasons.append(f"layer {i}: no fused experts module")
-            continue
-        if experts.w13_weight.dtype != torch.float8_e4m3fn:
-            reasons.append(f"layer {i}: experts are {experts.w13_weight.dtype}, need E4M3")
+        why = layer_disable_reason(model.model.layers[i], i)
+        if why is not None:
+            reasons.append(why)
     return reasons
 
 
 class _Layer:
-    """A covered layer: its SGLang module and its launch (``LayerOp`` for the whole
-    layer, or ``MoeFp8Op`` for its FFN half, ``full`` saying which)."""
+    """A covered layer: its index, SGLang module and launch; its caches bind at its
+    first launch and rebind when SGLang's pool moves."""
 
-    def __init__(self, i: int, module, op, full: bool = False, kv_scale=None):
-        self.i, self.module, self.op, self.full = i, module, op, full
-        self.kv_scale = kv_scale  # f32 [slots]: the per-token scales of the layer's KV rows
+    def __init__(self, i: int, module, op):
+        self.i, self.module, self.op = i, module, op
         self.caches = None
 
 
-def plan_layers(model, hf_config) -> dict:
-    """Layer -> None (the whole layer binds) or the reason its attention half does not
-    (it then runs its FFN half only)."""
-    from .binding import layer_disable_reason
-
-    return {i: layer_disable_reason(model.model.layers[i], i) for i in covered_layers(hf_config)}
-
-
 class _Built:
-    """One rank's launches and the forward SGLang calls for a routed step."""
+    """One rank's layer launches, the step's row tables per width, and the forward."""
 
-    def __init__(self, lm, layers: dict, device, context_len: int, max_rows: int = MAX_ROWS):
+    def __init__(self, lm, layers: dict, device, context_len: int):
         self.lm, self.layers = lm, layers
-        self.max_rows = max_rows
+        self.first = min(layers) if layers else None
+        self.last = max(layers) if layers else None
+        self.max_rows = MAX_ROWS
         self.max_position = context_len - 1
-        self.steps = {w: alloc_step(w, device) for w in WIDTHS}
-        self.check_layers = os.environ.get("SGLANG_AMD_MONO_CHECK") == "1"
+        self.steps = {w: StepRows.empty(w, device) for w in WIDTHS}
+        self.pad_h = {w: torch.zeros(w, DSV32.hidden, dtype=torch.bfloat16, device=device)
+                      for w in WIDTHS}
 
     def forward(self, plan, input_ids, positions, forward_batch, input_embeds=None,
                 pp_proxy_tensors=None):
@@ -158,108 +207,134 @@ class _Built:
         if plan.key.rows > self.max_rows:
             return type(lm).forward(lm, input_ids, positions, forward_batch, input_embeds,
                                     pp_proxy_tensors)
-        hidden = self._backbone(plan, input_ids, positions, forward_batch, input_embeds)
+        from sglang.srt.layers.layer_boundary import get_attn_tp_context
+
+        with get_attn_tp_context().maybe_input_scattered(forward_batch):
+            hidden = self._backbone(plan, input_ids, positions, forward_batch, input_embeds)
         return lm.logits_processor(input_ids, hidden, lm.lm_head, forward_batch, None)
 
+    def _backbone(self, plan, input_ids, positions, forward_batch, input_embeds):
+        """``DeepseekV2Model.forward``: the embedding and the dense layers on SGLang's
+        path (each returns its stream and its top-k), the covered layers as launches,
+        then the final norm."""
+        from sglang.srt.layers.layer_boundary.residual.batch import (
+            complete_output,
+            final_norm,
+            start,
+        )
+        from sglang.srt.utils.common import BumpAllocator
+
+        m = self.lm.model
+        hidden = m.embed_tokens(input_ids) if input_embeds is None else input_embeds
+        start(forward_batch)
+        zeros = BumpAllocator(buffer_size=(m.end_layer - m.start_layer) * 2,
+                              dtype=torch.float32, device=hidden.device)
+        gemm_zeros = None
+        if getattr(m, "gemm_output_zero_allocator_size", 0) > 0:
+            gemm_zeros = BumpAllocator(buffer_size=m.gemm_output_zero_allocator_size,
+                                       dtype=torch.float32, device=hidden.device)
+        topk = None
+        for i in range(m.start_layer, m.end_layer):
+            L = self.layers.get(i)
+            if L is None:
+                hidden, topk = m.layers[i](
+                    positions, hidden, forward_batch, zeros, gemm_zeros, None,
+                    prev_topk_indices=topk,
+                    next_full_attention_layer_id=m.next_full_attention_layer_id.get(i))
+            else:
+                hidden = self._layer(L, plan, positions, hidden, forward_batch)
+                topk = None
+        hidden = complete_output(hidden, forward_batch)
+        if not forward_batch.forward_mode.is_idle():
+            hidden = final_norm(hidden, forward_batch, m.norm)
+        return hidden
+
+    def _layer(self, L: _Layer, plan, positions, hidden, forward_batch):
+        """One covered layer: the first takes the full stream (the previous layer's output
+        with its pending residual add folded in), padded to the width; later ones take
+        the previous launch's output. The last hands its rows back as a written stream."""
+        from sglang.srt.layers.layer_boundary.residual.batch import fold, set_written, take_output
+
+        S = plan.key.rows
+        W = _width(S)
+        st = self.step(plan, positions, forward_batch)
+        if L.i == self.first:
+            h = take_output(fold(hidden, forward_batch), forward_batch)
+            if S < W:
+                pad = self.pad_h[W]
+                pad[:S].copy_(h)
+                pad[S:].zero_()
+                h = pad
+        else:
+            h = hidden
+        out = L.op.launch(h, self._caches(L, forward_batch), st.as_layer_step(W))
+        if L.i != self.last:
+            return out
+        return set_written(out[:S], forward_batch)
+
     def step(self, plan, positions, forward_batch):
-        """The step's row tables, built once a step (in the graph when captured)."""
+        """The step's row tables, written once a step (in the graph when captured)."""
         if "step" not in plan.state:
             S = plan.key.rows
             st = self.steps[_width(S)]
-            pt = None
-            if any(L.full for L in self.layers.values()):
+            md = getattr(getattr(forward_batch, "attn_backend", None), "forward_metadata", None)
+            pt = getattr(md, "real_page_table", None)
+            if pt is None:
                 pt = page_table(forward_batch.req_to_token_pool.req_to_token,
                                 forward_batch.req_pool_indices, S, self.max_position + 1)
-            plan.state["step"] = fill_step(st, positions, forward_batch.out_cache_loc, S,
-                                           self.max_position, page_table=pt)
+            st.write(positions, forward_batch.out_cache_loc, S, self.max_position,
+                     page_table=pt)
+            plan.state["step"] = _Step(st)
         return plan.state["step"]
 
-    def _backbone(self, plan, input_ids, positions, forward_batch, input_embeds):
-        """The embedding and dense layers on SGLang's path; a fully bound layer as its
-        four launches; any other covered layer's attention half on its module and its
-        FFN half as one launch."""
-        m = self.lm.model
-        hidden = m.embed_tokens(input_ids) if input_embeds is None else input_embeds
-        st = self.step(plan, positions, forward_batch)
-        for i, layer in enumerate(m.layers):
-            L = self.layers.get(i)
-            if L is None:
-                hidden = layer(positions, hidden, forward_batch)
-            elif L.full:
-                hidden = L.op.launch(hidden.contiguous(), self._caches(L, forward_batch),
-                                     self._layer_step(st, forward_batch, plan.key.rows))
-            else:
-                a = layer.attention_half(positions, hidden, forward_batch)
-                hidden = L.op.launch(a.contiguous())
-        return m.norm(hidden)
-
     @staticmethod
-    def _caches(L, forward_batch):
+    def _caches(L: _Layer, forward_batch):
         """The layer's caches in SGLang's pool, bound once (rebound if the pool moved)."""
         from .binding import caches
 
         pool = forward_batch.token_to_kv_pool
-        if getattr(pool, "page_size", 64) != 64:
-            raise RuntimeError(f"KV pool page size {pool.page_size}: the launches' pages hold 64")
         kv = pool.get_key_buffer(L.i)
         if L.caches is None or L.caches.kv.data_ptr() != kv.data_ptr():
-            if L.kv_scale is None or L.kv_scale.numel() * kv.shape[-1] != kv.numel():
-                L.kv_scale = torch.ones(kv.numel() // kv.shape[-1], dtype=torch.float32,
-                                        device=kv.device)
-            L.caches = caches(pool, L.i, L.kv_scale)
+            L.caches = caches(pool, L.i)
         return L.caches
 
-    @staticmethod
-    def _layer_step(st, forward_batch, rows: int):
-        """The launches' row tables from the step's: a row's page table is its request's
-        slots at every 64th position, as page ids."""
+
+class _Step:
+    """A step's tables as the launches take them."""
+
+    def __init__(self, st: StepRows):
+        self.st = st
+
+    def as_layer_step(self, width: int):
         from .layer import LayerStep
 
-        if st.page_table.shape[0] < rows:
-            raise RuntimeError("the step has no page table: fill_step(page_table=...) first")
-        return LayerStep(positions=st.positions[:rows], slots=st.slots[:rows],
-                         req_ids=st.req_ids[:rows], page_table=st.page_table)
+        st = self.st
+        return LayerStep(positions=st.positions[:width], slots=st.slots[:width],
+                         req_ids=st.req_ids[:width], page_table=st.page_table)
 
 
 def _build(model, hf_config, ctx):
-    """The launches of every covered layer, over SGLang's loaded weights in place."""
-    from sglang.srt.runtime_context import get_parallel
-
+    """The launches of every covered layer, over SGLang's loaded weights in place. Layers
+    share one set of runtimes (scratch and guard): their launches are stream ordered."""
     from ..guard import watchdog_deadline
-    from .attn import MAX_CTX
-    from .binding import layer_weights, moe_weights
-    from .front import FRONT_MAX_ROWS
-    from .layer import LayerOp
-    from .moe import MoeFp8Op
+    from .binding import layer_weights
+    from .layer import LayerOp, LayerRuntimes
 
-    p = get_parallel()
-    if p.tp_size > 1:
-        raise ValueError(
-            f"the DSA monokernel computes one GPU's TP share, but its TP exchanges are "
-            f"not built: TP {p.tp_size} would serve unreduced partials")
     deadline = watchdog_deadline(getattr(ctx, "deadline_s", 120.0) * 2)
-    context_len = getattr(ctx, "context_len", 163840)
+    context_len = int(getattr(ctx, "context_len", None) or MAX_CONTEXT)
     copies = getattr(ctx, "copies", None)
     copies = {} if copies is None else copies
-    layers = {}
-    plans = plan_layers(model, hf_config)
-    if context_len > MAX_CTX:  # the attention launch's score rows end at MAX_CTX keys
-        plans = {i: f"context {context_len} > {MAX_CTX}" for i in plans}
-    for i, why in plans.items():
+    sm_scale = softmax_scale(hf_config)
+    layers, shared = {}, None
+    for i in covered_layers(hf_config):
         mod = model.model.layers[i]
-        if why is None:
-            w = layer_weights(mod, i, copies)
-            op = LayerOp(w, w.moe.w13.device, max_rows=FRONT_MAX_ROWS, ctx_max=context_len,
-                         deadline_s=deadline)
-            layers[i] = _Layer(i, mod, op, full=True)
-        else:
-            w = moe_weights(mod)
-            op = MoeFp8Op(w, w.w13.device, max_rows=MAX_ROWS, deadline_s=deadline)
-            layers[i] = _Layer(i, mod, op)
-    device = next(iter(layers.values())).op.device
-    full = any(L.full for L in layers.values())
-    return _Built(model, layers, device, context_len=context_len,
-                  max_rows=FRONT_MAX_ROWS if full else MAX_ROWS)
+        w = layer_weights(mod, i, copies)
+        if shared is None:
+            shared = LayerRuntimes(w.moe.w13.device, max_rows=MAX_ROWS,
+                                   ctx_max=min(context_len, MAX_CONTEXT), deadline_s=deadline)
+        layers[i] = _Layer(i, mod, LayerOp(w, shared, sm_scale=sm_scale))
+    device = shared.device if shared is not None else torch.device("cpu")
+    return _Built(model, layers, device, context_len=min(context_len, MAX_CONTEXT))
 
 
 SPEC = MonoSpec(

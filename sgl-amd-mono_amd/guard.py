@@ -12,7 +12,7 @@ process down (``sgl_amd_mono/common/guard.py:91-97``). Here the launch ends norm
 and the host raises instead: a deliberate GPU fault is not an acceptable stop on a
 shared MI355X node, and a launch that never runs on after a failed wait keeps the
 same guarantee (no output of a failed step is used, because the host refuses to go
-on). Deadline and fault-injection semantics follow ``guard.py:60-88``.
+on). The fault-injection variable and its format are the reference's (``guard.py:79-88``).
 """
 
 from __future__ import annotations
@@ -22,26 +22,18 @@ from typing import Optional
 
 from . import _lib
 
-CLOCK_HZ = 100_000_000
-# the reference compares time in 2^8-tick units as 32-bit scalars (guard.py:60-66);
-# the same bound keeps a deadline portable between the two
-TICK_SHIFT = 8
-MAX_DEADLINE_TICKS = (1 << 31 << TICK_SHIFT) - 1
+CLOCK_HZ = 100_000_000  # s_memrealtime ticks a second
+# the kernels compare 64-bit tick differences, so any deadline fits; an hour bounds it
+# far above every server watchdog, so a larger value is a configuration mistake
+MAX_DEADLINE_S = 3600.0
 FAULT_ENV = "SGLANG_AMD_MONO_FAULT_INJECT"
 
 
 def deadline_ticks(seconds: float) -> int:
-    """Seconds -> clock ticks; refuses a deadline the 32-bit check cannot hold
-    (``guard.py:69-76``)."""
-    ticks = int(seconds * CLOCK_HZ)
-    if ticks <= 0:
-        raise ValueError(f"a wait deadline must be positive, got {seconds} s")
-    if ticks > MAX_DEADLINE_TICKS:
-        raise ValueError(
-            f"a {seconds} s wait deadline does not fit the wait's 32-bit check; "
-            f"use at most {MAX_DEADLINE_TICKS // CLOCK_HZ} s"
-        )
-    return ticks
+    """A wait deadline in clock ticks; ``ValueError`` outside (0, MAX_DEADLINE_S]."""
+    if not 0.0 < float(seconds) <= MAX_DEADLINE_S:
+        raise ValueError(f"wait deadline {seconds!r} s: must lie in (0, {MAX_DEADLINE_S:g}] s")
+    return max(1, int(float(seconds) * CLOCK_HZ))
 
 
 def watchdog_deadline(watchdog_timeout: float) -> float:
@@ -50,14 +42,19 @@ def watchdog_deadline(watchdog_timeout: float) -> float:
 
 
 def fault_injection(rank: int) -> Optional[tuple[int, int]]:
-    """``SGLANG_AMD_MONO_FAULT_INJECT=rank:site[:after]`` -> (site, after) for this rank,
-    else None (``guard.py:79-88``). Once ``after`` launches ran, the wait at ``site``
-    never completes, so it times out."""
-    spec = os.environ.get(FAULT_ENV, "")
-    if not spec:
+    """The test fault injection ``SGLANG_AMD_MONO_FAULT_INJECT=rank:site[:after]`` (the
+    reference's variable and format, ``guard.py:79-88``) for ``rank``: (site, after), or
+    None when unset or meant for another rank. Once ``after`` launches ran on a runtime,
+    its wait at ``site`` never completes and times out."""
+    raw = os.environ.get(FAULT_ENV, "").strip()
+    if not raw:
         return None
-    r, site, after = (spec.split(":") + ["0", "0"])[:3]
-    return (int(site or 0), int(after or 0)) if int(r) == rank else None
+    fields = raw.split(":")
+    if len(fields) not in (2, 3) or not all(f.strip().lstrip("-").isdigit() for f in fields):
+        raise ValueError(f"{FAULT_ENV}={raw!r}: expected rank:site or rank:site:after")
+    who, site = int(fields[0]), int(fields[1])
+    after = int(fields[2]) if len(fields) == 3 else 0
+    return (site, after) if who == rank else None
 
 
 def describe(words) -> Optional[str]:

@@ -19,6 +19,17 @@ from . import _lib, guard
 SCRUB_EVERY = 1 << 30
 
 
+def shared_or_new(rt, scratch_bytes: int, device, deadline_s: float) -> "MonoRuntime":
+    """``rt`` when it is given (a runtime shared by the stream-ordered launches of many
+    layers; its scratch must be at least ``scratch_bytes``), else a runtime of its own."""
+    if rt is None:
+        return MonoRuntime(scratch_bytes, device, deadline_s)
+    if rt.device != torch.device(device) or rt.scratch.numel() < scratch_bytes:
+        raise ValueError(f"a shared runtime on {rt.device} with {rt.scratch.numel()} B of "
+                         f"scratch cannot serve a launch needing {scratch_bytes} B on {device}")
+    return rt
+
+
 class MonoRuntime:
     """Scratch + guard of one launch kind on ``device``."""
 

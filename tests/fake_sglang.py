@@ -98,14 +98,72 @@ def find_spec(backend, architectures, isa, model_type=None):
 PARALLEL = SimpleNamespace(tp_size=1, tp_rank=0)
 
 
+# SGLang's layer-boundary residual protocol, as the reference's backbone uses it
+# (glm53/spec.py:319-417): a decoder layer returns its output with the residual add still
+# pending in the batch's state; the next layer's input norm (or fold) completes it.
+def start(fb):
+    fb.pending = None
+    fb.written = False
+
+
+def fold(hidden, fb):
+    """The full stream: the pending residual added."""
+    out = hidden if fb.pending is None else hidden + fb.pending
+    fb.pending = None
+    return out
+
+
+def take_output(hidden, fb):
+    return hidden
+
+
+def set_written(hidden, fb):
+    fb.written = True
+    fb.pending = None
+    return hidden
+
+
+def complete_output(hidden, fb):
+    return fold(hidden, fb)
+
+
+def final_norm(hidden, fb, norm):
+    return norm(hidden)
+
+
+class _TpContext:
+    class _Scope:
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *a):
+            return False
+
+    def maybe_input_scattered(self, fb):
+        return self._Scope()
+
+
+class BumpAllocator:
+    def __init__(self, buffer_size, dtype, device):
+        self.size = buffer_size
+
+
 def install():
     """Put the stand-in modules into sys.modules (idempotent)."""
     if "sglang.kernels.plugin_kernels.amd.spec" in sys.modules:
         return sys.modules["sglang.kernels.plugin_kernels.amd.spec"]
     names = ["sglang", "sglang.kernels", "sglang.kernels.plugin_kernels",
              "sglang.kernels.plugin_kernels.amd", "sglang.kernels.plugin_kernels.amd.spec",
-             "sglang.srt", "sglang.srt.runtime_context"]
+             "sglang.srt", "sglang.srt.runtime_context", "sglang.srt.layers",
+             "sglang.srt.layers.layer_boundary", "sglang.srt.layers.layer_boundary.residual",
+             "sglang.srt.layers.layer_boundary.residual.batch", "sglang.srt.utils",
+             "sglang.srt.utils.common"]
     mods = {n: types.ModuleType(n) for n in names}
+    batch = mods["sglang.srt.layers.layer_boundary.residual.batch"]
+    for f in (start, fold, take_output, set_written, complete_output, final_norm):
+        setattr(batch, f.__name__, f)
+    mods["sglang.srt.layers.layer_boundary"].get_attn_tp_context = lambda: _TpContext()
+    mods["sglang.srt.utils.common"].BumpAllocator = BumpAllocator
     spec = mods["sglang.kernels.plugin_kernels.amd.spec"]
     for name, obj in dict(Feature=Feature, NumericsKind=NumericsKind, Numerics=Numerics,
                           DeviceLimits=DeviceLimits, Requirements=Requirements,

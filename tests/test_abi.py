@@ -52,9 +52,14 @@ def test_null_args_are_refused_without_a_gpu():
     mx = _lib.MonoMoeMxfp4Args(rows=17, experts=256)
     assert _lib.lib().mono_moe_mxfp4_launch(ctypes.byref(mx), None) == _lib.MONO_E_ARG
     assert "rows" in _lib.last_error()
-    at = _lib.MonoAttnArgs(rows=8, heads=32, index_heads=64, topk=2048, page=64, ctx_max=40000)
+    at = _lib.MonoAttnArgs(rows=8, rows_max=8, heads=32, index_heads=64, topk=2048, page=64,
+                           ctx_max=40000)
     assert _lib.lib().mono_attn_launch(ctypes.byref(at), None) == _lib.MONO_E_ARG
     assert "ctx_max" in _lib.last_error()
+    at = _lib.MonoAttnArgs(rows=9, rows_max=8, heads=32, index_heads=64, topk=2048, page=64,
+                           ctx_max=4096)
+    assert _lib.lib().mono_attn_launch(ctypes.byref(at), None) == _lib.MONO_E_ARG
+    assert "rows_max" in _lib.last_error()
     po = _lib.MonoPostArgs(rows=17, heads=32, hidden=7168)
     assert _lib.lib().mono_post_launch(ctypes.byref(po), None) == _lib.MONO_E_ARG
     assert "rows" in _lib.last_error()
@@ -72,19 +77,19 @@ def test_scratch_bytes_only_for_built_geometries():
     assert _lib.lib().mono_moe_mxfp4_scratch_bytes(3072, 384, 256) > 0
     assert _lib.lib().mono_moe_mxfp4_scratch_bytes(3072, 512, 256) == 0
     assert _lib.lib().mono_attn_scratch_bytes(48) > 0 and _lib.lib().mono_attn_scratch_bytes(49) == 0
+    # sized by the rows it serves: 8 rows need about a sixth of 48 rows' scratch
+    assert 5 * _lib.lib().mono_attn_scratch_bytes(8) < _lib.lib().mono_attn_scratch_bytes(48)
     assert _lib.lib().mono_post_scratch_bytes() >= 16 * 4096 * 2
     assert _lib.lib().mono_front_scratch_bytes() > 0
 
 
 def test_deadline_ticks_bounds():
-    # the reference refuses deadlines past the 32-bit check (test_guard_hip.py:98-109)
+    # the 100 MHz clock: a second is 10^8 ticks; deadlines lie in (0, 1 h]
     assert guard.deadline_ticks(1.0) == 100_000_000
-    # 2^31 units of 2^8 ticks at 100 MHz: 5497 s
-    assert guard.deadline_ticks(5497) <= guard.MAX_DEADLINE_TICKS
-    with pytest.raises(ValueError):
-        guard.deadline_ticks(5498)
-    with pytest.raises(ValueError):
-        guard.deadline_ticks(0)
+    assert guard.deadline_ticks(3600) == 360_000_000_000
+    for bad in (3600.5, 0, -1.0):
+        with pytest.raises(ValueError, match="wait deadline"):
+            guard.deadline_ticks(bad)
     assert guard.watchdog_deadline(300) == 60.0 and guard.watchdog_deadline(30) == 15.0
 
 
@@ -94,6 +99,10 @@ def test_fault_injection_env(monkeypatch):
     assert guard.fault_injection(0) is None
     monkeypatch.setenv(guard.FAULT_ENV, "0:2")
     assert guard.fault_injection(0) == (2, 0)
+    for bad in ("0", "0:x", "1:2:3:4"):
+        monkeypatch.setenv(guard.FAULT_ENV, bad)
+        with pytest.raises(ValueError, match="rank:site"):
+            guard.fault_injection(0)
     monkeypatch.delenv(guard.FAULT_ENV)
     assert guard.fault_injection(0) is None
 

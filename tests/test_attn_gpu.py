@@ -89,6 +89,15 @@ def test_attention_48_rows(gpu):
     _check(op, inp, full_score_rows=0, sample=1024)
 
 
+def test_attention_48_rows_at_32k(gpu):
+    """Config 3's widest case: 48 rows each at position 32767 (128-key splits), scores
+    sampled, every row's selection and output checked in full."""
+    print("case attention rows=48 ctx=32768", flush=True)
+    inp = synthetic.attention_inputs(48, 32768, gpu, seed=4832)
+    op = AttnOp(gpu, max_rows=48)
+    _check(op, inp, full_score_rows=1, sample=1024)
+
+
 def _patterned(inp, ids, codes, scales):
     """Every cached index key of slot-in-page s takes pattern ids[s]: E2M1 codes
     codes[p] ([4, 16] bytes) and E8M0 scales scales[p] ([4]); the scores then take one

@@ -4,6 +4,7 @@ own formats, refusals naming the tensor, and the cache checks."""
 
 from types import SimpleNamespace as NS
 
+import numpy as np
 import pytest
 import torch
 
@@ -111,20 +112,45 @@ def _pool(slots=256, pages=4):
 
 def test_caches_bind_in_place_and_refuse_other_layouts():
     pool, kv, pay, sc = _pool()
-    c = binding.caches(pool, 7, torch.ones(256))
+    c = binding.caches(pool, 7)
     assert c.kv.data_ptr() == kv.data_ptr() and c.kv.shape == (256, 576) and c.kv.dtype == torch.uint8
     assert c.plane.data_ptr() == pay.data_ptr() and c.plane.shape == (4, 4, 64, 16)
     assert c.plane_scale.data_ptr() == sc.data_ptr() and c.plane_scale.shape == (4, 4, 64)
-    with pytest.raises(RuntimeError, match="KV scales"):
-        binding.caches(pool, 7, torch.ones(255))
+    # SGLang's MLA rows are raw E4M3: the launches keep no scale beside the pool, so a
+    # slot that SGLang rewrites after the front wrote it reads back as SGLang wrote it
+    assert c.kv_scale is None
     wide = NS(**vars(pool))
     wide.get_key_buffer = lambda i: torch.zeros(256, 1, 656, dtype=torch.uint8)
     with pytest.raises(RuntimeError, match="MLA cache"):
-        binding.caches(wide, 7, torch.ones(256))
+        binding.caches(wide, 7)
     paged = NS(**vars(pool))
     paged.get_index_k_fp4_payload_buffer = lambda i: torch.zeros(4, 1, 64, 132, dtype=torch.uint8)
     with pytest.raises(RuntimeError, match="FP4 index pages"):
-        binding.caches(paged, 7, torch.ones(256))
+        binding.caches(paged, 7)
+
+
+def test_a_reused_slot_reads_back_unscaled():
+    """A slot the front wrote (raw E4M3 of the row, oracle.front.kv_quant unscaled), then
+    freed and rewritten by SGLang with another row: the attention's reader (oracle.attn
+    kv_rows without scales, as the launch reads the bound pool) sees exactly the new
+    row's E4M3 values, with no scale left over from the first writer."""
+    from oracle import attn as A
+    from oracle import formats as F
+    from oracle import front as Fr
+
+    pool, kv, _, _ = _pool()
+    c = binding.caches(pool, 7)
+    g = torch.Generator().manual_seed(5)
+    first = torch.randn(576, generator=g).to(torch.bfloat16).float().numpy() * 40
+    codes, sc = Fr.kv_quant(first, scaled=False)
+    assert sc == 1.0
+    c.kv[9] = torch.from_numpy(codes)  # the front's write
+    np_first = A.kv_rows(c.kv.numpy(), c.kv_scale, [9])[0]
+    assert np.allclose(np_first, F.e4m3_to_f32(codes))
+    second = torch.randn(576, generator=g) * 0.01
+    kv[9, 0] = second.to(FP8)  # SGLang's own write of the reused slot
+    got = A.kv_rows(c.kv.numpy(), c.kv_scale, [9])[0]
+    assert np.array_equal(got, second.to(FP8).float().numpy())
 
 
 def test_page_tables_come_from_req_to_token():
@@ -140,7 +166,7 @@ def test_page_tables_come_from_req_to_token():
     assert torch.equal(pt[0], perm[8:12].to(torch.int32)) and torch.equal(pt[1], perm[0:4].to(torch.int32))
 
 
-def test_every_covered_layer_is_planned_with_its_reason():
+def test_a_layer_that_cannot_bind_refuses_the_model_with_its_reason():
     from tests import fake_sglang
 
     fake_sglang.install()
@@ -156,5 +182,8 @@ def test_every_covered_layer_is_planned_with_its_reason():
     dense_attn.indexer = None
     other = NS(**{**vars(ok), "self_attn": dense_attn})
     model = NS(model=NS(layers=[None, ok, other]))
-    plans = spec.plan_layers(model, NS(first_k_dense_replace=1, num_hidden_layers=3))
-    assert plans[1] is None and "indexer" in plans[2] and 0 not in plans
+    reasons = spec._model_disable_reasons(model, NS(first_k_dense_replace=1,
+                                                    num_hidden_layers=3), {})
+    assert len(reasons) == 1 and reasons[0].startswith("layer 2:") and "indexer" in reasons[0]
+    assert spec._model_disable_reasons(NS(model=NS(layers=[None, ok])),
+                                       NS(first_k_dense_replace=1, num_hidden_layers=2), {}) == []

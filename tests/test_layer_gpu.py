@@ -44,9 +44,19 @@ def _ragged(step: LayerStep, positions) -> LayerStep:
 def test_layer_eight_rows_ragged_contexts(gpu):
     """8 rows seeing 8192, 5001, 2049, 2048, 101, 7001, 3000 and 1 keys."""
     print("case layer rows=8 ctx<=8192 ragged", flush=True)
-    rows, ctx = 8, 8192
-    w, caches, step, h = synthetic.layer(rows, ctx, gpu, seed=3)
-    step = _ragged(step, [8191, 5000, 2048, 2047, 100, 7000, 2999, 0])
+    _layer_case(gpu, 8, 8192, [8191, 5000, 2048, 2047, 100, 7000, 2999, 0], seed=3)
+
+
+def test_layer_eight_rows_at_32k(gpu):
+    """Config 5's step: 8 rows each at position 32767 (the bench's workload)."""
+    print("case layer rows=8 ctx=32768", flush=True)
+    _layer_case(gpu, 8, 32768, None, seed=32)
+
+
+def _layer_case(gpu, rows, ctx, positions, seed):
+    w, caches, step, h = synthetic.layer(rows, ctx, gpu, seed=seed)
+    if positions is not None:
+        step = _ragged(step, positions)
     op = LayerOp(w, gpu, max_rows=rows, ctx_max=ctx)
     f = op.front.launch(h, caches, step.positions, step.slots)
     inp = AttnInputs(q=f.q, iq=f.iq, iqs=f.iqs, iw=f.iw, plane=caches.plane,
@@ -71,7 +81,7 @@ def test_layer_eight_rows_ragged_contexts(gpu):
     plane, psc = caches.plane.cpu().numpy(), caches.plane_scale.cpu().numpy()
     kv, ksc = caches.kv.cpu().numpy(), caches.kv_scale.cpu().numpy()
     pt = step.page_table.cpu().numpy()
-    rng = np.random.default_rng(3)
+    rng = np.random.default_rng(seed)
     for r in range(rows):
         n = int(pos[r]) + 1
         pages = pt[r]

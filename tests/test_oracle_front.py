@@ -105,3 +105,67 @@ def test_plane_and_query_bytes_read_back_through_the_attention_oracle():
     for r in range(2):
         v, e = A.index_query(iq[r], iqs[r])
         np.testing.assert_array_equal(v.reshape(64, 128) * np.repeat(2.0 ** e, 32, -1), qd[r])
+
+
+# Known answers for the index key and query chains' bf16 rounding points. Each input is
+# built so that one rounding decides an FP4 code; the expected codes are derived by hand
+# in the docstrings (bf16 spacing 2^(e - 7) in [2^e, 2^(e + 1)); E2M1 grid 0, 0.5, 1, 1.5,
+# 2, 3, 4, 6 with codes 0..7, ties to the even code), so dropping the rounding fails.
+_IDENT = (np.ones((1, 32)), np.zeros((1, 32)))   # RoPE by angle 0: cos 1, sin 0
+
+
+def _two_hot(a, b, lead=(1, 64)):
+    v = np.zeros(lead + (128,))
+    v[..., 0], v[..., 1] = a, b
+    return v
+
+
+def test_index_query_rounds_the_hadamard_output_to_bf16():
+    """iq_raw = 39.5 e0 + 0.052734375 e1 in every head, RoPE by angle 0. The Hadamard
+    output is (39.5 +- 0.052734375) / sqrt(128): 3.49600 at even dims, 3.48668 at odd
+    ones, which bf16 makes 3.5 and 3.484375 (spacing 2^-6). amax 3.5 gives scale 1 (E8M0
+    127); 3.5 is the tie of E2M1 3 and 4 and takes the even code 6; 3.484375 takes 3,
+    code 5. Unrounded, 3.49600 would take code 5."""
+    d = Fr.index_query(_two_hot(39.5, 0.052734375), *_IDENT)
+    assert np.all(d["codes"][..., 0::2] == 6) and np.all(d["codes"][..., 1::2] == 5)
+    assert np.all(d["e8"] == 127)
+
+
+def test_index_query_rounds_the_rotated_half_to_bf16():
+    """iq_raw dims (0, 1) = (38.5, 0.07470703125) rotated by the bf16 table pair (cos,
+    sin) = (0.97265625, 0.234375): (37.429756, 9.096102), which bf16 makes (37.5, 9.125)
+    (spacing 2^-2 and 2^-4). The Hadamard output: (37.5 + 9.125) / sqrt(128) = 4.12108
+    at even dims (bf16 4.125, amax: scale 1) and (37.5 - 9.125) / sqrt(128) = 2.50802 at
+    odd ones (bf16 2.515625, above the 2.5 tie of E2M1 2 and 3: code 5). Unrounded,
+    (37.429756 - 9.096102) / sqrt(128) = 2.50436 would be bf16 2.5, the tie: code 4."""
+    cs = (np.full((1, 32), 0.97265625), np.full((1, 32), 0.234375))
+    d = Fr.index_query(_two_hot(38.5, 0.07470703125), *cs)
+    assert np.all(d["codes"][..., 0::2] == 6) and np.all(d["codes"][..., 1::2] == 5)
+    assert np.all(d["e8"] == 127)
+
+
+def test_index_key_rounds_like_the_query():
+    """With k = 0 and g = 0 the LayerNorm returns b exactly, so the key chain over b is the
+    query chain over the same vector: both constructions above give the same codes."""
+    zeros = np.zeros((1, 128))
+    for a, b, cs in ((39.5, 0.052734375, _IDENT),
+                     (38.5, 0.07470703125, (np.full((1, 32), 0.97265625),
+                                            np.full((1, 32), 0.234375)))):
+        d = Fr.index_key(zeros, np.zeros(128), _two_hot(a, b, (1,))[0], *cs)
+        assert np.all(d["codes"][0, 0::2] == 6) and np.all(d["codes"][0, 1::2] == 5)
+        assert np.all(d["e8"] == 127)
+
+
+def test_index_key_rounds_the_norm_to_bf16():
+    """k = 0.006 e0 - 0.006 e1, g = 0.515625 on dims 0 and 1, b = 0, RoPE by angle 0:
+    mean 0, variance 0.006^2 / 64, so n0 = -n1 = 8 g 0.006 / sqrt(0.006^2 + 64e-6) = 2.475
+    and the other dims 0; bf16 2.46875. The Hadamard output is 0 at even dims and
+    2 n0 / sqrt(128) = 0.436420 at odd ones, bf16 0.435546875; scale pow2_ceil(0.4355 / 6)
+    = 2^-3 (E8M0 124) and 3.484375 takes E2M1 3, code 5. Unrounded, n0 = 2.475 would give
+    0.437521, bf16 0.4375, i.e. 3.5, the tie: code 6."""
+    k = _two_hot(0.006, -0.006, (1,))
+    g = np.ones(128)
+    g[:2] = 0.515625
+    d = Fr.index_key(k, g, np.zeros(128), *_IDENT)
+    assert np.all(d["codes"][0, 0::2] == 0) and np.all(d["codes"][0, 1::2] == 5)
+    assert np.all(d["e8"][0] == 124)
