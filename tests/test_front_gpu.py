@@ -17,9 +17,11 @@ once where the reference rounds):
   the other bf16 and so the adjacent E2M1 value: at most max(2, 0.05%) of the codes;
 * end to end from h (q_an and the projections may round one bf16 ulp apart between the
   f32 and f64 paths; through the FWHT that moves every value of a head by ~2^-8 of the
-  block's magnitude, ~0.01 in units of the scale): codes differing only where the
-  oracle's scaled value sits within 0.02 of the midpoint of two adjacent grid values,
-  then only to the adjacent value, for at most 1% of codes;
+  block's magnitude, ~0.01 in units of the scale, and with bf16 inputs an FP4 tie is
+  exactly representable, so such a value can land on either side of it): codes differing
+  only where the oracle's scaled value sits within 0.02 of the midpoint of two adjacent
+  grid values, then only to the adjacent value, for at most 2% of the query's codes and
+  4% of the keys' (a few hundred codes: a one-row case sees a handful of such ties);
 * every cache slot the rows do not own unchanged, a pad row (slot -1) writes nothing."""
 
 import numpy as np
@@ -42,7 +44,7 @@ def front_w(request, gpu):
     return w, synthetic.rowmajor_front(w)
 
 
-def _fp4_close(codes_dev, e8_dev, pre, codes_ora, e8_ora, what):
+def _fp4_close(codes_dev, e8_dev, pre, codes_ora, e8_ora, what, max_frac=0.02):
     """Device FP4 (codes [.., n], e8 [.., n/32]) against the oracle's, as in the header."""
     assert np.array_equal(e8_dev, e8_ora), what
     sc = np.repeat(2.0 ** (e8_ora.astype(np.float64) - 127), 32, -1)
@@ -58,7 +60,8 @@ def _fp4_close(codes_dev, e8_dev, pre, codes_ora, e8_ora, what):
         ia = np.searchsorted(grid, np.abs(a))
         ib = np.searchsorted(grid, np.abs(b))
         assert np.all((np.abs(ia - ib) <= 1) & (np.sign(a) * np.sign(b) >= 0)), what
-        assert diff.sum() <= 0.01 * diff.size, (what, int(diff.sum()))
+        assert diff.sum() <= max_frac * diff.size, (what, int(diff.sum()))
+    print(f"{what}: {int(diff.sum())} of {diff.size} codes one step apart", flush=True)
     return int(diff.sum())
 
 
@@ -76,6 +79,8 @@ def _fp4_tight(codes_dev, e8_dev, codes_ora, e8_ora, what):
         ib = np.searchsorted(grid, np.abs(ov[diff]))
         assert np.all((np.abs(ia - ib) <= 1) & (np.sign(dv[diff]) * np.sign(ov[diff]) >= 0)), what
     assert diff.sum() <= max(2, 5e-4 * diff.size), (what, int(diff.sum()))
+    if diff.any():
+        print(f"{what}: {int(diff.sum())} of {diff.size} codes one step apart", flush=True)
     return int(diff.sum())
 
 
@@ -136,6 +141,7 @@ def _run_case(gpu, front_w, rows, positions, slots, seed, scaled=True):
     plane, psc = caches.plane.cpu().numpy(), caches.plane_scale.cpu().numpy()
     exp_kv, exp_ksc = before["kv"].cpu().numpy().copy(), before["kv_scale"].cpu().numpy().copy()
     exp_plane, exp_psc = before["plane"].cpu().numpy().copy(), before["plane_scale"].cpu().numpy().copy()
+    key_dev, key_ora = [], []
     for r, s in enumerate(slots):
         if s < 0:
             continue
@@ -153,11 +159,16 @@ def _run_case(gpu, front_w, rows, positions, slots, seed, scaled=True):
         page, sl_ = divmod(s, 64)
         codes = _nibbles(plane[page, :, sl_, :].reshape(-1))
         e8k = psc[page, :, (sl_ % 16) * 4 + sl_ // 16]
-        _fp4_close(codes, e8k, ref["ik"][r], ref["ik_codes"][r], ref["ik_e8"][r], f"index key {r}")
+        key_dev.append((codes, e8k))
+        key_ora.append((ref["ik"][r], ref["ik_codes"][r], ref["ik_e8"][r]))
         _fp4_tight(codes, e8k, kd["codes"][r], kd["e8"][r], f"index key {r} from ik_raw")
         exp_kv[s], exp_ksc[s] = kv[s], ksc[s]
         exp_plane[page, :, sl_, :] = plane[page, :, sl_, :]
         exp_psc[page, :, (sl_ % 16) * 4 + sl_ // 16] = e8k
+    if key_dev:
+        _fp4_close(np.stack([c for c, _ in key_dev]), np.stack([e for _, e in key_dev]),
+                   np.stack([p for p, _, _ in key_ora]), np.stack([c for _, c, _ in key_ora]),
+                   np.stack([e for _, _, e in key_ora]), "index keys", max_frac=0.04)
     assert np.array_equal(kv, exp_kv) and np.array_equal(ksc, exp_ksc)
     assert np.array_equal(plane, exp_plane) and np.array_equal(psc, exp_psc)
     return op, out
