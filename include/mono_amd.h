@@ -137,6 +137,19 @@ typedef struct {
 size_t mono_moe_fp8_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts);
 int mono_moe_fp8_launch(const MonoMoeFp8Args* args, mono_stream_t stream);
 
+/* mono_moe_fp8_launch without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The scratch and the guard block live in
+ * a static device array of this library (18.9 MiB a GPU, held until the process ends,
+ * its address looked up once per device on the first call there): args->scratch and
+ * args->guard must be null; hidden 7168, inter 512, 256 experts and at most 16 rows,
+ * else MONO_E_ARG. Every call on one GPU shares that GPU's block and its launch tags, so
+ * calls that overlap on one GPU (two streams, no ordering) race; calls ordered on one
+ * stream are safe. The waits use the library's default 10 s deadline. A timed-out call
+ * leaves the block unusable: pass a pinned host_error word, and a call seeing it
+ * non-zero is refused with MONO_E_FAILED. */
+int mono_moe_fp8_launch_static(const MonoMoeFp8Args* args, mono_stream_t stream);
+
 /* ------------------------------------------------------------------------------
  * MXFP4 (A16W4) routed MoE as one persistent launch: the gate logits are given, the
  * rows x are bf16 and stay bf16 (no activation quant); experts are E2M1 codes (two a

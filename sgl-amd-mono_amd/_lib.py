@@ -244,6 +244,7 @@ SIGNATURES = {
     "mono_reset": (c_int32, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "mono_moe_fp8_scratch_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "mono_moe_fp8_launch": (c_int32, [ctypes.POINTER(MonoMoeFp8Args), c_void_p]),
+    "mono_moe_fp8_launch_static": (c_int32, [ctypes.POINTER(MonoMoeFp8Args), c_void_p]),
     "mono_moe_mxfp4_scratch_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "mono_moe_mxfp4_launch": (c_int32, [ctypes.POINTER(MonoMoeMxfp4Args), c_void_p]),
     "mono_attn_scratch_bytes": (c_size_t, [c_int32]),

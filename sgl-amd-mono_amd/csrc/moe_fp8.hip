@@ -30,7 +30,9 @@
 // :1575-1629 (route_top8), :4352-4999 (up/gate), :5001-5187 (down), :1440-1450
 // (quant_scaled), :1665-1669 (W == 1 residual add).
 #include <hip/hip_runtime.h>
+#include <stdio.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "moe_common.h"
@@ -887,15 +889,19 @@ extern "C" size_t mono_moe_fp8_scratch_bytes(int32_t hidden, int32_t inter, int3
   return 0;
 }
 
-extern "C" int mono_moe_fp8_launch(const MonoMoeFp8Args* a, mono_stream_t stream) {
-  if (!a) return set_error(MONO_E_ARG, "mono_moe_fp8_launch: null args");
-  if (a->rows < 1 || a->rows > MOE_MAXR)
-    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: rows must be 1..16");
-  if (a->experts != MOE_NEXP)
-    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: experts must be 256");
+// the launch over the given scratch and guard block (the caller's, or the static one)
+static int moe_fp8_launch_on(const MonoMoeFp8Args* a, mono_stream_t stream, void* scratch_ptr,
+                             int32_t* guard_ptr, const char* who) {
+  char msg[160];
+  auto fail = [&](int code, const char* what) {
+    snprintf(msg, sizeof msg, "%s: %s", who, what);
+    return set_error(code, msg);
+  };
+  if (a->rows < 1 || a->rows > MOE_MAXR) return fail(MONO_E_ARG, "rows must be 1..16");
+  if (a->experts != MOE_NEXP) return fail(MONO_E_ARG, "experts must be 256");
   if (!a->a || !a->out || !a->g_post || !a->w_r || !a->bias || !a->w13 || !a->s13 || !a->w2 ||
-      !a->s2 || !a->scratch || !a->guard)
-    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: null tensor");
+      !a->s2 || !scratch_ptr || !guard_ptr)
+    return fail(MONO_E_ARG, "null tensor");
   MoeFp8Params p;
   p.rows = a->rows;
   p.eps = a->eps;
@@ -913,13 +919,13 @@ extern "C" int mono_moe_fp8_launch(const MonoMoeFp8Args* a, mono_stream_t stream
   p.scores = a->scores;
   p.ids = a->ids;
   p.weights = a->weights;
-  p.scratch = static_cast<uint8_t*>(a->scratch);
-  p.guard = a->guard;
+  p.scratch = static_cast<uint8_t*>(scratch_ptr);
+  p.guard = guard_ptr;
   p.host_err = nullptr;
   if (a->host_error) {
     void* dptr = nullptr;
     if (hipHostGetDevicePointer(&dptr, a->host_error, 0) != hipSuccess || !dptr)
-      return set_error(MONO_E_ARG, "mono_moe_fp8_launch: host_error is not pinned host memory");
+      return fail(MONO_E_ARG, "host_error is not pinned host memory");
     p.host_err = static_cast<uint32_t*>(dptr);
   }
   p.fault_site = a->fault_site;
@@ -929,16 +935,78 @@ extern "C" int mono_moe_fp8_launch(const MonoMoeFp8Args* a, mono_stream_t stream
   int rc = monokernel_grid(&grid);
   if (rc) return rc;
   if (a->layout != MONO_LAYOUT_ROWMAJOR && a->layout != MONO_LAYOUT_AITER16)
-    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: unknown weight layout");
-  if (a->hidden == 7168 && a->inter == 512) {
-    auto k = a->layout == MONO_LAYOUT_AITER16 ? moe_fp8_kernel<7168, 512, true>
-                                              : moe_fp8_kernel<7168, 512, false>;
-    rc = check_coresident(k, 1024, 0,
-                          "mono_moe_fp8_launch: one 1024-thread CTA per CU does not fit");
-    if (rc) return rc;
-    hipLaunchKernelGGL(k, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);
-  } else {
-    return set_error(MONO_E_ARG, "mono_moe_fp8_launch: unsupported hidden/inter");
+    return fail(MONO_E_ARG, "unknown weight layout");
+  if (a->hidden != 7168 || a->inter != 512) return fail(MONO_E_ARG, "unsupported hidden/inter");
+  auto k = a->layout == MONO_LAYOUT_AITER16 ? moe_fp8_kernel<7168, 512, true>
+                                            : moe_fp8_kernel<7168, 512, false>;
+  rc = check_coresident(k, 1024, 0, "mono_moe_fp8: one 1024-thread CTA per CU does not fit");
+  if (rc) return rc;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);
+  return check_launch(who);
+}
+
+extern "C" int mono_moe_fp8_launch(const MonoMoeFp8Args* a, mono_stream_t stream) {
+  if (!a) return set_error(MONO_E_ARG, "mono_moe_fp8_launch: null args");
+  return moe_fp8_launch_on(a, stream, a->scratch, a->guard, "mono_moe_fp8_launch");
+}
+
+// ------------------------------------------------------------------ allocation-free launch
+// The guard block (256 B, its 16 words first) and the launch's scratch in one static
+// device array: every GPU the library runs on holds its own copy until the process ends,
+// zeroed when the code object loads. Host code never uses the array's name as an address:
+// its per-device address comes from hipGetSymbolAddress on the first call on a device.
+constexpr size_t MOE_STATIC_GUARD = 256;
+constexpr size_t MOE_STATIC_BYTES = MOE_STATIC_GUARD + MoeFp8Geom<7168, 512>::BYTES;
+static_assert(MONO_GUARD_WORDS * 4 <= MOE_STATIC_GUARD, "the guard block fits its slot");
+
+static __device__ __align__(256) uint8_t scratch[MOE_STATIC_BYTES];
+
+namespace {
+constexpr int STATIC_MAX_DEV = 64;
+std::mutex g_static_mu;
+void* g_static_ptr[STATIC_MAX_DEV];
+
+// this device's address of the static block, looked up once per device (device current)
+int static_block(int dev, uint8_t** out) {
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  if (dev < 0 || dev >= STATIC_MAX_DEV)
+    return set_error(MONO_E_DEVICE, "mono_moe_fp8_launch_static: device index out of range");
+  if (!g_static_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      char msg[200];
+      snprintf(msg, sizeof msg, "mono_moe_fp8_launch_static: hipGetSymbolAddress: %s",
+               hipGetErrorString(e));
+      return set_error(MONO_E_DEVICE, msg);
+    }
+    g_static_ptr[dev] = ptr;
   }
-  return check_launch("mono_moe_fp8_launch");
+  *out = static_cast<uint8_t*>(g_static_ptr[dev]);
+  return MONO_OK;
+}
+}  // namespace
+
+extern "C" int mono_moe_fp8_launch_static(const MonoMoeFp8Args* a, mono_stream_t stream) {
+  if (!a) return set_error(MONO_E_ARG, "mono_moe_fp8_launch_static: null args");
+  if (a->scratch || a->guard)
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch_static: scratch and guard must be null "
+                                 "(they live in the library's static block)");
+  if (a->rows < 1 || a->rows > MOE_MAXR)
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch_static: rows must be 1..16 (the static "
+                                 "block holds the hand-offs of at most 16 rows)");
+  if (a->hidden != 7168 || a->inter != 512 || a->experts != MOE_NEXP)
+    return set_error(MONO_E_ARG, "mono_moe_fp8_launch_static: the static block is sized for "
+                                 "hidden 7168, inter 512, 256 experts");
+  if (a->host_error && *a->host_error != 0u)
+    return set_error(MONO_E_FAILED, "mono_moe_fp8_launch_static: an earlier call timed out "
+                                    "(host_error set): the static block cannot be reset");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return set_error(MONO_E_DEVICE, "mono_moe_fp8_launch_static: no current HIP device");
+  uint8_t* base = nullptr;
+  const int rc = static_block(dev, &base);
+  if (rc) return rc;
+  return moe_fp8_launch_on(a, stream, base + MOE_STATIC_GUARD, reinterpret_cast<int32_t*>(base),
+                           "mono_moe_fp8_launch_static");
 }

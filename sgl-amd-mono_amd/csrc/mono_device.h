@@ -268,6 +268,8 @@ struct Guard {
     host_err = he;
     const uint32_t epoch = head[MONO_GUARD_EPOCH];
     deadline = ((uint64_t)head[MONO_GUARD_DEADLINE_HI] << 32) | head[MONO_GUARD_DEADLINE_LO];
+    // a block nobody set a deadline on (the library's static block starts zeroed): 10 s
+    if (deadline == 0) deadline = 10ull * MONO_CLOCK_HZ;
     fault_site = (fsite > 0 && epoch >= fafter) ? fsite : 0;
     // the injected wait times out first: waits downstream of it (which stall as a
     // consequence) get four times as long, so the error word names the injected site
