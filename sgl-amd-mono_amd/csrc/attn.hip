@@ -33,6 +33,7 @@
 
 #include "mono_abi.h"
 #include "mono_device.h"
+#include "phase.h"
 #include "topk_lds.h"
 
 namespace mono {
@@ -122,23 +123,37 @@ __device__ inline v4f mfma_bf16(v8bf a, v8bf b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int SPLIT>
-__global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
+// LDS of the attention phase: the top-k arena (carved per stage), then small words
+constexpr int AT_LDS_WSUM = TOPK_ARENA_WORDS * 4;         // int [2][16], 16-byte aligned
+constexpr int AT_LDS_RES = AT_LDS_WSUM + 2 * AT_WAVES * 4;  // int [4]
+constexpr int AT_LDS_MM = AT_LDS_RES + 16;                  // u32 [2]
+constexpr int AT_LDS_WSP = AT_LDS_MM + 16;                  // f32 [NSPLIT]
+constexpr int AT_LDS_LINV = AT_LDS_WSP + AT_NSPLIT * 4;     // f32
+constexpr int AT_LDS_BYTES = AT_LDS_LINV + 16;
+
+// The attention phase (stages 1-4) in one CTA of a launch. FUSED: it runs after the front
+// in the same launch, so its inputs (q, iq, iqs, iw and the rows' own cache entries) are
+// read device-coherent, after `ready` (the front's barrier), which it calls once, after
+// its first index-page loads are in flight. Always inlined: it is instantiated in more
+// than one kernel, and as a real call it would spill around the call.
+template <int SPLIT, bool FUSED, class Ready>
+__device__ __attribute__((always_inline)) inline void attn_phase(const AttnParams& p,
+                                                                 uint8_t* lds, Guard& guard,
+                                                                 uint32_t tag, int& ok_s,
+                                                                 Ready ready) {
   const AttnScratch S(p.rows_max);
   static_assert(SPLIT == 64 || SPLIT == 128, "64- or 128-key splits");
   constexpr int NSP = AT_TOPK / SPLIT;  // splits a row
+  constexpr int XCP = FUSED ? CP_DEV : CP_NONE;  // loads of the front's outputs
   const int tid = threadIdx.x, l = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R = p.rows;
   const int nblk = gridDim.x, b = blockIdx.x;
 
-  // one LDS arena, carved per stage
-  __shared__ __attribute__((aligned(16))) uint8_t smem[TOPK_ARENA_WORDS * 4];
-  __shared__ uint32_t head_s[4];
-  __shared__ int ok_s;
-  __shared__ __attribute__((aligned(16))) int wsum[2 * AT_WAVES];
-  __shared__ int res_s[4];
-  __shared__ uint32_t mm_s[2];
+  uint8_t* smem = lds;
+  int* wsum = reinterpret_cast<int*>(lds + AT_LDS_WSUM);
+  int* res_s = reinterpret_cast<int*>(lds + AT_LDS_RES);
+  uint32_t* mm_s = reinterpret_cast<uint32_t*>(lds + AT_LDS_MM);
 
   float* scores = reinterpret_cast<float*>(p.scratch + S.scores);
   uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S.score_done);
@@ -146,19 +161,15 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   float* accs = reinterpret_cast<float*>(p.scratch + S.acc);
   float* mls = reinterpret_cast<float*>(p.scratch + S.ml);
   uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S.split_done);
-
-  stamp(p.timeline, MONO_TL_START);
-  if (tid == 0) {
-    const v4i h = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)h[i];
-    ok_s = 1;
-  }
-  __syncthreads();
-  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
-  Guard guard;
-  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
   bool ok = true;
+  // the wait for the phase before (fused), once a CTA: CTA-uniform
+  bool waited = !FUSED;
+  auto enter = [&]() {
+    if (!waited) {
+      waited = true;
+      ok = ready() && ok;
+    }
+  };
 
   // keys a row sees (its position + 1, within the launch's context bound)
   auto row_n = [&](int r) -> int {
@@ -184,31 +195,44 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     const int n = row_n(r);
     if (c * AT_CHUNK >= n) continue;
     const int pg = c * (AT_CHUNK / AT_PAGE) + w;
-    if (pg * AT_PAGE < n) {
-      const int pid = __builtin_amdgcn_readfirstlane(page_of(r, pg));
+    const bool live = pg * AT_PAGE < n;
+    const int pid = live ? __builtin_amdgcn_readfirstlane(page_of(r, pg)) : 0;
+    // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
+    // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword. Loaded before
+    // the wait for the front: only the row's own key (its last) is written this launch
+    const uint32_t kofs = live ? (uint32_t)pid * 4096u : 0x80000000u;
+    const uint32_t sofs = live ? (uint32_t)pid * 256u : 0x80000000u;
+    v4i kb[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      kb[nt] = ld16<CP_NT>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
+    int ks = ld4<CP_NT>(rpsc, sofs + (uint32_t)l * 4);
+    enter();
+    if (!ok) break;
+    if (live) {
+      // the row's own key (the last page of the row) is the front's store of this
+      // launch: read it again, device coherent
+      if (FUSED && pg == (n - 1) / AT_PAGE) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          kb[nt] = ld16<CP_DEV>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
+        ks = ld4<CP_DEV>(rpsc, sofs + (uint32_t)l * 4);
+      }
       // the row's query as A operands: head tile mi, lane l: head 16 mi + l % 16, dims
       // 32 (l / 16) .. (16 bytes); its scales: the dword of lane l holds tile mi's byte mi
       const __amdgpu_buffer_rsrc_t rq = rsrc(p.iq + (size_t)r * AT_IHEADS * 64, AT_IHEADS * 64);
       v4i qa[4];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
-        qa[mi] = ld16<CP_NONE>(rq, (uint32_t)((16 * mi + (l & 15)) * 64 + 16 * (l >> 4)));
-      const int qs = ld4<CP_NONE>(rsrc(p.iqs + (size_t)r * 256, 256), (uint32_t)l * 4);
+        qa[mi] = ld16<XCP>(rq, (uint32_t)((16 * mi + (l & 15)) * 64 + 16 * (l >> 4)));
+      const int qs = ld4<XCP>(rsrc(p.iqs + (size_t)r * 256, 256), (uint32_t)l * 4);
       // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
       v4f wv[4];
       const __amdgpu_buffer_rsrc_t rw = rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4);
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
         wv[mi] = __builtin_bit_cast(
-            v4f, ld16<CP_NONE>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
-      // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
-      // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword
-      v4i kb[4];
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        kb[nt] = ld16<CP_NT>(rplane, (uint32_t)pid * 4096u +
-                                         (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
-      const int ks = ld4<CP_NT>(rpsc, (uint32_t)pid * 256u + (uint32_t)l * 4);
+            v4f, ld16<XCP>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
       float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
       auto tile = [&](auto nt_c) {
         constexpr int NT = decltype(nt_c)::value;
@@ -244,10 +268,11 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     __syncthreads();
     if (tid == 0) st_dev(&score_done[r * AT_NCHUNK + c], tag);
   }
+  enter();  // a CTA without a score task
 
   // ---------------------------------------------------------------- 2: top-k
   stamp(p.timeline, MONO_TL_STAGED);
-  for (int r = b; r < R; r += nblk) {
+  for (int r = b; r < (ok ? R : 0); r += nblk) {
     const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
     const int n = row_n(r);
     uint64_t* sel = topk + (size_t)r * AT_TOPK;
@@ -299,7 +324,7 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     int32_t* pt_s = reinterpret_cast<int32_t*>(ksc + SPLIT);
     static_assert(SPLIT * KSTR + AT_HEADS * QSTR + NSB * AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
                           SPLIT * 8 + NPG * 4 <=
-                      (int)sizeof(smem),
+                      TOPK_ARENA_WORDS * 4,
                   "split LDS");
     static_assert(NPG <= AT_THREADS, "a page-table entry a thread");
     constexpr int QP = AT_HEADS * AT_KV / 8;  // 16-byte pieces of a row's q
@@ -308,7 +333,7 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
     // without per-token scales every row is raw E4M3 (scale 1)
     const bool scaled = p.kv_scale != nullptr;
     const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, scaled ? p.kv_slots * 4u : 0u);
-    const int nt = R * NSP;
+    const int nt = ok ? R * NSP : 0;
     for (int t0 = 0; t0 < nt; t0 += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
       const int task = t0 + (b + nblk - (R % nblk)) % nblk;  // rows' top-k CTAs go last
@@ -325,7 +350,7 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
 #pragma unroll
       for (int i = 0; i < NQP; ++i) {
         const int pc = tid + AT_THREADS * i;
-        qv[i] = ld16<CP_NONE>(rq, pc < QP ? (uint32_t)pc * 16u : 0x80000000u);
+        qv[i] = ld16<XCP>(rq, pc < QP ? (uint32_t)pc * 16u : 0x80000000u);
       }
       const int npg = (n + AT_PAGE - 1) / AT_PAGE;
       const int pgv = ld4<CP_NONE>(
@@ -360,8 +385,10 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
         constexpr int GP = SPLIT * (AT_KV / 16);
         constexpr int NGP = (GP + AT_THREADS - 1) / AT_THREADS;
         const int slot = tid < SPLIT ? slot_s[tid] : -1;
-        const float sc = __int_as_float(
-            ld4<CP_NONE>(rks, slot >= 0 ? (uint32_t)slot * 4u : 0x80000000u));
+        // the row's own KV row is the front's store of this launch (fused): coherent
+        const int own = FUSED ? pt_s[(n - 1) >> 6] * AT_PAGE + ((n - 1) & 63) : -2;
+        const uint32_t so = slot >= 0 ? (uint32_t)slot * 4u : 0x80000000u;
+        const float sc = __int_as_float(slot == own ? ld4<CP_DEV>(rks, so) : ld4<CP_NONE>(rks, so));
         // every load issued before the first is stored (a load-store loop would wait
         // one round trip an iteration)
         v4i gv[NGP];
@@ -370,7 +397,8 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
           const int idx = tid + AT_THREADS * i;
           const int j = idx / (AT_KV / 16), c = idx % (AT_KV / 16);
           const int sj = idx < GP ? slot_s[j] : -1;
-          gv[i] = ld16<CP_NT>(rkv, sj >= 0 ? (uint32_t)sj * AT_KV + c * 16 : 0x80000000u);
+          const uint32_t go = sj >= 0 ? (uint32_t)sj * AT_KV + c * 16 : 0x80000000u;
+          gv[i] = (FUSED && sj == own) ? ld16<CP_DEV>(rkv, go) : ld16<CP_NT>(rkv, go);
         }
 #pragma unroll
         for (int i = 0; i < NGP; ++i) {
@@ -505,8 +533,8 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   stamp(p.timeline, MONO_TL_UPGATE);
   {
     float* red = reinterpret_cast<float*>(smem);  // [NSPLIT][512]
-    __shared__ float wsp_s[AT_NSPLIT];
-    __shared__ float linv_s;
+    float* wsp_s = reinterpret_cast<float*>(lds + AT_LDS_WSP);
+    float& linv_s = *reinterpret_cast<float*>(lds + AT_LDS_LINV);
     for (int task = b; task < R * AT_HEADS; task += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
       if (!ok) break;
@@ -559,24 +587,27 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
       if (tid < AT_LAT) {
         float s = 0.f;
         for (int sp = 0; sp < nsp; ++sp) s += red[sp * AT_LAT + tid];
-        p.out[((size_t)r * AT_HEADS + h) * AT_LAT + tid] = (uint16_t)bf16_bits(s * linv_s);
+        // device coherent: in the layer launch the output block reads it next
+        __builtin_amdgcn_raw_buffer_store_b16(
+            (uint16_t)bf16_bits(s * linv_s), rsrc(p.out, (uint32_t)R * AT_HEADS * AT_LAT * 2u),
+            (uint32_t)((r * AT_HEADS + h) * AT_LAT + tid) * 2u, 0, CP_DEV);
       }
       __syncthreads();
     }
   }
 
-  // ---------------------------------------------------------------- exit
+}
+
+template <int SPLIT>
+__global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[AT_LDS_BYTES];
+  __shared__ LaunchShared sh;
+  stamp(p.timeline, MONO_TL_START);
+  Guard guard;
+  const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
+  attn_phase<SPLIT, false>(p, lds, guard, tag, sh.ok, NoWait());
   stamp(p.timeline, MONO_TL_DOWN);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
-    drain();
-    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
-    if (old == (uint32_t)nblk - 1u) {
-      st_dev(gw + MONO_GUARD_EXIT, 0u);
-      st_dev(gw + MONO_GUARD_EPOCH, tag);
-    }
-  }
+  launch_end(p.guard, tag, []() {});
   stamp(p.timeline, MONO_TL_END);
 }
 

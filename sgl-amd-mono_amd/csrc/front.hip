@@ -32,6 +32,7 @@
 
 #include "gemv.h"
 #include "mono_abi.h"
+#include "phase.h"
 
 namespace mono {
 
@@ -182,26 +183,26 @@ __device__ inline float block_red(float v, float* sred, bool is_max) {
   return s;
 }
 
-__global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
-  const int b = blockIdx.x, G = gridDim.x, R = p.rows;
-  __shared__ __align__(16) uint16_t xs[FR_XG * FR_XS];
-  __shared__ v4f red[32][64];
-  __shared__ float sred[8 * 16];
-  __shared__ float rs_s[FR_XG];
-  __shared__ uint32_t head_s[4];
-  __shared__ int ok_s;
+// LDS of the front: x (or q_an) rows, the reduction tiles, small sums
+constexpr int FR_LDS_XS = 0;                                   // bf16 [8][FR_XS]
+constexpr int FR_LDS_RED = FR_LDS_XS + FR_XG * FR_XS * 2;      // v4f [32][64]
+constexpr int FR_LDS_SRED = FR_LDS_RED + 32 * 64 * 16;         // f32 [8 * 16]
+constexpr int FR_LDS_RS = FR_LDS_SRED + 8 * 16 * 4;            // f32 [8]
+constexpr int FR_LDS_BYTES = FR_LDS_RS + FR_XG * 4;
+static_assert(FR_LDS_RED % 16 == 0, "16-byte aligned reduction tiles");
 
-  stamp(p.timeline, MONO_TL_START);
-  if (threadIdx.x == 0) {
-    const v4i hd = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)hd[i];
-    ok_s = 1;
-  }
-  __syncthreads();
-  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
-  Guard guard;
-  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
+// The front in one CTA of a launch (the layer launch's first phase: nothing to wait for).
+// Its outputs (q, iq, iqs, iw, the rows' KV and index-key cache entries) are stored
+// device coherent, so the attention phase of the same launch can read them.
+__device__ __attribute__((always_inline)) inline void front_phase(const FrontParams& p,
+                                                                  uint8_t* lds, Guard& guard,
+                                                                  uint32_t tag, int& ok_s) {
+  const int b = blockIdx.x, G = gridDim.x, R = p.rows;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds + FR_LDS_XS);
+  v4f (*red)[64] = reinterpret_cast<v4f (*)[64]>(lds + FR_LDS_RED);
+  float* sred = reinterpret_cast<float*>(lds + FR_LDS_SRED);
+  float* rs_s = reinterpret_cast<float*>(lds + FR_LDS_RS);
+
   uint8_t* cur = p.scratch + (tag & 1u) * FrontScratch::PARITY;
   uint8_t* nxt = p.scratch + ((tag + 1u) & 1u) * FrontScratch::PARITY;
   // the hand-off buffers of this launch
@@ -470,8 +471,8 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
             const bool live = slot >= 0 && (uint64_t)slot < (uint64_t)p.kv_slots;
             if (live && on && (tid & 1) == 0)
               __builtin_amdgcn_raw_buffer_store_b32((int)word, rsrc(p.kv, p.kv_slots * (uint32_t)FR_KVA),
-                                                    (uint32_t)slot * FR_KVA + 2u * tid, 0, 0);
-            if (live && tid == 0 && p.kv_scale) p.kv_scale[slot] = sc;
+                                                    (uint32_t)slot * FR_KVA + 2u * tid, 0, CP_DEV);
+            if (live && tid == 0 && p.kv_scale) st_devf(p.kv_scale + slot, sc);
           }
         } else if (kind == 2) {
           // the index key -> LayerNorm, RoPE, FWHT, FP4 -> the index plane (wave 0)
@@ -516,11 +517,11 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
               if ((l & 3) == 0)
                 __builtin_amdgcn_raw_buffer_store_b32(
                     (int)word, rsrc(p.plane, p.plane_pages * 4096u),
-                    ((page * 4 + c) * 64 + s) * 16 + (uint32_t)(l & 15), 0, 0);
+                    ((page * 4 + c) * 64 + s) * 16 + (uint32_t)(l & 15), 0, CP_DEV);
               if ((l & 15) == 0)
                 __builtin_amdgcn_raw_buffer_store_b8(
                     (uint8_t)e8, rsrc(p.plane_scale, p.plane_pages * 256u),
-                    (page * 4 + c) * 64 + (s % 16) * 4 + s / 16, 0, 0);
+                    (page * 4 + c) * 64 + (s % 16) * 4 + s / 16, 0, CP_DEV);
             }
           }
         } else {
@@ -542,7 +543,7 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
             float s = dec_f(pw[0]);
 #pragma unroll
             for (int c = 1; c < FR_WCH; ++c) s += dec_f(pw[c]);
-            p.iw[r * FR_IH + tid] = bf16_round(s) * (0.08838834764831845f * 0.125f);
+            st_devf(p.iw + r * FR_IH + tid, bf16_round(s) * (0.08838834764831845f * 0.125f));
           }
         }
         (void)ok;
@@ -702,9 +703,11 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
       uint32_t e8;
       const uint32_t byte = fp4_pair(v0, v1, e8);
       const uint32_t word = gather4(byte, l);
-      if ((l & 3) == 0)
-        *reinterpret_cast<uint32_t*>(p.iq + (r * FR_IH + hi) * 64 + l) = word;
-      if ((l & 15) == 0) p.iqs[((r * 4 + (l >> 4)) * 16 + hi % 16) * 4 + hi / 16] = (uint8_t)e8;
+      if ((l & 3) == 0) st_dev(reinterpret_cast<uint32_t*>(p.iq + (r * FR_IH + hi) * 64 + l), word);
+      if ((l & 15) == 0)
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)e8, rsrc(p.iqs, (uint32_t)R * 256u),
+                                             ((r * 4 + (l >> 4)) * 16 + hi % 16) * 4 + hi / 16,
+                                             0, CP_DEV);
     }
   }
 
@@ -744,18 +747,17 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
     }
   }
 
-  // ---------------------------------------------------------------- exit
+}
+
+__global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[FR_LDS_BYTES];
+  __shared__ LaunchShared sh;
+  stamp(p.timeline, MONO_TL_START);
+  Guard guard;
+  const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
+  front_phase(p, lds, guard, tag, sh.ok);
   stamp(p.timeline, MONO_TL_MIDQ);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
-    drain();
-    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
-    if (old == (uint32_t)G - 1u) {
-      st_dev(gw + MONO_GUARD_EXIT, 0u);
-      st_dev(gw + MONO_GUARD_EPOCH, tag);
-    }
-  }
+  launch_end(p.guard, tag, []() {});
   stamp(p.timeline, MONO_TL_END);
 }
 

@@ -37,6 +37,7 @@
 
 #include "moe_common.h"
 #include "mono_abi.h"
+#include "phase.h"
 
 namespace mono {
 
@@ -130,10 +131,37 @@ __device__ inline v8i cat8(v4i a, v4i b) {
 // SHUF: expert weights in AITER's (16, 16) layout, [rows / 16, K / 32, 2, 16 rows, 16 B]
 // (what SGLang's gfx950 MoE load leaves in place): a 16-row x 128-K MFMA tile is then one
 // contiguous 2 KB, and each load instruction reads 8 whole cache lines
-template <int H, int I, bool SHUF>
-__global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
+// LDS of the MoE phase (offsets in bytes)
+template <int H, int I>
+struct MoeLds {
   using G = MoeFp8Geom<H, I>;
+  static constexpr int RL = 0;  // RouteLds
+  static constexpr int XQ = (int)((sizeof(RouteLds) + 15) & ~(size_t)15);  // v4i [QW KCW 2 64]
+  static constexpr int XS = XQ + G::QW * G::KCW * 2 * 64 * 16;   // f32 [QW KCW][16]
+  static constexpr int RED = XS + G::QW * G::KCW * 16 * 4;       // v4f [16][64]
+  static constexpr int RSM = RED + G::WAVES * 64 * 16;           // f32 [2][2][16]
+  static constexpr int RSTD = RSM + 2 * 2 * 16 * 4;              // f32 [16]
+  static constexpr int NEXT = RSTD + MOE_MAXR * 4;               // int
+  static constexpr int N1 = NEXT + 4;                            // int
+  static constexpr int HEAD = N1 + 12;                           // u32 [4], 16-byte aligned
+  static constexpr int BYTES = HEAD + 16;
+  static_assert(XS % 16 == 0 && RED % 16 == 0 && HEAD % 16 == 0, "aligned LDS carving");
+};
+
+// The MoE in one CTA of a launch. Standalone it reads the guard head itself, behind its
+// first row loads, and sets `guard` and `tag`. FUSED: it is the layer launch's last phase
+// (`guard` and `tag` given): it issues the norm weight and its router tile's weights,
+// waits at `ready` (the output block's barrier), then reads the stream `a` the output
+// block stored, device coherent.
+template <int H, int I, bool SHUF, bool FUSED, class Ready>
+__device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Params& p,
+                                                                uint8_t* lds, Guard& guard,
+                                                                uint32_t& tag, int& ok_s,
+                                                                Ready ready) {
+  using G = MoeFp8Geom<H, I>;
+  using LO = MoeLds<H, I>;
   constexpr int KCW = G::KCW, NUG = G::NUG, NKB = G::NKB, QW = G::QW;
+  constexpr int XCP = FUSED ? CP_DEV : CP_NONE;  // loads of the stream a
   const int tid = threadIdx.x, l = tid & 63;
   // the wave index in an SGPR: every per-wave address term stays scalar
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -142,56 +170,59 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   const int R = p.rows;
   const int nblk = gridDim.x, b = blockIdx.x;
 
-  __shared__ RouteLds rl;
+  RouteLds& rl = *reinterpret_cast<RouteLds*>(lds + LO::RL);
   // the E4M3 activations as each lane's MFMA B operand: [slice][chunk][half][lane]
-  __shared__ v4i xq_lds[QW * KCW * 2 * 64];
-  __shared__ float xs_lds[QW * KCW][16];  // activation block scale per (chunk, row)
-  __shared__ v4f red[G::WAVES][64];
-  __shared__ float red_small[2][2][16];
-  __shared__ int next_s;
-  __shared__ float rstd_s[MOE_MAXR];
-  __shared__ int ok_s;
+  v4i* xq_lds = reinterpret_cast<v4i*>(lds + LO::XQ);
+  float (*xs_lds)[16] = reinterpret_cast<float (*)[16]>(lds + LO::XS);  // scale per (chunk, row)
+  v4f (*red)[64] = reinterpret_cast<v4f (*)[64]>(lds + LO::RED);
+  float (*red_small)[2][16] = reinterpret_cast<float (*)[2][16]>(lds + LO::RSM);
+  int& next_s = *reinterpret_cast<int*>(lds + LO::NEXT);
+  float* rstd_s = reinterpret_cast<float*>(lds + LO::RSTD);
+  uint32_t* head_s = reinterpret_cast<uint32_t*>(lds + LO::HEAD);
 
   uint64_t* mid_pairs = reinterpret_cast<uint64_t*>(p.scratch + G::OFF_MID);
   uint8_t* mq = p.scratch + G::OFF_MQ;
   float* mcoef = reinterpret_cast<float*>(p.scratch + G::OFF_MCOEF);
-  uint32_t* ready = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
+  uint32_t* ready_w = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
   uint32_t* queue = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_QUEUE);
 
-  __shared__ uint32_t head_s[4];
-  stamp(p.timeline, MONO_TL_START);
   // the first eight rows: two waves a row, lane l the 8 values at q * 512 + l * 8 of its
-  // half's 7 slices; issued first so they fly with the staging and guard loads below
+  // half's 7 slices; issued first (standalone) so they fly with the staging and guard loads
   constexpr int NQ0 = H / 1024;
   v4i av0[NQ0];
-  {
+  auto load_rows0 = [&]() {
     const int r = w / 2, ch = w % 2;
     const bool live = r < R;
     const __amdgpu_buffer_rsrc_t rar = rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
     const uint32_t base = (uint32_t)(ch * NQ0 * 512 + l * 8) * 2;
 #pragma unroll
-    for (int q = 0; q < NQ0; ++q) av0[q] = ld16<CP_NONE>(rar, base + q * 1024);
-  }
+    for (int q = 0; q < NQ0; ++q) av0[q] = ld16<XCP>(rar, base + q * 1024);
+  };
+  if constexpr (!FUSED) load_rows0();
   // the post-attention norm weight, the same for every row, goes to LDS (over the
   // reduction buffer, idle until stage 2); every load of the prologue is issued before
   // the first is waited on, none under a branch (absent ones read through an empty
   // range), so the one barrier below waits for a single round trip
   v4i* g_lds = reinterpret_cast<v4i*>(&red[0][0]);
-  static_assert(H * 2 <= (int)sizeof(red), "norm weight staging");
+  static_assert(H * 2 <= G::WAVES * 64 * 16, "norm weight staging");
   static_assert(H / 8 <= G::THREADS, "one norm-weight piece a thread");
   const v4i gv = ld16<CP_NONE>(rsrc(p.g_post, H * 2), tid < H / 8 ? (uint32_t)tid * 16u : 0x80000000u);
   // this CTA's stage-0 task (the first of them: a grid below NTASK0 loops, unprefetched):
-  // router tile
-  // tile (et, ks), wave w takes K [ks 512 + 32 w, + 32); lane l the A operand of expert
-  // 16 et + l % 16 at K + 8 (l / 16) and the B operand of row l % 16 there
-  auto router_loads = [&](int task, v4i& wa, v4i& xa) {
+  // router tile (et, ks), wave w takes K [ks 512 + 32 w, + 32); lane l the A operand of
+  // expert 16 et + l % 16 at K + 8 (l / 16) and the B operand of row l % 16 there
+  auto router_w = [&](int task) {
     const bool on = task < G::NROUTER;
     const int et = on ? task / G::NKS : 0, ks = on ? task % G::NKS : 0;
     const int k = ks * 512 + 32 * w + 8 * grp;
-    wa = ld16<CP_NT>(rsrc(p.w_r, on ? MOE_NEXP * H * 2 : 0u),
-                     (uint32_t)((et * 16 + t) * H + k) * 2u);
-    xa = ld16<CP_NONE>(rsrc(p.a, on ? (uint32_t)R * H * 2 : 0u),
-                       t < R ? (uint32_t)(t * H + k) * 2u : 0x80000000u);
+    return ld16<CP_NT>(rsrc(p.w_r, on ? MOE_NEXP * H * 2 : 0u),
+                       (uint32_t)((et * 16 + t) * H + k) * 2u);
+  };
+  auto router_x = [&](int task) {
+    const bool on = task < G::NROUTER;
+    const int ks = on ? task % G::NKS : 0;
+    const int k = ks * 512 + 32 * w + 8 * grp;
+    return ld16<XCP>(rsrc(p.a, on ? (uint32_t)R * H * 2 : 0u),
+                     t < R ? (uint32_t)(t * H + k) * 2u : 0x80000000u);
   };
   // publisher pt: thread tid the 8 values at 128 kc + 8 m of rows r and r + 8, with
   // kc = 8 pt + tid / 128, r = (tid / 16) % 8, m = tid % 16
@@ -202,26 +233,37 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int row = r + 8 * hh;
-      pa[hh] = ld16<CP_NONE>(rsrc(p.a, on ? (uint32_t)R * H * 2 : 0u),
-                             row < R ? (uint32_t)(row * H + kc * 128 + 8 * m) * 2u : 0x80000000u);
+      pa[hh] = ld16<XCP>(rsrc(p.a, on ? (uint32_t)R * H * 2 : 0u),
+                         row < R ? (uint32_t)(row * H + kc * 128 + 8 * m) * 2u : 0x80000000u);
     }
   };
   v4i wa0, xa0, pa0[2];
-  router_loads(b, wa0, xa0);
-  pub_loads(b, pa0);
-  const v4i hd = ld16<CP_DEV>(rsrc(p.guard, 16), tid == 0 ? 0u : 0x80000000u);
-  if (tid < H / 8) g_lds[tid] = gv;
-  if (tid == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)hd[i];
-  }
-  for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
-  if (tid == 0) ok_s = 1;
-  __syncthreads();
-  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
-  Guard guard;
-  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
   bool ok = true;
+  wa0 = router_w(b);
+  if constexpr (FUSED) {
+    ok = ready();
+    load_rows0();
+    xa0 = router_x(b);
+    pub_loads(b, pa0);
+    if (tid < H / 8) g_lds[tid] = gv;
+    for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
+    if (tid == 0) ok_s = ok ? 1 : 0;
+    __syncthreads();
+  } else {
+    xa0 = router_x(b);
+    pub_loads(b, pa0);
+    const v4i hd = ld16<CP_DEV>(rsrc(p.guard, 16), tid == 0 ? 0u : 0x80000000u);
+    if (tid < H / 8) g_lds[tid] = gv;
+    if (tid == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)hd[i];
+    }
+    for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
+    if (tid == 0) ok_s = 1;
+    __syncthreads();
+    tag = head_s[MONO_GUARD_EPOCH] + 1u;
+    guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
+  }
   uint8_t* hcur = p.scratch + G::OFF_H + (tag & 1u) * G::SZ_HPAR;
   uint8_t* hnxt = p.scratch + G::OFF_H + ((tag + 1u) & 1u) * G::SZ_HPAR;
   uint32_t* hxq = reinterpret_cast<uint32_t*>(hcur);
@@ -259,17 +301,18 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       const uint32_t base = (uint32_t)(ch * NQ0 * 512 + l * 8) * 2;
       v4i av1[NQ0];
 #pragma unroll
-      for (int q = 0; q < NQ0; ++q) av1[q] = ld16<CP_NONE>(rar, base + q * 1024);
+      for (int q = 0; q < NQ0; ++q) av1[q] = ld16<XCP>(rar, base + q * 1024);
       ss_pass(8, av1);
     } else if (tid >= 8 && tid < 16) {
       rstd_s[tid] = 0.f;
     }
   }
   // the task(s): router tiles publish partial logits, publishers the B image and scales
-  for (int task = b; task < G::NTASK0; task += nblk) {
+  for (int task = b; task < (ok ? G::NTASK0 : 0); task += nblk) {
     v4i wa = wa0, xa = xa0, pa[2] = {pa0[0], pa0[1]};
     if (task != b) {
-      router_loads(task, wa, xa);
+      wa = router_w(task);
+      xa = router_x(task);
       pub_loads(task, pa);
       // a previous router tile's reduction overwrote the norm weight (red overlays it)
       __syncthreads();
@@ -703,7 +746,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       }
       drain();
       const bool all_ok = cta_ok(ok, guard, ok_s);
-      if (tid == 0 && all_ok) st_dev(&ready[u * NKB + kb], tag);
+      if (tid == 0 && all_ok) st_dev(&ready_w[u * NKB + kb], tag);
     }
     ok = cta_ok(ok, guard, ok_s);
   }
@@ -721,7 +764,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
     const int ntask = ok ? G::NDN : 0;
     uint8_t* mql = reinterpret_cast<uint8_t*>(xq_lds);  // [9 R slots][I] E4M3
     float* mcl = reinterpret_cast<float*>(mql + MOE_MAXR * MOE_SLOTS * I);  // [slots][NKB]
-    static_assert(MOE_MAXR * MOE_SLOTS * (I + NKB * 4) <= (int)sizeof(xq_lds), "mid slots");
+    static_assert(MOE_MAXR * MOE_SLOTS * (I + NKB * 4) <= LO::XS - LO::XQ, "mid slots");
     // one tile of weight chunks a wave; each chunk is refilled with the next step's as
     // soon as its MFMA issued, the last expert of a task running into the next task
     v4i buf[NKB][2];
@@ -773,14 +816,14 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
       asm volatile("" ::: "memory");  // the LDS reads after the barrier stay after it
     };
     // the leading experts already quantised: one pass over the ready words
-    __shared__ int n1_s;
+    int& n1_s = *reinterpret_cast<int*>(lds + LO::N1);
     if (tid == 0) n1_s = nd;
     __syncthreads();
     if (ntask) {
       const int i = tid;
       static_assert(MOE_NDIST * NKB <= 2 * G::THREADS, "two ready words a thread");
-      const uint32_t r0 = ld4<CP_DEV>(rsrc(ready, (uint32_t)(nd * NKB) * 4u), (uint32_t)i * 4u);
-      const uint32_t r1 = ld4<CP_DEV>(rsrc(ready, (uint32_t)(nd * NKB) * 4u),
+      const uint32_t r0 = ld4<CP_DEV>(rsrc(ready_w, (uint32_t)(nd * NKB) * 4u), (uint32_t)i * 4u);
+      const uint32_t r1 = ld4<CP_DEV>(rsrc(ready_w, (uint32_t)(nd * NKB) * 4u),
                                       (uint32_t)(i + G::THREADS) * 4u);
       if (i < nd * NKB && r0 != tag) atomicMin(&n1_s, i / NKB);
       if (i + G::THREADS < nd * NKB && r1 != tag) atomicMin(&n1_s, (i + G::THREADS) / NKB);
@@ -831,7 +874,7 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         rest = false;
         const int i = w * 64 + l;
         ok = wait_until(guard, MONO_SITE_MQ, [&]() {
-          const uint32_t rv = i < nd * NKB && i >= n1 * NKB ? ld_dev(&ready[i]) : tag;
+          const uint32_t rv = i < nd * NKB && i >= n1 * NKB ? ld_dev(&ready_w[i]) : tag;
           return __all(rv == tag);
         });
         ok = cta_all(ok, ok_s);
@@ -852,7 +895,8 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
         for (int i = 0; i < QW; ++i) ys += red[h * QW + i][L][v];
         if (tok < R) {
           const int col = f * G::DNT + row;
-          const float av = bf16_lo(p.a[tok * H + col]);
+          const float av = bf16_lo((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+              rsrc(p.a, (uint32_t)R * H * 2u), (uint32_t)(tok * H + col) * 2u, 0, XCP));
           p.out[tok * H + col] = (uint16_t)bf16_bits(av + ys);
           if (p.y) p.y[tok * H + col] = ys;
         }
@@ -861,21 +905,29 @@ __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
     }
   }
 
-  // ---------------------------------------------------------------- exit
-  stamp(p.timeline, MONO_TL_DOWN);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
-    drain();
-    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
-    if (old == (uint32_t)nblk - 1u) {
-      // every other CTA is past its last queue grab: the counters restart at zero
+}
+
+// the MoE's work-queue counters, which the launch's last CTA out zeroes for the next
+template <int H, int I>
+__device__ inline void moe_reset_queues(const MoeFp8Params& p) {
+  using G = MoeFp8Geom<H, I>;
+  uint32_t* queue = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_QUEUE);
 #pragma unroll
-      for (int i = 0; i < G::NQUEUE; ++i) st_dev(queue + i, 0u);
-      st_dev(gw + MONO_GUARD_EXIT, 0u);
-      st_dev(gw + MONO_GUARD_EPOCH, tag);
-    }
-  }
+  for (int i = 0; i < G::NQUEUE; ++i) st_dev(queue + i, 0u);
+}
+
+template <int H, int I, bool SHUF>
+__global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[MoeLds<H, I>::BYTES];
+  __shared__ int ok_s;
+  stamp(p.timeline, MONO_TL_START);
+  Guard guard;
+  uint32_t tag = 0;
+  moe_phase<H, I, SHUF, false>(p, lds, guard, tag, ok_s, NoWait());
+  stamp(p.timeline, MONO_TL_DOWN);
+  // every other CTA is past its last queue grab once the last one leaves: the counters
+  // restart at zero
+  launch_end(p.guard, tag, [&]() { moe_reset_queues<H, I>(p); });
   stamp(p.timeline, MONO_TL_END);
 }
 

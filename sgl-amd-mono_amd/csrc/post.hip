@@ -19,6 +19,7 @@
 
 #include "gemv.h"
 #include "mono_abi.h"
+#include "phase.h"
 
 namespace mono {
 
@@ -55,23 +56,17 @@ struct PostParams {
   uint64_t* timeline;
 };
 
-__global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
-  const int b = blockIdx.x, nblk = gridDim.x, R = p.rows;
-  __shared__ v4f red[40][64];  // o_proj: [0, 32) two tiles x 16 waves; W_UV: [32, 40)
-  __shared__ uint32_t head_s[4];
-  __shared__ int ok_s;
+constexpr int PO_LDS_BYTES = 40 * 64 * 16;  // red[40][64]: o_proj [0, 32) two tiles, W_UV [32, 40)
 
-  stamp(p.timeline, MONO_TL_START);
-  if (threadIdx.x == 0) {
-    const v4i hd = ld16<CP_DEV>(rsrc(p.guard, 16), 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)hd[i];
-    ok_s = 1;
-  }
-  __syncthreads();
-  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
-  Guard guard;
-  guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
+// The output block in one CTA of a launch. FUSED: it runs after the attention phase in
+// the same launch, so o_lat is read device coherent, after `ready` (the attention's
+// barrier), which it calls once its weight prefetch and the residual rows are in flight.
+template <bool FUSED, class Ready>
+__device__ __attribute__((always_inline)) inline void post_phase(const PostParams& p, uint8_t* lds,
+                                                                 Guard& guard, uint32_t tag,
+                                                                 int& ok_s, Ready ready) {
+  const int b = blockIdx.x, nblk = gridDim.x, R = p.rows;
+  v4f (*red)[64] = reinterpret_cast<v4f (*)[64]>(lds);
   uint16_t* obuf = reinterpret_cast<uint16_t*>(p.scratch + (tag & 1u) * PostScratch::OBUF);
   uint8_t* onext = p.scratch + ((tag + 1u) & 1u) * PostScratch::OBUF;
 
@@ -122,20 +117,30 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
   const bool uv0 = b < PO_UV_TILES;
   v4i wu[1], xu[1][2];
   float su[1];
-  gu.issue(ju, b / UV_TPR, b % UV_TPR, wu, su, uv0);
-  gu.load_x<CP_NONE>(ju, b / UV_TPR, R, xu, uv0);
-  __syncthreads();
   int a0 = b, a1 = b + nblk;
   v4i w0[4], w1[4];
   float s0[4], s1[4];
-  go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
   auto load_h = [&](int t0, int t1) -> int {
     const int t = tid < 256 ? t0 : t1;
     const bool v = etok < R && tid < 512 && t < PO_TILES;
     return __builtin_amdgcn_raw_buffer_load_b16(
         rh, v ? (uint32_t)(etok * PO_HID + t * 16 + erow) * 2u : 0x80000000u, 0, 0);
   };
-  int hres = load_h(a0, a1);
+  int hres;
+  bool ok = true;
+  gu.issue(ju, b / UV_TPR, b % UV_TPR, wu, su, uv0);
+  if constexpr (FUSED) {
+    // every weight and the residual in flight, then the wait for o_lat
+    go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
+    hres = load_h(a0, a1);
+    ok = ready();
+    gu.load_x<CP_DEV>(ju, b / UV_TPR, R, xu, uv0 && ok);
+  } else {
+    gu.load_x<CP_NONE>(ju, b / UV_TPR, R, xu, uv0);
+    __syncthreads();
+    go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
+    hres = load_h(a0, a1);
+  }
 
   // ---------------------------------------------------------------- W_UV
   // tile b from the prefetch (no loads in this branch: the wait for wu / xu stays exact)
@@ -151,9 +156,9 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
     __syncthreads();
   }
   // more W_UV tiles than CTAs (fewer than 256 CUs): the rest without prefetch
-  for (int u = b + nblk; u < PO_UV_TILES; u += nblk) {
+  for (int u = b + nblk; u < (ok ? PO_UV_TILES : 0); u += nblk) {
     gu.issue(ju, u / UV_TPR, u % UV_TPR, wu, su);
-    gu.load_x<CP_NONE>(ju, u / UV_TPR, R, xu);
+    gu.load_x<FUSED ? CP_DEV : CP_NONE>(ju, u / UV_TPR, R, xu);
     gu.dot(wu, su, xu, red + 32);
     __syncthreads();
     if (tid < UV_STORE) GemvUV::epilogue(ju, u / UV_TPR, u % UV_TPR, R, tid, red + 32);
@@ -171,7 +176,7 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
   stamp(p.timeline, MONO_TL_STAGED);
 
   // ---------------------------------------------------------------- o_proj
-  for (int pass = 0; a0 < PO_TILES; ++pass, a0 += 2 * nblk, a1 += 2 * nblk) {
+  for (int pass = 0; ok && a0 < PO_TILES; ++pass, a0 += 2 * nblk, a1 += 2 * nblk) {
     if (pass > 0) {
       go.issue(jo, 0, a0, w0, s0);
       go.issue(jo, 0, a1, w1, s1, a1 < PO_TILES);
@@ -181,7 +186,7 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
     v4i xa[4][2];
     const __amdgpu_buffer_rsrc_t rx = rsrc(obuf, (uint32_t)PostScratch::OBUF);
     const int t = l & 15, grp = l >> 4;
-    bool ok = wait_until(guard, MONO_SITE_O, [&]() {
+    ok = wait_until(guard, MONO_SITE_O, [&]() {
       uint32_t mn = 0xFFFFFFFFu;
 #pragma unroll
       for (int st = 0; st < 4; ++st)
@@ -214,18 +219,17 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
     stamp(p.timeline, MONO_TL_MIDQ);
   }
 
-  // ---------------------------------------------------------------- exit
+}
+
+__global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[PO_LDS_BYTES];
+  __shared__ LaunchShared sh;
+  stamp(p.timeline, MONO_TL_START);
+  Guard guard;
+  const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
+  post_phase<false>(p, lds, guard, tag, sh.ok, NoWait());
   stamp(p.timeline, MONO_TL_ROUTED);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
-    drain();
-    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
-    if (old == (uint32_t)nblk - 1u) {
-      st_dev(gw + MONO_GUARD_EXIT, 0u);
-      st_dev(gw + MONO_GUARD_EPOCH, tag);
-    }
-  }
+  launch_end(p.guard, tag, []() {});
   stamp(p.timeline, MONO_TL_END);
 }
 
