@@ -54,6 +54,7 @@ typedef void* mono_stream_t;
 #define MONO_SITE_FRONT_A 8  /* a row task waits on the q_a | kv_a | index-key outputs */
 #define MONO_SITE_QAN 9      /* q_b / W_iq wait on the normalised q_a */
 #define MONO_SITE_QB 10      /* W_UK / the index query wait on q_b / W_iq outputs */
+#define MONO_SITE_PHASE 11   /* a phase of the layer launch waits for the phase before it */
 
 int mono_version(void);
 const char* mono_last_error(void);
@@ -353,6 +354,81 @@ typedef struct {
 
 size_t mono_front_scratch_bytes(void);
 int mono_front_launch(const MonoFrontArgs* args, mono_stream_t stream);
+
+/* ------------------------------------------------------------------------------
+ * The whole decoder layer as ONE persistent launch: the front, the attention phase, the
+ * output block and the FP8 MoE above, run back to back in every CTA of one launch with a
+ * deadline-guarded grid barrier between phases (each phase's input-independent loads,
+ * weights and index pages, issued before it waits). out = the layer's output stream
+ * (h + attention block + MoE), bf16 [R, 7168].
+ * Replaces the reference's per-layer launch Glm53LayerOp.launch(h, caches, cos, sin, step)
+ * (sgl_amd_mono/glm53/gfx950/runner.py:240-321) and its one-launch kernel
+ * (sgl_amd_mono/glm53/gfx950/kernel.py:171-5282, arguments :5191-5234), for one GPU's
+ * TP=4 share with the W == 1 reduces as local residual adds (:1665-1669). Every tensor
+ * has the meaning and layout of the per-phase launches' arguments above. */
+typedef struct {
+  int32_t rows;          /* R, 1..rows_max */
+  int32_t rows_max;      /* 1..8: the rows the scratch was sized for (mono_layer_scratch_bytes) */
+  int32_t hidden;        /* 7168 */
+  int32_t heads;         /* 32 */
+  int32_t inter;         /* 512 */
+  int32_t experts;       /* 256 */
+  int32_t layout;        /* MONO_LAYOUT_* of every FP8 weight */
+  int32_t ctx_max;       /* keys a row may see at most, 1..32768 */
+  int32_t pt_stride;     /* page_table row stride */
+  int32_t pt_rows;       /* page_table rows */
+  int32_t rope_rows;     /* rows of cos / sin */
+  uint32_t kv_slots;     /* rows of kv */
+  uint32_t plane_pages;  /* pages of the index plane */
+  float eps;             /* RMSNorm epsilon */
+  float sm_scale;        /* softmax scale */
+  float route_scale;     /* routed_scaling_factor */
+  const void* h;         /* bf16 [R, 7168]: the layer's input stream */
+  void* out;             /* bf16 [R, 7168]: the layer's output stream */
+  const int64_t* positions; /* [R] */
+  const int64_t* slots;     /* [R] cache slot of the row's key (-1: none) */
+  const int32_t* req_ids;   /* [R] */
+  const int32_t* page_table; /* [pt_rows, pt_stride] */
+  uint8_t* kv; float* kv_scale;            /* E4M3 [kv_slots, 576] (+ optional per-token scales) */
+  uint8_t* plane; uint8_t* plane_scale;    /* FP4 index plane [pages, 4, 64, 16] + [pages, 4, 64] */
+  const void* g_in; const void* g_q; const void* g_kv;   /* bf16 RMSNorm weights */
+  const uint8_t* w_qkv_a; const float* s_qkv_a;
+  const uint8_t* w_k; const float* s_k;
+  const void* w_w;
+  const float* g_k; const float* b_k;
+  const uint8_t* w_qb; const float* s_qb;
+  const uint8_t* w_iq; const float* s_iq;
+  const uint8_t* w_uk; const float* s_uk;
+  const void* cos; const void* sin;
+  const uint8_t* w_uv; const float* s_uv;
+  const uint8_t* w_o; const float* s_o;
+  const void* g_post; const void* w_r; const float* bias;
+  const uint8_t* w13; const float* s13; const uint8_t* w2; const float* s2;
+  /* optional: where the phases hand their results to each other (null: in scratch) */
+  void* q;               /* bf16 [R, 32, 576] */
+  uint8_t* iq;           /* [R, 64, 64] */
+  uint8_t* iqs;          /* [R, 4, 16, 4] */
+  float* iw;             /* f32 [R, 64] */
+  void* o_lat;           /* bf16 [R, 32, 512] */
+  void* a;               /* bf16 [R, 7168]: the stream after attention */
+  /* optional outputs */
+  float* scores;         /* f32 [R, ctx_max]: the indexer scores */
+  int32_t* topk_pos;     /* i32 [R, 2048] */
+  float* y;              /* f32 [R, 7168]: the MoE sum alone */
+  float* moe_scores;     /* f32 [R, 256] */
+  int32_t* ids;          /* i32 [R, 9] */
+  float* weights;        /* f32 [R, 9] */
+  void* scratch;         /* runtime owned, mono_layer_scratch_bytes(rows_max), zeroed */
+  int32_t* guard;        /* runtime owned guard block */
+  uint32_t* host_error;  /* optional pinned host word: 1 + failed site */
+  int32_t fault_site;    /* test fault injection: any MONO_SITE_* */
+  int32_t fault_after;
+  uint64_t* timeline;    /* optional u64 [grid, 8]: start, front, attention, output block,
+                            MoE done, exit */
+} MonoLayerArgs;
+
+size_t mono_layer_scratch_bytes(int32_t rows_max);
+int mono_layer_launch(const MonoLayerArgs* args, mono_stream_t stream);
 
 #ifdef __cplusplus
 }

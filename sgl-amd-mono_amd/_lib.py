@@ -43,7 +43,10 @@ TL_COLS = 8
 
 # wait sites (the deadline error word holds 1 + site)
 SITES = {1: "logits", 2: "mid", 3: "mq", 4: "scores", 5: "topk", 6: "split", 7: "o",
-         8: "front_a", 9: "q_an", 10: "q_b"}
+         8: "front_a", 9: "q_an", 10: "q_b", 11: "phase"}
+SITE_PHASE = 11
+# timeline marks of the layer launch (same columns)
+TL_LAYER_MARKS = ("start", "front", "attn", "post", "moe", "end")
 SITE_MID, SITE_SCORES, SITE_TOPK, SITE_SPLIT, SITE_O = 2, 4, 5, 6, 7
 SITE_FRONT_A, SITE_QAN, SITE_QB = 8, 9, 10
 # timeline marks of the attention launch (same columns)
@@ -235,6 +238,23 @@ class MonoFrontArgs(ctypes.Structure):
     ]
 
 
+class MonoLayerArgs(ctypes.Structure):
+    """Mirror of ``MonoLayerArgs`` in mono_amd.h (same order and types)."""
+
+    _fields_ = [(n, c_int32) for n in ("rows", "rows_max", "hidden", "heads", "inter", "experts",
+                                       "layout", "ctx_max", "pt_stride", "pt_rows", "rope_rows")]
+    _fields_ += [("kv_slots", c_uint32), ("plane_pages", c_uint32), ("eps", c_float),
+                 ("sm_scale", c_float), ("route_scale", c_float)]
+    _fields_ += [(n, c_void_p) for n in (
+        "h", "out", "positions", "slots", "req_ids", "page_table", "kv", "kv_scale", "plane",
+        "plane_scale", "g_in", "g_q", "g_kv", "w_qkv_a", "s_qkv_a", "w_k", "s_k", "w_w", "g_k",
+        "b_k", "w_qb", "s_qb", "w_iq", "s_iq", "w_uk", "s_uk", "cos", "sin", "w_uv", "s_uv",
+        "w_o", "s_o", "g_post", "w_r", "bias", "w13", "s13", "w2", "s2", "q", "iq", "iqs", "iw",
+        "o_lat", "a", "scores", "topk_pos", "y", "moe_scores", "ids", "weights", "scratch",
+        "guard", "host_error")]
+    _fields_ += [("fault_site", c_int32), ("fault_after", c_int32), ("timeline", c_void_p)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mono_version": (c_int32, []),
@@ -253,6 +273,8 @@ SIGNATURES = {
     "mono_post_launch": (c_int32, [ctypes.POINTER(MonoPostArgs), c_void_p]),
     "mono_front_scratch_bytes": (c_size_t, []),
     "mono_front_launch": (c_int32, [ctypes.POINTER(MonoFrontArgs), c_void_p]),
+    "mono_layer_scratch_bytes": (c_size_t, [c_int32]),
+    "mono_layer_launch": (c_int32, [ctypes.POINTER(MonoLayerArgs), c_void_p]),
 }
 
 _lock = threading.Lock()

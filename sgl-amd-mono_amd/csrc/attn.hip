@@ -1,602 +1,7 @@
-// The attention phase of the DSA layer as one persistent gfx950 launch: the FP4
-// indexer's scores, their exact top-2048, and sparse MLA decode over the selected
-// tokens' FP8 cache rows.
-//
-// Stages, every CTA in order (task t of a stage runs on CTA (t + offset) mod grid):
-//   1  scores: task (row, 1024-token chunk), one 64-token page a wave. Per 16-token
-//      tile and 16-head group one scaled 16x16x128 MFMA with E2M1 operands and their
-//      E8M0 scales (query rows = heads, key columns = tokens, K = the 128 dims); relu,
-//      the head weights and the sum over heads stay in the lane, then two permlane
-//      swaps sum the lane groups. Scores go to scratch; the chunk's done word follows.
-//   2  top-k: task = row (topk_lds.h): thread t holds the radix keys of positions
-//      32 t .. in registers; a sample narrows the range, histograms over the live range
-//      keep the bin of the 2048th key until its few candidates rank themselves; the
-//      selection (every element up to the threshold element of the order key
-//      descending, position ascending) is published as (position, tag) pairs.
-//   3  split: task (row, SPLIT-key split), all 32 heads (SPLIT 64 when the rows' 32
-//      splits each fill the grid once, else 128). The split's tokens (through the
-//      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
-//      widened exactly), times the token's scale and the softmax scale; per head the
-//      split's max m and sum l; P, with the token's scale folded in, as bf16; O = P V on
-//      MFMAs, V read from the same rows. O, m and l go to scratch.
-//   4  merge: task (row, head): o = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s,
-//      rounded to bf16.
-// Every hand-off is a (word = launch tag) wait under the guard's deadline.
-//
-// Reference: FP4 scores sgl_amd_mono/deepseek_v41/gfx950/indexer/score_fp4.py:1-20,
-// 254-296 (plane layout, formula); exact top-k sgl_amd_mono/glm53/gfx950/kernel.py:
-// 3002-3636 (rule: glm53/check.py:94-117); sparse MLA split and merge kernel.py:
-// 3638-4123; softmax scale glm53/gfx950/config.py:180-181.
-#include <hip/hip_runtime.h>
-
-#include <type_traits>
-
-#include "mono_abi.h"
-#include "mono_device.h"
-#include "phase.h"
-#include "topk_lds.h"
+// The attention launch of the layer (its phase: attn_phase.h) and its C entry points.
+#include "attn_phase.h"
 
 namespace mono {
-
-constexpr int AT_HEADS = 32;     // attention heads of one GPU's TP=4 share
-constexpr int AT_IHEADS = 64;    // index heads
-constexpr int AT_KV = 576;       // cached row: latent 512 + rope 64
-constexpr int AT_LAT = 512;
-constexpr int AT_PAGE = 64;
-constexpr int AT_CHUNK = 1024;    // tokens of a score task
-constexpr int AT_NCHUNK = AT_MAXCTX / AT_CHUNK;
-// keys of a split task: 64 when the rows' splits (32 a row) fill the grid once, else 128
-// (16 a row); scratch is laid out for the most splits a row
-constexpr int AT_NSPLIT = AT_TOPK / 64;
-constexpr int AT_MAXR = 48;
-
-constexpr size_t at_align(size_t v) { return (v + 255) & ~(size_t)255; }
-
-// scratch of a runtime sized for `rm` rows (every launch on it passes the same rm, so a
-// word keeps its meaning from launch to launch and a stale tag can never match)
-struct AttnScratch {
-  size_t scores;      // f32 [rm][MAXCTX]
-  size_t score_done;  // u32 [rm][NCHUNK]
-  size_t topk;        // the selection as (position, tag) pairs [rm][TOPK]
-  size_t acc;         // f32 [rm][split][h][512]
-  size_t ml;          // f32 [rm][split][h][2]
-  size_t split_done;  // u32 [rm][split]
-  size_t bytes;
-  __host__ __device__ explicit AttnScratch(int rm) {
-    const size_t r = (size_t)rm;
-    scores = 0;
-    score_done = at_align(scores + r * AT_MAXCTX * 4);
-    topk = at_align(score_done + r * AT_NCHUNK * 4);
-    acc = at_align(topk + r * AT_TOPK * 8);
-    ml = at_align(acc + r * AT_NSPLIT * AT_HEADS * AT_LAT * 4);
-    split_done = at_align(ml + r * AT_NSPLIT * AT_HEADS * 8);
-    bytes = at_align(split_done + r * AT_NSPLIT * 4);
-  }
-};
-
-struct AttnParams {
-  int rows, rows_max, ctx_max, pt_stride, pt_rows;
-  float sm_scale;
-  uint32_t plane_pages, kv_slots;
-  const int64_t* positions;
-  const int32_t* req_ids;
-  const int32_t* page_table;
-  const uint16_t* q;
-  const uint8_t* iq;
-  const uint8_t* iqs;
-  const float* iw;
-  const uint8_t* plane;
-  const uint8_t* plane_scale;
-  const uint8_t* kv;
-  const float* kv_scale;
-  uint16_t* out;
-  float* scores_out;
-  int32_t* topk_out;
-  uint8_t* scratch;
-  int32_t* guard;
-  uint32_t* host_err;
-  int fault_site, fault_after;
-  uint64_t* timeline;
-};
-
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-
-// 16x16x128 E2M1 x E2M1 -> f32, each operand's E8M0 scale the byte OA / OB of its dword
-template <int OA, int OB>
-__device__ inline v4f mfma_fp4(v4i a, v4i b, int sa, int sb) {
-  const v8i A = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
-  const v8i B = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
-  const v4f z = {0.f, 0.f, 0.f, 0.f};
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, z, 4, 4, OA, sa, OB, sb);
-}
-
-// 8 E4M3 (two dwords) -> 8 bf16 (exact)
-__device__ inline v8bf fp8x8_bf16(uint32_t lo, uint32_t hi) {
-  const v2bf a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
-  const v2bf b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
-  const v2bf c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
-  const v2bf d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
-  return v8bf{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-__device__ inline v4f mfma_bf16(v8bf a, v8bf b, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// LDS of the attention phase: the top-k arena (carved per stage), then small words
-constexpr int AT_LDS_WSUM = TOPK_ARENA_WORDS * 4;         // int [2][16], 16-byte aligned
-constexpr int AT_LDS_RES = AT_LDS_WSUM + 2 * AT_WAVES * 4;  // int [4]
-constexpr int AT_LDS_MM = AT_LDS_RES + 16;                  // u32 [2]
-constexpr int AT_LDS_WSP = AT_LDS_MM + 16;                  // f32 [NSPLIT]
-constexpr int AT_LDS_LINV = AT_LDS_WSP + AT_NSPLIT * 4;     // f32
-constexpr int AT_LDS_BYTES = AT_LDS_LINV + 16;
-
-// The attention phase (stages 1-4) in one CTA of a launch. FUSED: it runs after the front
-// in the same launch, so its inputs (q, iq, iqs, iw and the rows' own cache entries) are
-// read device-coherent, after `ready` (the front's barrier), which it calls once, after
-// its first index-page loads are in flight. Always inlined: it is instantiated in more
-// than one kernel, and as a real call it would spill around the call.
-template <int SPLIT, bool FUSED, class Ready>
-__device__ __attribute__((always_inline)) inline void attn_phase(const AttnParams& p,
-                                                                 uint8_t* lds, Guard& guard,
-                                                                 uint32_t tag, int& ok_s,
-                                                                 Ready ready) {
-  const AttnScratch S(p.rows_max);
-  static_assert(SPLIT == 64 || SPLIT == 128, "64- or 128-key splits");
-  constexpr int NSP = AT_TOPK / SPLIT;  // splits a row
-  constexpr int XCP = FUSED ? CP_DEV : CP_NONE;  // loads of the front's outputs
-  const int tid = threadIdx.x, l = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int R = p.rows;
-  const int nblk = gridDim.x, b = blockIdx.x;
-
-  uint8_t* smem = lds;
-  int* wsum = reinterpret_cast<int*>(lds + AT_LDS_WSUM);
-  int* res_s = reinterpret_cast<int*>(lds + AT_LDS_RES);
-  uint32_t* mm_s = reinterpret_cast<uint32_t*>(lds + AT_LDS_MM);
-
-  float* scores = reinterpret_cast<float*>(p.scratch + S.scores);
-  uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S.score_done);
-  uint64_t* topk = reinterpret_cast<uint64_t*>(p.scratch + S.topk);
-  float* accs = reinterpret_cast<float*>(p.scratch + S.acc);
-  float* mls = reinterpret_cast<float*>(p.scratch + S.ml);
-  uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S.split_done);
-  bool ok = true;
-  // the wait for the phase before (fused), once a CTA: CTA-uniform
-  bool waited = !FUSED;
-  auto enter = [&]() {
-    if (!waited) {
-      waited = true;
-      ok = ready() && ok;
-    }
-  };
-
-  // keys a row sees (its position + 1, within the launch's context bound)
-  auto row_n = [&](int r) -> int {
-    const int64_t pos = p.positions[r];
-    return (int)(pos < 0 ? 0 : (pos + 1 > p.ctx_max ? p.ctx_max : pos + 1));
-  };
-  // the page table through a bounded resource: an entry past it reads page 0
-  const __amdgpu_buffer_rsrc_t rpt =
-      rsrc(p.page_table, (uint32_t)p.pt_rows * (uint32_t)p.pt_stride * 4u);
-  auto page_of = [&](int r, int pg) -> int {
-    return ld4<CP_NONE>(rpt, ((uint32_t)p.req_ids[r] * (uint32_t)p.pt_stride + (uint32_t)pg) * 4u);
-  };
-  const __amdgpu_buffer_rsrc_t rplane = rsrc(p.plane, p.plane_pages * 4096u);
-  const __amdgpu_buffer_rsrc_t rpsc = rsrc(p.plane_scale, p.plane_pages * 256u);
-
-  // ---------------------------------------------------------------- 1: scores
-  // Each stage takes the thread index through an opaque copy: conditions on it are then
-  // computed inside the stage, not hoisted to the kernel's top where they would hold
-  // registers through every stage.
-  for (int task = b; task < R * AT_NCHUNK; task += nblk) {
-    const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-    const int r = task / AT_NCHUNK, c = task % AT_NCHUNK;
-    const int n = row_n(r);
-    if (c * AT_CHUNK >= n) continue;
-    const int pg = c * (AT_CHUNK / AT_PAGE) + w;
-    const bool live = pg * AT_PAGE < n;
-    const int pid = live ? __builtin_amdgcn_readfirstlane(page_of(r, pg)) : 0;
-    // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
-    // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword. Loaded before
-    // the wait for the front: only the row's own key (its last) is written this launch
-    const uint32_t kofs = live ? (uint32_t)pid * 4096u : 0x80000000u;
-    const uint32_t sofs = live ? (uint32_t)pid * 256u : 0x80000000u;
-    v4i kb[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      kb[nt] = ld16<CP_NT>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
-    int ks = ld4<CP_NT>(rpsc, sofs + (uint32_t)l * 4);
-    enter();
-    if (!ok) break;
-    if (live) {
-      // the row's own key (the last page of the row) is the front's store of this
-      // launch: read it again, device coherent
-      if (FUSED && pg == (n - 1) / AT_PAGE) {
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          kb[nt] = ld16<CP_DEV>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
-        ks = ld4<CP_DEV>(rpsc, sofs + (uint32_t)l * 4);
-      }
-      // the row's query as A operands: head tile mi, lane l: head 16 mi + l % 16, dims
-      // 32 (l / 16) .. (16 bytes); its scales: the dword of lane l holds tile mi's byte mi
-      const __amdgpu_buffer_rsrc_t rq = rsrc(p.iq + (size_t)r * AT_IHEADS * 64, AT_IHEADS * 64);
-      v4i qa[4];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        qa[mi] = ld16<XCP>(rq, (uint32_t)((16 * mi + (l & 15)) * 64 + 16 * (l >> 4)));
-      const int qs = ld4<XCP>(rsrc(p.iqs + (size_t)r * 256, 256), (uint32_t)l * 4);
-      // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
-      v4f wv[4];
-      const __amdgpu_buffer_rsrc_t rw = rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4);
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        wv[mi] = __builtin_bit_cast(
-            v4f, ld16<XCP>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
-      float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
-      auto tile = [&](auto nt_c) {
-        constexpr int NT = decltype(nt_c)::value;
-        float acc = 0.f;
-        auto head_tile = [&](auto mi_c) {
-          constexpr int MI = decltype(mi_c)::value;
-          const v4f d = mfma_fp4<MI, NT>(qa[MI], kb[NT], qs, ks);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc = fmaf(fmaxf(d[e], 0.f), wv[MI][e], acc);
-        };
-        head_tile(std::integral_constant<int, 0>());
-        head_tile(std::integral_constant<int, 1>());
-        head_tile(std::integral_constant<int, 2>());
-        head_tile(std::integral_constant<int, 3>());
-        // sum the four lane groups (heads 4 (l / 16) ..): lane l keeps token l % 16
-        float a, bb;
-        swap16(acc, a, bb);
-        acc = a + bb;
-        swap32(acc, a, bb);
-        acc = a + bb;
-        if (l < 16) {
-          st_devf(dst + 16 * NT + l, acc);
-          const int tok = pg * AT_PAGE + 16 * NT + l;
-          if (p.scores_out && tok < n) p.scores_out[(size_t)r * p.ctx_max + tok] = acc;
-        }
-      };
-      tile(std::integral_constant<int, 0>());
-      tile(std::integral_constant<int, 1>());
-      tile(std::integral_constant<int, 2>());
-      tile(std::integral_constant<int, 3>());
-    }
-    drain();
-    __syncthreads();
-    if (tid == 0) st_dev(&score_done[r * AT_NCHUNK + c], tag);
-  }
-  enter();  // a CTA without a score task
-
-  // ---------------------------------------------------------------- 2: top-k
-  stamp(p.timeline, MONO_TL_STAGED);
-  for (int r = b; r < (ok ? R : 0); r += nblk) {
-    const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-    const int n = row_n(r);
-    uint64_t* sel = topk + (size_t)r * AT_TOPK;
-    if (n <= AT_TOPK) {
-      // every key of the row, in position order
-      for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
-        if (i < n) st_dev64(sel + i, pair((uint32_t)i, tag));
-        if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = i < n ? i : -1;
-      }
-    } else {
-      const int nch = (n + AT_CHUNK - 1) / AT_CHUNK;
-      if (w == 0)
-        ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
-          return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + l]) == tag);
-        });
-      if (tid == 0) {  // topk_select's minimum / maximum words, set before the barrier
-        mm_s[0] = 0xFFFFFFFFu;
-        mm_s[1] = 0u;
-      }
-      ok = cta_all(ok, ok_s);
-      if (ok) {
-        const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
-        const int32_t* sel_l = topk_select(tid, rs, n, smem, wsum, mm_s, res_s);
-        for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
-          const int v = sel_l[i];
-          st_dev64(sel + i, pair((uint32_t)v, tag));
-          if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = v;
-        }
-      }
-    }
-    __syncthreads();  // the LDS arena is reused by the next row
-  }
-
-  // ---------------------------------------------------------------- 3: split
-  stamp(p.timeline, MONO_TL_ROUTED);
-  {
-    // LDS: K rows (E4M3, 576 + 16 bytes apart), q (bf16, 1152 + 16), S (f32), P (bf16),
-    // the split's slots and token scales, the row's page-table entries
-    constexpr int KSTR = AT_KV + 16, QSTR = AT_KV * 2 + 16, SSTR = SPLIT + 4,
-                  PSTR = SPLIT * 2 + 16;
-    constexpr int NSB = SPLIT == 64 ? 2 : 1;  // S buffers: the two K chains (64), or summed
-    constexpr int NPG = AT_MAXCTX / AT_PAGE;
-    uint8_t* kbuf = smem;
-    uint8_t* qbuf = kbuf + SPLIT * KSTR;
-    float* sbuf = reinterpret_cast<float*>(qbuf + AT_HEADS * QSTR);
-    uint8_t* pbuf = reinterpret_cast<uint8_t*>(sbuf + NSB * AT_HEADS * SSTR);
-    int32_t* slot_s = reinterpret_cast<int32_t*>(pbuf + AT_HEADS * PSTR);
-    float* ksc = reinterpret_cast<float*>(slot_s + SPLIT);
-    int32_t* pt_s = reinterpret_cast<int32_t*>(ksc + SPLIT);
-    static_assert(SPLIT * KSTR + AT_HEADS * QSTR + NSB * AT_HEADS * SSTR * 4 + AT_HEADS * PSTR +
-                          SPLIT * 8 + NPG * 4 <=
-                      TOPK_ARENA_WORDS * 4,
-                  "split LDS");
-    static_assert(NPG <= AT_THREADS, "a page-table entry a thread");
-    constexpr int QP = AT_HEADS * AT_KV / 8;  // 16-byte pieces of a row's q
-    constexpr int NQP = (QP + AT_THREADS - 1) / AT_THREADS;
-    const __amdgpu_buffer_rsrc_t rkv = rsrc(p.kv, p.kv_slots * (uint32_t)AT_KV);
-    // without per-token scales every row is raw E4M3 (scale 1)
-    const bool scaled = p.kv_scale != nullptr;
-    const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, scaled ? p.kv_slots * 4u : 0u);
-    const int nt = ok ? R * NSP : 0;
-    for (int t0 = 0; t0 < nt; t0 += nblk) {
-      const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-      const int task = t0 + (b + nblk - (R % nblk)) % nblk;  // rows' top-k CTAs go last
-      if (task >= nt) continue;
-      const int r = task / NSP, sp = task % NSP;
-      const int n = row_n(r);
-      const int k = n < AT_TOPK ? n : AT_TOPK;
-      const int kcnt = k - sp * SPLIT < SPLIT ? k - sp * SPLIT : SPLIT;
-      if (kcnt <= 0) continue;
-      // ahead of the wait (neither depends on the selection): the row's q, all heads
-      // ([32][576] bf16), and its page-table entries
-      const __amdgpu_buffer_rsrc_t rq = rsrc(p.q + (size_t)r * AT_HEADS * AT_KV, AT_HEADS * AT_KV * 2);
-      v4i qv[NQP];
-#pragma unroll
-      for (int i = 0; i < NQP; ++i) {
-        const int pc = tid + AT_THREADS * i;
-        qv[i] = ld16<XCP>(rq, pc < QP ? (uint32_t)pc * 16u : 0x80000000u);
-      }
-      const int npg = (n + AT_PAGE - 1) / AT_PAGE;
-      const int pgv = ld4<CP_NONE>(
-          rpt, tid < npg ? ((uint32_t)p.req_ids[r] * (uint32_t)p.pt_stride + (uint32_t)tid) * 4u
-                         : 0x80000000u);
-      // the split's tokens, polled as (position, tag) pairs
-      int pos = -1;
-      if (tid < SPLIT) {
-        uint64_t v = 0;
-        const uint64_t* src = topk + (size_t)r * AT_TOPK + sp * SPLIT + tid;
-        ok = wait_until(guard, MONO_SITE_TOPK, [&]() {
-          v = tid < kcnt ? ld_dev64(src) : pair(0u, tag);
-          return __all((uint32_t)(v >> 32) == tag);
-        });
-        if (ok && tid < kcnt) pos = (int)(uint32_t)v;
-      }
-#pragma unroll
-      for (int i = 0; i < NQP; ++i) {
-        const int pc = tid + AT_THREADS * i;
-        if (pc < QP)
-          *reinterpret_cast<v4i*>(qbuf + (pc / (AT_KV / 8)) * QSTR + (pc % (AT_KV / 8)) * 16) = qv[i];
-      }
-      if (tid < NPG) pt_s[tid] = pgv;
-      ok = cta_all(ok, ok_s);
-      if (!ok) break;
-      // position -> cache slot through the page table in LDS
-      if (tid < SPLIT) slot_s[tid] = pos >= 0 ? pt_s[pos >> 6] * AT_PAGE + (pos & 63) : -1;
-      __syncthreads();
-      // gather the rows: 36 pieces of 16 bytes a row (a dead slot reads zeros), and the
-      // token scales, in one round trip
-      {
-        constexpr int GP = SPLIT * (AT_KV / 16);
-        constexpr int NGP = (GP + AT_THREADS - 1) / AT_THREADS;
-        const int slot = tid < SPLIT ? slot_s[tid] : -1;
-        // the row's own KV row is the front's store of this launch (fused): coherent
-        const int own = FUSED ? pt_s[(n - 1) >> 6] * AT_PAGE + ((n - 1) & 63) : -2;
-        const uint32_t so = slot >= 0 ? (uint32_t)slot * 4u : 0x80000000u;
-        const float sc = __int_as_float(slot == own ? ld4<CP_DEV>(rks, so) : ld4<CP_NONE>(rks, so));
-        // every load issued before the first is stored (a load-store loop would wait
-        // one round trip an iteration)
-        v4i gv[NGP];
-#pragma unroll
-        for (int i = 0; i < NGP; ++i) {
-          const int idx = tid + AT_THREADS * i;
-          const int j = idx / (AT_KV / 16), c = idx % (AT_KV / 16);
-          const int sj = idx < GP ? slot_s[j] : -1;
-          const uint32_t go = sj >= 0 ? (uint32_t)sj * AT_KV + c * 16 : 0x80000000u;
-          gv[i] = (FUSED && sj == own) ? ld16<CP_DEV>(rkv, go) : ld16<CP_NT>(rkv, go);
-        }
-#pragma unroll
-        for (int i = 0; i < NGP; ++i) {
-          const int idx = tid + AT_THREADS * i;
-          const int j = idx / (AT_KV / 16), c = idx % (AT_KV / 16);
-          if (idx < GP) *reinterpret_cast<v4i*>(kbuf + j * KSTR + c * 16) = gv[i];
-        }
-        if (tid < SPLIT) ksc[tid] = slot >= 0 ? (scaled ? sc : 1.0f) : 0.f;
-      }
-      __syncthreads();
-      // S = q K^T: wave w takes heads 16 (w / 8) .., keys 16 (w % 4) .. and the even (w / 4
-      // even) or odd K steps: two MFMA chains a tile, summed (even + odd) by the softmax
-      if constexpr (SPLIT == 64) {
-        const int h0 = 16 * (w >> 3), j0 = 16 * (w & 3), odd = (w >> 2) & 1;
-        v4f d = {0.f, 0.f, 0.f, 0.f};
-        const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4) + odd * 64;
-        const uint8_t* kr = kbuf + (j0 + (l & 15)) * KSTR + 8 * (l >> 4) + odd * 32;
-        static_assert(AT_KV / 32 % 2 == 0, "K steps in pairs");
-#pragma unroll 3
-        for (int ks = 0; ks < AT_KV / 32; ks += 2) {
-          const v8bf a0 = *reinterpret_cast<const v8bf*>(qa + ks * 64);
-          const v2i k0 = *reinterpret_cast<const v2i*>(kr + ks * 32);
-          d = mfma_bf16(a0, fp8x8_bf16((uint32_t)k0[0], (uint32_t)k0[1]), d);
-        }
-        float* sb = sbuf + odd * AT_HEADS * SSTR;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sb[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e];
-      } else {
-        // wave w takes heads 16 (w / 8) .. and keys 16 (w % 8) ..; two accumulators (even
-        // and odd K steps): two MFMA chains in flight, summed, then scaled
-        const int h0 = 16 * (w >> 3), j0 = 16 * (w & 7);
-        v4f d = {0.f, 0.f, 0.f, 0.f}, d1 = d;
-        const uint8_t* qa = qbuf + (h0 + (l & 15)) * QSTR + 16 * (l >> 4);
-        const uint8_t* kr = kbuf + (j0 + (l & 15)) * KSTR + 8 * (l >> 4);
-#pragma unroll 3
-        for (int ks = 0; ks < AT_KV / 32; ks += 2) {
-          const v8bf a0 = *reinterpret_cast<const v8bf*>(qa + ks * 64);
-          const v2i k0 = *reinterpret_cast<const v2i*>(kr + ks * 32);
-          const v8bf a1 = *reinterpret_cast<const v8bf*>(qa + ks * 64 + 64);
-          const v2i k1 = *reinterpret_cast<const v2i*>(kr + ks * 32 + 32);
-          d = mfma_bf16(a0, fp8x8_bf16((uint32_t)k0[0], (uint32_t)k0[1]), d);
-          d1 = mfma_bf16(a1, fp8x8_bf16((uint32_t)k1[0], (uint32_t)k1[1]), d1);
-        }
-        d += d1;
-        const float f = ksc[j0 + (l & 15)] * p.sm_scale;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sbuf[(h0 + 4 * (l >> 4) + e) * SSTR + j0 + (l & 15)] = d[e] * f;
-      }
-      __syncthreads();
-      // softmax of the split, per head: wave w takes heads 2w, 2w + 1; lane l keys l (and
-      // l + 64 in a 128-key split)
-      float* ml = mls + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * 2;
-      const float f0 = ksc[l] * p.sm_scale;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int h = 2 * w + hh;
-        const bool v0 = l < kcnt, v1 = SPLIT == 128 && l + 64 < kcnt;
-        float s0, s1 = -INFINITY;
-        if constexpr (SPLIT == 64) {
-          s0 = v0 ? (sbuf[h * SSTR + l] + sbuf[(AT_HEADS + h) * SSTR + l]) * f0 : -INFINITY;
-        } else {
-          s0 = v0 ? sbuf[h * SSTR + l] : -INFINITY;
-          s1 = v1 ? sbuf[h * SSTR + l + 64] : -INFINITY;
-        }
-        const float m = wave_max(fmaxf(s0, s1));
-        const float p0 = v0 ? expf(s0 - m) : 0.f, p1 = v1 ? expf(s1 - m) : 0.f;
-        const float lsum = wave_sum(p0 + p1);
-        // P with the token's scale folded in (V = E4M3 value x scale)
-        reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l] = (uint16_t)bf16_bits(p0 * ksc[l]);
-        if constexpr (SPLIT == 128)
-          reinterpret_cast<uint16_t*>(pbuf + h * PSTR)[l + 64] = (uint16_t)bf16_bits(p1 * ksc[l + 64]);
-        if (l == 0) {
-          st_devf(ml + 2 * h, m);
-          st_devf(ml + 2 * h + 1, lsum);
-        }
-      }
-      __syncthreads();
-      // O = P V: wave w takes heads 16 (w / 8) .. and dims 64 (w % 8) ..; MFMA j4 covers
-      // dims d0 + 4 c + j4 (column c), so one dword of a row feeds four MFMAs
-      {
-        const int h0 = 16 * (w >> 3), d0 = 64 * (w & 7);
-        const int c = l & 15, g = l >> 4;
-        v4f o0 = {0.f, 0.f, 0.f, 0.f}, o1 = o0, o2 = o0, o3 = o0;
-        const uint8_t* pa = pbuf + (h0 + c) * PSTR + 16 * g;
-#pragma unroll
-        for (int kst = 0; kst < SPLIT / 32; ++kst) {
-          const v8bf a = *reinterpret_cast<const v8bf*>(pa + kst * 64);
-          uint32_t dv[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            dv[i] = *reinterpret_cast<const uint32_t*>(kbuf + (32 * kst + 8 * g + i) * KSTR + d0 +
-                                                       4 * c);
-          // byte j of keys (2i, 2i + 1): perm picks bytes j and j + 1 of both dwords
-          uint32_t pr[4][2];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pr[i][0] = __builtin_amdgcn_perm(dv[2 * i + 1], dv[2 * i], 0x05010400u);  // j 0, 1
-            pr[i][1] = __builtin_amdgcn_perm(dv[2 * i + 1], dv[2 * i], 0x07030602u);  // j 2, 3
-          }
-          auto gather = [&](auto hi_c, int which) {
-            constexpr bool HI = decltype(hi_c)::value;
-            const v2bf q0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[0][which], 1.0f, HI);
-            const v2bf q1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[1][which], 1.0f, HI);
-            const v2bf q2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[2][which], 1.0f, HI);
-            const v2bf q3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(pr[3][which], 1.0f, HI);
-            return v8bf{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
-          };
-          const v8bf bj[4] = {gather(std::false_type(), 0), gather(std::true_type(), 0),
-                              gather(std::false_type(), 1), gather(std::true_type(), 1)};
-          o0 = mfma_bf16(a, bj[0], o0);
-          o1 = mfma_bf16(a, bj[1], o1);
-          o2 = mfma_bf16(a, bj[2], o2);
-          o3 = mfma_bf16(a, bj[3], o3);
-        }
-        float* acc = accs + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * AT_LAT;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int h = h0 + 4 * g + e;
-          const v4f v = {o0[e], o1[e], o2[e], o3[e]};
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(v4i, v), rsrc(acc, AT_HEADS * AT_LAT * 4),
-              (uint32_t)(h * AT_LAT + d0 + 4 * c) * 4, 0, CP_DEV);
-        }
-      }
-      drain();
-      __syncthreads();
-      if (tid == 0) st_dev(&split_done[r * AT_NSPLIT + sp], tag);
-    }
-  }
-
-  // ---------------------------------------------------------------- 4: merge
-  stamp(p.timeline, MONO_TL_UPGATE);
-  {
-    float* red = reinterpret_cast<float*>(smem);  // [NSPLIT][512]
-    float* wsp_s = reinterpret_cast<float*>(lds + AT_LDS_WSP);
-    float& linv_s = *reinterpret_cast<float*>(lds + AT_LDS_LINV);
-    for (int task = b; task < R * AT_HEADS; task += nblk) {
-      const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-      if (!ok) break;
-      const int r = task / AT_HEADS, h = task % AT_HEADS;
-      const int n = row_n(r);
-      const int k = n < AT_TOPK ? n : AT_TOPK;
-      const int nsp = (k + SPLIT - 1) / SPLIT;
-      if (w == 0 && nsp > 0)
-        ok = wait_until(guard, MONO_SITE_SPLIT, [&]() {
-          return __all(l >= nsp || ld_dev(&split_done[r * AT_NSPLIT + l]) == tag);
-        });
-      ok = cta_all(ok, ok_s);
-      if (!ok) break;
-      // the split partials and their (m, l) in one round trip: TPS threads a split, VPT
-      // values a thread
-      constexpr int TPS = AT_THREADS / NSP, VPT = AT_LAT / TPS;
-      static_assert(VPT % 4 == 0, "merge thread map");
-      const int sp = tid / TPS, dv = tid % TPS;
-      v4i a[VPT / 4];
-      {
-        const __amdgpu_buffer_rsrc_t ra = rsrc(
-            accs + ((size_t)(r * AT_NSPLIT + (sp < nsp ? sp : 0)) * AT_HEADS + h) * AT_LAT,
-            sp < nsp ? AT_LAT * 4 : 0);
-#pragma unroll
-        for (int i = 0; i < VPT / 4; ++i) a[i] = ld16<CP_DEV>(ra, (uint32_t)(dv * VPT * 4 + 16 * i));
-      }
-      if (w == 0) {
-        const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
-        const bool on = l < nsp;
-        const v2i mlv = ld8<CP_DEV>(rsrc(ml, on ? AT_NSPLIT * AT_HEADS * 8 : 0),
-                                    (uint32_t)((l * AT_HEADS + h) * 8));
-        const float m = on ? __int_as_float(mlv[0]) : -INFINITY;
-        const float ls = on ? __int_as_float(mlv[1]) : 0.f;
-        const float M = wave_max(m);
-        const float ws = on ? expf(m - M) : 0.f;
-        const float L = wave_sum(ws * ls);
-        if (l < AT_NSPLIT) wsp_s[l] = ws;
-        if (l == 0) linv_s = L > 0.f ? 1.0f / L : 0.f;
-      }
-      __syncthreads();
-      {
-        const float ws = sp < nsp ? wsp_s[sp] : 0.f;
-#pragma unroll
-        for (int i = 0; i < VPT / 4; ++i) {
-          const v4f v = __builtin_bit_cast(v4f, a[i]) * ws;
-          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + VPT * dv + 4 * i]) = v;
-        }
-      }
-      __syncthreads();
-      if (tid < AT_LAT) {
-        float s = 0.f;
-        for (int sp = 0; sp < nsp; ++sp) s += red[sp * AT_LAT + tid];
-        // device coherent: in the layer launch the output block reads it next
-        __builtin_amdgcn_raw_buffer_store_b16(
-            (uint16_t)bf16_bits(s * linv_s), rsrc(p.out, (uint32_t)R * AT_HEADS * AT_LAT * 2u),
-            (uint32_t)((r * AT_HEADS + h) * AT_LAT + tid) * 2u, 0, CP_DEV);
-      }
-      __syncthreads();
-    }
-  }
-
-}
 
 template <int SPLIT>
 __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {

@@ -23,7 +23,7 @@ struct LaunchShared {
 
 // Read the guard head (one coherent load, shared in LDS) and set up the guard; returns
 // the launch tag (epoch + 1). Every thread calls it.
-__device__ inline uint32_t launch_begin(LaunchShared& sh, Guard& guard, int32_t* gw,
+__device__ __attribute__((always_inline)) inline uint32_t launch_begin(LaunchShared& sh, Guard& guard, int32_t* gw,
                                         uint32_t* host_err, int fault_site, int fault_after) {
   if (threadIdx.x == 0) {
     const v4i hd = ld16<CP_DEV>(rsrc(gw, 16), 0);
@@ -39,7 +39,7 @@ __device__ inline uint32_t launch_begin(LaunchShared& sh, Guard& guard, int32_t*
 // The CTA leaves the launch: the last one out resets the exit counter, runs `last`
 // (state the next launch expects zero) and advances the epoch to this launch's tag.
 template <class Last>
-__device__ inline void launch_end(int32_t* gw, uint32_t tag, Last last) {
+__device__ __attribute__((always_inline)) inline void launch_end(int32_t* gw, uint32_t tag, Last last) {
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t* w = reinterpret_cast<uint32_t*>(gw);
@@ -65,7 +65,9 @@ struct PhaseBarrier {
   uint32_t* count;
   uint32_t* flag;
 
-  __device__ void arrive(uint32_t tag) const {
+  // always inlined: a call would take the address of the kernel argument holding the
+  // barrier, which keeps the whole argument block in scratch memory
+  __device__ __attribute__((always_inline)) void arrive(uint32_t tag) const {
     drain();
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -88,7 +90,7 @@ struct BarrierWait {
   int site;
   int* ok_s;
 
-  __device__ bool operator()() const {
+  __device__ __attribute__((always_inline)) bool operator()() const {
     bool ok = true;
     if ((threadIdx.x >> 6) == 0)
       ok = wait_until<4>(*guard, site, [&]() { return __all(ld_dev(bar->flag) == tag); });

@@ -1,225 +1,7 @@
-// The attention output block as one persistent gfx950 launch: the merged latent o_lat
-// through W_UV per head, then o_proj and the residual add of the W == 1 reduce.
-//   W_UV  o[r][h * 128 + v] = sum_c W_UV[h][v][c] o_lat[r][h][c], handed over in bf16 (the
-//         reference rounds o to bf16 before o_proj, kernel.py:4080-4123): 256 tiles of 16
-//         rows, one a CTA, issued before anything else so they lead every CU's queue.
-//   o_proj a[r][n] = bf16(h[r][n] + sum_k W_o[n][k] o[r][k]): 448 tiles of 16 rows, two
-//         at a time a CTA: the first tile's weights and h in flight from the launch's
-//         start, the second's from the moment W_UV's outputs are stored.
-// The hand-off of o needs no flag, drain or poll: W_UV stores the complement of each bf16
-// pair into one of two scratch buffers (by the launch tag's parity), and clears the other
-// for the next launch; a zero word is "not written yet". o_proj's x loads are its wait:
-// issued right behind the weights, they return right behind them (a wave's loads return
-// in order) and are loaded again only if a word is still zero. Every prefetch is
-// unconditional (absent tiles read zeros through a zero-size buffer resource), so the
-// compiler keeps exact wait counts instead of waiting for everything after a branch.
-// Reference: sgl_amd_mono/glm53/gfx950/kernel.py:3975-4123 (W_UV), :4125-4197 (o_proj,
-// residual), :1665-1669 (W == 1 reduce).
-#include <hip/hip_runtime.h>
-
-#include "gemv.h"
-#include "mono_abi.h"
-#include "phase.h"
+// The output-block launch of the layer (its phase: post_phase.h) and its C entry points.
+#include "post_phase.h"
 
 namespace mono {
-
-constexpr int PO_HEADS = 32, PO_V = 128, PO_LAT = 512, PO_HID = 7168;
-constexpr int PO_O = PO_HEADS * PO_V;
-constexpr int PO_MAXR = 16;
-constexpr int PO_MAX_GRID = 1024;
-constexpr int PO_TILES = PO_HID / 16;   // o_proj tiles of 16 rows
-
-using GemvUV = Gemv<8, 1, 1>;   // 16 rows of a head: 8 K-splits of 64 (waves 0-7)
-using GemvO = Gemv<16, 1, 4>;   // 16 rows: 16 K-splits of 256
-constexpr int PO_UV_TILES = PO_HEADS * PO_V / GemvUV::ROWS;
-
-struct PostScratch {
-  // two hand-off buffers of o, u32 [16][4096 / 2] complemented bf16 pairs
-  static constexpr size_t OBUF = (size_t)PO_MAXR * PO_O * 2;
-  static constexpr size_t BYTES = 2 * OBUF;
-};
-
-struct PostParams {
-  int rows, shuf;
-  const uint16_t* o_lat;
-  const uint16_t* h;
-  const uint8_t* w_uv;
-  const float* s_uv;
-  const uint8_t* w_o;
-  const float* s_o;
-  uint16_t* out;
-  uint16_t* o;  // bf16 [R][4096]: the caller's, or scratch
-  uint8_t* scratch;
-  int32_t* guard;
-  uint32_t* host_err;
-  int fault_site, fault_after;
-  uint64_t* timeline;
-};
-
-constexpr int PO_LDS_BYTES = 40 * 64 * 16;  // red[40][64]: o_proj [0, 32) two tiles, W_UV [32, 40)
-
-// The output block in one CTA of a launch. FUSED: it runs after the attention phase in
-// the same launch, so o_lat is read device coherent, after `ready` (the attention's
-// barrier), which it calls once its weight prefetch and the residual rows are in flight.
-template <bool FUSED, class Ready>
-__device__ __attribute__((always_inline)) inline void post_phase(const PostParams& p, uint8_t* lds,
-                                                                 Guard& guard, uint32_t tag,
-                                                                 int& ok_s, Ready ready) {
-  const int b = blockIdx.x, nblk = gridDim.x, R = p.rows;
-  v4f (*red)[64] = reinterpret_cast<v4f (*)[64]>(lds);
-  uint16_t* obuf = reinterpret_cast<uint16_t*>(p.scratch + (tag & 1u) * PostScratch::OBUF);
-  uint8_t* onext = p.scratch + ((tag + 1u) & 1u) * PostScratch::OBUF;
-
-  const int tid = opaque_v((int)threadIdx.x);
-  const int l = tid & 63, w = tid >> 6;
-  GemvJob ju{};
-  ju.x = p.o_lat;
-  ju.x_stride = PO_HEADS * PO_LAT;
-  ju.x_gstride = PO_LAT;
-  ju.w = p.w_uv;
-  ju.s = p.s_uv;
-  ju.N = PO_V;
-  ju.K = PO_LAT;
-  ju.G = PO_HEADS;
-  ju.shuf = p.shuf;
-  ju.out_bf = obuf;
-  ju.out_stride = PO_O;
-  ju.out_gstride = PO_V;
-  ju.out_xor = 0xFFFFFFFFu;
-  ju.out_plain = p.o;
-  GemvJob jo{};
-  jo.x = obuf;
-  jo.x_stride = PO_O;
-  jo.w = p.w_o;
-  jo.s = p.s_o;
-  jo.N = PO_HID;
-  jo.K = PO_O;
-  jo.G = 1;
-  jo.shuf = p.shuf;
-  jo.out_bf = p.out;
-  jo.out_stride = PO_HID;
-  jo.res = p.h;
-  jo.res_stride = PO_HID;
-  const GemvUV gu(tid);
-  const GemvO go(tid);
-  constexpr int UV_TPR = PO_V / GemvUV::ROWS;            // W_UV tiles a head
-  constexpr int UV_STORE = GemvUV::ROWS * 16;            // threads of a W_UV epilogue
-  const __amdgpu_buffer_rsrc_t rh = rsrc(p.h, (uint32_t)R * PO_HID * 2u);
-  const int etok = (tid >> 4) & 15, erow = tid & 15;     // o_proj epilogue coordinates
-
-  // ---------------------------------------------------------------- prefetch
-  // W_UV tile b (waves 0-7), then o_proj tile b (all waves) and h; o_proj tile b + nblk
-  // only once W_UV's outputs are stored. The barrier puts every W_UV load of the CU ahead
-  // of every o_proj load: the CU's vector memory path serves its waves' requests in
-  // issue order, stores included, and drains a prefetch at the CU's share of HBM
-  // bandwidth (~23 KB/us), so a store issued behind both tiles (128 KB) would wait ~4 us
-  // and hold back the o hand-off; one tile keeps HBM busy through W_UV.
-  const bool uv0 = b < PO_UV_TILES;
-  v4i wu[1], xu[1][2];
-  float su[1];
-  int a0 = b, a1 = b + nblk;
-  v4i w0[4], w1[4];
-  float s0[4], s1[4];
-  auto load_h = [&](int t0, int t1) -> int {
-    const int t = tid < 256 ? t0 : t1;
-    const bool v = etok < R && tid < 512 && t < PO_TILES;
-    return __builtin_amdgcn_raw_buffer_load_b16(
-        rh, v ? (uint32_t)(etok * PO_HID + t * 16 + erow) * 2u : 0x80000000u, 0, 0);
-  };
-  int hres;
-  bool ok = true;
-  gu.issue(ju, b / UV_TPR, b % UV_TPR, wu, su, uv0);
-  if constexpr (FUSED) {
-    // every weight and the residual in flight, then the wait for o_lat
-    go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
-    hres = load_h(a0, a1);
-    ok = ready();
-    gu.load_x<CP_DEV>(ju, b / UV_TPR, R, xu, uv0 && ok);
-  } else {
-    gu.load_x<CP_NONE>(ju, b / UV_TPR, R, xu, uv0);
-    __syncthreads();
-    go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
-    hres = load_h(a0, a1);
-  }
-
-  // ---------------------------------------------------------------- W_UV
-  // tile b from the prefetch (no loads in this branch: the wait for wu / xu stays exact)
-  if (uv0) {
-    gu.dot(wu, su, xu, red + 32);
-    // The W_UV loads retire here on every wave: the waves outside the tile skip the dot,
-    // and on their path the compiler would otherwise wait at later register writes for
-    // loads behind them too (the o_proj prefetch). 7 loads follow them: an o_proj tile's
-    // 4 weight and 2 scale loads, and h.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(7));
-    __syncthreads();
-    if (tid < UV_STORE) GemvUV::epilogue(ju, b / UV_TPR, b % UV_TPR, R, tid, red + 32);
-    __syncthreads();
-  }
-  // more W_UV tiles than CTAs (fewer than 256 CUs): the rest without prefetch
-  for (int u = b + nblk; u < (ok ? PO_UV_TILES : 0); u += nblk) {
-    gu.issue(ju, u / UV_TPR, u % UV_TPR, wu, su);
-    gu.load_x<FUSED ? CP_DEV : CP_NONE>(ju, u / UV_TPR, R, xu);
-    gu.dot(wu, su, xu, red + 32);
-    __syncthreads();
-    if (tid < UV_STORE) GemvUV::epilogue(ju, u / UV_TPR, u % UV_TPR, R, tid, red + 32);
-    __syncthreads();
-  }
-  go.issue(jo, 0, a1, w1, s1, a1 < PO_TILES);
-  // clear this CTA's slice of the next launch's hand-off buffer
-  {
-    constexpr uint32_t OB = (uint32_t)PostScratch::OBUF;
-    const uint32_t slice = (OB / 16 + nblk - 1) / nblk * 16;
-    const __amdgpu_buffer_rsrc_t rn = rsrc(onext, OB);
-    for (uint32_t i = (uint32_t)tid * 16; i < slice; i += 1024 * 16)
-      st16<CP_DEV>(rn, b * slice + i, v4i{0, 0, 0, 0});
-  }
-  stamp(p.timeline, MONO_TL_STAGED);
-
-  // ---------------------------------------------------------------- o_proj
-  for (int pass = 0; ok && a0 < PO_TILES; ++pass, a0 += 2 * nblk, a1 += 2 * nblk) {
-    if (pass > 0) {
-      go.issue(jo, 0, a0, w0, s0);
-      go.issue(jo, 0, a1, w1, s1, a1 < PO_TILES);
-      hres = load_h(a0, a1);
-    }
-    // o in this wave's K range, for rows t < R; complemented: zero = not written yet
-    v4i xa[4][2];
-    const __amdgpu_buffer_rsrc_t rx = rsrc(obuf, (uint32_t)PostScratch::OBUF);
-    const int t = l & 15, grp = l >> 4;
-    ok = wait_until(guard, MONO_SITE_O, [&]() {
-      uint32_t mn = 0xFFFFFFFFu;
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const uint32_t off =
-              t < R ? (uint32_t)(t * PO_O + go.k0(st) + 16 * grp + 8 * m) * 2u : 0x80000000u;
-          xa[st][m] = ld16<CP_DEV>(rx, off);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) mn = __builtin_elementwise_min(mn, (uint32_t)xa[st][m][q]);
-        }
-      return __all(t >= R || mn != 0u);
-    });
-    ok = cta_all(ok, ok_s);
-    if (!ok) break;
-    stamp(p.timeline, MONO_TL_UPGATE);
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int m = 0; m < 2; ++m) xa[st][m] = ~xa[st][m];
-    const bool two = a1 < PO_TILES;
-    go.dot(w0, s0, xa, red);
-    if (two) go.dot(w1, s1, xa, red + 16);
-    __syncthreads();
-    if (tid < 256)
-      GemvO::epilogue(jo, 0, a0, R, tid, red, hres);
-    else if (two && tid < 512)
-      GemvO::epilogue(jo, 0, a1, R, tid - 256, red + 16, hres);
-    __syncthreads();
-    stamp(p.timeline, MONO_TL_MIDQ);
-  }
-
-}
 
 __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[PO_LDS_BYTES];

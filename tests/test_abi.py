@@ -35,6 +35,7 @@ def _c_layout(struct, fields, tmp_path):
                                         (_lib.MonoAttnArgs, "MonoAttnArgs"),
                                         (_lib.MonoPostArgs, "MonoPostArgs"),
                                         (_lib.MonoFrontArgs, "MonoFrontArgs"),
+                                        (_lib.MonoLayerArgs, "MonoLayerArgs"),
                                         (_lib.MonoDeviceInfo, "MonoDeviceInfo")])
 def test_ctypes_mirrors_match_the_c_layout(cls, cname, tmp_path):
     fields = [f for f, _ in cls._fields_]
@@ -69,6 +70,17 @@ def test_null_args_are_refused_without_a_gpu():
     po = _lib.MonoPostArgs(rows=4, heads=16, hidden=7168)
     assert _lib.lib().mono_post_launch(ctypes.byref(po), None) == _lib.MONO_E_ARG
     assert "32 heads" in _lib.last_error()
+    ly = _lib.MonoLayerArgs(rows=9, rows_max=8, hidden=7168, heads=32, inter=512, experts=256)
+    assert _lib.lib().mono_layer_launch(ctypes.byref(ly), None) == _lib.MONO_E_ARG
+    assert "rows" in _lib.last_error()
+    ly = _lib.MonoLayerArgs(rows=8, rows_max=8, hidden=7168, heads=32, inter=384, experts=256)
+    assert _lib.lib().mono_layer_launch(ctypes.byref(ly), None) == _lib.MONO_E_ARG
+    assert "intermediate 512" in _lib.last_error()
+    ly = _lib.MonoLayerArgs(rows=8, rows_max=8, hidden=7168, heads=32, inter=512, experts=256,
+                            ctx_max=4096, pt_stride=64, pt_rows=8, rope_rows=4096, kv_slots=64,
+                            plane_pages=1)
+    assert _lib.lib().mono_layer_launch(ctypes.byref(ly), None) == _lib.MONO_E_ARG
+    assert "null tensor" in _lib.last_error()
 
 
 def test_scratch_bytes_only_for_built_geometries():
@@ -81,6 +93,8 @@ def test_scratch_bytes_only_for_built_geometries():
     assert 5 * _lib.lib().mono_attn_scratch_bytes(8) < _lib.lib().mono_attn_scratch_bytes(48)
     assert _lib.lib().mono_post_scratch_bytes() >= 16 * 4096 * 2
     assert _lib.lib().mono_front_scratch_bytes() > 0
+    assert _lib.lib().mono_layer_scratch_bytes(8) > _lib.lib().mono_attn_scratch_bytes(8)
+    assert _lib.lib().mono_layer_scratch_bytes(9) == 0
 
 
 def test_deadline_ticks_bounds():

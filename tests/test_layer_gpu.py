@@ -1,5 +1,7 @@
-"""The four launches of one decoder layer chained on one stream (config 5), every phase
-checked against the CPU oracle on the inputs that phase received from the one before.
+"""One decoder layer (config 5): the four launches chained on one stream, every phase
+checked against the CPU oracle on the inputs that phase received from the one before,
+and the one-launch layer (``mono_layer_launch``) bit-equal to the chain at every hand-off
+(q, the index query and weights, scores, top-k, o_lat, a, routing, y) and at its output.
 
 Bars as the per-phase tests: q and the output block within 2e-2 max-abs + 1e-2 relative
 and 1e-2 relative in norm of the oracle's f64; indexer scores within 1e-5 of the row's
@@ -18,7 +20,7 @@ from oracle import moe as M
 from oracle.topk import topk_sort
 from sgl_amd_mono_amd.dsv32 import synthetic
 from sgl_amd_mono_amd.dsv32.attn import AttnInputs
-from sgl_amd_mono_amd.dsv32.layer import LayerOp, LayerStep
+from sgl_amd_mono_amd.dsv32.layer import FusedLayerOp, LayerDebug, LayerOp, LayerStep
 from sgl_amd_mono_amd.dsv32.moe import MoeRouting
 
 pytestmark = pytest.mark.gpu
@@ -71,6 +73,27 @@ def _layer_case(gpu, rows, ctx, positions, seed):
                     device=gpu), torch.empty(rows, 9, device=gpu))
     out = op.moe.launch(a, y=y, routing=rt)
     op.check()
+
+    # the same layer as one launch, on the same caches (its cache writes are the same
+    # bytes at the same slots): bit-equal at every hand-off and at its output
+    fused = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=ctx)
+    dbg = LayerDebug(q=torch.empty_like(f.q), iq=torch.empty_like(f.iq),
+                     iqs=torch.empty_like(f.iqs), iw=torch.empty_like(f.iw),
+                     o_lat=torch.empty_like(o_lat), a=torch.empty_like(a),
+                     scores=torch.full_like(scores, float("nan")),
+                     topk=torch.full_like(topk, -7), y=torch.empty_like(y),
+                     moe_scores=torch.empty_like(rt.scores), ids=torch.empty_like(rt.ids),
+                     weights=torch.empty_like(rt.weights))
+    fout = fused.launch(h, caches, step, debug=dbg)
+    fused.check()
+    for name, got, want in (("q", dbg.q, f.q), ("iq", dbg.iq, f.iq), ("iqs", dbg.iqs, f.iqs),
+                            ("iw", dbg.iw, f.iw), ("topk", dbg.topk, topk),
+                            ("o_lat", dbg.o_lat, o_lat), ("a", dbg.a, a), ("y", dbg.y, y),
+                            ("moe scores", dbg.moe_scores, rt.scores), ("ids", dbg.ids, rt.ids),
+                            ("weights", dbg.weights, rt.weights), ("out", fout, out)):
+        assert torch.equal(got, want), f"one launch vs four: {name}"
+    assert torch.equal(dbg.scores.isnan(), scores.isnan())
+    assert torch.equal(dbg.scores.nan_to_num(0.0), scores.nan_to_num(0.0))
 
     pos = step.positions.cpu().numpy()
     fr = Fr.front(h.cpu(), positions=pos, **synthetic.rowmajor_front(w.front))
@@ -186,3 +209,63 @@ def test_layer_bound_from_sglang_modules_matches_the_direct_launch(gpu):
     got = op.launch(h, caches, step)
     op.check()
     assert torch.equal(got, want)
+
+
+def test_one_launch_layer_graph_replay_matches_eager(gpu):
+    """The one-launch layer captured in a graph: three replays, eager launches between
+    them, every replay bit-equal to the eager result; 3 rows, one of them a pad row."""
+    print("case one-launch layer graph replay rows=3 ctx=4096", flush=True)
+    rows = 3
+    w, caches, step, h = synthetic.layer(rows, 4096, gpu, seed=41)
+    step = LayerStep(positions=step.positions, slots=step.slots.clone(), req_ids=step.req_ids,
+                     page_table=step.page_table)
+    step.slots[2] = -1  # a pad row: writes no cache entry
+    op = FusedLayerOp(w, gpu, max_rows=8, ctx_max=4096)
+    want = op.launch(h, caches, step).clone()
+    again = op.launch(h, caches, step).clone()
+    op.check()
+    assert torch.equal(want, again)
+    out = torch.empty_like(want)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op.launch(h, caches, step, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        op.launch(h, caches, step, out=out)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        op.launch(h, caches, step)
+        torch.cuda.synchronize()
+    op.check()
+
+
+@pytest.mark.parametrize("site", [11, 5, 2])
+def test_one_launch_layer_deadline_stops_and_reports(gpu, site):
+    """A wait forced to stall from the host (the phase barrier, a split's top-k wait, a mid
+    quant's wait): it times out after 5 ms, every CTA runs to the end of the launch, the
+    host raises naming the site, and a reset runtime launches cleanly."""
+    from sgl_amd_mono_amd import _lib
+
+    print(f"case one-launch layer fault injection site={site}", flush=True)
+    rows = 2
+    w, caches, step, h = synthetic.layer(rows, 4096, gpu, seed=43)
+    op = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096, deadline_s=0.005, fault=(site, 0))
+    op.launch(h, caches, step)
+    with pytest.raises(RuntimeError, match=f"timed out at {_lib.SITES[site]} "):
+        op.check()
+    words = op.rt.guard.cpu().tolist()
+    assert words[3] == site + 1 and words[5] == 1
+    op.fault = (0, 0)
+    op.rt.reset()
+    op.rt.set_deadline(10.0)
+    clean = op.launch(h, caches, step).clone()
+    op.check()
+    ref = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096).launch(h, caches, step)
+    torch.cuda.synchronize()
+    assert torch.equal(clean, ref)
