@@ -5,19 +5,20 @@ TP=4 share of a DeepSeek-V3.2 DSA decoder layer at 8 decode rows, each row its o
 request at position 32767 (context 32768): the front (RMSNorm, q_a | kv_a, q_b, RoPE,
 W_UK, the KV and FP4 index-key cache writes, the FP4 index query), the attention phase
 (FP4 indexer scores, exact top-2048, sparse MLA), the output block (W_UV, o_proj,
-residual) and the FP8 MoE (RMSNorm, router, top-8 + shared experts, residual), as four
-persistent launches. A step is one layer over one batch; ``--layers`` independently
-seeded layers (about 3 GB each, 0.5 GB of it touched a step, so the 256 MB MALL cannot
-serve them) are rotated. Inputs are resident in HBM before the timed region; the timed
-region replays a HIP graph of the four launches of every layer, is bracketed by
-``torch.cuda.synchronize()`` and is measured with HIP events on the replay stream.
+residual) and the FP8 MoE (RMSNorm, router, top-8 + shared experts, residual), as ONE
+persistent launch a layer (``mono_layer_launch``). A step is one layer over one batch;
+``--layers`` independently seeded layers (about 3 GB each, 0.5 GB of it touched a step,
+so the 256 MB MALL cannot serve them) are rotated. Inputs are resident in HBM before the
+timed region; the timed region replays a HIP graph of every layer's launch, is bracketed
+by ``torch.cuda.synchronize()`` and is measured with HIP events on the replay stream.
 ``value`` is the average µs per layer.
 
-``roofline``: the dominant kernel's (the MoE launch's) algorithmic bytes per launch --
-every distinct expert the batch routed to (shared included) x 11,012,736 B + the router
-3,670,016 B + the rows in and out -- over its own average launch time (a graph of that
-launch alone over the same layers), against 8 TB/s; ``config.phases`` gives every
-phase's time and achieved bandwidth. ``cpu_baseline``: the CPU oracle chain
+``roofline``: the layer kernel's (the step's only kernel) algorithmic bytes per launch --
+the front's, output block's and router's weights, every distinct expert the batch routed
+to (shared included) x 11,012,736 B, the KV rows gathered and index keys scanned, the
+rows in and out -- over its average launch time, against 8 TB/s. ``config`` also gives
+each phase's end inside the launch (timeline stamps) and each phase's time and achieved
+bandwidth as a launch of its own (the four-launch chain). ``cpu_baseline``: the CPU oracle chain
 (``oracle/front.py``, ``oracle/attn.py``, ``oracle/dense.py``, ``oracle/moe.py``) for the
 whole layer at all rows on this host's cores (the box's thread share), one warm-up then
 the median of five runs, with the core count and CPU model.
@@ -477,14 +478,33 @@ def cpu_baseline_layer(h, w, caches, step, rows):
                       f"{len(times)} runs", times)
 
 
+def layer_timeline(op, h, caches, step, grid):
+    """In-launch phase ends of one eager launch (µs from the launch's start, median and
+    max over CTAs): the front, attention, output block and MoE done, and the exit."""
+    import torch
+
+    from sgl_amd_mono_amd import _lib
+
+    tl = torch.zeros(grid, _lib.TL_COLS, dtype=torch.int64, device=h.device)
+    op.launch(h, caches, step, timeline=tl)
+    op.check()
+    t = tl.cpu().numpy().astype("float64")
+    t0 = t[:, 0].min()
+    out = {}
+    for k, name in enumerate(_lib.TL_LAYER_MARKS[1:], start=1):
+        v = (t[:, k] - t0) / 100.0  # 100 MHz clock -> µs
+        out[name] = {"median_us": round(float(sorted(v)[len(v) // 2]), 2),
+                     "max_us": round(float(v.max()), 2)}
+    return out
+
+
 def bench_layer(args):
     import numpy as np
     import torch
 
     from sgl_amd_mono_amd.dsv32 import synthetic
     from sgl_amd_mono_amd.dsv32.attn import AttnInputs
-    from sgl_amd_mono_amd.dsv32.layer import LayerOp
-    from sgl_amd_mono_amd.dsv32.moe import MoeRouting
+    from sgl_amd_mono_amd.dsv32.layer import FusedLayerOp, LayerDebug, LayerOp, layer_runtime
 
     dev = torch.device("cuda:0")
     rows, ctx = args.rows, args.ctx
@@ -496,74 +516,83 @@ def bench_layer(args):
         layers.append(synthetic.layer(rows, ctx, dev, seed=1000 + i, layout=args.layout))
         if (i + 1) % 8 == 0:
             print(f"bench: {i + 1} layers", file=sys.stderr, flush=True)
-    ops = [LayerOp(w, dev, max_rows=rows, ctx_max=ctx) for w, _, _, _ in layers]
+    # the one-launch layers share one runtime, as a served model's layers do
+    rt = layer_runtime(dev, max_rows=rows)
+    fused = [FusedLayerOp(w, dev, max_rows=rows, ctx_max=ctx, rt=rt) for w, _, _, _ in layers]
     outs = [torch.empty(rows, 7168, dtype=torch.bfloat16, device=dev) for _ in range(L)]
-    # one eager pass, stage by stage: every phase's inputs for the per-phase timings, and
-    # the experts each layer's batch routes to
-    fr_out, att_in, olat, a_in, distinct, ids0 = [], [], [], [], [], None
-    for i, (op, (w, caches, step, h)) in enumerate(zip(ops, layers)):
+    # the experts each layer's batch routes to (an eager launch with the routing out)
+    distinct = []
+    for i, (op, (w, caches, step, h)) in enumerate(zip(fused, layers)):
+        ids = torch.empty(rows, 9, dtype=torch.int32, device=dev)
+        op.launch(h, caches, step, out=outs[i], debug=LayerDebug(ids=ids))
+        op.check()
+        distinct.append(len(np.unique(ids.cpu().numpy())))
+    per = [phase_bytes(rows, ctx, d) for d in distinct]
+    avg = {k: sum(p[k] for p in per) / L for k in per[0]}
+    total = sum(avg.values())
+    us, wall, steps = time_graph(
+        lambda i: fused[i].launch(layers[i][3], layers[i][1], layers[i][2], out=outs[i]), L,
+        args.steps, args.warmup)
+    rt.check()
+    print(f"bench: {steps} layers, {us:.1f} us each as one launch (wall "
+          f"{wall * 1e3 / steps:.1f} ms/layer), distinct experts {distinct}", file=sys.stderr,
+          flush=True)
+    inside = layer_timeline(fused[0], layers[0][3], layers[0][1], layers[0][2], rt.grid)
+    print(f"bench: in-launch phase ends {inside}", file=sys.stderr, flush=True)
+    # each phase as its own launch (the four-launch chain), for the per-phase figures
+    chain = [LayerOp(w, dev, max_rows=rows, ctx_max=ctx) for w, _, _, _ in layers]
+    fr_out, att_in, olat, a_in = [], [], [], []
+    for i, (op, (w, caches, step, h)) in enumerate(zip(chain, layers)):
         f = op.front.launch(h, caches, step.positions, step.slots)
         inp = AttnInputs(q=f.q, iq=f.iq, iqs=f.iqs, iw=f.iw, plane=caches.plane,
                          plane_scale=caches.plane_scale, kv=caches.kv, kv_scale=caches.kv_scale,
                          positions=step.positions, req_ids=step.req_ids, page_table=step.page_table)
         o = op.attn.launch(inp).clone()
         a = op.post.launch(o, h).clone()
-        rt = MoeRouting(torch.empty(rows, 256, device=dev),
-                        torch.empty(rows, 9, dtype=torch.int32, device=dev),
-                        torch.empty(rows, 9, device=dev))
-        op.moe.launch(a, routing=rt, out=outs[i])
+        op.moe.launch(a, out=outs[i])
         op.check()
-        ids = rt.ids.cpu().numpy()
-        distinct.append(len(np.unique(ids)))
-        ids0 = ids if i == 0 else ids0
         fr_out.append(f)
         att_in.append(inp)
         olat.append(o)
         a_in.append(a)
-    per = [phase_bytes(rows, ctx, d) for d in distinct]
-    avg = {k: sum(p[k] for p in per) / L for k in per[0]}
-    total = sum(avg.values())
-    us, wall, steps = time_graph(
-        lambda i: ops[i].launch(layers[i][3], layers[i][1], layers[i][2], out=outs[i]), L,
-        args.steps, args.warmup)
-    for op in ops:
-        op.check()
-    print(f"bench: {steps} layers, {us:.1f} us each (wall {wall * 1e3 / steps:.1f} ms/layer), "
-          f"distinct experts {distinct}", file=sys.stderr, flush=True)
-    # each phase alone (its launches over the L layers in one graph)
+    chain_us = time_graph(
+        lambda i: chain[i].launch(layers[i][3], layers[i][1], layers[i][2], out=outs[i]), L,
+        args.steps, args.warmup)[0]
     phase_us = {
-        "front": time_graph(lambda i: ops[i].front.launch(layers[i][3], layers[i][1],
-                                                          layers[i][2].positions,
-                                                          layers[i][2].slots, out=fr_out[i]),
+        "front": time_graph(lambda i: chain[i].front.launch(layers[i][3], layers[i][1],
+                                                            layers[i][2].positions,
+                                                            layers[i][2].slots, out=fr_out[i]),
                             L, args.steps, args.warmup)[0],
-        "attn": time_graph(lambda i: ops[i].attn.launch(att_in[i], out=olat[i]), L, args.steps,
+        "attn": time_graph(lambda i: chain[i].attn.launch(att_in[i], out=olat[i]), L, args.steps,
                            args.warmup)[0],
-        "post": time_graph(lambda i: ops[i].post.launch(olat[i], layers[i][3], out=a_in[i]), L,
+        "post": time_graph(lambda i: chain[i].post.launch(olat[i], layers[i][3], out=a_in[i]), L,
                            args.steps, args.warmup)[0],
-        "moe": time_graph(lambda i: ops[i].moe.launch(a_in[i], out=outs[i]), L, args.steps,
+        "moe": time_graph(lambda i: chain[i].moe.launch(a_in[i], out=outs[i]), L, args.steps,
                           args.warmup)[0],
     }
-    for op in ops:
+    for op in chain:
         op.check()
     phases = {k: {"us": round(v, 2), "bytes": int(avg[k]),
                   "achieved_GBs": round(avg[k] / (v * 1e-6) / 1e9, 1)} for k, v in phase_us.items()}
-    print(f"bench: phases {phases}", file=sys.stderr, flush=True)
+    print(f"bench: four launches {chain_us:.1f} us; phases alone {phases}", file=sys.stderr,
+          flush=True)
     cpu = None if args.no_cpu else cpu_baseline_layer(layers[0][3], layers[0][0], layers[0][1],
                                                       layers[0][2], rows)
     config = {
         "workload": "BASELINE configs[4]: full DeepSeek-V3.2 DSA decoder layer, one GPU's TP=4 "
-                    "share, 8 rows at position 32767 (context 32768): front (RMSNorm, q_a/kv_a, "
-                    "q_b, RoPE, W_UK, KV + FP4 index-key cache writes, FP4 index query), FP4 "
-                    "indexer + exact top-2048 + sparse MLA, W_UV + o_proj + residual, FP8 MoE "
-                    "(norm, router, top-8 + shared, residual): 4 persistent launches a layer",
-        "rows": rows, "context": ctx, "layers_rotated": L, "launches_per_layer": 4,
-        "weight_layout": args.layout, "distinct_experts": distinct, "phases": phases,
+                    "share, 8 rows at position 32767 (context 32768), ONE persistent launch a "
+                    "layer: front (RMSNorm, q_a/kv_a, q_b, RoPE, W_UK, KV + FP4 index-key cache "
+                    "writes, FP4 index query), FP4 indexer + exact top-2048 + sparse MLA, W_UV + "
+                    "o_proj + residual, FP8 MoE (norm, router, top-8 + shared, residual)",
+        "rows": rows, "context": ctx, "layers_rotated": L, "launches_per_layer": 1,
+        "weight_layout": args.layout, "distinct_experts": distinct,
+        "in_launch_phase_ends_us": inside,
+        "four_launch_chain_us": round(chain_us, 2), "phases_as_own_launches": phases,
         "bytes_per_layer": int(total), "layer_achieved_GBs": round(total / (us * 1e-6) / 1e9, 1),
         "model_layers": 61, "us_per_token_step_61_layers": round(us * 61, 1),
     }
-    # the roofline line is the dominant phase's (the MoE launch)
-    return (us, steps, avg["moe"], "fp8 / fp4 idx / bf16", config, "layer_moe", cpu,
-            phase_us["moe"])
+    # the roofline line is the layer kernel's: the only kernel of the step
+    return us, steps, total, "fp8 / fp4 idx / bf16", config, "layer", cpu, us
 
 
 def main():

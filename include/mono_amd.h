@@ -425,6 +425,9 @@ typedef struct {
   int32_t fault_after;
   uint64_t* timeline;    /* optional u64 [grid, 8]: start, front, attention, output block,
                             MoE done, exit */
+  uint64_t* phase_timeline; /* optional u64 [4, grid, 8]: each phase's own stamps (the
+                               marks of its launch of its own), front, attention, output
+                               block, MoE */
 } MonoLayerArgs;
 
 size_t mono_layer_scratch_bytes(int32_t rows_max);

@@ -252,7 +252,8 @@ class MonoLayerArgs(ctypes.Structure):
         "w_o", "s_o", "g_post", "w_r", "bias", "w13", "s13", "w2", "s2", "q", "iq", "iqs", "iw",
         "o_lat", "a", "scores", "topk_pos", "y", "moe_scores", "ids", "weights", "scratch",
         "guard", "host_error")]
-    _fields_ += [("fault_site", c_int32), ("fault_after", c_int32), ("timeline", c_void_p)]
+    _fields_ += [("fault_site", c_int32), ("fault_after", c_int32), ("timeline", c_void_p),
+                 ("phase_timeline", c_void_p)]
 
 
 # name -> (restype, argtypes)

@@ -133,7 +133,10 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   const AttnScratch S(p.rows_max);
   static_assert(SPLIT == 64 || SPLIT == 128, "64- or 128-key splits");
   constexpr int NSP = AT_TOPK / SPLIT;  // splits a row
-  constexpr int XCP = FUSED ? CP_DEV : CP_NONE;  // loads of the front's outputs
+  // the front's outputs (q, iq, iqs, iw) are read after the barrier through L2: their
+  // lines are only stored (write-through) before it in this launch, so no cache holds a
+  // stale copy (phase.h)
+  constexpr int XCP = CP_NONE;
   const int tid = threadIdx.x, l = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R = p.rows;

@@ -274,6 +274,13 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   int grid = 0;
   int rc = monokernel_grid(&grid);
   if (rc) return rc;
+  if (a->phase_timeline) {
+    const size_t per = (size_t)grid * MONO_TL_COLS;
+    f.timeline = a->phase_timeline;
+    at.timeline = a->phase_timeline + per;
+    po.timeline = a->phase_timeline + 2 * per;
+    m.timeline = a->phase_timeline + 3 * per;
+  }
   // the front's placement: every stage-A task, every row task and every W_UK tile on a
   // CTA of its own, at most two B tiles a CTA
   if (grid > FR_MAX_GRID || grid < FR_ATASKS + 4 * R || grid < FR_CT || 2 * grid < FR_BT)

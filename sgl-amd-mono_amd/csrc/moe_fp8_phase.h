@@ -163,7 +163,9 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   using G = MoeFp8Geom<H, I>;
   using LO = MoeLds<H, I>;
   constexpr int KCW = G::KCW, NUG = G::NUG, NKB = G::NKB, QW = G::QW;
-  constexpr int XCP = FUSED ? CP_DEV : CP_NONE;  // loads of the stream a
+  // the stream a is read through L2 in both forms: fused, its lines are only stored
+  // (write-through) before the barrier in this launch, so no cache holds a stale copy
+  constexpr int XCP = CP_NONE;
   const int tid = threadIdx.x, l = tid & 63;
   // the wave index in an SGPR: every per-wave address term stays scalar
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);

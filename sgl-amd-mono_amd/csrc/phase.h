@@ -7,8 +7,12 @@
 // CTA; between two phases sits a grid barrier (every CTA's stores of phase k drained
 // before it arrives, the last arrival raises the barrier's flag to the launch tag), and
 // each phase waits for it only after issuing the loads that do not depend on the phase
-// before it (weights, cache pages). Every hand-off from one phase to the next is a
-// device-coherent (sc1) store and load, since no kernel boundary separates them.
+// before it (weights, cache pages). Every hand-off from one phase to the next is stored
+// device coherent (sc1, write-through) and drained before its CTA arrives. The next phase
+// reads it through L2: no cache line survives a kernel boundary, and within the launch no
+// CU reads a hand-off buffer before its barrier, so no L2 can hold a stale copy of it. The
+// one exception is a row's own cache entry, which the attention phase prefetches (its
+// page) before the barrier: that one is read again device coherent after it.
 #pragma once
 
 #include "mono_device.h"

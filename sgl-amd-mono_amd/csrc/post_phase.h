@@ -136,7 +136,7 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
     go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
     hres = load_h(a0, a1);
     ok = ready();
-    gu.load_x<CP_DEV>(ju, b / UV_TPR, R, xu, uv0 && ok);
+    gu.load_x<CP_NONE>(ju, b / UV_TPR, R, xu, uv0 && ok);
   } else {
     gu.load_x<CP_NONE>(ju, b / UV_TPR, R, xu, uv0);
     __syncthreads();
@@ -160,7 +160,7 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
   // more W_UV tiles than CTAs (fewer than 256 CUs): the rest without prefetch
   for (int u = b + nblk; u < (ok ? PO_UV_TILES : 0); u += nblk) {
     gu.issue(ju, u / UV_TPR, u % UV_TPR, wu, su);
-    gu.load_x<FUSED ? CP_DEV : CP_NONE>(ju, u / UV_TPR, R, xu);
+    gu.load_x<CP_NONE>(ju, u / UV_TPR, R, xu);
     gu.dot(wu, su, xu, red + 32);
     __syncthreads();
     if (tid < UV_STORE) GemvUV::epilogue(ju, u / UV_TPR, u % UV_TPR, R, tid, red + 32);

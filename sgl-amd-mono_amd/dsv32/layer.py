@@ -192,7 +192,10 @@ class FusedLayerOp:
     def launch(self, h: torch.Tensor, caches: FrontCaches, step: LayerStep,
                out: Optional[torch.Tensor] = None, stream=None,
                debug: Optional[LayerDebug] = None,
-               timeline: Optional[torch.Tensor] = None) -> torch.Tensor:
+               timeline: Optional[torch.Tensor] = None,
+               phase_timeline: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``timeline`` i64 [grid, 8] takes the launch's marks (start, each phase done,
+        exit); ``phase_timeline`` i64 [4, grid, 8] each phase's own stamps."""
         cfg, dev, w = self.cfg, self.device, self.w
         r = h.shape[0] if h.dim() == 2 else -1
         if not 1 <= r <= self.max_rows:
@@ -222,6 +225,9 @@ class FusedLayerOp:
         d.check(r, self.ctx_max, cfg, dev)
         if timeline is not None:
             _need(timeline, "timeline", torch.int64, (self.rt.grid, _lib.TL_COLS), dev)
+        if phase_timeline is not None:
+            _need(phase_timeline, "phase_timeline", torch.int64, (4, self.rt.grid, _lib.TL_COLS),
+                  dev)
         self.rt.before_launch()
         ptr = lambda t: t.data_ptr() if t is not None else None
         f, po, m = w.front, w.post, w.moe
@@ -250,7 +256,8 @@ class FusedLayerOp:
             moe_scores=ptr(d.moe_scores), ids=ptr(d.ids), weights=ptr(d.weights),
             scratch=self.rt.scratch.data_ptr(), guard=self.rt.guard.data_ptr(),
             host_error=self.rt.host_error.data_ptr(), fault_site=int(self.fault[0]),
-            fault_after=int(self.fault[1]), timeline=ptr(timeline))
+            fault_after=int(self.fault[1]), timeline=ptr(timeline),
+            phase_timeline=ptr(phase_timeline))
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().mono_layer_launch(ctypes.byref(args), _lib.stream_handle(stream)),
                        "mono_layer_launch")
