@@ -177,13 +177,29 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   const __amdgpu_buffer_rsrc_t rplane = rsrc(p.plane, p.plane_pages * 4096u);
   const __amdgpu_buffer_rsrc_t rpsc = rsrc(p.plane_scale, p.plane_pages * 256u);
 
+  // XCD-local placement (up to 8 rows on 256 CTAs; the hardware hands CTA b to XCD b % 8):
+  // row r's 32 score tasks, its top-k (CTA r), its 32 splits and its 32 merges all run on
+  // XCD r, so the scores, the row's q and the split partials each cross HBM once and are
+  // then read from that XCD's L2. Each stage has 32 tasks a row: CTA b takes task b / 8
+  // of row b % 8. Otherwise task t is task t % 32 of row t / 32, CTA b taking t = b, b +
+  // grid, ...
+  const bool xcd = R <= 8 && nblk == 8 * 32;
+  const int ntask32 = xcd ? nblk : R * 32;
+  auto task_of = [&](int t, int& r, int& i) {
+    r = xcd ? (t & 7) : t / 32;
+    i = xcd ? (t >> 3) : t % 32;
+  };
+
   // ---------------------------------------------------------------- 1: scores
   // Each stage takes the thread index through an opaque copy: conditions on it are then
   // computed inside the stage, not hoisted to the kernel's top where they would hold
   // registers through every stage.
-  for (int task = b; task < R * AT_NCHUNK; task += nblk) {
+  static_assert(AT_NCHUNK == 32, "32 score tasks a row");
+  for (int task = b; task < ntask32; task += nblk) {
     const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-    const int r = task / AT_NCHUNK, c = task % AT_NCHUNK;
+    int r, c;
+    task_of(task, r, c);
+    if (r >= R) continue;
     const int n = row_n(r);
     if (c * AT_CHUNK >= n) continue;
     const int pg = c * (AT_CHUNK / AT_PAGE) + w;
@@ -325,12 +341,15 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     // without per-token scales every row is raw E4M3 (scale 1)
     const bool scaled = p.kv_scale != nullptr;
     const __amdgpu_buffer_rsrc_t rks = rsrc(p.kv_scale, scaled ? p.kv_slots * 4u : 0u);
-    const int nt = ok ? R * NSP : 0;
+    const bool xsp = xcd && NSP == 32;
+    const int nt = ok ? (xsp ? nblk : R * NSP) : 0;
     for (int t0 = 0; t0 < nt; t0 += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-      const int task = t0 + (b + nblk - (R % nblk)) % nblk;  // rows' top-k CTAs go last
+      // XCD-local (task b / 8 of row b % 8), else task t0 + b with the rows' top-k CTAs last
+      const int task = xsp ? b : t0 + (b + nblk - (R % nblk)) % nblk;
       if (task >= nt) continue;
-      const int r = task / NSP, sp = task % NSP;
+      const int r = xsp ? (task & 7) : task / NSP, sp = xsp ? (task >> 3) : task % NSP;
+      if (r >= R) continue;
       const int n = row_n(r);
       const int k = n < AT_TOPK ? n : AT_TOPK;
       const int kcnt = k - sp * SPLIT < SPLIT ? k - sp * SPLIT : SPLIT;
@@ -527,10 +546,13 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     float* red = reinterpret_cast<float*>(smem);  // [NSPLIT][512]
     float* wsp_s = reinterpret_cast<float*>(lds + AT_LDS_WSP);
     float& linv_s = *reinterpret_cast<float*>(lds + AT_LDS_LINV);
-    for (int task = b; task < R * AT_HEADS; task += nblk) {
+    static_assert(AT_HEADS == 32, "32 merge tasks a row");
+    for (int task = b; task < ntask32; task += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
       if (!ok) break;
-      const int r = task / AT_HEADS, h = task % AT_HEADS;
+      int r, h;
+      task_of(task, r, h);
+      if (r >= R) continue;
       const int n = row_n(r);
       const int k = n < AT_TOPK ? n : AT_TOPK;
       const int nsp = (k + SPLIT - 1) / SPLIT;
@@ -551,12 +573,14 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
             accs + ((size_t)(r * AT_NSPLIT + (sp < nsp ? sp : 0)) * AT_HEADS + h) * AT_LAT,
             sp < nsp ? AT_LAT * 4 : 0);
 #pragma unroll
-        for (int i = 0; i < VPT / 4; ++i) a[i] = ld16<CP_DEV>(ra, (uint32_t)(dv * VPT * 4 + 16 * i));
+        // through L2: within the launch the partials are only stored (write-through) before
+        // the done words this CTA waited for, so no L2 holds a stale copy
+        for (int i = 0; i < VPT / 4; ++i) a[i] = ld16<CP_NONE>(ra, (uint32_t)(dv * VPT * 4 + 16 * i));
       }
       if (w == 0) {
         const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
         const bool on = l < nsp;
-        const v2i mlv = ld8<CP_DEV>(rsrc(ml, on ? AT_NSPLIT * AT_HEADS * 8 : 0),
+        const v2i mlv = ld8<CP_NONE>(rsrc(ml, on ? AT_NSPLIT * AT_HEADS * 8 : 0),
                                     (uint32_t)((l * AT_HEADS + h) * 8));
         const float m = on ? __int_as_float(mlv[0]) : -INFINITY;
         const float ls = on ? __int_as_float(mlv[1]) : 0.f;

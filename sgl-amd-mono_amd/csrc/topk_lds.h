@@ -196,8 +196,10 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
 
 // The exact top-TOPK of one row's n scores (TOPK < n <= 32768), in LDS: returns the
 // selected positions in ascending order (sel[0 .. TOPK)). Ranked by the radix key of
-// the f32 score, larger first, ties to the lower position. `rs` covers the n scores
-// (f32, device coherent loads); `arena` holds TOPK_ARENA_WORDS words. Every thread of the
+// the f32 score, larger first, ties to the lower position. `rs` covers the n scores (f32,
+// read through L2: the caller has seen their done words, and within the launch the
+// scores are only stored, write-through, before them, so no L2 holds a stale copy);
+// `arena` holds TOPK_ARENA_WORDS words. Every thread of the
 // CTA calls it. With `ts` non-null, thread 0 records the shader clock after each step.
 //
 // Thread t keeps the keys of positions 32 t .. 32 t + 31 in registers (loaded through a
@@ -223,7 +225,7 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_select(
   constexpr int NLD = AT_MAXCTX / 4 / AT_THREADS;
   v4i raw[NLD];
 #pragma unroll
-  for (int q = 0; q < NLD; ++q) raw[q] = ld16<CP_DEV>(rs, (uint32_t)(4 * (tid + AT_THREADS * q)) * 4);
+  for (int q = 0; q < NLD; ++q) raw[q] = ld16<CP_NONE>(rs, (uint32_t)(4 * (tid + AT_THREADS * q)) * 4);
   reinterpret_cast<v4i*>(hist)[tid] = v4i{0, 0, 0, 0};  // select_pass expects it zero
   // a position past the row holds key 0, below every real key (a score keeps key >= 1:
   // only the all-ones NaN would map to 0, and it ranks next to it)
