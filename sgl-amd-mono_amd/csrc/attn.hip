@@ -12,7 +12,9 @@ __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
   attn_phase<SPLIT, false>(p, lds, guard, tag, sh.ok, NoWait());
   stamp(p.timeline, MONO_TL_DOWN);
-  launch_end(p.guard, tag, []() {});
+  launch_end(sh, p.guard, tag, p.scratch, (uint32_t)AttnScratch(p.rows_max).bytes,
+             Poison{p.out, (uint32_t)p.rows * AT_HEADS * AT_LAT * 2u, NAN_BF16X2},
+             Poison{nullptr, 0, 0}, []() {});
   stamp(p.timeline, MONO_TL_END);
 }
 

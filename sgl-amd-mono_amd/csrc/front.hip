@@ -11,7 +11,9 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
   const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
   front_phase(p, lds, guard, tag, sh.ok);
   stamp(p.timeline, MONO_TL_MIDQ);
-  launch_end(p.guard, tag, []() {});
+  launch_end(sh, p.guard, tag, p.scratch, (uint32_t)FrontScratch::BYTES,
+             Poison{p.q, (uint32_t)p.rows * FR_HEADS * FR_Q * 2u, NAN_BF16X2},
+             Poison{p.iw, (uint32_t)p.rows * FR_IH * 4u, NAN_F32}, []() {});
   stamp(p.timeline, MONO_TL_END);
 }
 

@@ -56,6 +56,7 @@ struct LayerParams {
   PostParams po;
   MoeFp8Params m;
   PhaseBarrier bar[3];
+  uint8_t* scratch;
   int32_t* guard;
   uint32_t* host_err;
   int fault_site, fault_after;
@@ -86,7 +87,11 @@ __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
   moe_phase<LY_H, LY_I, SHUF, true>(p.m, lds, guard, tag, sh.ok,
                                     BarrierWait{&p.bar[2], &guard, tag, MONO_SITE_PHASE, &sh.ok});
   stamp(p.timeline, LY_TL_MOE);
-  launch_end(p.guard, tag, [&]() { moe_reset_queues<LY_H, LY_I>(p.m); });
+  launch_end(sh, p.guard, tag, p.scratch,
+             (uint32_t)LayerScratch(p.at.rows_max).bytes,
+             Poison{p.m.out, (uint32_t)p.m.rows * LY_H * 2u, NAN_BF16X2},
+             Poison{p.m.y, (uint32_t)p.m.rows * LY_H * 4u, NAN_F32},
+             [&]() { moe_reset_queues<LY_H, LY_I>(p.m); });
   stamp(p.timeline, LY_TL_END);
 }
 
@@ -265,6 +270,7 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
     p.bar[k].count = reinterpret_cast<uint32_t*>(sc + LayerScratch::BARRIERS + 256 * k);
     p.bar[k].flag = reinterpret_cast<uint32_t*>(sc + LayerScratch::BARRIERS + 256 * k + 128);
   }
+  p.scratch = sc;
   p.guard = a->guard;
   p.host_err = host_err;
   p.fault_site = a->fault_site;

@@ -6,15 +6,18 @@ namespace mono {
 template <int H, int I, bool SHUF>
 __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[MoeLds<H, I>::BYTES];
-  __shared__ int ok_s;
+  __shared__ LaunchShared sh;
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
   uint32_t tag = 0;
-  moe_phase<H, I, SHUF, false>(p, lds, guard, tag, ok_s, NoWait());
+  moe_phase<H, I, SHUF, false>(p, lds, guard, tag, sh.ok, NoWait());
   stamp(p.timeline, MONO_TL_DOWN);
   // every other CTA is past its last queue grab once the last one leaves: the counters
   // restart at zero
-  launch_end(p.guard, tag, [&]() { moe_reset_queues<H, I>(p); });
+  launch_end(sh, p.guard, tag, p.scratch, (uint32_t)MoeFp8Geom<H, I>::BYTES,
+             Poison{p.out, (uint32_t)p.rows * H * 2u, NAN_BF16X2},
+             Poison{p.y, (uint32_t)p.rows * H * 4u, NAN_F32},
+             [&]() { moe_reset_queues<H, I>(p); });
   stamp(p.timeline, MONO_TL_END);
 }
 

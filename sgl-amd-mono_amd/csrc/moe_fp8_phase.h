@@ -265,7 +265,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     for (int i = tid; i < MOE_NDIST; i += G::THREADS) rl.mask[i] = 0;
     if (tid == 0) ok_s = 1;
     __syncthreads();
-    tag = head_s[MONO_GUARD_EPOCH] + 1u;
+    tag = tag_after(head_s[MONO_GUARD_EPOCH]);
     guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
   }
   uint8_t* hcur = p.scratch + G::OFF_H + (tag & 1u) * G::SZ_HPAR;
@@ -901,8 +901,14 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
           const int col = f * G::DNT + row;
           const float av = bf16_lo((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
               rsrc(p.a, (uint32_t)R * H * 2u), (uint32_t)(tok * H + col) * 2u, 0, XCP));
-          p.out[tok * H + col] = (uint16_t)bf16_bits(av + ys);
-          if (p.y) p.y[tok * H + col] = ys;
+          // write-through: a failed launch's NaN fill must not meet a dirty line
+          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_bits(av + ys),
+                                                rsrc(p.out, (uint32_t)R * H * 2u),
+                                                (uint32_t)(tok * H + col) * 2u, 0, CP_DEV);
+          if (p.y)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ys),
+                                                  rsrc(p.y, (uint32_t)R * H * 4u),
+                                                  (uint32_t)(tok * H + col) * 4u, 0, CP_DEV);
         }
       }
       __syncthreads();

@@ -29,6 +29,7 @@
 
 #include "moe_common.h"
 #include "mono_abi.h"
+#include "phase.h"
 
 namespace mono {
 
@@ -158,6 +159,7 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   static_assert(G::NKS * 4 * 64 * 16 <= (int)sizeof(mid_lds), "B operand staging");
   __shared__ float wslot[MOE_MAXR * MOE_SLOTS];  // route weight of each (expert, row) slot
   __shared__ uint32_t head_s[4];
+  __shared__ LaunchShared sh;  // the launch end's role word
   __shared__ int ok_s;
 
   uint16_t* mid = reinterpret_cast<uint16_t*>(p.scratch + G::OFF_MID);
@@ -210,7 +212,7 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
     for (int i = 0; i < 4; ++i) head_s[i] = (uint32_t)head[i];
   }
   __syncthreads();
-  const uint32_t tag = head_s[MONO_GUARD_EPOCH] + 1u;
+  const uint32_t tag = tag_after(head_s[MONO_GUARD_EPOCH]);
   Guard guard;
   guard.init(p.guard, p.host_err, p.fault_site, head_s, (uint32_t)p.fault_after);
   if (w == 0) build_experts(rl, R);  // the slot tables follow the first weight loads
@@ -400,9 +402,13 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v)
             h[v] = bf16_bits((p.res ? bf16_lo(p.res[t * H + col + v]) : 0.f) + ys[v]);
-          *reinterpret_cast<uint64_t*>(p.out + t * H + col) =
-              (uint64_t)(h[0] | (h[1] << 16)) | ((uint64_t)(h[2] | (h[3] << 16)) << 32);
-          if (p.y) *reinterpret_cast<v4f*>(p.y + t * H + col) = ys;
+          // write-through: a failed launch's NaN fill must not meet a dirty line
+          const v2i hv = {(int32_t)(h[0] | (h[1] << 16)), (int32_t)(h[2] | (h[3] << 16))};
+          __builtin_amdgcn_raw_buffer_store_b64(hv, rsrc(p.out, (uint32_t)R * H * 2u),
+                                                (uint32_t)(t * H + col) * 2u, 0, CP_DEV);
+          if (p.y)
+            st16<CP_DEV>(rsrc(p.y, (uint32_t)R * H * 4u), (uint32_t)(t * H + col) * 4u,
+                         __builtin_bit_cast(v4i, ys));
         }
       }
       __syncthreads();
@@ -411,16 +417,9 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
 
   // ---------------------------------------------------------------- exit
   stamp(p.timeline, MONO_TL_DOWN);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t* gw = reinterpret_cast<uint32_t*>(p.guard);
-    drain();
-    const uint32_t old = add_dev(gw + MONO_GUARD_EXIT, 1u);
-    if (old == (uint32_t)nblk - 1u) {
-      st_dev(gw + MONO_GUARD_EXIT, 0u);
-      st_dev(gw + MONO_GUARD_EPOCH, tag);
-    }
-  }
+  launch_end(sh, p.guard, tag, p.scratch, (uint32_t)G::BYTES,
+             Poison{p.out, (uint32_t)R * H * 2u, NAN_BF16X2},
+             Poison{p.y, (uint32_t)R * H * 4u, NAN_F32}, []() {});
   stamp(p.timeline, MONO_TL_END);
 }
 

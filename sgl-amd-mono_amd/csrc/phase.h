@@ -19,10 +19,34 @@
 
 namespace mono {
 
-// CTA-shared words of a launch: the guard head as read once, and the CTA's ok flag
+// CTA-shared words of a launch: the guard head as read once, the CTA's ok flag and its
+// part in the launch's end (0: not the last CTA out, 1: last, 2: last of a failed launch)
 struct LaunchShared {
   uint32_t head[4];
   int ok;
+  int role;
+};
+
+// The launch tag after `epoch`. Tags run 1 .. 0xFFFFFFFE and then start again at 1:
+// never 0 (the tag of a pair nobody wrote or the scrub cleared), and the cycle is even,
+// so the buffers indexed by the tag's parity keep alternating across the wrap.
+__device__ inline uint32_t tag_after(uint32_t epoch) {
+  return epoch >= 0xFFFFFFFEu ? 1u : epoch + 1u;
+}
+
+// bytes of the launch's scratch the last CTA out zeroes per launch, in turn: a pair
+// left unwritten is cleared within (scratch bytes / SCRUB_CHUNK) launches, long before
+// its tag could come round again
+constexpr uint32_t SCRUB_CHUNK = 16384;
+constexpr uint32_t NAN_BF16X2 = 0x7FC07FC0u;  // two bf16 quiet NaNs
+constexpr uint32_t NAN_F32 = 0x7FC00000u;
+
+// An output a failed launch overwrites with NaN: `bytes` (a multiple of 16) of the
+// 32-bit pattern `fill`; p == nullptr: none
+struct Poison {
+  void* p;
+  uint32_t bytes;
+  uint32_t fill;
 };
 
 // Read the guard head (one coherent load, shared in LDS) and set up the guard; returns
@@ -37,23 +61,59 @@ __device__ __attribute__((always_inline)) inline uint32_t launch_begin(LaunchSha
   }
   __syncthreads();
   guard.init(gw, host_err, fault_site, sh.head, (uint32_t)fault_after);
-  return sh.head[MONO_GUARD_EPOCH] + 1u;
+  return tag_after(sh.head[MONO_GUARD_EPOCH]);
 }
 
-// The CTA leaves the launch: the last one out resets the exit counter, runs `last`
-// (state the next launch expects zero) and advances the epoch to this launch's tag.
+// The CTA leaves the launch. The last CTA out (every other CTA has drained its stores
+// and left) zeroes one SCRUB_CHUNK of the launch's scratch, and, if the launch failed
+// (the guard's abort word is set: a wait timed out in this launch or in an earlier one
+// of the same guard block, which stays set until the host resets the block), fills the
+// outputs `o0` and `o1` with NaN, so no step that failed can hand on numbers that look
+// valid, also where no host code runs between launches (a replayed graph). Every output
+// store of the launch is device coherent (sc1, write-through), so no L2 of another XCD
+// holds a dirty line that could overwrite the NaN when the kernel ends. Then thread 0
+// runs `last` (state the next launch expects zero), resets the exit counter and
+// advances the epoch to this launch's tag. Every thread calls it.
 template <class Last>
-__device__ __attribute__((always_inline)) inline void launch_end(int32_t* gw, uint32_t tag, Last last) {
+__device__ __attribute__((always_inline)) inline void launch_end(LaunchShared& sh, int32_t* gw,
+                                                                uint32_t tag, uint8_t* scratch,
+                                                                uint32_t scratch_bytes, Poison o0,
+                                                                Poison o1, Last last) {
+  uint32_t* w = reinterpret_cast<uint32_t*>(gw);
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t* w = reinterpret_cast<uint32_t*>(gw);
     drain();
     const uint32_t old = add_dev(w + MONO_GUARD_EXIT, 1u);
-    if (old == gridDim.x - 1u) {
-      last();
-      st_dev(w + MONO_GUARD_EXIT, 0u);
-      st_dev(w + MONO_GUARD_EPOCH, tag);
+    sh.role = old != gridDim.x - 1u ? 0 : (ld_dev(w + MONO_GUARD_ABORT) ? 2 : 1);
+  }
+  __syncthreads();
+  const int role = sh.role;
+  if (role == 0) return;
+  const uint32_t nchunk = (scratch_bytes + SCRUB_CHUNK - 1) / SCRUB_CHUNK;
+  if (nchunk) {
+    // past the end of the scratch the buffer resource drops the store
+    const __amdgpu_buffer_rsrc_t r = rsrc(scratch, scratch_bytes);
+    const uint32_t base = (tag % nchunk) * SCRUB_CHUNK;
+    for (uint32_t o = threadIdx.x * 16u; o < SCRUB_CHUNK; o += blockDim.x * 16u)
+      st16<CP_DEV>(r, base + o, v4i{0, 0, 0, 0});
+  }
+  if (role == 2) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const Poison& o = k ? o1 : o0;
+      if (!o.p) continue;
+      const __amdgpu_buffer_rsrc_t r = rsrc(o.p, o.bytes);
+      const int32_t f = (int32_t)o.fill;
+      for (uint32_t off = threadIdx.x * 16u; off < o.bytes; off += blockDim.x * 16u)
+        st16<CP_DEV>(r, off, v4i{f, f, f, f});
     }
+  }
+  drain();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    last();
+    st_dev(w + MONO_GUARD_EXIT, 0u);
+    st_dev(w + MONO_GUARD_EPOCH, tag);
   }
 }
 

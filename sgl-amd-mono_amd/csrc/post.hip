@@ -11,7 +11,9 @@ __global__ void __launch_bounds__(1024, 1) post_kernel(PostParams p) {
   const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
   post_phase<false>(p, lds, guard, tag, sh.ok, NoWait());
   stamp(p.timeline, MONO_TL_ROUTED);
-  launch_end(p.guard, tag, []() {});
+  launch_end(sh, p.guard, tag, p.scratch, (uint32_t)PostScratch::BYTES,
+             Poison{p.out, (uint32_t)p.rows * PO_HID * 2u, NAN_BF16X2}, Poison{nullptr, 0, 0},
+             []() {});
   stamp(p.timeline, MONO_TL_END);
 }
 

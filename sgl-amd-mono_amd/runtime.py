@@ -5,6 +5,13 @@ Mirrors the ownership of ``Glm53Runtime`` (``sgl_amd_mono/glm53/gfx950/runner.py
 the runtime allocates the hand-off scratch and the epoch/guard block once; the caller
 owns every weight, cache and step table. Launches reuse the same scratch, so launches
 of one runtime must be stream-ordered (they are: one stream per rank).
+
+Nothing here has to run between launches: each launch's last CTA clears one 16 KiB
+chunk of the scratch in turn (so no tagged pair outlives the tag cycle; the reference
+runs a scrub kernel after each step for this, deepseek_v4/gfx950/kernels/layer.py:843-895),
+and a launch that failed, or follows a failure on the same guard block, fills its outputs
+with NaN before it ends, so a replayed graph cannot turn a failed step into tokens. The
+host reads the error word when it can (``check``, ``before_launch``) and ``reset``s.
 """
 
 from __future__ import annotations
@@ -12,11 +19,6 @@ from __future__ import annotations
 import torch
 
 from . import _lib, guard
-
-# a 32-bit tag repeats after 2^32 launches: scrub the scratch every 2^30, well before
-# a stale pair could match again (the reference's scrub kernel, deepseek_v4
-# layer.py:843-895, serves the same purpose)
-SCRUB_EVERY = 1 << 30
 
 
 def shared_or_new(rt, scratch_bytes: int, device, deadline_s: float) -> "MonoRuntime":
@@ -51,7 +53,6 @@ class MonoRuntime:
             # pinned host mirror of the first failure (written by the kernel, read here
             # without a device synchronisation)
             self.host_error = torch.zeros(1, dtype=torch.int32, pin_memory=True)
-        self.launches = 0
         self.set_deadline(deadline_s)
 
     # ------------------------------------------------------------------ guard
@@ -84,13 +85,10 @@ class MonoRuntime:
             raise RuntimeError(msg)
 
     def before_launch(self) -> None:
-        """Refuse to launch after a failure; scrub the scratch before the tag wraps."""
+        """Refuse to launch after a failure (a launch would only write NaN)."""
         msg = self.failed()
         if msg:
             raise RuntimeError(f"{msg}; reset() the runtime before launching again")
-        if self.launches and self.launches % SCRUB_EVERY == 0:
-            self.reset(keep_error=False)
-        self.launches += 1
 
     def reset(self, keep_error: bool = False) -> None:
         """Zero the scratch and the guard words (the deadline stays)."""

@@ -181,11 +181,14 @@ def test_attention_deterministic_and_graph_replay(gpu):
 
 def test_attention_deadline_stops_and_reports(gpu):
     """A split's wait for its row's top-k is forced to stall from the host: it times
-    out after 5 ms, every CTA exits, the host raises, and a reset launches cleanly."""
+    out after 5 ms, every CTA exits, the output is all NaN, the host raises, and a reset
+    launches cleanly."""
     print("case attention fault injection site=topk", flush=True)
     inp = synthetic.attention_inputs(2, 4096, gpu, seed=9)
     op = AttnOp(gpu, max_rows=2, ctx_max=4096, deadline_s=0.005, fault=(5, 0))
-    op.launch(inp)
+    bad = op.launch(inp)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad.float()).all()
     with pytest.raises(RuntimeError, match="topk"):
         op.rt.check()
     words = op.rt.guard.cpu().tolist()

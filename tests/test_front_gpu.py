@@ -228,7 +228,8 @@ def test_front_deterministic_and_graph_replay(gpu, front_w):
 
 def test_front_deadline_stops_and_reports(gpu, front_w):
     """A row task's wait for the stage-A outputs is forced to stall from the host: it
-    times out after 5 ms, every CTA exits, the host raises, and a reset launches cleanly."""
+    times out after 5 ms, every CTA exits, q and the index head weights are all NaN, the
+    host raises, and a reset launches cleanly."""
     w, _ = front_w
     print(f"case front fault injection site=front_a layout={w.layout}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(4)
@@ -237,7 +238,9 @@ def test_front_deadline_stops_and_reports(gpu, front_w):
     pos = torch.tensor([10, 20], dtype=torch.int64, device=gpu)
     sl = torch.tensor([10, 20], dtype=torch.int64, device=gpu)
     op = FrontOp(w, gpu, max_rows=2, deadline_s=0.005, fault=(8, 0))
-    op.launch(h, caches, pos, sl)
+    bad = op.launch(h, caches, pos, sl)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad.q.float()).all() and torch.isnan(bad.iw).all()
     with pytest.raises(RuntimeError, match="timed out at front_a "):
         op.rt.check()
     words = op.rt.guard.cpu().tolist()

@@ -249,14 +249,17 @@ def test_one_launch_layer_graph_replay_matches_eager(gpu):
 def test_one_launch_layer_deadline_stops_and_reports(gpu, site):
     """A wait forced to stall from the host (the phase barrier, a split's top-k wait, a mid
     quant's wait): it times out after 5 ms, every CTA runs to the end of the launch, the
-    host raises naming the site, and a reset runtime launches cleanly."""
+    output is all NaN, the host raises naming the site, and a reset runtime launches
+    cleanly."""
     from sgl_amd_mono_amd import _lib
 
     print(f"case one-launch layer fault injection site={site}", flush=True)
     rows = 2
     w, caches, step, h = synthetic.layer(rows, 4096, gpu, seed=43)
     op = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096, deadline_s=0.005, fault=(site, 0))
-    op.launch(h, caches, step)
+    bad = op.launch(h, caches, step)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad.float()).all()
     with pytest.raises(RuntimeError, match=f"timed out at {_lib.SITES[site]} "):
         op.check()
     words = op.rt.guard.cpu().tolist()
@@ -269,3 +272,76 @@ def test_one_launch_layer_deadline_stops_and_reports(gpu, site):
     ref = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096).launch(h, caches, step)
     torch.cuda.synchronize()
     assert torch.equal(clean, ref)
+
+
+def test_one_launch_layer_fail_stop_inside_graph_replay(gpu):
+    """Fail-stop with no host code between launches: the one-launch layer captured in a
+    graph whose wait for the top-k is armed, through fault injection set from the host, to
+    stall from the launch that starts at epoch 4 on. Replays 1-3 equal the eager output;
+    replay 4 times out after 5 ms, its output is all NaN and the pinned error word names
+    the site; replay 5 is all NaN again (the abort word stays set); after a reset the same
+    graph replays cleanly."""
+    from sgl_amd_mono_amd import _lib
+
+    print("case one-launch layer fail-stop in graph replay rows=2 ctx=4096", flush=True)
+    rows = 2
+    w, caches, step, h = synthetic.layer(rows, 4096, gpu, seed=44)
+    ref = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096).launch(h, caches, step).clone()
+    site = next(k for k, v in _lib.SITES.items() if v == "topk")
+    op = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096, deadline_s=0.005, fault=(site, 4))
+    out = torch.empty_like(ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op.launch(h, caches, step, out=out)  # epoch 0 -> 1
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        op.launch(h, caches, step, out=out)
+    for i in range(5):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        if i < 3:
+            assert torch.equal(out, ref), f"replay {i}"
+            assert int(op.rt.host_error[0]) == 0
+        else:
+            assert torch.isnan(out.float()).all(), f"replay {i}"
+            assert int(op.rt.host_error[0]) == site + 1
+    words = op.rt.guard.cpu().tolist()
+    assert words[3] == site + 1 and words[7] == 1
+    op.rt.reset()
+    out.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    op.check()
+
+
+def test_one_launch_layer_across_the_tag_wrap(gpu):
+    """Launch tags run 1 .. 2^32 - 2 and start again at 1. With the epoch set just short of
+    the end of the cycle (on a cleared scratch, as the scrub leaves a pair that old), four
+    launches cross the wrap, each bit-equal to a fresh runtime's output, and the epoch ends
+    at 3. After each launch the 16 KiB chunk of scratch its last CTA cleared (tag mod the
+    number of chunks) reads zero."""
+    from sgl_amd_mono_amd import _lib
+
+    print("case one-launch layer tag wrap rows=2 ctx=4096", flush=True)
+    rows = 2
+    w, caches, step, h = synthetic.layer(rows, 4096, gpu, seed=45)
+    ref = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096).launch(h, caches, step).clone()
+    op = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=4096)
+    op.rt.reset()
+    op.rt.guard[0] = 0xFFFFFFFD - (1 << 32)  # epoch 2^32 - 3 as an int32 word
+    nchunk = -(-_lib.lib().mono_layer_scratch_bytes(rows) // 16384)
+    for want_tag in (0xFFFFFFFE, 1, 2, 3):
+        got = op.launch(h, caches, step).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), hex(want_tag)
+        assert int(op.rt.guard[0]) & 0xFFFFFFFF == want_tag
+        c = want_tag % nchunk
+        chunk = op.rt.scratch[c * 16384:(c + 1) * 16384]
+        assert int(chunk.count_nonzero()) == 0, (hex(want_tag), c)
+    op.check()

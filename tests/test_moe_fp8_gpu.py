@@ -149,12 +149,14 @@ def test_moe_fp8_graph_replay_matches_eager(layer, gpu):
 
 def test_moe_fp8_deadline_stops_and_reports(layer, gpu):
     """Fault injection from the host: the mid-quant wait never completes, so it times
-    out after a 5 ms deadline; every CTA still exits, the host raises, and a reset
-    runtime launches cleanly again."""
+    out after a 5 ms deadline; every CTA still exits, the output is all NaN, the host
+    raises, and a reset runtime launches cleanly again."""
     print("case fault injection site=mid", flush=True)
     a = synthetic.rows_bf16(2, H, gpu, seed=3)
     op = MoeFp8Op(layer, gpu, max_rows=16, deadline_s=0.005, fault=(2, 0))
-    op.launch(a)
+    bad = op.launch(a)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad.float()).all()
     with pytest.raises(RuntimeError, match="mid"):
         op.rt.check()
     with pytest.raises(RuntimeError):

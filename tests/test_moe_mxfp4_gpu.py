@@ -138,13 +138,15 @@ def test_moe_mxfp4_graph_replay_matches_eager(mx_aiter, gpu):
 
 def test_moe_mxfp4_deadline_stops_and_reports(mx_rowmajor, gpu):
     """The down stage's wait for the mid tiles is forced to stall from the host; it
-    times out after 5 ms, every CTA exits, the host raises, and a reset runtime launches
-    cleanly again."""
+    times out after 5 ms, every CTA exits, the output is all NaN, the host raises, and a
+    reset runtime launches cleanly again."""
     print("case mxfp4 fault injection site=mid", flush=True)
     x = synthetic.rows_bf16(2, H, gpu, seed=3)
     logits = synthetic.logits_f32(2, E, gpu, seed=3)
     op = MoeMxfp4Op(mx_rowmajor, gpu, max_rows=16, deadline_s=0.005, fault=(2, 0))
-    op.launch(x, logits)
+    bad = op.launch(x, logits)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad.float()).all()
     with pytest.raises(RuntimeError, match="mid"):
         op.rt.check()
     words = op.rt.guard.cpu().tolist()

@@ -84,12 +84,15 @@ def test_post_deterministic_and_graph_replay(gpu, post_w):
 
 def test_post_deadline_stops_and_reports(gpu, post_w):
     """o_proj's wait for the W_UV outputs is forced to stall from the host: it times out
-    after 5 ms, every CTA exits, the host raises, and a reset launches cleanly."""
+    after 5 ms, every CTA exits, the output is all NaN, the host raises, and a reset
+    launches cleanly."""
     w, _ = post_w
     print(f"case post fault injection site=o layout={w.layout}", flush=True)
     o_lat, h = _inputs(2, gpu, seed=9)
     op = PostOp(w, gpu, max_rows=2, deadline_s=0.005, fault=(7, 0))
-    op.launch(o_lat, h)
+    bad = op.launch(o_lat, h)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad.float()).all()
     with pytest.raises(RuntimeError, match="timed out at o "):
         op.rt.check()
     words = op.rt.guard.cpu().tolist()
