@@ -55,6 +55,7 @@ typedef void* mono_stream_t;
 #define MONO_SITE_QAN 9      /* q_b / W_iq wait on the normalised q_a */
 #define MONO_SITE_QB 10      /* W_UK / the index query wait on q_b / W_iq outputs */
 #define MONO_SITE_PHASE 11   /* a phase of the layer launch waits for the phase before it */
+#define MONO_SITE_BLOCKS 12  /* a long row's final top-k waits on its blocks' selections */
 
 int mono_version(void);
 const char* mono_last_error(void);
@@ -225,7 +226,7 @@ typedef struct {
   int32_t index_heads;   /* 64 */
   int32_t topk;          /* 2048 */
   int32_t page;          /* 64 */
-  int32_t ctx_max;       /* keys a row may see at most (positions clamp to it): 1..32768;
+  int32_t ctx_max;       /* keys a row may see at most (positions clamp to it): 1..163840;
                             the row stride of `scores` */
   int32_t pt_stride;     /* page_table row stride (entries), >= ceil(ctx_max / 64) */
   int32_t pt_rows;       /* page_table rows */
@@ -374,7 +375,7 @@ typedef struct {
   int32_t inter;         /* 512 */
   int32_t experts;       /* 256 */
   int32_t layout;        /* MONO_LAYOUT_* of every FP8 weight */
-  int32_t ctx_max;       /* keys a row may see at most, 1..32768 */
+  int32_t ctx_max;       /* keys a row may see at most, 1..163840 */
   int32_t pt_stride;     /* page_table row stride */
   int32_t pt_rows;       /* page_table rows */
   int32_t rope_rows;     /* rows of cos / sin */

@@ -3,14 +3,14 @@
 
 namespace mono {
 
-template <int SPLIT>
+template <int SPLIT, bool LONG>
 __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[AT_LDS_BYTES];
   __shared__ LaunchShared sh;
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
   const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
-  attn_phase<SPLIT, false>(p, lds, guard, tag, sh.ok, NoWait());
+  attn_phase<SPLIT, false, LONG>(p, lds, guard, tag, sh.ok, NoWait());
   stamp(p.timeline, MONO_TL_DOWN);
   launch_end(sh, p.guard, tag, p.scratch, (uint32_t)AttnScratch(p.rows_max).bytes,
              Poison{p.out, (uint32_t)p.rows * AT_HEADS * AT_LAT * 2u, NAN_BF16X2},
@@ -35,7 +35,7 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
     return set_error(MONO_E_ARG, "mono_attn_launch: built for 32 heads, 64 index heads, "
                                  "top-2048 and 64-token pages");
   if (a->ctx_max < 1 || a->ctx_max > AT_MAXCTX)
-    return set_error(MONO_E_ARG, "mono_attn_launch: ctx_max must be 1..32768");
+    return set_error(MONO_E_ARG, "mono_attn_launch: ctx_max must be 1..163840");
   if (a->pt_stride < (a->ctx_max + AT_PAGE - 1) / AT_PAGE || a->pt_rows < 1 ||
       (uint64_t)a->pt_rows * a->pt_stride * 4 > 0x7FFFFFFFull)
     return set_error(MONO_E_ARG, "mono_attn_launch: page table rows shorter than ctx_max");
@@ -84,7 +84,10 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
   int rc = monokernel_grid(&grid);
   if (rc) return rc;
   // 64-key splits when the rows' 32 splits each take one CTA, else 128-key splits
-  auto kern = p.rows * (AT_TOPK / 64) <= grid ? attn_kernel<64> : attn_kernel<128>;
+  // rows that may span more than one top-k block take the multi-block variant
+  const bool s64 = p.rows * (AT_TOPK / 64) <= grid, lng = p.ctx_max > AT_TKBLOCK;
+  auto kern = s64 ? (lng ? attn_kernel<64, true> : attn_kernel<64, false>)
+                  : (lng ? attn_kernel<128, true> : attn_kernel<128, false>);
   rc = check_coresident(kern, AT_THREADS, 0,
                         "mono_attn_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;

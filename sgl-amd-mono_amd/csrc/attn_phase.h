@@ -8,11 +8,13 @@
 //      E8M0 scales (query rows = heads, key columns = tokens, K = the 128 dims); relu,
 //      the head weights and the sum over heads stay in the lane, then two permlane
 //      swaps sum the lane groups. Scores go to scratch; the chunk's done word follows.
-//   2  top-k: task = row (topk_lds.h): thread t holds the radix keys of positions
-//      32 t .. in registers; a sample narrows the range, histograms over the live range
-//      keep the bin of the 2048th key until its few candidates rank themselves; the
-//      selection (every element up to the threshold element of the order key
-//      descending, position ascending) is published as (position, tag) pairs.
+//   2  top-k: task = (row, 32768-key block) (topk_lds.h): thread t holds the radix keys
+//      of block positions 32 t .. in registers; a sample narrows the range, histograms
+//      over the live range keep the bin of the 2048th key until its few candidates rank
+//      themselves; the selection (every element up to the threshold element of the order
+//      key descending, position ascending) is published as (position, tag) pairs. A row
+//      longer than one block publishes each block's selection as candidates with their
+//      keys, and one more task ranks the candidates of the row's blocks the same way.
 //   3  split: task (row, SPLIT-key split), all 32 heads (SPLIT 64 when the rows' 32
 //      splits each fill the grid once, else 128). The split's tokens (through the
 //      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
@@ -61,6 +63,8 @@ struct AttnScratch {
   size_t scores;      // f32 [rm][MAXCTX]
   size_t score_done;  // u32 [rm][NCHUNK]
   size_t topk;        // the selection as (position, tag) pairs [rm][TOPK]
+  size_t cand;        // a long row's block selections: u64 (position | key << 32) [rm][MAXBLK][TOPK]
+  size_t blk_done;    // u32 [rm][MAXBLK]
   size_t acc;         // f32 [rm][split][h][512]
   size_t ml;          // f32 [rm][split][h][2]
   size_t split_done;  // u32 [rm][split]
@@ -70,7 +74,9 @@ struct AttnScratch {
     scores = 0;
     score_done = at_align(scores + r * AT_MAXCTX * 4);
     topk = at_align(score_done + r * AT_NCHUNK * 4);
-    acc = at_align(topk + r * AT_TOPK * 8);
+    cand = at_align(topk + r * AT_TOPK * 8);
+    blk_done = at_align(cand + r * AT_MAXBLK * AT_TOPK * 8);
+    acc = at_align(blk_done + r * AT_MAXBLK * 4);
     ml = at_align(acc + r * AT_NSPLIT * AT_HEADS * AT_LAT * 4);
     split_done = at_align(ml + r * AT_NSPLIT * AT_HEADS * 8);
     bytes = at_align(split_done + r * AT_NSPLIT * 4);
@@ -120,12 +126,14 @@ constexpr int AT_LDS_WSP = AT_LDS_MM + 16;                  // f32 [NSPLIT]
 constexpr int AT_LDS_LINV = AT_LDS_WSP + AT_NSPLIT * 4;     // f32
 constexpr int AT_LDS_BYTES = AT_LDS_LINV + 16;
 
-// The attention phase (stages 1-4) in one CTA of a launch. FUSED: it runs after the front
+// The attention phase (stages 1-4) in one CTA of a launch. LONG: rows may span more than
+// one top-k block (a context bound above AT_TKBLOCK); the launch picks it, so a launch
+// within one block carries none of the multi-block code. FUSED: it runs after the front
 // in the same launch, so its inputs (q, iq, iqs, iw and the rows' own cache entries) are
 // read device-coherent, after `ready` (the front's barrier), which it calls once, after
 // its first index-page loads are in flight. Always inlined: it is instantiated in more
 // than one kernel, and as a real call it would spill around the call.
-template <int SPLIT, bool FUSED, class Ready>
+template <int SPLIT, bool FUSED, bool LONG, class Ready>
 __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParams& p,
                                                                  uint8_t* lds, Guard& guard,
                                                                  uint32_t tag, int& ok_s,
@@ -150,6 +158,8 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   float* scores = reinterpret_cast<float*>(p.scratch + S.scores);
   uint32_t* score_done = reinterpret_cast<uint32_t*>(p.scratch + S.score_done);
   uint64_t* topk = reinterpret_cast<uint64_t*>(p.scratch + S.topk);
+  uint64_t* cands = reinterpret_cast<uint64_t*>(p.scratch + S.cand);
+  uint32_t* blk_done = reinterpret_cast<uint32_t*>(p.scratch + S.blk_done);
   float* accs = reinterpret_cast<float*>(p.scratch + S.acc);
   float* mls = reinterpret_cast<float*>(p.scratch + S.ml);
   uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S.split_done);
@@ -178,13 +188,14 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   const __amdgpu_buffer_rsrc_t rpsc = rsrc(p.plane_scale, p.plane_pages * 256u);
 
   // XCD-local placement (up to 8 rows on 256 CTAs; the hardware hands CTA b to XCD b % 8):
-  // row r's 32 score tasks, its top-k (CTA r), its 32 splits and its 32 merges all run on
-  // XCD r, so the scores, the row's q and the split partials each cross HBM once and are
-  // then read from that XCD's L2. Each stage has 32 tasks a row: CTA b takes task b / 8
-  // of row b % 8. Otherwise task t is task t % 32 of row t / 32, CTA b taking t = b, b +
-  // grid, ...
+  // row r's score tasks, its top-k tasks, its 32 splits and its 32 merges all run on XCD r,
+  // so the scores, the row's q and the split partials each cross HBM once and are then read
+  // from that XCD's L2: task t of a stage belongs to row t % 8 (`rs8` = 8). Otherwise task
+  // t of a 32-task-a-row stage is task t % 32 of row t / 32, and a stage with a run-time
+  // task count numbers row-fastest (`rs8` = rows). CTA b takes tasks b, b + grid, ...
   const bool xcd = R <= 8 && nblk == 8 * 32;
   const int ntask32 = xcd ? nblk : R * 32;
+  const int rs8 = xcd ? 8 : R;
   auto task_of = [&](int t, int& r, int& i) {
     r = xcd ? (t & 7) : t / 32;
     i = xcd ? (t >> 3) : t % 32;
@@ -194,11 +205,11 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   // Each stage takes the thread index through an opaque copy: conditions on it are then
   // computed inside the stage, not hoisted to the kernel's top where they would hold
   // registers through every stage.
-  static_assert(AT_NCHUNK == 32, "32 score tasks a row");
-  for (int task = b; task < ntask32; task += nblk) {
+  // tasks (row, 1024-key chunk), as many chunks a row as the launch's context bound needs
+  const int nchr = (p.ctx_max + AT_CHUNK - 1) / AT_CHUNK;
+  for (int task = b; task < rs8 * nchr; task += nblk) {
     const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-    int r, c;
-    task_of(task, r, c);
+    const int r = task % rs8, c = task / rs8;
     if (r >= R) continue;
     const int n = row_n(r);
     if (c * AT_CHUNK >= n) continue;
@@ -280,38 +291,131 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
 
   // ---------------------------------------------------------------- 2: top-k
   stamp(p.timeline, MONO_TL_STAGED);
-  for (int r = b; r < (ok ? R : 0); r += nblk) {
-    const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-    const int n = row_n(r);
+  // a row's selection as (position, tag) pairs, and the caller's copy of it
+  auto publish = [&](int tid, int r, const int32_t* sel_l) {
     uint64_t* sel = topk + (size_t)r * AT_TOPK;
-    if (n <= AT_TOPK) {
-      // every key of the row, in position order
-      for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
-        if (i < n) st_dev64(sel + i, pair((uint32_t)i, tag));
-        if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = i < n ? i : -1;
-      }
-    } else {
-      const int nch = (n + AT_CHUNK - 1) / AT_CHUNK;
-      if (w == 0)
-        ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
-          return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + l]) == tag);
-        });
-      if (tid == 0) {  // topk_select's minimum / maximum words, set before the barrier
-        mm_s[0] = 0xFFFFFFFFu;
-        mm_s[1] = 0u;
-      }
-      ok = cta_all(ok, ok_s);
-      if (ok) {
-        const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
-        const int32_t* sel_l = topk_select(tid, rs, n, smem, wsum, mm_s, res_s);
+    for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
+      const int v = sel_l[i];
+      st_dev64(sel + i, pair((uint32_t)v, tag));
+      if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = v;
+    }
+  };
+  if constexpr (!LONG) {
+    // every row within one block: task = row (XCD-local: row r on CTA r)
+    for (int r = b; r < (ok ? R : 0); r += nblk) {
+      const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
+      const int n = row_n(r);
+      if (n <= AT_TOPK) {
+        // every key of the row, in position order
+        uint64_t* sel = topk + (size_t)r * AT_TOPK;
         for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
-          const int v = sel_l[i];
-          st_dev64(sel + i, pair((uint32_t)v, tag));
-          if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = v;
+          if (i < n) st_dev64(sel + i, pair((uint32_t)i, tag));
+          if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = i < n ? i : -1;
+        }
+      } else {
+        const int nch = (n + AT_CHUNK - 1) / AT_CHUNK;
+        if (w == 0)
+          ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
+            return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + l]) == tag);
+          });
+        if (tid == 0) {  // topk_select's minimum / maximum words, set before the barrier
+          mm_s[0] = 0xFFFFFFFFu;
+          mm_s[1] = 0u;
+        }
+        ok = cta_all(ok, ok_s);
+        if (ok) {
+          const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
+          publish(tid, r, topk_select(tid, rs, n, smem, wsum, mm_s, res_s));
         }
       }
+      __syncthreads();  // the LDS arena is reused by the next row
     }
-    __syncthreads();  // the LDS arena is reused by the next row
+  } else {
+    const int nbr = (p.ctx_max + AT_TKBLOCK - 1) / AT_TKBLOCK;  // blocks of the longest row
+    // tasks: (row, block) for every block of the longest row, then one final task a row.
+    // Every final task comes after every block task in the numbering, so no CTA waits on
+    // a task it has yet to run.
+    for (int task = b; task < (ok ? rs8 * (nbr + 1) : 0); task += nblk) {
+      const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
+      const int r = task % rs8, blk = task / rs8;
+      if (r >= R) continue;
+      const int n = row_n(r);
+      // blocks of this row (a row seeing no key has one, empty: its selection is all -1)
+      const int nb = n > AT_TKBLOCK ? (n + AT_TKBLOCK - 1) / AT_TKBLOCK : 1;
+      if (blk < nbr) {
+        // ---- a block task
+        if (blk >= nb) continue;
+        const int b0 = blk * AT_TKBLOCK;
+        const int nk = n - b0 < AT_TKBLOCK ? n - b0 : AT_TKBLOCK;
+        const bool last = nb == 1;  // the block's selection is the row's
+        if (last && n <= AT_TOPK) {
+          uint64_t* sel = topk + (size_t)r * AT_TOPK;
+          for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
+            if (i < n) st_dev64(sel + i, pair((uint32_t)i, tag));
+            if (p.topk_out) p.topk_out[(size_t)r * AT_TOPK + i] = i < n ? i : -1;
+          }
+        } else {
+          const int nch = (nk + AT_CHUNK - 1) / AT_CHUNK;
+          const int c0 = b0 / AT_CHUNK;
+          if (w == 0)
+            ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
+              return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + c0 + l]) == tag);
+            });
+          if (tid == 0) {
+            mm_s[0] = 0xFFFFFFFFu;
+            mm_s[1] = 0u;
+          }
+          ok = cta_all(ok, ok_s);
+          if (!ok) break;
+          const __amdgpu_buffer_rsrc_t rs =
+              rsrc(scores + (size_t)r * AT_MAXCTX + b0, (uint32_t)nk * 4);
+          uint64_t* cand = cands + ((size_t)r * AT_MAXBLK + blk) * AT_TOPK;
+          if (nk > AT_TOPK) {
+            const int32_t* sel_l = topk_select(tid, rs, nk, smem, wsum, mm_s, res_s);
+            if (last) {
+              publish(tid, r, sel_l);
+            } else {
+              for (int i = tid; i < AT_TOPK; i += AT_THREADS) {
+                const int v = sel_l[i];
+                st_dev64(cand + i, (uint64_t)(uint32_t)(b0 + v) |
+                                       ((uint64_t)topk_key_at(smem, v) << 32));
+              }
+            }
+          } else {
+            // a short last block: every key is a candidate (keys as topk_select makes them)
+            for (int i = tid; i < nk; i += AT_THREADS) {
+              const uint32_t k = radix_key(__int_as_float(ld4<CP_NONE>(rs, (uint32_t)i * 4u)));
+              st_dev64(cand + i, (uint64_t)(uint32_t)(b0 + i) | ((uint64_t)(k > 1u ? k : 1u) << 32));
+            }
+          }
+          if (!last) {
+            drain();
+            __syncthreads();
+            if (tid == 0) st_dev(&blk_done[r * AT_MAXBLK + blk], tag);
+          }
+        }
+      } else {
+        // ---- the final task of a row spanning several blocks
+        if (nb < 2) continue;
+        const int nl = n - (nb - 1) * AT_TKBLOCK;
+        const int C = AT_TOPK * (nb - 1) + (nl < AT_TOPK ? nl : AT_TOPK);
+        if (w == 0)
+          ok = wait_until(guard, MONO_SITE_BLOCKS, [&]() {
+            return __all(l >= nb || ld_dev(&blk_done[r * AT_MAXBLK + l]) == tag);
+          });
+        if (tid == 0) {
+          mm_s[0] = 0xFFFFFFFFu;
+          mm_s[1] = 0u;
+        }
+        ok = cta_all(ok, ok_s);
+        if (!ok) break;
+        const __amdgpu_buffer_rsrc_t rc =
+            rsrc(cands + (size_t)r * AT_MAXBLK * AT_TOPK, (uint32_t)C * 8u);
+        publish(tid, r,
+                topk_final<AT_MAXBLK * AT_TOPK / AT_THREADS>(tid, rc, C, smem, wsum, mm_s, res_s));
+      }
+      __syncthreads();  // the LDS arena is reused by the next task
+    }
   }
 
   // ---------------------------------------------------------------- 3: split
@@ -322,7 +426,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     constexpr int KSTR = AT_KV + 16, QSTR = AT_KV * 2 + 16, SSTR = SPLIT + 4,
                   PSTR = SPLIT * 2 + 16;
     constexpr int NSB = SPLIT == 64 ? 2 : 1;  // S buffers: the two K chains (64), or summed
-    constexpr int NPG = AT_MAXCTX / AT_PAGE;
+    constexpr int NPG = (LONG ? AT_MAXCTX : AT_TKBLOCK) / AT_PAGE;
     uint8_t* kbuf = smem;
     uint8_t* qbuf = kbuf + SPLIT * KSTR;
     float* sbuf = reinterpret_cast<float*>(qbuf + AT_HEADS * QSTR);
@@ -334,7 +438,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
                           SPLIT * 8 + NPG * 4 <=
                       TOPK_ARENA_WORDS * 4,
                   "split LDS");
-    static_assert(NPG <= AT_THREADS, "a page-table entry a thread");
+    constexpr int NPT = (NPG + AT_THREADS - 1) / AT_THREADS;  // page-table entries a thread
     constexpr int QP = AT_HEADS * AT_KV / 8;  // 16-byte pieces of a row's q
     constexpr int NQP = (QP + AT_THREADS - 1) / AT_THREADS;
     const __amdgpu_buffer_rsrc_t rkv = rsrc(p.kv, p.kv_slots * (uint32_t)AT_KV);
@@ -364,9 +468,14 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         qv[i] = ld16<XCP>(rq, pc < QP ? (uint32_t)pc * 16u : 0x80000000u);
       }
       const int npg = (n + AT_PAGE - 1) / AT_PAGE;
-      const int pgv = ld4<CP_NONE>(
-          rpt, tid < npg ? ((uint32_t)p.req_ids[r] * (uint32_t)p.pt_stride + (uint32_t)tid) * 4u
-                         : 0x80000000u);
+      int pgv[NPT];
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        const int pi = tid + AT_THREADS * i;
+        pgv[i] = ld4<CP_NONE>(
+            rpt, pi < npg ? ((uint32_t)p.req_ids[r] * (uint32_t)p.pt_stride + (uint32_t)pi) * 4u
+                          : 0x80000000u);
+      }
       // the split's tokens, polled as (position, tag) pairs
       int pos = -1;
       if (tid < SPLIT) {
@@ -384,7 +493,9 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         if (pc < QP)
           *reinterpret_cast<v4i*>(qbuf + (pc / (AT_KV / 8)) * QSTR + (pc % (AT_KV / 8)) * 16) = qv[i];
       }
-      if (tid < NPG) pt_s[tid] = pgv;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i)
+        if (tid + AT_THREADS * i < NPG) pt_s[tid + AT_THREADS * i] = pgv[i];
       ok = cta_all(ok, ok_s);
       if (!ok) break;
       // position -> cache slot through the page table in LDS

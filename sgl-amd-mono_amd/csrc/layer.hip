@@ -66,7 +66,7 @@ struct LayerParams {
 // layer timeline marks: start, each phase's end, exit
 constexpr int LY_TL_FRONT = 1, LY_TL_ATTN = 2, LY_TL_POST = 3, LY_TL_MOE = 4, LY_TL_END = 5;
 
-template <bool SHUF, int SPLIT>
+template <bool SHUF, int SPLIT, bool LONG>
 __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[LY_LDS_BYTES];
   __shared__ LaunchShared sh;
@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
   front_phase(p.f, lds, guard, tag, sh.ok);
   p.bar[0].arrive(tag);
   stamp(p.timeline, LY_TL_FRONT);
-  attn_phase<SPLIT, true>(p.at, lds, guard, tag, sh.ok,
+  attn_phase<SPLIT, true, LONG>(p.at, lds, guard, tag, sh.ok,
                           BarrierWait{&p.bar[0], &guard, tag, MONO_SITE_PHASE, &sh.ok});
   p.bar[1].arrive(tag);
   stamp(p.timeline, LY_TL_ATTN);
@@ -113,7 +113,7 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   if (a->layout != MONO_LAYOUT_ROWMAJOR && a->layout != MONO_LAYOUT_AITER16)
     return set_error(MONO_E_ARG, "mono_layer_launch: unknown weight layout");
   if (a->ctx_max < 1 || a->ctx_max > AT_MAXCTX)
-    return set_error(MONO_E_ARG, "mono_layer_launch: ctx_max must be 1..32768");
+    return set_error(MONO_E_ARG, "mono_layer_launch: ctx_max must be 1..163840");
   if (a->pt_stride < (a->ctx_max + AT_PAGE - 1) / AT_PAGE || a->pt_rows < 1 ||
       (uint64_t)a->pt_rows * a->pt_stride * 4 > 0x7FFFFFFFull)
     return set_error(MONO_E_ARG, "mono_layer_launch: page table rows shorter than ctx_max");
@@ -293,8 +293,15 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
     return set_error(MONO_E_DEVICE, "mono_layer_launch: needs 224..1024 CUs (and 168 + 4 rows)");
   // 64-key splits when the rows' 32 splits each take one CTA, else 128-key splits
   const bool s64 = R * (AT_TOPK / 64) <= grid;
-  auto kern = shuf ? (s64 ? layer_kernel<true, 64> : layer_kernel<true, 128>)
-                   : (s64 ? layer_kernel<false, 64> : layer_kernel<false, 128>);
+  // rows that may span more than one top-k block take the multi-block variant
+  const bool lng = a->ctx_max > AT_TKBLOCK;
+  using K = void (*)(LayerParams);
+  const K kerns[2][2][2] = {
+      {{layer_kernel<false, 128, false>, layer_kernel<false, 128, true>},
+       {layer_kernel<false, 64, false>, layer_kernel<false, 64, true>}},
+      {{layer_kernel<true, 128, false>, layer_kernel<true, 128, true>},
+       {layer_kernel<true, 64, false>, layer_kernel<true, 64, true>}}};
+  const K kern = kerns[shuf][s64][lng];
   rc = check_coresident(kern, 1024, 0, "mono_layer_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);

@@ -2,6 +2,12 @@
 // Rule (sgl_amd_mono/glm53/gfx950/kernel.py:3002-3636; glm53/check.py:94-117): rank by
 // the radix order key of the f32 score bits, larger first, ties to the lower position;
 // the selection in ascending position order.
+//
+// A row of up to AT_TKBLOCK keys is ranked by one CTA (topk_select). A longer row is cut
+// into blocks of AT_TKBLOCK keys, each ranked by a CTA of its own; since every element of
+// the row's top-TOPK is in its own block's top-TOPK (fewer than TOPK elements of the row,
+// so of the block, rank above it), one more CTA ranks the blocks' selections (topk_final)
+// and its result is exactly the row's.
 #pragma once
 
 #include <type_traits>
@@ -11,7 +17,9 @@
 namespace mono {
 
 constexpr int AT_TOPK = 2048;
-constexpr int AT_MAXCTX = 32768;  // keys a row may see (the LDS image)
+constexpr int AT_TKBLOCK = 32768;  // keys one CTA ranks (its LDS image): a block
+constexpr int AT_MAXBLK = 5;       // blocks a row may span
+constexpr int AT_MAXCTX = AT_TKBLOCK * AT_MAXBLK;  // keys a row may see: 163840
 constexpr int AT_THREADS = 1024;
 constexpr int AT_WAVES = AT_THREADS / WAVE;
 constexpr int CAND = 256;  // a threshold bin this small is ranked directly
@@ -194,7 +202,7 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
   __syncthreads();
 }
 
-// The exact top-TOPK of one row's n scores (TOPK < n <= 32768), in LDS: returns the
+// The exact top-TOPK of one block's n scores (TOPK < n <= AT_TKBLOCK), in LDS: returns the
 // selected positions in ascending order (sel[0 .. TOPK)). Ranked by the radix key of
 // the f32 score, larger first, ties to the lower position. `rs` covers the n scores (f32,
 // read through L2: the caller has seen their done words, and within the launch the
@@ -222,7 +230,7 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_select(
   // [TOPK], past the candidates and masks of topk_refine (dead when it is written)
   int32_t* sel = reinterpret_cast<int32_t*>(hist + 3 * CAND + AT_THREADS);
   static_assert(3 * CAND + AT_THREADS + AT_TOPK <= 4096, "the selection fits the histogram");
-  constexpr int NLD = AT_MAXCTX / 4 / AT_THREADS;
+  constexpr int NLD = AT_TKBLOCK / 4 / AT_THREADS;
   v4i raw[NLD];
 #pragma unroll
   for (int q = 0; q < NLD; ++q) raw[q] = ld16<CP_NONE>(rs, (uint32_t)(4 * (tid + AT_THREADS * q)) * 4);
@@ -280,6 +288,57 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_select(
   topk_refine<32>(tid, key, [&](int j) { return 32 * tid + j; }, kmin, kmax, n, cut, sampled,
                   hist, wsum, phase, res_s, sel);
   mark(7);
+  return sel;
+}
+
+// After topk_select: the order key it ranked block position `pos` by (its LDS image)
+__device__ inline uint32_t topk_key_at(const uint8_t* arena, int pos) {
+  return reinterpret_cast<const uint32_t*>(arena)[(pos >> 5) * 33 + (pos & 31)];
+}
+
+// The exact top-TOPK of a row that spans several blocks, from the C candidates of its
+// blocks' selections: `rc` covers them as u64 (position | order key << 32), block after
+// block and each block's in ascending position order, so the whole list is in ascending
+// position order. Thread t holds candidates NK t .. NK t + NK - 1 (past C: key 0, below
+// every real key, which is >= 1); topk_refine ranks them as topk_select ranks a block.
+// Their positions wait in LDS past the histogram (a register array indexed at run time
+// would live in scratch memory). `mm` is set to ~0 and 0 by the caller before its last
+// barrier. Returns the selected positions of the row, ascending, at sel[0 .. TOPK).
+template <int NK>
+__device__ __attribute__((always_inline)) inline int32_t* topk_final(
+    int tid, __amdgpu_buffer_rsrc_t rc, int C, uint8_t* arena, int* wsum, uint32_t* mm,
+    int* res_s) {
+  static_assert(NK * AT_THREADS >= AT_MAXBLK * AT_TOPK, "every candidate has a thread");
+  int phase = 0;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(arena);
+  int32_t* sel = reinterpret_cast<int32_t*>(hist + 3 * CAND + AT_THREADS);
+  int32_t* cpos = reinterpret_cast<int32_t*>(hist + 4096);  // [NK x 1024]
+  static_assert((4096 + NK * AT_THREADS) * 4 <= TOPK_ARENA_WORDS * 4, "positions fit the arena");
+  v2i raw[NK];
+#pragma unroll
+  for (int j = 0; j < NK; ++j) raw[j] = ld8<CP_DEV>(rc, (uint32_t)(NK * tid + j) * 8u);
+  reinterpret_cast<v4i*>(hist)[tid] = v4i{0, 0, 0, 0};  // select_pass expects it zero
+  uint32_t key[NK];
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    cpos[NK * tid + j] = raw[j][0];
+    const uint32_t k = NK * tid + j < C ? (uint32_t)raw[j][1] : 0u;
+    key[j] = k;
+    kmin = (k && k < kmin) ? k : kmin;
+    kmax = k > kmax ? k : kmax;
+  }
+  kmax = wave_max_u32(kmax);
+  kmin = ~wave_max_u32(~kmin);
+  if ((tid & (WAVE - 1)) == 0) {
+    atomicMin(&mm[0], kmin);
+    atomicMax(&mm[1], kmax);
+  }
+  __syncthreads();
+  kmin = mm[0];
+  kmax = mm[1];
+  topk_refine<NK>(tid, key, [&](int j) { return cpos[NK * tid + j]; }, kmin, kmax, C, kmin,
+                  false, hist, wsum, phase, res_s, sel);
   return sel;
 }
 

@@ -25,7 +25,7 @@ from .config import DSV32, LayerConfig
 from .moe import _need
 
 ATTN_MAX_ROWS = 48
-MAX_CTX = 32768
+MAX_CTX = 163840  # DeepSeek-V3.2's context: five 32768-key top-k blocks a row
 U8 = torch.uint8
 
 
@@ -62,7 +62,7 @@ class AttnOp:
     most ``ctx_max`` keys each."""
 
     def __init__(self, device, cfg: LayerConfig = DSV32, max_rows: int = 8,
-                 ctx_max: int = MAX_CTX, sm_scale: Optional[float] = None,
+                 ctx_max: int = 32768, sm_scale: Optional[float] = None,
                  deadline_s: float = 10.0, fault=(0, 0), rt: Optional[MonoRuntime] = None):
         self.cfg, self.device = cfg, torch.device(device)
         if not 1 <= max_rows <= ATTN_MAX_ROWS:

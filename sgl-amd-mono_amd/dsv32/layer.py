@@ -25,7 +25,7 @@ import ctypes
 
 from .. import _lib, layouts
 from ..runtime import MonoRuntime, shared_or_new
-from .attn import AttnInputs, AttnOp
+from .attn import MAX_CTX, AttnInputs, AttnOp
 from .config import DSV32, LayerConfig
 from .front import FrontCaches, FrontOp, FrontWeights
 from .moe import MoeFp8Op, MoeFp8Weights, _need
@@ -169,8 +169,8 @@ class FusedLayerOp:
         self.cfg, self.device = cfg, torch.device(device)
         if not 1 <= max_rows <= 8:
             raise ValueError("max_rows must be 1..8")
-        if not 1 <= ctx_max <= 32768:
-            raise ValueError("ctx_max must be 1..32768")
+        if not 1 <= ctx_max <= MAX_CTX:
+            raise ValueError(f"ctx_max must be 1..{MAX_CTX}")
         weights.front.validate(cfg, self.device)
         weights.post.validate(cfg, self.device)
         weights.moe.validate(cfg, self.device)

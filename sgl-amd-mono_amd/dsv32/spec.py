@@ -54,7 +54,7 @@ WIDTHS = tuple(range(1, MAX_ROWS + 1))  # one build serves every row count up to
 TP_SIZES = (1,)
 BLOCKS = 256  # one CTA per MI355X CU
 PAGE_SIZE = DSV32.page
-MAX_CONTEXT = 32768  # keys a row's exact top-k ranks in one CTA's LDS
+MAX_CONTEXT = 163840  # keys a row's exact top-k ranks (five 32768-key blocks)
 
 # the bounds a check-mode step is held to (the north star's parity bar)
 NUMERICS = Numerics(

@@ -54,7 +54,7 @@ def test_null_args_are_refused_without_a_gpu():
     assert _lib.lib().mono_moe_mxfp4_launch(ctypes.byref(mx), None) == _lib.MONO_E_ARG
     assert "rows" in _lib.last_error()
     at = _lib.MonoAttnArgs(rows=8, rows_max=8, heads=32, index_heads=64, topk=2048, page=64,
-                           ctx_max=40000)
+                           ctx_max=163841)
     assert _lib.lib().mono_attn_launch(ctypes.byref(at), None) == _lib.MONO_E_ARG
     assert "ctx_max" in _lib.last_error()
     at = _lib.MonoAttnArgs(rows=9, rows_max=8, heads=32, index_heads=64, topk=2048, page=64,

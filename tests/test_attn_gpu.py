@@ -201,3 +201,28 @@ def test_attention_deadline_stops_and_reports(gpu):
     ref = AttnOp(gpu, max_rows=2, ctx_max=4096).launch(inp)
     torch.cuda.synchronize()
     assert torch.equal(clean, ref)
+
+
+def test_attention_rows_longer_than_one_block(gpu):
+    """Rows spanning several 32768-key top-k blocks, up to DeepSeek-V3.2's 163840: each
+    block ranks its own keys, one more task ranks the blocks' selections. Rows at 163840,
+    131072 and 65536 keys, one a single key into its second block (32769) and one whose
+    last block is shorter than 2048 keys (34000); scores sampled, every selection checked
+    in full against the exact top-2048 of the launch's own scores."""
+    print("case attention long rows ctx<=163840", flush=True)
+    inp = synthetic.attention_inputs(5, 163840, gpu, seed=1638,
+                                     positions=[163839, 131071, 65535, 32768, 33999])
+    op = AttnOp(gpu, max_rows=8, ctx_max=163840)
+    _check(op, inp, full_score_rows=0, sample=2048)
+
+
+def test_attention_long_row_ties_across_blocks(gpu):
+    """Head weights 0 at 65536 keys: every score is 0 in both blocks, so the row's
+    selection is its first 2048 positions, all from block 0 (ties to the lower position
+    across blocks)."""
+    print("case attention long row all equal ctx=65536", flush=True)
+    inp = synthetic.attention_inputs(2, 65536, gpu, seed=655)
+    inp.iw.zero_()
+    op = AttnOp(gpu, max_rows=2, ctx_max=65536)
+    _, _, topk = _check(op, inp, full_score_rows=0, sample=1024)
+    assert np.array_equal(topk[0], np.arange(TOPK, dtype=np.int32))

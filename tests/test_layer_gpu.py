@@ -345,3 +345,10 @@ def test_one_launch_layer_across_the_tag_wrap(gpu):
         chunk = op.rt.scratch[c * 16384:(c + 1) * 16384]
         assert int(chunk.count_nonzero()) == 0, (hex(want_tag), c)
     op.check()
+
+
+def test_layer_rows_longer_than_one_block(gpu):
+    """The layer at 131072 keys (four top-k blocks) and 70001 keys (a short third block):
+    the four launches against the oracle and the one launch bit-equal to them."""
+    print("case layer rows=2 ctx=131072", flush=True)
+    _layer_case(gpu, 2, 131072, [131071, 70000], seed=1310)

@@ -65,7 +65,7 @@ def test_a_served_config_has_no_reasons():
     (dict(rope_interleave=False), "interleaved pairs"),
     (dict(rope_scaling={"rope_type": "linear", "factor": 4.0}), "RoPE 'linear'"),
     (dict(quantization_config=None), "FP8 checkpoint"),
-    (dict(max_position_embeddings=163840), "context 163840"),
+    (dict(max_position_embeddings=262144), "context 262144"),
 ])
 def test_config_reasons_name_each_mismatch(change, words):
     reasons = dsv32._config_disable_reasons(SERVER, _with(MODEL, **change))
@@ -76,7 +76,7 @@ def test_config_reasons_name_each_mismatch(change, words):
     (dict(tp_size=4), "TP 4"),
     (dict(page_size=16), "--page-size 16"),
     (dict(speculative_algorithm="EAGLE"), "decode rows only"),
-    (dict(context_length=65536), "context 65536"),
+    (dict(context_length=200000), "context 200000"),
 ])
 def test_server_reasons_are_reasons_not_exceptions(change, words):
     reasons = dsv32._config_disable_reasons(_with(SERVER, **change), MODEL)
@@ -84,8 +84,8 @@ def test_server_reasons_are_reasons_not_exceptions(change, words):
 
 
 def test_a_shorter_served_context_is_accepted():
-    long = _with(MODEL, max_position_embeddings=163840)
-    assert dsv32._config_disable_reasons(_with(SERVER, context_length=32768), long) == []
+    long = _with(MODEL, max_position_embeddings=262144)
+    assert dsv32._config_disable_reasons(_with(SERVER, context_length=163840), long) == []
 
 
 def test_yarn_scales_the_softmax_by_mscale_squared():
