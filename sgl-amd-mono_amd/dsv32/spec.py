@@ -314,27 +314,39 @@ class _Step:
 
 
 def _build(model, hf_config, ctx):
-    """The launches of every covered layer, over SGLang's loaded weights in place. Layers
-    share one set of runtimes (scratch and guard): their launches are stream ordered."""
-    from ..guard import watchdog_deadline
+    """The launch of every covered layer, over SGLang's loaded weights in place: one
+    persistent launch a layer. Layers share one runtime (scratch and guard block): their
+    launches are stream ordered, and a failure raises the block's abort word, which every
+    later launch of the step sees, so each of them ends with NaN outputs too. A layer whose
+    projections SGLang left in mixed FP8 layouts runs as the four launches instead.
+    ``SGLANG_AMD_MONO_FAULT_INJECT`` (``rank:site[:after]``) arms a test stall."""
+    from ..guard import fault_injection, watchdog_deadline
     from .binding import layer_weights
-    from .layer import LayerOp, LayerRuntimes
+    from .layer import FusedLayerOp, LayerOp, LayerRuntimes, layer_runtime
 
     deadline = watchdog_deadline(getattr(ctx, "deadline_s", 120.0) * 2)
-    context_len = int(getattr(ctx, "context_len", None) or MAX_CONTEXT)
+    context_len = min(int(getattr(ctx, "context_len", None) or MAX_CONTEXT), MAX_CONTEXT)
     copies = getattr(ctx, "copies", None)
     copies = {} if copies is None else copies
     sm_scale = softmax_scale(hf_config)
-    layers, shared = {}, None
+    fault = fault_injection(int(getattr(ctx, "tp_rank", 0) or 0)) or (0, 0)
+    layers, rt, chained, device = {}, None, None, None
     for i in covered_layers(hf_config):
         mod = model.model.layers[i]
         w = layer_weights(mod, i, copies)
-        if shared is None:
-            shared = LayerRuntimes(w.moe.w13.device, max_rows=MAX_ROWS,
-                                   ctx_max=min(context_len, MAX_CONTEXT), deadline_s=deadline)
-        layers[i] = _Layer(i, mod, LayerOp(w, shared, sm_scale=sm_scale))
-    device = shared.device if shared is not None else torch.device("cpu")
-    return _Built(model, layers, device, context_len=min(context_len, MAX_CONTEXT))
+        device = w.moe.w13.device
+        if rt is None:
+            rt = layer_runtime(device, MAX_ROWS, deadline)
+        try:
+            op = FusedLayerOp(w, device, max_rows=MAX_ROWS, ctx_max=context_len,
+                              sm_scale=sm_scale, fault=fault, rt=rt)
+        except ValueError:  # mixed layouts: the four launches read each struct's own
+            if chained is None:
+                chained = LayerRuntimes(device, max_rows=MAX_ROWS, ctx_max=context_len,
+                                        deadline_s=deadline)
+            op = LayerOp(w, chained, sm_scale=sm_scale)
+        layers[i] = _Layer(i, mod, op)
+    return _Built(model, layers, device or torch.device("cpu"), context_len=context_len)
 
 
 SPEC = MonoSpec(

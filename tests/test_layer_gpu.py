@@ -166,8 +166,9 @@ def test_layer_graph_replay_matches_eager(gpu):
 
 def test_layer_bound_from_sglang_modules_matches_the_direct_launch(gpu):
     """A layer as SGLang loads it (its module attribute names, W_UK / W_UV as per-tensor
-    w_kc / w_vc, the RoPE table as f32 cos_sin_cache) bound by ``binding``: the launches
-    give the same bits as launches over the structs built directly."""
+    w_kc / w_vc, the RoPE table as f32 cos_sin_cache) bound by ``binding``: the four
+    launches and the one launch give the same bits as launches over the structs built
+    directly."""
     from types import SimpleNamespace as NS
 
     from sgl_amd_mono_amd import layouts
@@ -208,6 +209,13 @@ def test_layer_bound_from_sglang_modules_matches_the_direct_launch(gpu):
     op = LayerOp(bound, gpu, max_rows=rows, ctx_max=ctx)
     got = op.launch(h, caches, step)
     op.check()
+    assert torch.equal(got, want)
+    # the one launch the spec serves, over the same bound weights
+    caches.kv.copy_(kv0)
+    caches.plane.copy_(plane0)
+    fused = FusedLayerOp(bound, gpu, max_rows=rows, ctx_max=ctx)
+    got = fused.launch(h, caches, step)
+    fused.check()
     assert torch.equal(got, want)
 
 

@@ -244,17 +244,29 @@ def test_a_narrow_step_runs_at_the_next_width_with_pad_rows(monkeypatch):
     assert out.shape == (3, 7168)
 
 
-def test_build_reads_each_layer_and_scales_the_softmax(monkeypatch):
-    """``_build`` binds every covered layer with one shared set of runtimes and the
-    model's softmax scale (CPU: the binding and launches are stand-ins)."""
+def _fake_build(monkeypatch, mixed=()):
+    """``_build`` with the binding and launches replaced by stand-ins (CPU): records the
+    runtimes made and the ops' arguments; layers in ``mixed`` refuse the one launch."""
     from sgl_amd_mono_amd.dsv32 import binding, layer
 
     made = []
 
+    class _Rt:
+        def __init__(self, device, max_rows, deadline_s):
+            self.device = torch.device("cpu")
+            made.append(("layer", max_rows))
+
     class _Rts:
         def __init__(self, device, max_rows, ctx_max, deadline_s):
             self.device = torch.device("cpu")
-            made.append((max_rows, ctx_max))
+            made.append(("chain", max_rows, ctx_max))
+
+    class _Fused:
+        def __init__(self, w, device, max_rows, ctx_max, sm_scale, fault, rt):
+            if w.i in mixed:
+                raise ValueError("one FP8 layout for the whole layer")
+            self.w, self.rt, self.sm_scale, self.fault = w, rt, sm_scale, fault
+            self.ctx_max = ctx_max
 
     class _LayerOp:
         def __init__(self, w, rts, sm_scale):
@@ -262,14 +274,52 @@ def test_build_reads_each_layer_and_scales_the_softmax(monkeypatch):
 
     monkeypatch.setattr(binding, "layer_weights",
                         lambda mod, i, copies: NS(moe=NS(w13=NS(device="cpu")), i=i))
+    monkeypatch.setattr(layer, "layer_runtime", _Rt)
     monkeypatch.setattr(layer, "LayerRuntimes", _Rts)
+    monkeypatch.setattr(layer, "FusedLayerOp", _Fused)
     monkeypatch.setattr(layer, "LayerOp", _LayerOp)
+    return made, _Fused, _LayerOp
+
+
+def test_build_reads_each_layer_and_scales_the_softmax(monkeypatch):
+    """``_build`` binds every covered layer as one launch, all on one shared runtime, with
+    the model's softmax scale and the served context bound."""
+    made, fused, _ = _fake_build(monkeypatch)
     cfg = _with(MODEL, num_hidden_layers=6, rope_scaling={"type": "yarn", "factor": 40,
                                                            "mscale_all_dim": 1.0})
     model = NS(model=NS(layers=[NS() for _ in range(6)]))
     built = dsv32._build(model, cfg, NS(context_len=8192, deadline_s=30.0))
-    assert sorted(built.layers) == [3, 4, 5] and made == [(8, 8192)]
+    assert sorted(built.layers) == [3, 4, 5] and made == [("layer", 8)]
     ops = [built.layers[i].op for i in (3, 4, 5)]
-    assert ops[0].rts is ops[1].rts is ops[2].rts
+    assert all(isinstance(op, fused) for op in ops)
+    assert ops[0].rt is ops[1].rt is ops[2].rt
     assert all(op.sm_scale == dsv32.softmax_scale(cfg) for op in ops)
+    assert all(op.ctx_max == 8192 and op.fault == (0, 0) for op in ops)
     assert built.max_position == 8191
+
+
+def test_build_falls_back_to_four_launches_for_mixed_layouts(monkeypatch):
+    """A layer whose FP8 projections SGLang left in two layouts runs as the four
+    launches (each reads its own struct's layout) on one shared set of their runtimes."""
+    made, fused, chain = _fake_build(monkeypatch, mixed=(4, 5))
+    model = NS(model=NS(layers=[NS() for _ in range(6)]))
+    cfg = _with(MODEL, num_hidden_layers=6)
+    built = dsv32._build(model, cfg, NS(context_len=4096, deadline_s=30.0))
+    assert isinstance(built.layers[3].op, fused)
+    assert isinstance(built.layers[4].op, chain) and isinstance(built.layers[5].op, chain)
+    assert built.layers[4].op.rts is built.layers[5].op.rts
+    assert made == [("layer", 8), ("chain", 8, 4096)]
+
+
+def test_build_arms_the_fault_injection_of_its_rank(monkeypatch):
+    """SGLANG_AMD_MONO_FAULT_INJECT=rank:site:after reaches the launches of that rank."""
+    _, _, _ = _fake_build(monkeypatch)
+    monkeypatch.setenv("SGLANG_AMD_MONO_FAULT_INJECT", "0:5:3")
+    model = NS(model=NS(layers=[NS() for _ in range(6)]))
+    built = dsv32._build(model, _with(MODEL, num_hidden_layers=6),
+                         NS(context_len=4096, deadline_s=30.0))
+    assert all(built.layers[i].op.fault == (5, 3) for i in (3, 4, 5))
+    monkeypatch.setenv("SGLANG_AMD_MONO_FAULT_INJECT", "1:5:3")
+    built = dsv32._build(model, _with(MODEL, num_hidden_layers=6),
+                         NS(context_len=4096, deadline_s=30.0))
+    assert all(built.layers[i].op.fault == (0, 0) for i in (3, 4, 5))
