@@ -20,7 +20,7 @@
 //      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
 //      widened exactly), times the token's scale and the softmax scale; per head the
 //      split's max m and sum l; P, with the token's scale folded in, as bf16; O = P V on
-//      MFMAs, V read from the same rows. O, m and l go to scratch.
+//      MFMAs, V read from the same rows. O (in bf16), m and l go to scratch.
 //   4  merge: task (row, head): o = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s,
 //      rounded to bf16.
 // Every hand-off is a (word = launch tag) wait under the guard's deadline.
@@ -65,7 +65,7 @@ struct AttnScratch {
   size_t topk;        // the selection as (position, tag) pairs [rm][TOPK]
   size_t cand;        // a long row's block selections: u64 (position | key << 32) [rm][MAXBLK][TOPK]
   size_t blk_done;    // u32 [rm][MAXBLK]
-  size_t acc;         // f32 [rm][split][h][512]
+  size_t acc;         // bf16 [rm][split][h][512]: a split's unnormalised P V
   size_t ml;          // f32 [rm][split][h][2]
   size_t split_done;  // u32 [rm][split]
   size_t bytes;
@@ -77,7 +77,7 @@ struct AttnScratch {
     cand = at_align(topk + r * AT_TOPK * 8);
     blk_done = at_align(cand + r * AT_MAXBLK * AT_TOPK * 8);
     acc = at_align(blk_done + r * AT_MAXBLK * 4);
-    ml = at_align(acc + r * AT_NSPLIT * AT_HEADS * AT_LAT * 4);
+    ml = at_align(acc + r * AT_NSPLIT * AT_HEADS * AT_LAT * 2);
     split_done = at_align(ml + r * AT_NSPLIT * AT_HEADS * 8);
     bytes = at_align(split_done + r * AT_NSPLIT * 4);
   }
@@ -160,7 +160,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   uint64_t* topk = reinterpret_cast<uint64_t*>(p.scratch + S.topk);
   uint64_t* cands = reinterpret_cast<uint64_t*>(p.scratch + S.cand);
   uint32_t* blk_done = reinterpret_cast<uint32_t*>(p.scratch + S.blk_done);
-  float* accs = reinterpret_cast<float*>(p.scratch + S.acc);
+  uint16_t* accs = reinterpret_cast<uint16_t*>(p.scratch + S.acc);
   float* mls = reinterpret_cast<float*>(p.scratch + S.ml);
   uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S.split_done);
   bool ok = true;
@@ -635,14 +635,16 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
           o2 = mfma_bf16(a, bj[2], o2);
           o3 = mfma_bf16(a, bj[3], o3);
         }
-        float* acc = accs + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * AT_LAT;
+        // the partial in bf16 (the merge's sum of 32 of them rounds to bf16 again)
+        uint16_t* acc = accs + ((size_t)(r * AT_NSPLIT + sp) * AT_HEADS) * AT_LAT;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int h = h0 + 4 * g + e;
-          const v4f v = {o0[e], o1[e], o2[e], o3[e]};
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(v4i, v), rsrc(acc, AT_HEADS * AT_LAT * 4),
-              (uint32_t)(h * AT_LAT + d0 + 4 * c) * 4, 0, CP_DEV);
+          const v2i v = {(int32_t)(bf16_bits(o0[e]) | (bf16_bits(o1[e]) << 16)),
+                         (int32_t)(bf16_bits(o2[e]) | (bf16_bits(o3[e]) << 16))};
+          __builtin_amdgcn_raw_buffer_store_b64(v, rsrc(acc, AT_HEADS * AT_LAT * 2),
+                                                (uint32_t)(h * AT_LAT + d0 + 4 * c) * 2, 0,
+                                                CP_DEV);
         }
       }
       drain();
@@ -676,17 +678,17 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       // the split partials and their (m, l) in one round trip: TPS threads a split, VPT
       // values a thread
       constexpr int TPS = AT_THREADS / NSP, VPT = AT_LAT / TPS;
-      static_assert(VPT % 4 == 0, "merge thread map");
+      static_assert(VPT % 8 == 0, "merge thread map");
       const int sp = tid / TPS, dv = tid % TPS;
-      v4i a[VPT / 4];
+      v4i a[VPT / 8];
       {
         const __amdgpu_buffer_rsrc_t ra = rsrc(
             accs + ((size_t)(r * AT_NSPLIT + (sp < nsp ? sp : 0)) * AT_HEADS + h) * AT_LAT,
-            sp < nsp ? AT_LAT * 4 : 0);
+            sp < nsp ? AT_LAT * 2 : 0);
 #pragma unroll
         // through L2: within the launch the partials are only stored (write-through) before
         // the done words this CTA waited for, so no L2 holds a stale copy
-        for (int i = 0; i < VPT / 4; ++i) a[i] = ld16<CP_NONE>(ra, (uint32_t)(dv * VPT * 4 + 16 * i));
+        for (int i = 0; i < VPT / 8; ++i) a[i] = ld16<CP_NONE>(ra, (uint32_t)(dv * VPT * 2 + 16 * i));
       }
       if (w == 0) {
         const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
@@ -705,9 +707,12 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       {
         const float ws = sp < nsp ? wsp_s[sp] : 0.f;
 #pragma unroll
-        for (int i = 0; i < VPT / 4; ++i) {
-          const v4f v = __builtin_bit_cast(v4f, a[i]) * ws;
-          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + VPT * dv + 4 * i]) = v;
+        for (int i = 0; i < VPT / 8; ++i) {
+          const uint32_t u0 = a[i][0], u1 = a[i][1], u2 = a[i][2], u3 = a[i][3];
+          const v4f v0 = {bf16_lo(u0), bf16_hi(u0), bf16_lo(u1), bf16_hi(u1)};
+          const v4f v1 = {bf16_lo(u2), bf16_hi(u2), bf16_lo(u3), bf16_hi(u3)};
+          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + VPT * dv + 8 * i]) = v0 * ws;
+          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + VPT * dv + 8 * i + 4]) = v1 * ws;
         }
       }
       __syncthreads();
