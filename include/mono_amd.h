@@ -124,6 +124,9 @@ typedef struct {
   uint64_t* timeline;      /* optional u64 [grid, 8]: per-CTA s_memrealtime stamps at the
                               stage boundaries (MONO_TL_*), as the reference's timeline
                               build (sgl_amd_mono/common/stamps.py:16-33) */
+  int32_t n_group;         /* group-limited routing (DeepSeek-V3's n_group): 0 or 1 none;
+                              else 2..16 groups of 256 / n_group consecutive experts */
+  int32_t topk_group;      /* groups kept (topk_group * 256 / n_group >= 8) */
 } MonoMoeFp8Args;
 
 /* timeline marks of the MoE launch */
@@ -194,6 +197,9 @@ typedef struct {
   int32_t fault_after;
   uint64_t* timeline;      /* optional u64 [grid, 8]: MONO_TL_* stamps (MIDQ: the wait for
                               every mid tile ended) */
+  int32_t n_group;         /* group-limited routing (DeepSeek-V3's n_group): 0 or 1 none;
+                              else 2..16 groups of 256 / n_group consecutive experts */
+  int32_t topk_group;      /* groups kept (topk_group * 256 / n_group >= 8) */
 } MonoMoeMxfp4Args;
 
 size_t mono_moe_mxfp4_scratch_bytes(int32_t hidden, int32_t inter, int32_t experts);
@@ -429,6 +435,8 @@ typedef struct {
   uint64_t* phase_timeline; /* optional u64 [4, grid, 8]: each phase's own stamps (the
                                marks of its launch of its own), front, attention, output
                                block, MoE */
+  int32_t n_group;       /* group-limited routing: 0 or 1 none, else 2..16 groups */
+  int32_t topk_group;    /* groups kept (topk_group * 256 / n_group >= 8) */
 } MonoLayerArgs;
 
 size_t mono_layer_scratch_bytes(int32_t rows_max);

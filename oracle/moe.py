@@ -52,13 +52,33 @@ def sigmoid(logits):
     return torch.sigmoid(torch.as_tensor(logits).float())
 
 
-def route_topk(scores, bias, top_k=TOP_K, route_scale=ROUTE_SCALE):
+def group_mask(choice, n_group, topk_group):
+    """Group-limited routing (DeepSeek-V3's noaux_tc, as SGLang's ``biased_grouped_topk``
+    computes it): experts in n_group groups of consecutive ids; a group scores the f32 sum
+    of its two largest choice values (larger first); the topk_group best groups stay, ties
+    to the lower group. Returns a bool mask [R, E] of the experts left."""
+    c = np.asarray(choice, dtype=np.float32)
+    r, e = c.shape
+    g = c.reshape(r, n_group, e // n_group)
+    top2 = -np.sort(-g, axis=-1)[..., :2]
+    gscore = (top2[..., 0] + top2[..., 1]).astype(np.float32)  # one f32 add, larger first
+    order = np.lexsort((np.broadcast_to(np.arange(n_group), gscore.shape), -gscore), axis=-1)
+    keep = np.zeros((r, n_group), bool)
+    np.put_along_axis(keep, order[:, :topk_group], True, axis=-1)
+    return np.repeat(keep, e // n_group, axis=-1)
+
+
+def route_topk(scores, bias, top_k=TOP_K, route_scale=ROUTE_SCALE, n_group=1, topk_group=1):
     """Top-k of (score + bias) by the radix order key, lowest expert id among equal
     keys (``kernel.py:1575-1629``). Weights = score[pick] / sum(score[picks]) *
-    route_scale, picks in selection order. Returns (ids int32 [R, k], weights f32 [R, k])."""
+    route_scale, picks in selection order. With n_group > 1, only the experts of the
+    groups ``group_mask`` keeps take part (the others rank below every real key).
+    Returns (ids int32 [R, k], weights f32 [R, k])."""
     s = np.asarray(torch.as_tensor(scores).float(), dtype=np.float32)
     b = np.asarray(torch.as_tensor(bias).float(), dtype=np.float32)
     keys = F.radix_key((s + b).astype(np.float32)).astype(np.int64)
+    if n_group > 1:
+        keys = np.where(group_mask((s + b).astype(np.float32), n_group, topk_group), keys, -1)
     n = s.shape[-1]
     # descending key, then ascending id: sort by (-key, id)
     order = np.lexsort((np.broadcast_to(np.arange(n), keys.shape), -keys), axis=-1)

@@ -87,6 +87,8 @@ class MonoMoeFp8Args(ctypes.Structure):
         ("fault_site", c_int32),
         ("fault_after", c_int32),
         ("timeline", c_void_p),
+        ("n_group", c_int32),
+        ("topk_group", c_int32),
     ]
 
 
@@ -119,6 +121,8 @@ class MonoMoeMxfp4Args(ctypes.Structure):
         ("fault_site", c_int32),
         ("fault_after", c_int32),
         ("timeline", c_void_p),
+        ("n_group", c_int32),
+        ("topk_group", c_int32),
     ]
 
 
@@ -253,7 +257,7 @@ class MonoLayerArgs(ctypes.Structure):
         "o_lat", "a", "scores", "topk_pos", "y", "moe_scores", "ids", "weights", "scratch",
         "guard", "host_error")]
     _fields_ += [("fault_site", c_int32), ("fault_after", c_int32), ("timeline", c_void_p),
-                 ("phase_timeline", c_void_p)]
+                 ("phase_timeline", c_void_p), ("n_group", c_int32), ("topk_group", c_int32)]
 
 
 # name -> (restype, argtypes)

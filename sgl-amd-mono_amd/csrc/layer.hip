@@ -112,6 +112,9 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
                                  "expert intermediate 512 and 256 experts");
   if (a->layout != MONO_LAYOUT_ROWMAJOR && a->layout != MONO_LAYOUT_AITER16)
     return set_error(MONO_E_ARG, "mono_layer_launch: unknown weight layout");
+  if (!route_groups_ok(a->n_group, a->topk_group))
+    return set_error(MONO_E_ARG, "mono_layer_launch: n_group / topk_group: 2..16 groups "
+                                 "dividing 256, keeping >= 8 experts");
   if (a->ctx_max < 1 || a->ctx_max > AT_MAXCTX)
     return set_error(MONO_E_ARG, "mono_layer_launch: ctx_max must be 1..163840");
   if (a->pt_stride < (a->ctx_max + AT_PAGE - 1) / AT_PAGE || a->pt_rows < 1 ||
@@ -246,6 +249,8 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   m.rows = R;
   m.eps = a->eps;
   m.route_scale = a->route_scale;
+  m.n_group = a->n_group;
+  m.topk_group = a->topk_group;
   m.a = st;
   m.out = static_cast<uint16_t*>(a->out);
   m.g_post = static_cast<const uint16_t*>(a->g_post);

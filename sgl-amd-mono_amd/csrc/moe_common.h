@@ -13,6 +13,15 @@ constexpr int MOE_TOPK = 8;
 constexpr int MOE_SLOTS = MOE_TOPK + 1;
 constexpr int MOE_SHARED = 256;  // the shared expert's id
 constexpr int MOE_NDIST = MOE_NEXP + 1;
+constexpr int MOE_MAXGROUP = 16;  // expert groups of group-limited routing
+
+// a launch's group-limited routing arguments: n_group 0 or 1 (none), or 2..MOE_MAXGROUP
+// groups dividing the 256 experts, of which topk_group stay, holding at least 8 experts
+__host__ __device__ inline bool route_groups_ok(int n_group, int topk_group) {
+  if (n_group <= 1) return n_group >= 0;
+  return n_group <= MOE_MAXGROUP && MOE_NEXP % n_group == 0 && topk_group >= 1 &&
+         topk_group <= n_group && topk_group * (MOE_NEXP / n_group) >= MOE_TOPK;
+}
 
 // LDS routing state of one CTA
 struct RouteLds {
@@ -37,13 +46,65 @@ struct RouteLds {
 // four keys (the pick's key becomes 0, below every non-NaN key). Writes slots 1..8 of row
 // t into `rl` and sets the row's bit in rl.mask; weights are raw / (sum of the 8 raw, in
 // pick order) * route_scale.
+//
+// Group-limited routing (n_group > 1, DeepSeek-V3's noaux_tc): the 256 experts form
+// n_group groups of consecutive ids; a group's score is the sum of its two largest
+// (score + bias) in f32 (the larger first); the topk_group groups of the largest scores
+// (ties to the lower group) stay and every expert of another group drops out (key 0,
+// below every real key) before the top-8. The caller checks 256 % n_group == 0,
+// n_group <= MOE_MAXGROUP and topk_group * 256 / n_group >= 8.
 __device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], const float (&bs)[4],
                                  float route_scale, float* scores_out, int32_t* ids_out,
-                                 float* weights_out) {
+                                 float* weights_out, int n_group = 1, int topk_group = 1) {
   const int l = lane_id();
   uint32_t key[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) key[i] = radix_key(sc[i] + bs[i]);
+  if (n_group > 1) {
+    const int gs = MOE_NEXP / n_group;  // experts a group
+    float gscore[MOE_MAXGROUP];
+    uint32_t live = 0;                  // bit g: group g kept
+#pragma unroll
+    for (int g = 0; g < MOE_MAXGROUP; ++g) {
+      gscore[g] = 0.f;
+      if (g < n_group) {
+        // the lane's two largest of group g, then the wave's: m1 the largest; m2 the
+        // largest of the rest (m1 again when two lanes hold it)
+        float a1 = -INFINITY, a2 = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = (l + 64 * i) / gs == g ? sc[i] + bs[i] : -INFINITY;
+          if (v > a1) {
+            a2 = a1;
+            a1 = v;
+          } else if (v > a2) {
+            a2 = v;
+          }
+        }
+        const float m1 = wave_max(a1);
+        const uint64_t holders = __ballot(a1 == m1);
+        const bool single = __popcll(holders) == 1;
+        const bool mine = single && l == __ffsll((long long)holders) - 1;
+        const float m2 = single ? wave_max(mine ? a2 : a1) : m1;
+        gscore[g] = m1 + m2;
+      }
+    }
+    // the topk_group best groups, ties to the lower group (uniform across the wave)
+    for (int k = 0; k < topk_group; ++k) {
+      int bg = -1;
+      float bv = 0.f;
+#pragma unroll
+      for (int g = 0; g < MOE_MAXGROUP; ++g)
+        if (g < n_group && !((live >> g) & 1u) && (bg < 0 || gscore[g] > bv)) {
+          bg = g;
+          bv = gscore[g];
+        }
+      live |= 1u << bg;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (!((live >> ((l + 64 * i) / gs)) & 1u)) key[i] = 0;
+  }
   uint32_t best;
   int bi;
   float braw;

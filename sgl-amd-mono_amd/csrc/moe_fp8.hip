@@ -44,10 +44,14 @@ static int moe_fp8_launch_on(const MonoMoeFp8Args* a, mono_stream_t stream, void
   if (!a->a || !a->out || !a->g_post || !a->w_r || !a->bias || !a->w13 || !a->s13 || !a->w2 ||
       !a->s2 || !scratch_ptr || !guard_ptr)
     return fail(MONO_E_ARG, "null tensor");
+  if (!route_groups_ok(a->n_group, a->topk_group))
+    return fail(MONO_E_ARG, "n_group / topk_group: 2..16 groups dividing 256, keeping >= 8 experts");
   MoeFp8Params p;
   p.rows = a->rows;
   p.eps = a->eps;
   p.route_scale = a->route_scale;
+  p.n_group = a->n_group;
+  p.topk_group = a->topk_group;
   p.a = static_cast<const uint16_t*>(a->a);
   p.out = static_cast<uint16_t*>(a->out);
   p.g_post = static_cast<const uint16_t*>(a->g_post);

@@ -95,6 +95,7 @@ struct MoeFp8Geom {
 struct MoeFp8Params {
   int rows;
   float eps, route_scale;
+  int n_group, topk_group;  // group-limited routing (n_group <= 1: none)
   const uint16_t* a;
   uint16_t* out;
   const uint16_t* g_post;
@@ -487,7 +488,8 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[i] = 1.0f / (1.0f + expf(-lg[i]));
-        route_row(rl, row, sc, bs, p.route_scale, p.scores, p.ids, p.weights);
+        route_row(rl, row, sc, bs, p.route_scale, p.scores, p.ids, p.weights, p.n_group,
+                  p.topk_group);
         // lanes l < 8 wrote slots 1 + l (LDS accesses of one wave complete in order)
         __builtin_amdgcn_wave_barrier();
         const int j = l & (MOE_TOPK - 1), c = l >> 3;

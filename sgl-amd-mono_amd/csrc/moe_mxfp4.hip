@@ -116,6 +116,7 @@ __device__ inline v4f fp4_step(v4i wv, uint32_t code, const v4i (&B)[4], v4f acc
 struct MoeMxParams {
   int rows;
   float route_scale;
+  int n_group, topk_group;  // group-limited routing (n_group <= 1: none)
   const uint16_t* x;
   const uint16_t* res;
   uint16_t* out;
@@ -203,7 +204,7 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
     for (int i = 0; i < 4; ++i) sc[i] = 1.0f / (1.0f + expf(-lg[i]));
     const bool out0 = b == 0;
     route_row(rl, w, sc, bs, p.route_scale, out0 ? p.scores : nullptr, out0 ? p.ids : nullptr,
-              out0 ? p.weights : nullptr);
+              out0 ? p.weights : nullptr, p.n_group, p.topk_group);
   }
 #pragma unroll
   for (int k = 0; k < XPT; ++k) x_lds[tid + THREADS * k] = xv[k];
@@ -444,9 +445,14 @@ extern "C" int mono_moe_mxfp4_launch(const MonoMoeMxfp4Args* a, mono_stream_t st
     return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: null tensor");
   if (a->layout != MONO_LAYOUT_ROWMAJOR && a->layout != MONO_LAYOUT_AITER16)
     return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: unknown weight layout");
+  if (!route_groups_ok(a->n_group, a->topk_group))
+    return set_error(MONO_E_ARG, "mono_moe_mxfp4_launch: n_group / topk_group: 2..16 groups "
+                                 "dividing 256, keeping >= 8 experts");
   MoeMxParams p;
   p.rows = a->rows;
   p.route_scale = a->route_scale;
+  p.n_group = a->n_group;
+  p.topk_group = a->topk_group;
   p.x = static_cast<const uint16_t*>(a->x);
   p.res = static_cast<const uint16_t*>(a->res);
   p.out = static_cast<uint16_t*>(a->out);

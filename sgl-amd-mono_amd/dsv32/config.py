@@ -31,6 +31,10 @@ class LayerConfig:
     top_k: int = 8
     inter: int = 2048 // TP  # local expert intermediate (FP8)
     route_scale: float = 2.5
+    # group-limited routing (DeepSeek-V3's n_group / topk_group); 1, 1: plain top-8, the
+    # benchmark configs' router; the DeepSeek-V3.2 checkpoint routes with 8, 4
+    n_group: int = 1
+    topk_group: int = 1
     rms_eps: float = 1e-6
     layers: int = 61
 
@@ -60,6 +64,8 @@ class Mxfp4MoeConfig:
     top_k: int = 8
     inter: int = 1536 // TP
     route_scale: float = 2.5
+    n_group: int = 1
+    topk_group: int = 1
 
 
 MXFP4_MOE = Mxfp4MoeConfig()

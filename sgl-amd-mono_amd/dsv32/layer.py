@@ -237,7 +237,8 @@ class FusedLayerOp:
             layout=_lib.LAYOUT_AITER16 if self.layout == layouts.AITER16 else _lib.LAYOUT_ROWMAJOR,
             ctx_max=self.ctx_max, pt_stride=pt.stride(0), pt_rows=pt.shape[0],
             rope_rows=f.cos.shape[0], kv_slots=kv.shape[0], plane_pages=pages, eps=cfg.rms_eps,
-            sm_scale=self.sm_scale, route_scale=cfg.route_scale, h=h.data_ptr(),
+            sm_scale=self.sm_scale, route_scale=cfg.route_scale, n_group=cfg.n_group,
+            topk_group=cfg.topk_group, h=h.data_ptr(),
             out=out.data_ptr(), positions=step.positions.data_ptr(), slots=step.slots.data_ptr(),
             req_ids=step.req_ids.data_ptr(), page_table=pt.data_ptr(), kv=kv.data_ptr(),
             kv_scale=ptr(caches.kv_scale), plane=caches.plane.data_ptr(),

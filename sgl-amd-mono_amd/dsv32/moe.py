@@ -129,7 +129,8 @@ class MoeFp8Op:
         args = _lib.MonoMoeFp8Args(
             rows=r, hidden=cfg.hidden, inter=cfg.inter, experts=cfg.experts,
             layout=_lib.LAYOUT_AITER16 if w.layout == layouts.AITER16 else _lib.LAYOUT_ROWMAJOR,
-            eps=cfg.rms_eps, route_scale=cfg.route_scale,
+            eps=cfg.rms_eps, route_scale=cfg.route_scale, n_group=cfg.n_group,
+            topk_group=cfg.topk_group,
             a=a.data_ptr(), out=out.data_ptr(), g_post=w.g_post.data_ptr(),
             w_r=w.w_r.data_ptr(), bias=w.bias.data_ptr(), w13=w.w13.data_ptr(),
             s13=w.s13.data_ptr(), w2=w.w2.data_ptr(), s2=w.s2.data_ptr(),
@@ -240,7 +241,8 @@ class MoeMxfp4Op:
         args = _lib.MonoMoeMxfp4Args(
             rows=r, hidden=cfg.hidden, inter=cfg.inter, experts=cfg.experts,
             layout=_lib.LAYOUT_AITER16 if w.layout == layouts.AITER16 else _lib.LAYOUT_ROWMAJOR,
-            route_scale=cfg.route_scale, x=x.data_ptr(), res=ptr(res), out=out.data_ptr(),
+            route_scale=cfg.route_scale, n_group=cfg.n_group, topk_group=cfg.topk_group,
+            x=x.data_ptr(), res=ptr(res), out=out.data_ptr(),
             logits=logits.data_ptr(), bias=w.bias.data_ptr(), w13=w.w13.data_ptr(),
             s13=w.s13.data_ptr(), w2=w.w2.data_ptr(), s2=w.s2.data_ptr(), y=ptr(y),
             scores=ptr(routing.scores) if routing else None,

@@ -23,6 +23,7 @@ are that share, and refuses any other with the reason.
 
 from __future__ import annotations
 
+import dataclasses
 import math
 
 import torch
@@ -83,8 +84,6 @@ HF_CONFIG = dict(
     routed_scaling_factor=DSV32.route_scale,
     scoring_func="sigmoid",
     topk_method="noaux_tc",
-    n_group=1,
-    topk_group=1,
     norm_topk_prob=True,
     hidden_act="silu",
     rms_norm_eps=DSV32.rms_eps,
@@ -125,6 +124,21 @@ def softmax_scale(hf_config) -> float:
     return scale
 
 
+def _groups(hf_config):
+    """The model's group-limited routing (n_group, topk_group); 1, 1 when it has none."""
+    return (int(getattr(hf_config, "n_group", 1) or 1),
+            int(getattr(hf_config, "topk_group", 1) or 1))
+
+
+def _groups_ok(n_group: int, topk_group: int) -> bool:
+    """What the launches route (route_groups_ok in csrc/moe_common.h)."""
+    if n_group == 1:
+        return True
+    experts = DSV32.experts
+    return (2 <= n_group <= 16 and experts % n_group == 0 and 1 <= topk_group <= n_group
+            and topk_group * (experts // n_group) >= DSV32.top_k)
+
+
 def _same(have, want) -> bool:
     if isinstance(want, float):
         return have is not None and abs(float(have) - want) <= 1e-9 * max(1.0, abs(want))
@@ -144,6 +158,10 @@ def _config_disable_reasons(cfg, hf_config) -> list:
                        "and scale the softmax for default or YaRN RoPE only")
     if getattr(hf_config, "moe_layer_freq", 1) != 1:
         reasons.append("needs every layer after the dense ones to be MoE")
+    n_group, topk_group = _groups(hf_config)
+    if not _groups_ok(n_group, topk_group):
+        reasons.append(f"n_group {n_group} / topk_group {topk_group}: the router keeps "
+                       "1..16 groups dividing the 256 experts, holding at least 8 of them")
     tp = int(getattr(cfg, "tp_size", 1) or 1)
     if tp not in TP_SIZES:
         reasons.append(f"TP {tp}: the launches compute one GPU's share and the TP "
@@ -329,6 +347,8 @@ def _build(model, hf_config, ctx):
     copies = getattr(ctx, "copies", None)
     copies = {} if copies is None else copies
     sm_scale = softmax_scale(hf_config)
+    n_group, topk_group = _groups(hf_config)
+    cfg = dataclasses.replace(DSV32, n_group=n_group, topk_group=topk_group)
     fault = fault_injection(int(getattr(ctx, "tp_rank", 0) or 0)) or (0, 0)
     layers, rt, chained, device = {}, None, None, None
     for i in covered_layers(hf_config):
@@ -338,13 +358,13 @@ def _build(model, hf_config, ctx):
         if rt is None:
             rt = layer_runtime(device, MAX_ROWS, deadline)
         try:
-            op = FusedLayerOp(w, device, max_rows=MAX_ROWS, ctx_max=context_len,
+            op = FusedLayerOp(w, device, cfg=cfg, max_rows=MAX_ROWS, ctx_max=context_len,
                               sm_scale=sm_scale, fault=fault, rt=rt)
         except ValueError:  # mixed layouts: the four launches read each struct's own
             if chained is None:
-                chained = LayerRuntimes(device, max_rows=MAX_ROWS, ctx_max=context_len,
+                chained = LayerRuntimes(device, cfg, max_rows=MAX_ROWS, ctx_max=context_len,
                                         deadline_s=deadline)
-            op = LayerOp(w, chained, sm_scale=sm_scale)
+            op = LayerOp(w, chained, cfg=cfg, sm_scale=sm_scale)
         layers[i] = _Layer(i, mod, op)
     return _Built(model, layers, device or torch.device("cpu"), context_len=context_len)
 

@@ -360,3 +360,31 @@ def test_layer_rows_longer_than_one_block(gpu):
     the four launches against the oracle and the one launch bit-equal to them."""
     print("case layer rows=2 ctx=131072", flush=True)
     _layer_case(gpu, 2, 131072, [131071, 70000], seed=1310)
+
+
+def test_one_launch_layer_group_limited_routing(gpu):
+    """The one launch with DeepSeek-V3.2's router (8 groups, 4 kept): the routing ids
+    bit-exact against the oracle's group-limited top-8 of the launch's own scores, and
+    the same bits as the four launches with that router."""
+    import dataclasses
+
+    from oracle import moe as om
+    from sgl_amd_mono_amd.dsv32.config import DSV32
+
+    print("case one-launch layer grouped routing rows=4 ctx=4096", flush=True)
+    cfg = dataclasses.replace(DSV32, n_group=8, topk_group=4)
+    rows = 4
+    w, caches, step, h = synthetic.layer(rows, 4096, gpu, seed=84)
+    kv0, plane0 = caches.kv.clone(), caches.plane.clone()
+    want = LayerOp(w, gpu, cfg=cfg, max_rows=rows, ctx_max=4096).launch(h, caches, step).clone()
+    caches.kv.copy_(kv0)
+    caches.plane.copy_(plane0)
+    dbg = LayerDebug(moe_scores=torch.empty(rows, 256, device=gpu),
+                     ids=torch.empty(rows, 9, dtype=torch.int32, device=gpu),
+                     weights=torch.empty(rows, 9, device=gpu))
+    op = FusedLayerOp(w, gpu, cfg=cfg, max_rows=rows, ctx_max=4096)
+    got = op.launch(h, caches, step, debug=dbg)
+    op.check()
+    assert torch.equal(got, want)
+    sel, _ = om.route_topk(dbg.moe_scores.cpu(), w.moe.bias.cpu(), n_group=8, topk_group=4)
+    assert np.array_equal(dbg.ids.cpu().numpy()[:, 1:], sel)

@@ -171,3 +171,34 @@ def test_moe_fp8_deadline_stops_and_reports(layer, gpu):
     ref = MoeFp8Op(layer, gpu, max_rows=16).launch(a)
     torch.cuda.synchronize()
     assert torch.equal(clean, ref)
+
+
+@pytest.mark.parametrize("n_group,topk_group", [(8, 4), (4, 1)])
+def test_moe_fp8_group_limited_routing(gpu, layer_aiter, n_group, topk_group):
+    """DeepSeek-V3.2's router (8 groups of 32 experts, 4 kept) and a narrow one (4 groups,
+    1 kept: all 8 picks from one group of 64): ids bit-exact against the oracle's
+    group-limited top-8 of the launch's own scores, every pick in a kept group, weights
+    and y against the oracle on that routing."""
+    import dataclasses
+
+    print(f"case fp8 grouped routing n_group={n_group} topk_group={topk_group}", flush=True)
+    cfg = dataclasses.replace(DSV32, n_group=n_group, topk_group=topk_group)
+    op = MoeFp8Op(layer_aiter, gpu, cfg=cfg, max_rows=16)
+    a = synthetic.rows_bf16(8, H, gpu, seed=80 + n_group)
+    out, y, rt = _run(op, a)
+    ids, wts = rt.ids.cpu().numpy(), rt.weights.cpu().numpy()
+    scores, bias = rt.scores.cpu(), layer_aiter.bias.cpu()
+    sel, sel_w = omoe.route_topk(scores, bias, n_group=n_group, topk_group=topk_group)
+    assert np.array_equal(ids[:, 1:], sel), "grouped router ids differ"
+    np.testing.assert_allclose(wts[:, 1:], sel_w, rtol=2e-6, atol=1e-7)
+    keep = omoe.group_mask((scores.numpy() + bias.numpy()).astype(np.float32), n_group,
+                           topk_group)
+    assert np.all(np.take_along_axis(keep, ids[:, 1:].astype(np.int64), 1))
+    if topk_group == 1:
+        assert np.all(ids[:, 1:] // (256 // n_group) == ids[:, 1:2] // (256 // n_group))
+    experts = {int(e): synthetic.rowmajor_expert(layer_aiter, int(e)) for e in np.unique(ids)}
+    ref = omoe.moe_fp8(a.cpu(), layer_aiter.g_post.cpu(), layer_aiter.w_r.cpu(), bias, None,
+                       None, None, None, experts=experts, routing=(ids, wts))
+    got, want = y.cpu().double(), ref["y"].double()
+    rel = float((got - want).norm() / want.norm())
+    assert rel <= 1e-2, rel

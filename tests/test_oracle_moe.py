@@ -39,6 +39,55 @@ def test_route_weights_closed_form():
     np.testing.assert_allclose(w[0], [0.9 / 1.7 * 2.5, 0.8 / 1.7 * 2.5], rtol=1e-6)
 
 
+def _brute_grouped(score, bias, k, n_group, topk_group):
+    """Group-limited top-k by hand: each group's two largest choice values summed (the
+    larger first), groups ranked by that sum (ties to the lower group), the kept groups'
+    experts ranked as ``_brute_topk`` ranks them."""
+    v = (np.float32(score) + np.float32(bias)).astype(np.float32)
+    gs = len(v) // n_group
+    sums = []
+    for g in range(n_group):
+        a, b2 = sorted(v[g * gs:(g + 1) * gs].tolist(), reverse=True)[:2]
+        sums.append(float(np.float32(a) + np.float32(b2)))
+    groups = sorted(range(n_group), key=lambda g: (sums[g], -g), reverse=True)[:topk_group]
+    keep = [i for i in range(len(v)) if i // gs in groups]
+    def key(i):
+        x = float(v[i])
+        return (x, 1 if (x == 0 and not np.signbit(v[i])) else 0, -i)
+    return sorted(keep, key=key, reverse=True)[:k]
+
+
+def test_grouped_route_against_brute_force_with_ties():
+    rng = np.random.default_rng(7)
+    for trial in range(300):
+        n_group, topk_group = [(2, 1), (4, 2), (8, 4), (8, 2), (16, 8)][trial % 5]
+        n = 64 if n_group <= 8 else 128
+        s = rng.choice(np.array([0.25, 0.5, 0.75, 0.875, 0.0], np.float32), n)
+        b = rng.choice(np.array([0.0, 0.125, -0.125], np.float32), n)
+        k = min(8, topk_group * n // n_group)
+        ids, _ = M.route_topk(s[None], b, top_k=k, n_group=n_group, topk_group=topk_group)
+        assert ids[0].tolist() == _brute_grouped(s, b, k, n_group, topk_group), trial
+
+
+def test_grouped_route_drops_the_best_expert_of_a_weak_group():
+    """Expert 0 alone has the largest score, but its group's second best is tiny: with
+    8 groups keeping 4, group 0 loses to four groups of two good experts each, so expert
+    0 is not picked although plain routing picks it first."""
+    s = np.full((1, 256), 0.01, np.float32)
+    s[0, 0] = 0.99
+    for g in (1, 2, 3, 4):
+        s[0, 32 * g] = s[0, 32 * g + 1] = 0.6
+    b = np.zeros(256, np.float32)
+    plain, _ = M.route_topk(s, b)
+    grouped, _ = M.route_topk(s, b, n_group=8, topk_group=4)
+    assert plain[0, 0] == 0
+    assert 0 not in grouped[0].tolist()
+    assert sorted(grouped[0].tolist())[:8] == sorted([32, 33, 64, 65, 96, 97, 128, 129])
+    # one group: the same as plain routing
+    one, _ = M.route_topk(s, b, n_group=1, topk_group=1)
+    assert np.array_equal(one, plain)
+
+
 def test_w8a8_gemv_equals_dequantised_matmul():
     rng = np.random.default_rng(1)
     n, k = 256, 384

@@ -60,7 +60,9 @@ def test_a_served_config_has_no_reasons():
 @pytest.mark.parametrize("change, words", [
     (dict(hidden_size=6144), "hidden_size"),
     (dict(num_attention_heads=128), "num_attention_heads"),
-    (dict(n_group=8, topk_group=4), "n_group"),
+    (dict(n_group=3, topk_group=1), "n_group 3"),
+    (dict(n_group=8, topk_group=9), "n_group 8"),
+    (dict(n_group=32, topk_group=4), "n_group 32"),
     (dict(indexer_rope_interleave=False), "indexer_rope_interleave"),
     (dict(rope_interleave=False), "interleaved pairs"),
     (dict(rope_scaling={"rope_type": "linear", "factor": 4.0}), "RoPE 'linear'"),
@@ -257,20 +259,20 @@ def _fake_build(monkeypatch, mixed=()):
             made.append(("layer", max_rows))
 
     class _Rts:
-        def __init__(self, device, max_rows, ctx_max, deadline_s):
+        def __init__(self, device, cfg, max_rows, ctx_max, deadline_s):
             self.device = torch.device("cpu")
             made.append(("chain", max_rows, ctx_max))
 
     class _Fused:
-        def __init__(self, w, device, max_rows, ctx_max, sm_scale, fault, rt):
+        def __init__(self, w, device, cfg, max_rows, ctx_max, sm_scale, fault, rt):
             if w.i in mixed:
                 raise ValueError("one FP8 layout for the whole layer")
             self.w, self.rt, self.sm_scale, self.fault = w, rt, sm_scale, fault
-            self.ctx_max = ctx_max
+            self.ctx_max, self.cfg = ctx_max, cfg
 
     class _LayerOp:
-        def __init__(self, w, rts, sm_scale):
-            self.w, self.rts, self.sm_scale = w, rts, sm_scale
+        def __init__(self, w, rts, cfg, sm_scale):
+            self.w, self.rts, self.sm_scale, self.cfg = w, rts, sm_scale, cfg
 
     monkeypatch.setattr(binding, "layer_weights",
                         lambda mod, i, copies: NS(moe=NS(w13=NS(device="cpu")), i=i))
@@ -323,3 +325,15 @@ def test_build_arms_the_fault_injection_of_its_rank(monkeypatch):
     built = dsv32._build(model, _with(MODEL, num_hidden_layers=6),
                          NS(context_len=4096, deadline_s=30.0))
     assert all(built.layers[i].op.fault == (0, 0) for i in (3, 4, 5))
+
+
+def test_group_limited_routing_is_served_and_reaches_the_launches(monkeypatch):
+    """DeepSeek-V3.2's own router (n_group 8, topk_group 4) is accepted, and every covered
+    layer's launch routes with it."""
+    _, _, _ = _fake_build(monkeypatch)
+    real = _with(MODEL, n_group=8, topk_group=4, num_hidden_layers=6)
+    assert dsv32._config_disable_reasons(SERVER, real) == []
+    model = NS(model=NS(layers=[NS() for _ in range(6)]))
+    built = dsv32._build(model, real, NS(context_len=4096, deadline_s=30.0))
+    assert all((built.layers[i].op.cfg.n_group, built.layers[i].op.cfg.topk_group) == (8, 4)
+               for i in (3, 4, 5))
