@@ -207,8 +207,11 @@ class _Layer:
 class _Built:
     """One rank's layer launches, the step's row tables per width, and the forward."""
 
-    def __init__(self, lm, layers: dict, device, context_len: int):
-        self.lm, self.layers = lm, layers
+    def __init__(self, lm, layers: dict, device, context_len: int, cfg=DSV32):
+        from . import check
+
+        self.lm, self.layers, self.cfg = lm, layers, cfg
+        self.check = check.enabled()  # SGLANG_AMD_MONO_CHECK=1: eager steps checked
         self.first = min(layers) if layers else None
         self.last = max(layers) if layers else None
         self.max_rows = MAX_ROWS
@@ -285,10 +288,39 @@ class _Built:
                 h = pad
         else:
             h = hidden
-        out = L.op.launch(h, self._caches(L, forward_batch), st.as_layer_step(W))
+        caches, lstep = self._caches(L, forward_batch), st.as_layer_step(W)
+        capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+        if self.check and not capturing:
+            out = self._checked(L, positions, h, caches, lstep, forward_batch, S)
+        else:
+            out = L.op.launch(h, caches, lstep)
         if L.i != self.last:
             return out
         return set_written(out[:S], forward_batch)
+
+    def _checked(self, L: _Layer, positions, h, caches, lstep, forward_batch, S: int):
+        """The launch, with SGLang's layer run first on the same rows (check mode)."""
+        from . import check
+        from .layer import FusedLayerOp, LayerDebug
+
+        ref = check.reference(L, positions, h[:S], forward_batch, S, self.cfg,
+                              forward_batch.token_to_kv_pool)
+        ids = topk = None
+        if isinstance(L.op, FusedLayerOp):
+            W, dev = h.shape[0], h.device
+            dbg = LayerDebug(ids=torch.empty(W, self.cfg.top_k + 1, dtype=torch.int32, device=dev),
+                             topk=torch.empty(W, self.cfg.index_topk, dtype=torch.int32,
+                                              device=dev))
+            out = L.op.launch(h, caches, lstep, debug=dbg)
+            ids = dbg.ids[:, 1:]
+            pos = dbg.topk[:S].long()
+            pages = lstep.page_table[lstep.req_ids[:S].long()[:, None],
+                                     (pos.clamp_min(0) // self.cfg.page)].long()
+            topk = torch.where(pos >= 0, pages * self.cfg.page + pos % self.cfg.page, -1)
+        else:
+            out = L.op.launch(h, caches, lstep)
+        check.compare(L, out[:S], ref, S, ids=ids, topk_slots=topk, numerics=NUMERICS.bounds)
+        return out
 
     def step(self, plan, positions, forward_batch):
         """The step's row tables, written once a step (in the graph when captured)."""
@@ -366,7 +398,7 @@ def _build(model, hf_config, ctx):
                                         deadline_s=deadline)
             op = LayerOp(w, chained, cfg=cfg, sm_scale=sm_scale)
         layers[i] = _Layer(i, mod, op)
-    return _Built(model, layers, device or torch.device("cpu"), context_len=context_len)
+    return _Built(model, layers, device or torch.device("cpu"), context_len=context_len, cfg=cfg)
 
 
 SPEC = MonoSpec(

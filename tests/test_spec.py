@@ -337,3 +337,33 @@ def test_group_limited_routing_is_served_and_reaches_the_launches(monkeypatch):
     built = dsv32._build(model, real, NS(context_len=4096, deadline_s=30.0))
     assert all((built.layers[i].op.cfg.n_group, built.layers[i].op.cfg.topk_group) == (8, 4)
                for i in (3, 4, 5))
+
+
+def test_check_mode_runs_sglang_first_and_compares(monkeypatch):
+    """SGLANG_AMD_MONO_CHECK=1: each covered launch of an eager step is preceded by
+    SGLang's layer on the same rows (``check.reference``) and compared with it."""
+    from sgl_amd_mono_amd.dsv32 import binding, check
+
+    monkeypatch.setattr(binding, "caches", lambda pool, i: ("caches", i))
+    monkeypatch.setenv("SGLANG_AMD_MONO_CHECK", "1")
+    calls = []
+
+    def reference(L, positions, h_rows, fb, S, cfg, pool):
+        calls.append(("ref", L.i, tuple(h_rows.shape)))
+        return {"out": h_rows * 5 + 1, "ids": None, "topk": None}
+
+    def compare(L, got, ref, S, *, ids=None, topk_slots=None, numerics=None):
+        calls.append(("cmp", L.i, float((got.float() - ref["out"].float()).abs().max())))
+        assert set(numerics) == set(dsv32.NUMERICS.bounds)
+        return {}
+
+    monkeypatch.setattr(check, "reference", reference)
+    monkeypatch.setattr(check, "compare", compare)
+    built, lm, ops = _model([2], [5, 7])
+    assert built.check
+    fb = _batch(3)
+    plan = registry.Plan(key=registry.ShapeKey("decode", 3, 1))
+    built.forward(plan, torch.tensor([1, 2, 3]), torch.tensor([10, 20, 30]), fb)
+    # layer 1's launch is h*5+1: its comparison finds no difference; layer 2's is h*7+1
+    assert [c[:2] for c in calls] == [("ref", 1), ("cmp", 1), ("ref", 2), ("cmp", 2)]
+    assert calls[1][2] == 0.0 and calls[3][2] > 0.0
