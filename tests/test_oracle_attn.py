@@ -95,3 +95,18 @@ def test_attention_row_selects_all_keys_up_to_topk_and_the_exact_topk_beyond():
     slots = table[big["sel"] // 64].astype(np.int64) * 64 + big["sel"] % 64
     o, _ = A.sparse_mla(qa, kv, ks, slots, 0.1)
     np.testing.assert_array_equal(o, big["o"])
+
+
+def test_kv_rows_raw_e4m3_at_scale_one_and_scaled():
+    """Without scales a row decodes as torch's float8_e4m3fn; with them each row is that
+    times its token's scale."""
+    rng = np.random.default_rng(9)
+    kv = rng.integers(0, 256, (16, 576), dtype=np.uint8)
+    kv[kv == 0x7F] = 0  # no NaN codes
+    kv[kv == 0xFF] = 0
+    slots = [3, 0, 15, 3]
+    raw = A.kv_rows(kv, None, slots)
+    want = torch.from_numpy(kv[slots]).view(torch.float8_e4m3fn).double().numpy()
+    np.testing.assert_array_equal(raw, want)
+    sc = np.linspace(0.5, 2.0, 16).astype(np.float32)
+    np.testing.assert_array_equal(A.kv_rows(kv, sc, slots), want * sc[slots][:, None])

@@ -87,6 +87,20 @@ def test_kv_quant_scale_and_roundtrip():
     np.testing.assert_array_equal(back, want)
 
 
+def test_kv_quant_unscaled_is_torchs_e4m3_cast_saturating_at_448():
+    """SGLang's pool rows: raw E4M3 of the bf16 values at scale 1, beyond +-448 clipped
+    (torch's cast would give NaN there)."""
+    rng = np.random.default_rng(5)
+    row = torch.from_numpy(rng.normal(0, 100, 576)).to(torch.bfloat16).double().numpy()
+    row[:3] = [900.0, -1000.0, 448.0]
+    codes, sc = Fr.kv_quant(row, scaled=False)
+    assert sc == 1.0
+    clipped = np.clip(row, -448.0, 448.0)
+    want = torch.from_numpy(clipped).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(codes, want)
+    assert F.e4m3_to_f32(codes[:3]).tolist() == [448.0, -448.0, 448.0]
+
+
 def test_plane_and_query_bytes_read_back_through_the_attention_oracle():
     rng = np.random.default_rng(5)
     pages = 3
