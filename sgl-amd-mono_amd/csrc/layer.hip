@@ -11,7 +11,8 @@
 //   MoE        the norm weight and its router tile's weights.
 // Every wait is deadline guarded; a failing wait lets every CTA run to the end of the
 // launch. The launch tag is the guard's epoch + 1, shared by the four phases (each keeps
-// its own scratch region), and the last CTA out advances the epoch.
+// its own scratch region), and the last CTA out zeroes the barrier counts and advances the
+// epoch.
 //
 // Replaces the reference's one-launch layer kernel, sgl_amd_mono/glm53/gfx950/kernel.py:
 // 171-5282 (launch arguments :5191-5234), driven per layer by Glm53LayerOp.launch
@@ -91,7 +92,11 @@ __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
              (uint32_t)LayerScratch(p.at.rows_max).bytes,
              Poison{p.m.out, (uint32_t)p.m.rows * LY_H * 2u, NAN_BF16X2},
              Poison{p.m.y, (uint32_t)p.m.rows * LY_H * 4u, NAN_F32},
-             [&]() { moe_reset_queues<LY_H, LY_I>(p.m); });
+             [&]() {
+               moe_reset_queues<LY_H, LY_I>(p.m);
+#pragma unroll
+               for (int k = 0; k < 3; ++k) p.bar[k].reset();
+             });
   stamp(p.timeline, LY_TL_END);
 }
 

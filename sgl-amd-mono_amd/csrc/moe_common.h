@@ -38,14 +38,11 @@ struct RouteLds {
 // The top-k of one row, called by one whole wave. Lane l holds the scores of experts
 // l + 64 i (i < 4) in `sc` and the matching biases in `bs`.
 // Order: radix key of f32(score + bias) descending, then lower expert id
-// (sgl_amd_mono/glm53/gfx950/kernel.py:1575-1629). Each lane keeps its best key (the
-// lowest slot among equal keys, i.e. its lowest id), that key's slot and raw score. A
-// round takes the wave maximum of the lanes' best keys (a DPP / permlane butterfly), then
-// the lowest id holding it: ids are slot-major (l + 64 i), so the first of four ballots
-// (one a slot) that is non-empty, and its first lane. Only the picking lane rescans its
-// four keys (the pick's key becomes 0, below every non-NaN key). Writes slots 1..8 of row
-// t into `rl` and sets the row's bit in rl.mask; weights are raw / (sum of the 8 raw, in
-// pick order) * route_scale.
+// (sgl_amd_mono/glm53/gfx950/kernel.py:1575-1629). Each lane sorts its four keys (ties
+// to the lower slot, i.e. its lower id); a round takes the wave maximum of the lanes'
+// heads (a DPP / permlane butterfly), then the lowest id holding it, and that lane pops
+// its head. Writes slots 1..8 of row t into `rl` and sets the row's bit in rl.mask;
+// weights are raw / (sum of the 8 raw, in pick order) * route_scale.
 //
 // Group-limited routing (n_group > 1, DeepSeek-V3's noaux_tc): the 256 experts form
 // n_group groups of consecutive ids; a group's score is the sum of its two largest
@@ -62,97 +59,102 @@ __device__ inline void route_row(RouteLds& rl, int t, const float (&sc)[4], cons
   for (int i = 0; i < 4; ++i) key[i] = radix_key(sc[i] + bs[i]);
   if (n_group > 1) {
     const int gs = MOE_NEXP / n_group;  // experts a group
-    float gscore[MOE_MAXGROUP];
-    uint32_t live = 0;                  // bit g: group g kept
+    float gsc = -INFINITY;              // lane g < n_group: group g's score
+#pragma unroll 1
+    for (int g = 0; g < n_group; ++g) {
+      // the lane's two largest of group g, then the wave's: m1 the largest; m2 the
+      // largest of the rest (m1 again when two lanes hold it)
+      float a1 = -INFINITY, a2 = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < MOE_MAXGROUP; ++g) {
-      gscore[g] = 0.f;
-      if (g < n_group) {
-        // the lane's two largest of group g, then the wave's: m1 the largest; m2 the
-        // largest of the rest (m1 again when two lanes hold it)
-        float a1 = -INFINITY, a2 = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = (l + 64 * i) / gs == g ? sc[i] + bs[i] : -INFINITY;
-          if (v > a1) {
-            a2 = a1;
-            a1 = v;
-          } else if (v > a2) {
-            a2 = v;
-          }
+      for (int i = 0; i < 4; ++i) {
+        const float v = (l + 64 * i) / gs == g ? sc[i] + bs[i] : -INFINITY;
+        if (v > a1) {
+          a2 = a1;
+          a1 = v;
+        } else if (v > a2) {
+          a2 = v;
         }
-        const float m1 = wave_max(a1);
-        const uint64_t holders = __ballot(a1 == m1);
-        const bool single = __popcll(holders) == 1;
-        const bool mine = single && l == __ffsll((long long)holders) - 1;
-        const float m2 = single ? wave_max(mine ? a2 : a1) : m1;
-        gscore[g] = m1 + m2;
       }
+      const float m1 = wave_max(a1);
+      const uint64_t holders = __ballot(a1 == m1);
+      const bool single = __popcll(holders) == 1;
+      const bool mine = single && l == __ffsll((long long)holders) - 1;
+      const float m2 = single ? wave_max(mine ? a2 : a1) : m1;
+      if (l == g) gsc = m1 + m2;
     }
-    // the topk_group best groups, ties to the lower group (uniform across the wave)
+    // the topk_group best groups, ties to the lower group
+    uint32_t live = 0;  // bit g: group g kept
+#pragma unroll 1
     for (int k = 0; k < topk_group; ++k) {
-      int bg = -1;
-      float bv = 0.f;
-#pragma unroll
-      for (int g = 0; g < MOE_MAXGROUP; ++g)
-        if (g < n_group && !((live >> g) & 1u) && (bg < 0 || gscore[g] > bv)) {
-          bg = g;
-          bv = gscore[g];
-        }
-      live |= 1u << bg;
+      const bool cand = l < n_group && !((live >> l) & 1u);
+      const float m = wave_max(cand ? gsc : -INFINITY);
+      live |= 1u << (__ffsll((long long)__ballot(cand && gsc == m)) - 1);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (!((live >> ((l + 64 * i) / gs)) & 1u)) key[i] = 0;
   }
-  uint32_t best;
-  int bi;
-  float braw;
-  auto rescan = [&]() {
-    best = key[0];
-    bi = 0;
-    braw = sc[0];
+  // the lane's four candidates sorted by (key desc, slot asc): the next pick is always a
+  // lane's head. Five compare-exchanges (a sorting network; the order is total, so
+  // equal keys keep the lower slot first).
+  uint32_t k[4];
+  int s[4];
+  float rw[4];
 #pragma unroll
-    for (int i = 1; i < 4; ++i)
-      if (key[i] > best) {  // strict: equal keys keep the lower slot (the lower id)
-        best = key[i];
-        bi = i;
-        braw = sc[i];
-      }
-  };
-  rescan();
-  float picked_raw[MOE_TOPK];
-  int picked_id[MOE_TOPK];
-#pragma unroll
-  for (int r = 0; r < MOE_TOPK; ++r) {
-    const uint32_t m = wave_max_u32(best);
-    const bool top = best == m;
-    const uint64_t b0 = __ballot(top && bi == 0), b1 = __ballot(top && bi == 1);
-    const uint64_t b2 = __ballot(top && bi == 2), b3 = __ballot(top && bi == 3);
-    const int slot = b0 ? 0 : b1 ? 1 : b2 ? 2 : 3;
-    const uint64_t bb = b0 ? b0 : b1 ? b1 : b2 ? b2 : b3;
-    const int owner = __ffsll((long long)bb) - 1;
-    picked_raw[r] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(braw), owner));
-    picked_id[r] = owner + 64 * slot;
-    if (l == owner) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i == slot) key[i] = 0;
-      rescan();
-    }
+  for (int i = 0; i < 4; ++i) {
+    k[i] = key[i];
+    s[i] = i;
+    rw[i] = sc[i];
   }
-  float tot = 0.f;
+  auto cx = [&](int a, int b) {
+    const bool sw = k[b] > k[a] || (k[b] == k[a] && s[b] < s[a]);
+    const uint32_t ka = k[a], kb = k[b];
+    const int sa = s[a], sb = s[b];
+    const float ra = rw[a], rb = rw[b];
+    k[a] = sw ? kb : ka;
+    k[b] = sw ? ka : kb;
+    s[a] = sw ? sb : sa;
+    s[b] = sw ? sa : sb;
+    rw[a] = sw ? rb : ra;
+    rw[b] = sw ? ra : rb;
+  };
+  cx(0, 1);
+  cx(2, 3);
+  cx(0, 2);
+  cx(1, 3);
+  cx(1, 2);
+  // A round takes the wave maximum of the heads; the pick is the lowest id holding it
+  // (a single lane almost always; on a tie between lanes, the lowest slot * 64 + lane).
+  // The owner pops its head. Rounds in a loop, not unrolled: this runs once a launch on
+  // a few CTAs, so its code is fetched cold. Lane r keeps pick r; the sum of the raw
+  // scores runs in pick order.
+  float tot = 0.f, raw = 0.f;
+  int e = 0;
+#pragma unroll 1
+  for (int r = 0; r < MOE_TOPK; ++r) {
+    const uint32_t m = wave_max_u32(k[0]);
+    const uint64_t held = __ballot(k[0] == m);
+    int owner = __ffsll((long long)held) - 1;
+    if (__popcll(held) != 1)
+      owner = (int)(wave_min_u32(k[0] == m ? (uint32_t)(s[0] * 64 + l) : 0xFFFFFFFFu) & 63u);
+    const float pr = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rw[0]), owner));
+    const int id = owner + 64 * __builtin_amdgcn_readlane(s[0], owner);
+    tot += pr;
+    if (l == r) {
+      raw = pr;
+      e = id;
+    }
+    const bool pop = l == owner;
 #pragma unroll
-  for (int r = 0; r < MOE_TOPK; ++r) tot += picked_raw[r];
+    for (int i = 0; i < 3; ++i) {
+      k[i] = pop ? k[i + 1] : k[i];
+      s[i] = pop ? s[i + 1] : s[i];
+      rw[i] = pop ? rw[i + 1] : rw[i];
+    }
+    k[3] = pop ? 0u : k[3];
+    s[3] = pop ? 4 : s[3];
+  }
   if (l < MOE_TOPK) {
-    float raw = 0.f;
-    int e = 0;
-#pragma unroll
-    for (int r = 0; r < MOE_TOPK; ++r)
-      if (r == l) {
-        raw = picked_raw[r];
-        e = picked_id[r];
-      }
     const float w = raw / tot * route_scale;
     rl.id[t][1 + l] = e;
     rl.w[t][1 + l] = w;

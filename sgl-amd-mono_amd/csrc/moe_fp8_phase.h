@@ -413,6 +413,10 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rxq, dst, 16, (uint32_t)(c * 1024 + l * 16), 0, 0, CP_NONE);
     }
   };
+  // a CTA that routes a row copies the image only after routing: LDS writes queued behind
+  // the copy's would hold up the router's own LDS traffic
+  bool routes_row = false;
+  for (int row = 0; row < R; ++row) routes_row |= (G::NTASK0 + row) % nblk == b;
   if (w >= 1) {
     constexpr int NCW = (int)(G::SZ_XQ / 1024) / (G::WAVES - 1) + 1;  // chunks a wave, at most
     const __amdgpu_buffer_rsrc_t rxs = rsrc(hxs, (uint32_t)G::SZ_XS);
@@ -438,7 +442,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
       }
       return !__any(missing);
     });
-    copy_image(1, G::WAVES - 1, false);
+    if (!routes_row) copy_image(1, G::WAVES - 1, false);
     // the scales polled above are final: both chunks of a 128-K chunk hold the same
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -456,9 +460,13 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     for (int row = 0; row < R && ok; ++row) {
       if ((G::NTASK0 + row) % nblk != b) continue;
       // the biases ahead of the poll: loaded after it, they would add a round trip
+      // (held here: left to the compiler, the loads sink past the poll into their use)
       float bs[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) bs[i] = p.bias[l + 64 * i];
+      for (int i = 0; i < 4; ++i) {
+        bs[i] = p.bias[l + 64 * i];
+        asm volatile("" : "+v"(bs[i]));
+      }
       float lg[4];
       ok = wait_until(guard, MONO_SITE_LOGITS, [&]() {
         // every load issued before the first is used: one round trip a poll
@@ -544,6 +552,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   __syncthreads();
   if (w == 0) build_experts(rl, R);  // the slot tables follow the first ring's loads
   __syncthreads();
+  if (routes_row) copy_image(0, G::WAVES, false);
   ok = ok_s != 0;
   const int nd = rl.nd;
 

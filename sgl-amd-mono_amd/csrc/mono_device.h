@@ -190,6 +190,19 @@ __device__ inline uint32_t wave_max_u32(uint32_t v) {
   return mx(c[0], c[1]);
 }
 
+// minimum of a u32 over the wave (every lane ends with it)
+__device__ inline uint32_t wave_min_u32(uint32_t v) {
+  auto mn = [](uint32_t a, uint32_t b) { return a < b ? a : b; };
+  v = mn(v, dpp_u<DPP_XOR1>(v));
+  v = mn(v, dpp_u<DPP_XOR2>(v));
+  v = mn(v, dpp_u<DPP_HALF_MIRROR>(v));
+  v = mn(v, dpp_u<DPP_MIRROR>(v));
+  auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = mn(a[0], a[1]);
+  auto c = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return mn(c[0], c[1]);
+}
+
 // ------------------------------------------------------------------ number formats
 // f32 -> bf16 bits, round to nearest even (finite inputs)
 __device__ inline uint32_t bf16_bits(float f) {

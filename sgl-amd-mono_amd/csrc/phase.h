@@ -122,9 +122,12 @@ struct NoWait {
   __device__ bool operator()() const { return true; }
 };
 
-// A grid barrier between two phases of the layer launch: `count` (zero between launches)
-// and `flag` words in scratch. Arriving: every wave drains its stores, then one thread
-// adds to the count; the last arrival resets the count and raises the flag to the tag.
+// A grid barrier between two phases of the layer launch: `count` and `flag` words in
+// scratch, a line apart (the arrivals' adds do not queue behind the polls). The count is
+// zero at launch entry; the last CTA out of a launch zeroes it again. Arriving: every
+// wave drains its stores (write-through, so they are acknowledged device-wide), then one
+// thread adds to the count; the last arrival raises the flag to the launch tag at once
+// (the count needs no reset on the way). Waiting: wave 0 polls the flag.
 struct PhaseBarrier {
   uint32_t* count;
   uint32_t* flag;
@@ -134,15 +137,10 @@ struct PhaseBarrier {
   __device__ __attribute__((always_inline)) void arrive(uint32_t tag) const {
     drain();
     __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t old = add_dev(count, 1u);
-      if (old == gridDim.x - 1u) {
-        st_dev(count, 0u);
-        drain();  // the reset lands before the flag lets anyone on
-        st_dev(flag, tag);
-      }
-    }
+    if (threadIdx.x == 0 && add_dev(count, 1u) == gridDim.x - 1u) st_dev(flag, tag);
   }
+  // for the last CTA out, once every CTA has arrived
+  __device__ __attribute__((always_inline)) void reset() const { st_dev(count, 0u); }
 };
 
 // Waiting for a barrier: wave 0 polls the flag under the guard's deadline, then the CTA
