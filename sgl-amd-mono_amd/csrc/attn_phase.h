@@ -8,13 +8,18 @@
 //      E8M0 scales (query rows = heads, key columns = tokens, K = the 128 dims); relu,
 //      the head weights and the sum over heads stay in the lane, then two permlane
 //      swaps sum the lane groups. Scores go to scratch; the chunk's done word follows.
-//   2  top-k: task = (row, 32768-key block) (topk_lds.h): thread t holds the radix keys
-//      of block positions 32 t .. in registers; a sample narrows the range, histograms
-//      over the live range keep the bin of the 2048th key until its few candidates rank
-//      themselves; the selection (every element up to the threshold element of the order
-//      key descending, position ascending) is published as (position, tag) pairs. A row
-//      longer than one block publishes each block's selection as candidates with their
-//      keys, and one more task ranks the candidates of the row's blocks the same way.
+//      A row within one top-k block also gets each chunk's candidate list (chunk_list:
+//      its keys at or above a histogram cut, 128-256 of them, with the cut).
+//   2  top-k: task = row (one block, topk_lds.h): the chunks' lists ranked by one CTA
+//      (topk_lists); where they cannot decide it (too few keys listed, or a chunk's cut
+//      above the lists' threshold), or for a longer row, the scores themselves: task =
+//      (row, 32768-key block), thread t holds the radix keys of block positions 32 t ..
+//      in registers; a sample narrows the range, histograms over the live range keep the
+//      bin of the 2048th key until its few candidates rank themselves; the selection
+//      (every element up to the threshold element of the order key descending, position
+//      ascending) is published as (position, tag) pairs. A row longer than one block
+//      publishes each block's selection as candidates with their keys, and one more task
+//      ranks the candidates of the row's blocks the same way.
 //   3  split: task (row, SPLIT-key split), all 32 heads (SPLIT 64 when the rows' 32
 //      splits each fill the grid once, else 128). The split's tokens (through the
 //      page table) are gathered as E4M3 rows into LDS; S = q K^T on bf16 MFMAs (E4M3
@@ -65,6 +70,8 @@ struct AttnScratch {
   size_t topk;        // the selection as (position, tag) pairs [rm][TOPK]
   size_t cand;        // a long row's block selections: u64 (position | key << 32) [rm][MAXBLK][TOPK]
   size_t blk_done;    // u32 [rm][MAXBLK]
+  size_t lists;       // a one-block row's chunk candidates: u64 [rm][TK_NLIST][TK_LIST]
+  size_t cuts;        // u32 [rm][TK_NLIST]: each chunk's cut
   size_t acc;         // bf16 [rm][split][h][512]: a split's unnormalised P V
   size_t ml;          // f32 [rm][split][h][2]
   size_t split_done;  // u32 [rm][split]
@@ -76,7 +83,9 @@ struct AttnScratch {
     topk = at_align(score_done + r * AT_NCHUNK * 4);
     cand = at_align(topk + r * AT_TOPK * 8);
     blk_done = at_align(cand + r * AT_MAXBLK * AT_TOPK * 8);
-    acc = at_align(blk_done + r * AT_MAXBLK * 4);
+    lists = at_align(blk_done + r * AT_MAXBLK * 4);
+    cuts = at_align(lists + r * TK_NLIST * TK_LIST * 8);
+    acc = at_align(cuts + r * TK_NLIST * 4);
     ml = at_align(acc + r * AT_NSPLIT * AT_HEADS * AT_LAT * 2);
     split_done = at_align(ml + r * AT_NSPLIT * AT_HEADS * 8);
     bytes = at_align(split_done + r * AT_NSPLIT * 4);
@@ -121,7 +130,7 @@ __device__ inline v4f mfma_fp4(v4i a, v4i b, int sa, int sb) {
 // LDS of the attention phase: the top-k arena (carved per stage), then small words
 constexpr int AT_LDS_WSUM = TOPK_ARENA_WORDS * 4;         // int [2][16], 16-byte aligned
 constexpr int AT_LDS_RES = AT_LDS_WSUM + 2 * AT_WAVES * 4;  // int [4]
-constexpr int AT_LDS_MM = AT_LDS_RES + 16;                  // u32 [2]
+constexpr int AT_LDS_MM = AT_LDS_RES + 16;                  // u32 [4]
 constexpr int AT_LDS_WSP = AT_LDS_MM + 16;                  // f32 [NSPLIT]
 constexpr int AT_LDS_LINV = AT_LDS_WSP + AT_NSPLIT * 4;     // f32
 constexpr int AT_LDS_BYTES = AT_LDS_LINV + 16;
@@ -160,6 +169,8 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   uint64_t* topk = reinterpret_cast<uint64_t*>(p.scratch + S.topk);
   uint64_t* cands = reinterpret_cast<uint64_t*>(p.scratch + S.cand);
   uint32_t* blk_done = reinterpret_cast<uint32_t*>(p.scratch + S.blk_done);
+  uint64_t* lists = reinterpret_cast<uint64_t*>(p.scratch + S.lists);
+  uint32_t* cuts = reinterpret_cast<uint32_t*>(p.scratch + S.cuts);
   uint16_t* accs = reinterpret_cast<uint16_t*>(p.scratch + S.acc);
   float* mls = reinterpret_cast<float*>(p.scratch + S.ml);
   uint32_t* split_done = reinterpret_cast<uint32_t*>(p.scratch + S.split_done);
@@ -205,7 +216,13 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   // Each stage takes the thread index through an opaque copy: conditions on it are then
   // computed inside the stage, not hoisted to the kernel's top where they would hold
   // registers through every stage.
-  // tasks (row, 1024-key chunk), as many chunks a row as the launch's context bound needs
+  // tasks (row, 1024-key chunk), as many chunks a row as the launch's context bound needs.
+  // A row within one top-k block that keeps fewer keys than it has also gets each chunk's
+  // candidate list (chunk_list): the chunk's order keys go through LDS (ckey).
+  static_assert(AT_CHUNK == AT_THREADS && TK_NLIST * AT_CHUNK == AT_TKBLOCK, "a key a thread");
+  uint32_t* ckey = reinterpret_cast<uint32_t*>(smem);   // [AT_CHUNK]
+  uint32_t* chist = ckey + AT_CHUNK;                     // [256]
+  int* cwsum = reinterpret_cast<int*>(chist + 256);      // [AT_WAVES]
   const int nchr = (p.ctx_max + AT_CHUNK - 1) / AT_CHUNK;
   for (int task = b; task < rs8 * nchr; task += nblk) {
     const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
@@ -213,8 +230,14 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     if (r >= R) continue;
     const int n = row_n(r);
     if (c * AT_CHUNK >= n) continue;
+    const bool listed = !LONG && n > AT_TOPK;
+    if (listed) {
+      if (tid < 64) reinterpret_cast<v4i*>(chist)[tid] = v4i{0, 0, 0, 0};
+      if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = v4i{-1, 0, 0, 0};
+    }
     const int pg = c * (AT_CHUNK / AT_PAGE) + w;
     const bool live = pg * AT_PAGE < n;
+    float sco[4];  // a listed chunk's scores (lanes < 16), stored after its list
     const int pid = live ? __builtin_amdgcn_readfirstlane(page_of(r, pg)) : 0;
     // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
     // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword. Loaded before
@@ -253,6 +276,9 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         wv[mi] = __builtin_bit_cast(
             v4f, ld16<XCP>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
       float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
+      // a listed chunk's scores are stored after its list is made: a store in flight would
+      // hold up the list making's waits
+      float sv[4];
       auto tile = [&](auto nt_c) {
         constexpr int NT = decltype(nt_c)::value;
         float acc = 0.f;
@@ -272,16 +298,44 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         acc = a + bb;
         swap32(acc, a, bb);
         acc = a + bb;
+        sv[NT] = acc;
         if (l < 16) {
-          st_devf(dst + 16 * NT + l, acc);
           const int tok = pg * AT_PAGE + 16 * NT + l;
-          if (p.scores_out && tok < n) p.scores_out[(size_t)r * p.ctx_max + tok] = acc;
+          if (listed) {
+            const uint32_t k = radix_key(acc);
+            ckey[w * AT_PAGE + 16 * NT + l] = tok < n ? (k > 1u ? k : 1u) : 0u;
+          } else {
+            st_devf(dst + 16 * NT + l, acc);
+            if (p.scores_out && tok < n) p.scores_out[(size_t)r * p.ctx_max + tok] = acc;
+          }
         }
       };
       tile(std::integral_constant<int, 0>());
       tile(std::integral_constant<int, 1>());
       tile(std::integral_constant<int, 2>());
       tile(std::integral_constant<int, 3>());
+      if (listed) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) sco[nt] = sv[nt];
+      }
+    } else if (listed) {
+      ckey[w * AT_PAGE + l] = 0u;
+    }
+    if (listed) {
+      __syncthreads();
+      const uint32_t cut =
+          chunk_list(tid, ckey[tid], c * AT_CHUNK, chist, cwsum, mm_s,
+                     rsrc(lists + ((size_t)r * TK_NLIST + c) * TK_LIST, TK_LIST * 8));
+      if (tid == 0) st_dev(&cuts[r * TK_NLIST + c], cut);
+      if (live && l < 16) {
+        float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          st_devf(dst + 16 * nt + l, sco[nt]);
+          const int tok = pg * AT_PAGE + 16 * nt + l;
+          if (p.scores_out && tok < n) p.scores_out[(size_t)r * p.ctx_max + tok] = sco[nt];
+        }
+      }
     }
     drain();
     __syncthreads();
@@ -318,14 +372,24 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
           ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
             return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + l]) == tag);
           });
-        if (tid == 0) {  // topk_select's minimum / maximum words, set before the barrier
-          mm_s[0] = 0xFFFFFFFFu;
-          mm_s[1] = 0u;
-        }
+        // topk_lists' / topk_select's minimum, maximum and flag words, set before the barrier
+        if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = v4i{-1, 0, 0, 0};
         ok = cta_all(ok, ok_s);
         if (ok) {
-          const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
-          publish(tid, r, topk_select(tid, rs, n, smem, wsum, mm_s, res_s));
+          // the chunks' candidate lists, or, where they cannot decide it, every score
+          int32_t* sel = topk_lists(
+              tid, rsrc(lists + (size_t)r * TK_NLIST * TK_LIST, (uint32_t)(nch * TK_LIST * 8)),
+              rsrc(cuts + r * TK_NLIST, (uint32_t)nch * 4u), nch, smem, wsum, mm_s, res_s);
+          if (!sel) {
+            if (tid == 0) {
+              mm_s[0] = 0xFFFFFFFFu;
+              mm_s[1] = 0u;
+            }
+            __syncthreads();
+            const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
+            sel = topk_select(tid, rs, n, smem, wsum, mm_s, res_s);
+          }
+          publish(tid, r, sel);
         }
       }
       __syncthreads();  // the LDS arena is reused by the next row

@@ -3,7 +3,11 @@
 // the radix order key of the f32 score bits, larger first, ties to the lower position;
 // the selection in ascending position order.
 //
-// A row of up to AT_TKBLOCK keys is ranked by one CTA (topk_select). A longer row is cut
+// A row of up to AT_TKBLOCK keys is ranked by one CTA: from its chunks' candidate lists
+// (chunk_list, topk_lists) when they decide it, else from every score (topk_select). Every
+// key a chunk leaves out lies below its cut; when every cut lies at or below the low edge
+// of the final bin of the lists' ranking, every key left out ranks below every selected
+// one, so the lists' selection is the row's. A longer row is cut
 // into blocks of AT_TKBLOCK keys, each ranked by a CTA of its own; since every element of
 // the row's top-TOPK is in its own block's top-TOPK (fewer than TOPK elements of the row,
 // so of the block, rank above it), one more CTA ranks the blocks' selections (topk_final)
@@ -23,6 +27,11 @@ constexpr int AT_MAXCTX = AT_TKBLOCK * AT_MAXBLK;  // keys a row may see: 163840
 constexpr int AT_THREADS = 1024;
 constexpr int AT_WAVES = AT_THREADS / WAVE;
 constexpr int CAND = 256;  // a threshold bin this small is ranked directly
+// a scored chunk of AT_THREADS keys lists its candidates for the row's top-TOPK: at most
+// TK_LIST, at least TK_LIST_MIN where one histogram pass can cut there
+constexpr int TK_LIST = 256;
+constexpr int TK_LIST_MIN = 128;
+constexpr int TK_NLIST = AT_TKBLOCK / AT_THREADS;  // chunks of a one-block row
 // LDS words topk_select needs: the padded key image, then the histogram
 constexpr int TOPK_ARENA_WORDS = AT_THREADS * 33 + 4096;
 
@@ -115,11 +124,13 @@ __device__ inline void select_pass(int tid, const uint32_t (&key)[NK], uint32_t 
 // positions. A thread's picks are a 32-bit mask; the scan of the pick counts places them,
 // in ascending position order, at sel[0 .. TOPK). `hist` (4096 words, zero on entry) holds
 // the passes' bins, then the candidates and the masks of the candidates' owners.
+// With `floor_out`, thread 0 stores there the low edge of the final bin: no selected key
+// lies below it.
 template <int NK, class PosF>
 __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_of, uint32_t lo,
                                    uint32_t hi, int cnt, uint32_t plo0, bool check0,
                                    uint32_t* hist, int* wsum, int& phase, int* res_s,
-                                   int32_t* sel) {
+                                   int32_t* sel, uint32_t* floor_out = nullptr) {
   static_assert(NK <= 32, "a thread's picks fit one 32-bit mask");
   uint32_t* ck = hist;                                       // candidates, after the passes
   int32_t* cp = reinterpret_cast<int32_t*>(hist + CAND);     // their positions
@@ -149,7 +160,10 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
   // every wave has read the last pass's results before res_s[0] is reused; the passes left
   // the histogram (masks included) zero
   __syncthreads();
-  if (tid == 0) res_s[0] = 0;
+  if (tid == 0) {
+    res_s[0] = 0;
+    if (floor_out) *floor_out = lo;
+  }
   __syncthreads();
   uint32_t pick = 0;  // bit j: key[j] is selected
   if (cnt <= CAND) {
@@ -340,6 +354,173 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_final(
   topk_refine<NK>(tid, key, [&](int j) { return cpos[NK * tid + j]; }, kmin, kmax, C, kmin,
                   false, hist, wsum, phase, res_s, sel);
   return sel;
+}
+
+// One chunk of a row (thread t: the chunk's position t, its order key k; 0: no key) lists
+// its candidates for the row's top-TOPK: every key at or above a cut, in ascending position
+// order, as u64 (row position | key << 32) at out[0 .. TK_LIST) through `rout` (the tail
+// zeroed). The cut comes from 256-bin histograms, each scanned by wave 0 from the top: the
+// low edge of the bin holding the TK_LIST_MIN-th key when that lists at most TK_LIST keys,
+// else a finer pass inside that bin, down to single key values (then just above the
+// value: fewer keys). A chunk of at most TK_LIST keys lists them all (cut 1). Returns the
+// cut: every key of the chunk below it is left out. `mm` (4 words) is set to ~0, 0, 0, 0
+// and `hist` (256 words) to zero by the caller before its last barrier; `wsum` holds 16
+// words. No __syncthreads_count (it reads the dispatch packet, so it waits for every
+// memory access in flight).
+__device__ inline uint32_t chunk_list(int tid, uint32_t k, int pos0, uint32_t* hist, int* wsum,
+                                      uint32_t* mm, __amdgpu_buffer_rsrc_t rout) {
+  const int l = tid & (WAVE - 1), w = tid >> 6;
+  const uint32_t kmx = wave_max_u32(k), kmn = ~wave_max_u32(k ? ~k : 0u);
+  const int wv = __popcll(__ballot(k != 0u));
+  if (l == 0) {
+    atomicMin(&mm[0], kmn);
+    atomicMax(&mm[1], kmx);
+    atomicAdd(&mm[3], (uint32_t)wv);
+  }
+  __syncthreads();
+  const int nv = (int)mm[3];
+  const uint32_t lo = mm[0], hi = mm[1];
+  uint32_t cut = 1u;
+  if (nv > TK_LIST) {  // CTA-uniform
+    // passes of 256 bins over [rlo, rhi], `above` keys above it, until the bin holding the
+    // TK_LIST_MIN-th key lists at most TK_LIST keys or is one key value wide: then the cut
+    // is its low edge, or just above it. The state crosses the barriers in mm (every
+    // thread read mm after the first barrier; wave 0 rewrites it after the next one).
+    uint32_t rlo = lo, rhi = hi;
+    int above0 = 0;
+    const uint32_t span = hi - lo;
+    const int bits = span ? 32 - __clz((int)span) : 0;
+    int sh = bits > 8 ? bits - 8 : 0;
+#pragma unroll 1
+    for (;;) {
+      if (k >= rlo && k <= rhi) atomicAdd(&hist[(k - rlo) >> sh], 1u);
+      __syncthreads();
+      if (w == 0) {
+        // lane l: bins 255 - 4 l .. 252 - 4 l (from the top), then an inclusive scan
+        const v4i h4 = reinterpret_cast<const v4i*>(hist)[63 - l];
+        reinterpret_cast<v4i*>(hist)[63 - l] = v4i{0, 0, 0, 0};
+        const int c4 = h4[0] + h4[1] + h4[2] + h4[3];
+        int above = above0 + wave_scan(c4) - c4;  // keys above the lane's four bins
+        int bin = -1, ab = 0, nb = 0;
+#pragma unroll
+        for (int g = 3; g >= 0; --g) {
+          const int n_b = h4[g];
+          if (bin < 0 && above < TK_LIST_MIN && TK_LIST_MIN <= above + n_b) {
+            bin = 4 * (63 - l) + g;
+            ab = above;
+            nb = n_b;
+          }
+          above += n_b;
+        }
+        // one lane finds it (the range holds the TK_LIST_MIN-th key)
+        const uint64_t fb = __ballot(bin >= 0);
+        const int src = fb ? (int)__ffsll((long long)fb) - 1 : 0;
+        const int fbin = __builtin_amdgcn_readlane(bin, src);
+        const int fab = __builtin_amdgcn_readlane(ab, src), fnb = __builtin_amdgcn_readlane(nb, src);
+        if (l == 0) {
+          const uint64_t edge = (uint64_t)rlo + ((uint64_t)(uint32_t)fbin << sh);
+          uint32_t st = 1u;  // bit 0: done
+          if (!fb) {
+            mm[2] = 0xFFFFFFFFu;
+          } else if (fab + fnb <= TK_LIST) {
+            mm[2] = (uint32_t)edge;
+          } else if (sh == 0) {
+            mm[2] = edge + 1ull > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)(edge + 1ull);
+          } else {  // refine inside the bin
+            const uint64_t top = edge + (1ull << sh) - 1ull;
+            mm[0] = (uint32_t)edge;
+            mm[1] = top > (uint64_t)rhi ? rhi : (uint32_t)top;
+            st = (uint32_t)fab << 1;
+          }
+          mm[3] = st;
+        }
+      }
+      __syncthreads();
+      const uint32_t st = mm[3];
+      if (st & 1u) break;
+      rlo = mm[0];
+      rhi = mm[1];
+      above0 = (int)(st >> 1);
+      sh = sh > 8 ? sh - 8 : 0;
+    }
+    cut = mm[2];
+  }
+  // ascending position order: the wave's prefix by ballot, the waves' totals through LDS
+  const bool on = k != 0u && k >= cut;
+  const uint64_t bal = __ballot(on);
+  const int pre = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+  if (l == 0) wsum[w] = __popcll(bal);
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < AT_WAVES; ++i) {
+    const int v = wsum[i];
+    base += i < w ? v : 0;
+    tot += v;
+  }
+  if (on)
+    __builtin_amdgcn_raw_buffer_store_b64(v2i{pos0 + tid, (int32_t)k}, rout,
+                                          (uint32_t)(base + pre) * 8u, 0, CP_DEV);
+  if (tid >= tot && tid < TK_LIST)
+    __builtin_amdgcn_raw_buffer_store_b64(v2i{0, 0}, rout, (uint32_t)tid * 8u, 0, CP_DEV);
+  return cut;
+}
+
+// The exact top-TOPK of a one-block row from its nch chunks' lists (chunk_list), or nullptr
+// when the lists cannot decide it. `rl` covers the lists ([nch][TK_LIST] u64, read through
+// L2 like the scores), `rcut` the chunks' cuts. Thread t holds entries 8 t .. 8 t + 7 (of
+// chunk t / 32), so the candidates run in ascending position order; their positions wait
+// in LDS past the histogram. The lists decide the selection when they hold at least TOPK
+// keys and no chunk's cut lies above the final bin's low edge: every key a chunk left out
+// then ranks below every selected key. `mm` (4 words) is set to ~0, 0, 0, 0 by the caller
+// before its last barrier. Returns the selected positions, ascending, at sel[0 .. TOPK).
+__device__ __attribute__((always_inline)) inline int32_t* topk_lists(
+    int tid, __amdgpu_buffer_rsrc_t rl, __amdgpu_buffer_rsrc_t rcut, int nch, uint8_t* arena,
+    int* wsum, uint32_t* mm, int* res_s) {
+  constexpr int NK = TK_NLIST * TK_LIST / AT_THREADS;
+  static_assert(NK * AT_THREADS == TK_NLIST * TK_LIST && TK_LIST % NK == 0, "list map");
+  int phase = 0;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(arena);
+  int32_t* sel = reinterpret_cast<int32_t*>(hist + 3 * CAND + AT_THREADS);
+  int32_t* cpos = reinterpret_cast<int32_t*>(hist + 4096);  // [NK x 1024]
+  static_assert((4096 + NK * AT_THREADS) * 4 <= TOPK_ARENA_WORDS * 4, "positions fit the arena");
+  const int ch = tid / (TK_LIST / NK);
+  v2i raw[NK];
+#pragma unroll
+  for (int j = 0; j < NK; ++j) raw[j] = ld8<CP_NONE>(rl, (uint32_t)(NK * tid + j) * 8u);
+  const uint32_t mycut =
+      (uint32_t)ld4<CP_NONE>(rcut, ch < nch && tid % (TK_LIST / NK) == 0 ? (uint32_t)ch * 4u
+                                                                          : 0x80000000u);
+  reinterpret_cast<v4i*>(hist)[tid] = v4i{0, 0, 0, 0};  // select_pass expects it zero
+  uint32_t key[NK];
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    cpos[NK * tid + j] = raw[j][0];
+    const uint32_t k = (uint32_t)raw[j][1];
+    key[j] = k;
+    cnt += k != 0u;
+    kmin = (k && k < kmin) ? k : kmin;
+    kmax = k > kmax ? k : kmax;
+  }
+  kmax = wave_max_u32(kmax);
+  kmin = ~wave_max_u32(~kmin);
+  if ((tid & (WAVE - 1)) == 0) {
+    atomicMin(&mm[0], kmin);
+    atomicMax(&mm[1], kmax);
+  }
+  int total;
+  (void)block_scan(cnt, wsum, phase, total);  // its barrier also publishes mm
+  if (total < AT_TOPK) return nullptr;
+  kmin = mm[0];
+  kmax = mm[1];
+  topk_refine<NK>(tid, key, [&](int j) { return cpos[NK * tid + j]; }, kmin, kmax, total, kmin,
+                  false, hist, wsum, phase, res_s, sel, &mm[1]);
+  if (mycut > mm[1]) atomicOr(&mm[2], 1u);
+  __syncthreads();
+  return mm[2] ? nullptr : sel;
 }
 
 }  // namespace mono

@@ -151,6 +151,27 @@ def test_attention_topk_sample_misled(gpu):
     assert np.array_equal(topk[0], want)
 
 
+def test_attention_topk_concentrated(gpu):
+    """Every score positive and the keys of the last 2048 positions scaled 2^9 above the
+    rest: the selection is exactly those positions. The chunks' candidate lists cannot
+    decide it (the last chunks' cuts lie above the lists' threshold), so the launch ranks
+    every score instead."""
+    print("case attention top-k concentrated in the last chunks", flush=True)
+    inp = synthetic.attention_inputs(2, 32768, gpu, seed=24)
+    inp.iq.fill_(0x22)  # every query code +1.0
+    inp.iqs.fill_(127)
+    inp.iw.abs_()
+    g = torch.Generator().manual_seed(24)
+    nib = torch.randint(1, 8, tuple(inp.plane.shape) + (2,), generator=g, dtype=torch.uint8)
+    inp.plane[:] = (nib[..., 0] | (nib[..., 1] << 4)).to(inp.plane.device)  # codes > 0
+    inp.plane_scale.fill_(118)
+    for r in range(2):
+        inp.plane_scale[inp.page_table[r, 480:].long()] = 127
+    _, _, topk = _check(AttnOp(gpu, max_rows=2), inp, full_score_rows=0)
+    for r in range(2):
+        assert np.array_equal(topk[r], np.arange(32768 - TOPK, 32768)), r
+
+
 def test_attention_deterministic_and_graph_replay(gpu):
     print("case attention determinism + graph", flush=True)
     inp = synthetic.attention_inputs(4, 32768, gpu, seed=5)
