@@ -80,6 +80,10 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
   p.fault_site = a->fault_site;
   p.fault_after = a->fault_after;
   p.timeline = a->timeline;
+  p.uv_w = nullptr;  // W_UV runs in the output block's own launch
+  p.uv_s = nullptr;
+  p.uv_shuf = 0;
+  p.uv_obuf[0] = p.uv_obuf[1] = nullptr;
   int grid = 0;
   int rc = monokernel_grid(&grid);
   if (rc) return rc;

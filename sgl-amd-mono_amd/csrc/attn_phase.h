@@ -115,6 +115,13 @@ struct AttnParams {
   uint32_t* host_err;
   int fault_site, fault_after;
   uint64_t* timeline;
+  // the one-launch layer (FUSED): W_UV runs in the merge (UvUnit) on the latents it has
+  // just merged, storing o as complemented bf16 pairs [16][4096] into the output block's
+  // hand-off buffer of the launch tag's parity (unused by a launch of its own)
+  const uint8_t* uv_w;
+  const float* uv_s;
+  int uv_shuf;
+  uint16_t* uv_obuf[2];
 };
 
 // 16x16x128 E2M1 x E2M1 -> f32, each operand's E8M0 scale the byte OA / OB of its dword
@@ -724,6 +731,11 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     float* wsp_s = reinterpret_cast<float*>(lds + AT_LDS_WSP);
     float& linv_s = *reinterpret_cast<float*>(lds + AT_LDS_LINV);
     static_assert(AT_HEADS == 32, "32 merge tasks a row");
+    constexpr bool uv = FUSED;  // the one-launch layer sets uv_w
+    float* uvx = red + AT_NSPLIT * AT_LAT;                    // [512] W_UV's x
+    uint16_t* uob = reinterpret_cast<uint16_t*>(uvx + AT_LAT);  // [128] its rows
+    static_assert((AT_NSPLIT * AT_LAT + AT_LAT) * 4 + 256 <= TOPK_ARENA_WORDS * 4, "merge LDS");
+    uint16_t* obuf = p.uv_obuf[tag & 1u];
     for (int task = b; task < ntask32; task += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
       if (!ok) break;
@@ -733,6 +745,9 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       const int n = row_n(r);
       const int k = n < AT_TOPK ? n : AT_TOPK;
       const int nsp = (k + SPLIT - 1) / SPLIT;
+      // W_UV's weights of head h, ahead of the wait (they depend on nothing of the launch)
+      UvUnit uu;
+      if constexpr (uv) uu.load(p.uv_w, p.uv_s, p.uv_shuf, h, tid, true);
       if (w == 0 && nsp > 0)
         ok = wait_until(guard, MONO_SITE_SPLIT, [&]() {
           return __all(l >= nsp || ld_dev(&split_done[r * AT_NSPLIT + l]) == tag);
@@ -783,12 +798,22 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       if (tid < AT_LAT) {
         float s = 0.f;
         for (int sp = 0; sp < nsp; ++sp) s += red[sp * AT_LAT + tid];
+        const uint32_t ob = bf16_bits(s * linv_s);
         // device coherent: in the layer launch the output block reads it next
         __builtin_amdgcn_raw_buffer_store_b16(
-            (uint16_t)bf16_bits(s * linv_s), rsrc(p.out, (uint32_t)R * AT_HEADS * AT_LAT * 2u),
+            (uint16_t)ob, rsrc(p.out, (uint32_t)R * AT_HEADS * AT_LAT * 2u),
             (uint32_t)((r * AT_HEADS + h) * AT_LAT + tid) * 2u, 0, CP_DEV);
+        if constexpr (uv) uvx[tid] = bf16_lo(ob);
       }
       __syncthreads();
+      if constexpr (uv) {
+        UvUnit::put(uu.dot(uvx, tid), tid, uob);
+        __syncthreads();
+        UvUnit::store(uob, tid,
+                      reinterpret_cast<uint32_t*>(obuf + ((size_t)r * AT_HEADS + h) * 128),
+                      0xFFFFFFFFu, nullptr);
+        __syncthreads();
+      }
     }
   }
 

@@ -1,14 +1,15 @@
 // The whole decoder layer as one persistent gfx950 launch: the front, the attention phase,
 // the output block and the FP8 MoE run back to back in every CTA of one 256-CTA launch.
 //
-// Between two phases sits a grid barrier (phase.h): a phase's stores are device coherent
-// and drained before its CTA arrives, the last arrival raises the barrier's flag to the
-// launch tag, and the next phase waits for the flag only after issuing the loads that do
-// not depend on the phase before it:
+// Before the attention and before the MoE sits a grid barrier (phase.h): a phase's stores
+// are device coherent and drained before its CTA arrives, the last arrival raises the
+// barrier's flag to the launch tag, and the next phase waits for the flag only after
+// issuing the loads that do not depend on the phase before it:
 //   attention  the index pages of its first score task (the rows' own keys, written by the
 //              front in this launch, are read again device coherent after the wait);
-//   output     its W_UV tile, its first o_proj tile and the residual rows;
 //   MoE        the norm weight and its router tile's weights.
+// The output block needs none: the attention's merge runs W_UV on the latents it merges
+// and stores o as complemented words, which o_proj's loads poll (zero: not written yet).
 // Every wait is deadline guarded; a failing wait lets every CTA run to the end of the
 // launch. The launch tag is the guard's epoch + 1, shared by the four phases (each keeps
 // its own scratch region), and the last CTA out zeroes the barrier counts and advances the
@@ -56,7 +57,7 @@ struct LayerParams {
   AttnParams at;
   PostParams po;
   MoeFp8Params m;
-  PhaseBarrier bar[3];
+  PhaseBarrier bar[2];  // front -> attention, output block -> MoE
   uint8_t* scratch;
   int32_t* guard;
   uint32_t* host_err;
@@ -79,14 +80,13 @@ __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
   stamp(p.timeline, LY_TL_FRONT);
   attn_phase<SPLIT, true, LONG>(p.at, lds, guard, tag, sh.ok,
                           BarrierWait{&p.bar[0], &guard, tag, MONO_SITE_PHASE, &sh.ok});
-  p.bar[1].arrive(tag);
   stamp(p.timeline, LY_TL_ATTN);
-  post_phase<true>(p.po, lds, guard, tag, sh.ok,
-                   BarrierWait{&p.bar[1], &guard, tag, MONO_SITE_PHASE, &sh.ok});
-  p.bar[2].arrive(tag);
+  // no barrier: the merge ran W_UV, and o's complemented words are their own hand-off
+  post_phase<true>(p.po, lds, guard, tag, sh.ok, NoWait{});
+  p.bar[1].arrive(tag);
   stamp(p.timeline, LY_TL_POST);
   moe_phase<LY_H, LY_I, SHUF, true>(p.m, lds, guard, tag, sh.ok,
-                                    BarrierWait{&p.bar[2], &guard, tag, MONO_SITE_PHASE, &sh.ok});
+                                    BarrierWait{&p.bar[1], &guard, tag, MONO_SITE_PHASE, &sh.ok});
   stamp(p.timeline, LY_TL_MOE);
   launch_end(sh, p.guard, tag, p.scratch,
              (uint32_t)LayerScratch(p.at.rows_max).bytes,
@@ -95,7 +95,7 @@ __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
              [&]() {
                moe_reset_queues<LY_H, LY_I>(p.m);
 #pragma unroll
-               for (int k = 0; k < 3; ++k) p.bar[k].reset();
+               for (int k = 0; k < 2; ++k) p.bar[k].reset();
              });
   stamp(p.timeline, LY_TL_END);
 }
@@ -231,6 +231,11 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   at.fault_site = a->fault_site;
   at.fault_after = a->fault_after;
   at.timeline = nullptr;
+  at.uv_w = a->w_uv;  // W_UV in the attention's merge
+  at.uv_s = a->s_uv;
+  at.uv_shuf = shuf;
+  for (int k = 0; k < 2; ++k)
+    at.uv_obuf[k] = reinterpret_cast<uint16_t*>(sc + S.post + k * PostScratch::OBUF);
 
   PostParams& po = p.po;
   po.rows = R;
@@ -276,7 +281,7 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   m.fault_after = a->fault_after;
   m.timeline = nullptr;
 
-  for (int k = 0; k < 3; ++k) {
+  for (int k = 0; k < 2; ++k) {
     p.bar[k].count = reinterpret_cast<uint32_t*>(sc + LayerScratch::BARRIERS + 256 * k);
     p.bar[k].flag = reinterpret_cast<uint32_t*>(sc + LayerScratch::BARRIERS + 256 * k + 128);
   }

@@ -1,8 +1,11 @@
 // The attention output block as one persistent gfx950 launch: the merged latent o_lat
 // through W_UV per head, then o_proj and the residual add of the W == 1 reduce.
 //   W_UV  o[r][h * 128 + v] = sum_c W_UV[h][v][c] o_lat[r][h][c], handed over in bf16 (the
-//         reference rounds o to bf16 before o_proj, kernel.py:4080-4123): 256 tiles of 16
-//         rows, one a CTA, issued before anything else so they lead every CU's queue.
+//         reference rounds o to bf16 before o_proj, kernel.py:4080-4123): a task a (token,
+//         head) on the vector units (UvUnit), issued before anything else so it leads
+//         every CU's queue. In the one-launch layer the attention's merge runs these tasks
+//         instead, on the latents it has just merged (same arithmetic, same bits), and
+//         this phase starts with o_proj, waiting for nothing but o itself.
 //   o_proj a[r][n] = bf16(h[r][n] + sum_k W_o[n][k] o[r][k]): 448 tiles of 16 rows, two
 //         at a time a CTA: the first tile's weights and h in flight from the launch's
 //         start, the second's from the moment W_UV's outputs are stored.
@@ -31,9 +34,7 @@ constexpr int PO_MAXR = 16;
 constexpr int PO_MAX_GRID = 1024;
 constexpr int PO_TILES = PO_HID / 16;   // o_proj tiles of 16 rows
 
-using GemvUV = Gemv<8, 1, 1>;   // 16 rows of a head: 8 K-splits of 64 (waves 0-7)
 using GemvO = Gemv<16, 1, 4>;   // 16 rows: 16 K-splits of 256
-constexpr int PO_UV_TILES = PO_HEADS * PO_V / GemvUV::ROWS;
 
 struct PostScratch {
   // two hand-off buffers of o, u32 [16][4096 / 2] complemented bf16 pairs
@@ -58,11 +59,12 @@ struct PostParams {
   uint64_t* timeline;
 };
 
-constexpr int PO_LDS_BYTES = 40 * 64 * 16;  // red[40][64]: o_proj [0, 32) two tiles, W_UV [32, 40)
+constexpr int PO_LDS_BYTES = 40 * 64 * 16;  // red[32][64] of o_proj's two tiles, then W_UV's x and rows
 
 // The output block in one CTA of a launch. FUSED: it runs after the attention phase in
-// the same launch, so o_lat is read device coherent, after `ready` (the attention's
-// barrier), which it calls once its weight prefetch and the residual rows are in flight.
+// the same launch, whose merge stored o; `ready` is called once the weight prefetch and
+// the residual rows are in flight (the layer passes NoWait: o's complemented words are
+// their own hand-off).
 template <bool FUSED, class Ready>
 __device__ __attribute__((always_inline)) inline void post_phase(const PostParams& p, uint8_t* lds,
                                                                  Guard& guard, uint32_t tag,
@@ -74,21 +76,6 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
 
   const int tid = opaque_v((int)threadIdx.x);
   const int l = tid & 63, w = tid >> 6;
-  GemvJob ju{};
-  ju.x = p.o_lat;
-  ju.x_stride = PO_HEADS * PO_LAT;
-  ju.x_gstride = PO_LAT;
-  ju.w = p.w_uv;
-  ju.s = p.s_uv;
-  ju.N = PO_V;
-  ju.K = PO_LAT;
-  ju.G = PO_HEADS;
-  ju.shuf = p.shuf;
-  ju.out_bf = obuf;
-  ju.out_stride = PO_O;
-  ju.out_gstride = PO_V;
-  ju.out_xor = 0xFFFFFFFFu;
-  ju.out_plain = p.o;
   GemvJob jo{};
   jo.x = obuf;
   jo.x_stride = PO_O;
@@ -102,23 +89,10 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
   jo.out_stride = PO_HID;
   jo.res = p.h;
   jo.res_stride = PO_HID;
-  const GemvUV gu(tid);
   const GemvO go(tid);
-  constexpr int UV_TPR = PO_V / GemvUV::ROWS;            // W_UV tiles a head
-  constexpr int UV_STORE = GemvUV::ROWS * 16;            // threads of a W_UV epilogue
   const __amdgpu_buffer_rsrc_t rh = rsrc(p.h, (uint32_t)R * PO_HID * 2u);
   const int etok = (tid >> 4) & 15, erow = tid & 15;     // o_proj epilogue coordinates
 
-  // ---------------------------------------------------------------- prefetch
-  // W_UV tile b (waves 0-7), then o_proj tile b (all waves) and h; o_proj tile b + nblk
-  // only once W_UV's outputs are stored. The barrier puts every W_UV load of the CU ahead
-  // of every o_proj load: the CU's vector memory path serves its waves' requests in
-  // issue order, stores included, and drains a prefetch at the CU's share of HBM
-  // bandwidth (~23 KB/us), so a store issued behind both tiles (128 KB) would wait ~4 us
-  // and hold back the o hand-off; one tile keeps HBM busy through W_UV.
-  const bool uv0 = b < PO_UV_TILES;
-  v4i wu[1], xu[1][2];
-  float su[1];
   int a0 = b, a1 = b + nblk;
   v4i w0[4], w1[4];
   float s0[4], s1[4];
@@ -130,41 +104,68 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
   };
   int hres;
   bool ok = true;
-  gu.issue(ju, b / UV_TPR, b % UV_TPR, wu, su, uv0);
-  if constexpr (FUSED) {
-    // every weight and the residual in flight, then the wait for o_lat
-    go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
-    hres = load_h(a0, a1);
-    ok = ready();
-    gu.load_x<CP_NONE>(ju, b / UV_TPR, R, xu, uv0 && ok);
-  } else {
-    gu.load_x<CP_NONE>(ju, b / UV_TPR, R, xu, uv0);
+  // W_UV tasks (token r, head h) = u = r * 32 + h, CTA b taking u = b, b + nblk, ...
+  // (UvUnit). In the one-launch layer the attention's merge runs them (FUSED: none here).
+  UvUnit uu;
+  v4i xv = {0, 0, 0, 0};
+  const int nuv = FUSED ? 0 : R * PO_HEADS;
+  float* uvx = reinterpret_cast<float*>(lds + 32 * 64 * 16);  // [512], past o_proj's red
+  uint16_t* uob = reinterpret_cast<uint16_t*>(uvx + PO_LAT);   // [128]
+  static_assert(32 * 64 * 16 + PO_LAT * 4 + PO_V * 2 <= PO_LDS_BYTES, "W_UV LDS");
+  auto uv_x = [&](int u) -> v4i {  // token r's latents of head h: 64 threads x 8 bf16
+    const int r = u / PO_HEADS, h = u % PO_HEADS;
+    return ld16<CP_NONE>(
+        rsrc(p.o_lat + ((size_t)r * PO_HEADS + h) * PO_LAT, u < nuv && tid < 64 ? PO_LAT * 2 : 0),
+        (uint32_t)(tid & 63) * 16u);
+  };
+  auto uv_run = [&](int u) {
+    const int r = u / PO_HEADS, h = u % PO_HEADS;
+    if (tid < 64) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uvx[tid * 8 + 2 * i] = bf16_lo((uint32_t)xv[i]);
+        uvx[tid * 8 + 2 * i + 1] = bf16_hi((uint32_t)xv[i]);
+      }
+    }
     __syncthreads();
-    go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
-    hres = load_h(a0, a1);
+    UvUnit::put(uu.dot(uvx, tid), tid, uob);
+    __syncthreads();
+    UvUnit::store(uob, tid, reinterpret_cast<uint32_t*>(obuf + (size_t)r * PO_O + h * PO_V),
+                  0xFFFFFFFFu,
+                  p.o ? reinterpret_cast<uint32_t*>(p.o + (size_t)r * PO_O + h * PO_V) : nullptr);
+  };
+
+  // ---------------------------------------------------------------- prefetch
+  // W_UV task b's weights and latents, then o_proj tile b (all waves) and h; o_proj tile
+  // b + nblk only once W_UV's outputs are stored. The barrier puts every W_UV load of the
+  // CU ahead of every o_proj load: the CU's vector memory path serves its waves' requests
+  // in issue order, stores included, and drains a prefetch at the CU's share of HBM
+  // bandwidth (~23 KB/us), so a store issued behind both tiles (128 KB) would wait ~4 us
+  // and hold back the o hand-off; one tile keeps HBM busy through W_UV.
+  if constexpr (!FUSED) {
+    uu.load(p.w_uv, p.s_uv, p.shuf, b % PO_HEADS, tid, b < nuv);
+    xv = uv_x(b);
+    __syncthreads();
   }
+  go.issue(jo, 0, a0, w0, s0, a0 < PO_TILES);
+  hres = load_h(a0, a1);
+  if constexpr (FUSED) ok = ready();
 
   // ---------------------------------------------------------------- W_UV
-  // tile b from the prefetch (no loads in this branch: the wait for wu / xu stays exact)
-  if (uv0) {
-    gu.dot(wu, su, xu, red + 32);
-    // The W_UV loads retire here on every wave: the waves outside the tile skip the dot,
-    // and on their path the compiler would otherwise wait at later register writes for
-    // loads behind them too (the o_proj prefetch). 7 loads follow them: an o_proj tile's
-    // 4 weight and 2 scale loads, and h.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(7));
-    __syncthreads();
-    if (tid < UV_STORE) GemvUV::epilogue(ju, b / UV_TPR, b % UV_TPR, R, tid, red + 32);
-    __syncthreads();
-  }
-  // more W_UV tiles than CTAs (fewer than 256 CUs): the rest without prefetch
-  for (int u = b + nblk; u < (ok ? PO_UV_TILES : 0); u += nblk) {
-    gu.issue(ju, u / UV_TPR, u % UV_TPR, wu, su);
-    gu.load_x<CP_NONE>(ju, u / UV_TPR, R, xu);
-    gu.dot(wu, su, xu, red + 32);
-    __syncthreads();
-    if (tid < UV_STORE) GemvUV::epilogue(ju, u / UV_TPR, u % UV_TPR, R, tid, red + 32);
-    __syncthreads();
+  if constexpr (!FUSED) {
+    if (b < nuv) {
+      // W_UV's loads retire here; 7 follow them: the o_proj tile's 4 weight and 2 scale
+      // loads, and h
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(7));
+      uv_run(b);
+    }
+    // more W_UV tasks than CTAs: the rest without prefetch
+    for (int u = b + nblk; u < nuv; u += nblk) {
+      __syncthreads();
+      uu.load(p.w_uv, p.s_uv, p.shuf, u % PO_HEADS, tid, true);
+      xv = uv_x(u);
+      uv_run(u);
+    }
   }
   go.issue(jo, 0, a1, w1, s1, a1 < PO_TILES);
   // clear this CTA's slice of the next launch's hand-off buffer
