@@ -375,18 +375,24 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         }
       } else {
         const int nch = (n + AT_CHUNK - 1) / AT_CHUNK;
-        if (w == 0)
-          ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
-            return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + l]) == tag);
-          });
-        // topk_lists' / topk_select's minimum, maximum and flag words, set before the barrier
+        // topk_lists' / topk_select's minimum, maximum and flag words, set before a barrier
         if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = v4i{-1, 0, 0, 0};
-        ok = cta_all(ok, ok_s);
+        __syncthreads();
+        // each wave waits for its own chunks' done words, then loads their lists at once
+        const uint32_t* dw = score_done + r * AT_NCHUNK;
+        int32_t* sel = topk_lists(
+            tid, rsrc(lists + (size_t)r * TK_NLIST * TK_LIST, (uint32_t)(nch * TK_LIST * 8)),
+            rsrc(cuts + r * TK_NLIST, (uint32_t)nch * 4u), nch, smem, wsum, mm_s, res_s,
+            [&](int c0, int c1) {
+              return wait_until(guard, MONO_SITE_SCORES, [&]() {
+                return __all((c0 >= nch || ld_dev(&dw[c0]) == tag) &&
+                             (c1 >= nch || ld_dev(&dw[c1]) == tag));
+              });
+            },
+            ok);
         if (ok) {
-          // the chunks' candidate lists, or, where they cannot decide it, every score
-          int32_t* sel = topk_lists(
-              tid, rsrc(lists + (size_t)r * TK_NLIST * TK_LIST, (uint32_t)(nch * TK_LIST * 8)),
-              rsrc(cuts + r * TK_NLIST, (uint32_t)nch * 4u), nch, smem, wsum, mm_s, res_s);
+          // where the lists cannot decide it (every chunk is done: each wave saw its own),
+          // every score
           if (!sel) {
             if (tid == 0) {
               mm_s[0] = 0xFFFFFFFFu;
@@ -732,9 +738,12 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     float& linv_s = *reinterpret_cast<float*>(lds + AT_LDS_LINV);
     static_assert(AT_HEADS == 32, "32 merge tasks a row");
     constexpr bool uv = FUSED;  // the one-launch layer sets uv_w
-    float* uvx = red + AT_NSPLIT * AT_LAT;                    // [512] W_UV's x
-    uint16_t* uob = reinterpret_cast<uint16_t*>(uvx + AT_LAT);  // [128] its rows
-    static_assert((AT_NSPLIT * AT_LAT + AT_LAT) * 4 + 256 <= TOPK_ARENA_WORDS * 4, "merge LDS");
+    v4f (*uvred)[64] = reinterpret_cast<v4f (*)[64]>(red + AT_NSPLIT * AT_LAT);  // [16][64]
+    uint16_t* uvx = reinterpret_cast<uint16_t*>(uvred + 16);                      // [512] x
+    uint16_t* uob = uvx + AT_LAT;                                                 // [128] rows
+    static_assert(AT_NSPLIT * AT_LAT * 4 + 16 * 64 * 16 + (AT_LAT + 128) * 2 <=
+                      TOPK_ARENA_WORDS * 4,
+                  "merge LDS");
     uint16_t* obuf = p.uv_obuf[tag & 1u];
     for (int task = b; task < ntask32; task += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
@@ -803,11 +812,13 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         __builtin_amdgcn_raw_buffer_store_b16(
             (uint16_t)ob, rsrc(p.out, (uint32_t)R * AT_HEADS * AT_LAT * 2u),
             (uint32_t)((r * AT_HEADS + h) * AT_LAT + tid) * 2u, 0, CP_DEV);
-        if constexpr (uv) uvx[tid] = bf16_lo(ob);
+        if constexpr (uv) uvx[tid] = (uint16_t)ob;
       }
       __syncthreads();
       if constexpr (uv) {
-        UvUnit::put(uu.dot(uvx, tid), tid, uob);
+        uu.dot(uvx, uvred, tid);
+        __syncthreads();
+        if (tid < 128) uob[tid] = (uint16_t)bf16_bits(UvUnit::row(uvred, tid));
         __syncthreads();
         UvUnit::store(uob, tid,
                       reinterpret_cast<uint32_t*>(obuf + ((size_t)r * AT_HEADS + h) * 128),

@@ -203,63 +203,61 @@ __device__ inline bool gemv_tasks(const GemvJob& j, int R, int b, int nblk, int 
   return ok;
 }
 
-// W_UV of one (token, head) on the vector units, the same arithmetic wherever it runs (the
-// output block's own launch, or the attention's merge in the one-launch layer, so both
-// give the same bits): o[v] = bf16(sum_c W[v][c] x[c] s[c / 128]) for the head's 128 rows
-// v, W in E4M3 [128][512] (row-major, or AITER's (16, 16) shuffle: 16 rows x 64 K a 1 KiB
-// tile, lane l's 16 bytes at 16 l), s the head's four f32 block scales, x the 512 latents
-// (f32 of their bf16 values) in LDS. Thread t takes row v = t / 8 and c in [64 (t % 8),
-// + 64): 64 exact E4M3 x f32 products summed in c order, times the block scale; a row's 8
-// partials then meet by a fixed butterfly (xor 1, xor 2, half-row mirror), after which
-// every lane of the 8 holds the same sum.
+// W_UV of one (token, head), the same arithmetic wherever it runs (the output block's own
+// launch, or the attention's merge in the one-launch layer, so both give the same bits):
+// o[v] = bf16(sum_c W[v][c] x[c] s[c / 128]) for the head's 128 rows v, W in E4M3
+// [128][512] (row-major or AITER's (16, 16) shuffle), s the head's four f32 block scales,
+// x the 512 latents in bf16 in LDS. Wave w takes rows 16 (w % 8) .. + 15 and K [256
+// (w / 8), + 256) as 4 steps of 64 K with Gemv's lane map (lane l: row l % 16, K + 16
+// (l / 16) .. + 15), two 16x16x32 bf16 MFMAs a step whose B operand is x in column 0
+// (the other columns zero), each step scaled by its block's scale; the two K halves of a
+// row are then summed in a fixed order.
 struct UvUnit {
-  static constexpr int THREADS = 1024;  // 128 rows x 8 K slices
+  static constexpr int THREADS = 1024;
   v4i w[4];
-  float s;
+  float s[4];
 
-  // this thread's 64 weight bytes and block scale of head h (on = false: zeros, no traffic)
+  // this wave's weight bytes and block scales of head h (on = false: zeros, no traffic)
   __device__ void load(const uint8_t* w_uv, const float* s_uv, int shuf, int h, int tid,
                        bool on) {
-    const int v = tid >> 3, kq = tid & 7;
+    const int l = tid & 63, wv = tid >> 6, rt = wv & 7, kh = wv >> 3;
     const __amdgpu_buffer_rsrc_t r = rsrc(w_uv + (size_t)h * 128 * 512, on ? 128u * 512u : 0u);
+    const uint32_t vo = shuf ? (uint32_t)l * 16 : (uint32_t)((l & 15) * 512 + 16 * (l >> 4));
+    const int sh = shuf ? 4 : 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t off = shuf ? (uint32_t)((v >> 4) * 8192 + kq * 1024 + (q * 16 + (v & 15)) * 16)
-                                : (uint32_t)(v * 512 + kq * 64 + q * 16);
-      w[q] = ld16<CP_NONE>(r, off);
+    for (int st = 0; st < 4; ++st)
+      w[st] = ld16s<CP_NONE>(r, vo, (uint32_t)(rt * 16 * 512) + ((uint32_t)(256 * kh + 64 * st) << sh));
+    const __amdgpu_buffer_rsrc_t rs = rsrc(s_uv + h * 4, on ? 16u : 0u);
+    s[0] = s[1] = __int_as_float(ld4<CP_NONE>(rs, (uint32_t)(2 * kh) * 4u));
+    s[2] = s[3] = __int_as_float(ld4<CP_NONE>(rs, (uint32_t)(2 * kh + 1) * 4u));
+  }
+  // the wave's scaled partial into red[w] (16 x 64 v4f of LDS; a barrier must follow)
+  __device__ void dot(const uint16_t* x, v4f (*red)[64], int tid) const {
+    const int l = tid & 63, wv = tid >> 6, kh = wv >> 3;
+    const bool col0 = (l & 15) == 0;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int k0 = 256 * kh + 64 * st + 16 * (l >> 4);
+      const v4i z = {0, 0, 0, 0};
+      const v4i x0 = col0 ? *reinterpret_cast<const v4i*>(x + k0) : z;
+      const v4i x1 = col0 ? *reinterpret_cast<const v4i*>(x + k0 + 8) : z;
+      v4f d = {0.f, 0.f, 0.f, 0.f};
+      d = mfma_bf16(fp8x8_bf16((uint32_t)w[st][0], (uint32_t)w[st][1]), __builtin_bit_cast(v8bf, x0), d);
+      d = mfma_bf16(fp8x8_bf16((uint32_t)w[st][2], (uint32_t)w[st][3]), __builtin_bit_cast(v8bf, x1), d);
+      acc += d * s[st];
     }
-    s = __builtin_bit_cast(float, ld4<CP_NONE>(rsrc(s_uv + h * 4, on ? 16u : 0u),
-                                              (uint32_t)(kq >> 1) * 4u));
+    red[wv][l] = acc;
   }
-  // the row's sum (every lane of its 8); x: the head's 512 latents in LDS
-  __device__ float dot(const float* x, int tid) const {
-    const v4f* xv = reinterpret_cast<const v4f*>(x + (tid & 7) * 64);
-    float acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)w[q][d], 1.0f, false);
-        const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)w[q][d], 1.0f, true);
-        const v4f xx = xv[q * 4 + d];
-        acc = fmaf(lo[0], xx[0], acc);
-        acc = fmaf(lo[1], xx[1], acc);
-        acc = fmaf(hi[0], xx[2], acc);
-        acc = fmaf(hi[1], xx[3], acc);
-      }
-    float p = acc * s;
-    p += dpp_f<DPP_XOR1>(p);
-    p += dpp_f<DPP_XOR2>(p);
-    p += dpp_f<DPP_HALF_MIRROR>(p);
-    return p;
+  // row v (< 128) after the barrier: its K halves in order
+  __device__ static float row(const v4f (*red)[64], int v) {
+    const int rt = v >> 4, L = 16 * ((v & 15) >> 2), j = v & 3;
+    return red[rt][L][j] + red[rt + 8][L][j];
   }
-  // rows -> bf16 pairs: lanes t % 8 == 0 put their row's bits in ob (u16 [128], LDS); after
-  // a barrier, threads t < 64 store pair t (rows 2t, 2t + 1) XOR `xr` at dst[t] (device
-  // coherent), and plainly at plain[t] if given. A pair of all-ones bits becomes two NaNs
-  // whose complement stays nonzero (a hand-off reads zero as "not written yet").
-  __device__ static void put(float y, int tid, uint16_t* ob) {
-    if ((tid & 7) == 0) ob[tid >> 3] = (uint16_t)bf16_bits(y);
-  }
+  // rows -> bf16 pairs: thread t < 64 stores pair t (rows 2t, 2t + 1, from ob: u16 [128]
+  // in LDS) XOR `xr` at dst[t] (device coherent), and plainly at plain[t] if given. A pair
+  // of all-ones bits becomes two NaNs whose complement stays nonzero (a hand-off reads zero
+  // as "not written yet").
   __device__ static void store(const uint16_t* ob, int tid, uint32_t* dst, uint32_t xr,
                                uint32_t* plain) {
     if (tid < 64) {

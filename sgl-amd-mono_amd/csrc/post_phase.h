@@ -59,7 +59,8 @@ struct PostParams {
   uint64_t* timeline;
 };
 
-constexpr int PO_LDS_BYTES = 40 * 64 * 16;  // red[32][64] of o_proj's two tiles, then W_UV's x and rows
+// red[32][64] of o_proj's two tiles, then W_UV's partials [16][64], x and rows
+constexpr int PO_LDS_BYTES = 48 * 64 * 16 + 512 * 2 + 128 * 2;
 
 // The output block in one CTA of a launch. FUSED: it runs after the attention phase in
 // the same launch, whose merge stored o; `ready` is called once the weight prefetch and
@@ -109,9 +110,10 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
   UvUnit uu;
   v4i xv = {0, 0, 0, 0};
   const int nuv = FUSED ? 0 : R * PO_HEADS;
-  float* uvx = reinterpret_cast<float*>(lds + 32 * 64 * 16);  // [512], past o_proj's red
-  uint16_t* uob = reinterpret_cast<uint16_t*>(uvx + PO_LAT);   // [128]
-  static_assert(32 * 64 * 16 + PO_LAT * 4 + PO_V * 2 <= PO_LDS_BYTES, "W_UV LDS");
+  v4f (*uvred)[64] = red + 32;                                       // [16][64], past o_proj's
+  uint16_t* uvx = reinterpret_cast<uint16_t*>(lds + 48 * 64 * 16);  // [512]
+  uint16_t* uob = uvx + PO_LAT;                                      // [128]
+  static_assert(48 * 64 * 16 + PO_LAT * 2 + PO_V * 2 <= PO_LDS_BYTES, "W_UV LDS");
   auto uv_x = [&](int u) -> v4i {  // token r's latents of head h: 64 threads x 8 bf16
     const int r = u / PO_HEADS, h = u % PO_HEADS;
     return ld16<CP_NONE>(
@@ -120,15 +122,11 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
   };
   auto uv_run = [&](int u) {
     const int r = u / PO_HEADS, h = u % PO_HEADS;
-    if (tid < 64) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uvx[tid * 8 + 2 * i] = bf16_lo((uint32_t)xv[i]);
-        uvx[tid * 8 + 2 * i + 1] = bf16_hi((uint32_t)xv[i]);
-      }
-    }
+    if (tid < 64) reinterpret_cast<v4i*>(uvx)[tid] = xv;
     __syncthreads();
-    UvUnit::put(uu.dot(uvx, tid), tid, uob);
+    uu.dot(uvx, uvred, tid);
+    __syncthreads();
+    if (tid < PO_V) uob[tid] = (uint16_t)bf16_bits(UvUnit::row(uvred, tid));
     __syncthreads();
     UvUnit::store(uob, tid, reinterpret_cast<uint32_t*>(obuf + (size_t)r * PO_O + h * PO_V),
                   0xFFFFFFFFu,

@@ -471,13 +471,17 @@ __device__ inline uint32_t chunk_list(int tid, uint32_t k, int pos0, uint32_t* h
 // when the lists cannot decide it. `rl` covers the lists ([nch][TK_LIST] u64, read through
 // L2 like the scores), `rcut` the chunks' cuts. Thread t holds entries 8 t .. 8 t + 7 (of
 // chunk t / 32), so the candidates run in ascending position order; their positions wait
-// in LDS past the histogram. The lists decide the selection when they hold at least TOPK
+// in LDS past the histogram. Wave w first waits for its chunks 2 w and 2 w + 1 (`wait`:
+// wave-uniform, false when the launch fails, then `ok` turns false CTA-wide and it
+// returns nullptr), so the loads of chunks already done are in flight while later ones
+// are still being scored. The lists decide the selection when they hold at least TOPK
 // keys and no chunk's cut lies above the final bin's low edge: every key a chunk left out
 // then ranks below every selected key. `mm` (4 words) is set to ~0, 0, 0, 0 by the caller
 // before its last barrier. Returns the selected positions, ascending, at sel[0 .. TOPK).
+template <class WaitChunks>
 __device__ __attribute__((always_inline)) inline int32_t* topk_lists(
     int tid, __amdgpu_buffer_rsrc_t rl, __amdgpu_buffer_rsrc_t rcut, int nch, uint8_t* arena,
-    int* wsum, uint32_t* mm, int* res_s) {
+    int* wsum, uint32_t* mm, int* res_s, WaitChunks wait, bool& ok) {
   constexpr int NK = TK_NLIST * TK_LIST / AT_THREADS;
   static_assert(NK * AT_THREADS == TK_NLIST * TK_LIST && TK_LIST % NK == 0, "list map");
   int phase = 0;
@@ -486,6 +490,9 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_lists(
   int32_t* cpos = reinterpret_cast<int32_t*>(hist + 4096);  // [NK x 1024]
   static_assert((4096 + NK * AT_THREADS) * 4 <= TOPK_ARENA_WORDS * 4, "positions fit the arena");
   const int ch = tid / (TK_LIST / NK);
+  static_assert(WAVE / (TK_LIST / NK) == 2, "two chunks a wave");
+  const int w2 = 2 * (tid >> 6);
+  if (!wait(w2, w2 + 1) && (tid & (WAVE - 1)) == 0) atomicOr(&mm[2], 2u);
   v2i raw[NK];
 #pragma unroll
   for (int j = 0; j < NK; ++j) raw[j] = ld8<CP_NONE>(rl, (uint32_t)(NK * tid + j) * 8u);
@@ -513,6 +520,10 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_lists(
   }
   int total;
   (void)block_scan(cnt, wsum, phase, total);  // its barrier also publishes mm
+  if (mm[2] & 2u) {
+    ok = false;
+    return nullptr;
+  }
   if (total < AT_TOPK) return nullptr;
   kmin = mm[0];
   kmax = mm[1];
@@ -520,7 +531,7 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_lists(
                   false, hist, wsum, phase, res_s, sel, &mm[1]);
   if (mycut > mm[1]) atomicOr(&mm[2], 1u);
   __syncthreads();
-  return mm[2] ? nullptr : sel;
+  return (mm[2] & 1u) ? nullptr : sel;
 }
 
 }  // namespace mono
