@@ -146,6 +146,7 @@ struct MoeLds {
   static constexpr int RSTD = RSM + 2 * 2 * 16 * 4;              // f32 [16]
   static constexpr int NEXT = RSTD + MOE_MAXR * 4;               // int
   static constexpr int N1 = NEXT + 4;                            // int
+  static constexpr int ORW = N1 + 4;                             // int: a CTA-wide OR
   static constexpr int HEAD = N1 + 12;                           // u32 [4], 16-byte aligned
   static constexpr int BYTES = HEAD + 16;
   static_assert(XS % 16 == 0 && RED % 16 == 0 && HEAD % 16 == 0, "aligned LDS carving");
@@ -610,6 +611,18 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     {
       uint32_t* xw = reinterpret_cast<uint32_t*>(xq_lds);
       bool got = ok_s != 0;  // set before the barrier above (CTA-uniform)
+      // a CTA-wide OR through an LDS word (zero on entry, left zero). Not
+      // __syncthreads_or: it reads the dispatch packet, and so waits for every load in
+      // flight, the whole ring
+      int& orw = *reinterpret_cast<int*>(lds + LO::ORW);
+      auto cta_or = [&](bool v) {
+        if (__ballot(v) && l == 0) atomicOr(&orw, 1);
+        __syncthreads();
+        const bool r = orw != 0;
+        __syncthreads();
+        if (tid == 0) orw = 0;
+        return r;
+      };
       auto check = [&]() {
         int zero = 0;
         static_assert(G::SZ_XQ / 4 % G::THREADS == 0, "whole passes over the image");
@@ -619,8 +632,9 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
           zero |= v == 0u;
           xw[i] = ~v;
         }
-        return __syncthreads_or(zero) != 0;
+        return cta_or(zero != 0);
       };
+      if (tid == 0) orw = 0;
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * KCW));
       asm volatile("" ::: "memory");
       __syncthreads();
@@ -638,7 +652,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
             got = false;
           }
         }
-        got = __syncthreads_or(got ? 0 : 1) == 0 && got;
+        got = !cta_or(!got) && got;
         if (!got) break;
         copy_image(0, G::WAVES, true);
         drain();
