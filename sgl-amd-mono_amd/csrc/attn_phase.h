@@ -805,8 +805,14 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       }
       __syncthreads();
       if (tid < AT_LAT) {
+        // every split's term read at once (independent LDS reads), then summed in split
+        // order over the row's splits
+        float v[AT_NSPLIT];
+#pragma unroll
+        for (int sp = 0; sp < AT_NSPLIT; ++sp) v[sp] = red[sp * AT_LAT + tid];
         float s = 0.f;
-        for (int sp = 0; sp < nsp; ++sp) s += red[sp * AT_LAT + tid];
+#pragma unroll
+        for (int sp = 0; sp < AT_NSPLIT; ++sp) s = sp < nsp ? s + v[sp] : s;
         const uint32_t ob = bf16_bits(s * linv_s);
         // device coherent: in the layer launch the output block reads it next
         __builtin_amdgcn_raw_buffer_store_b16(

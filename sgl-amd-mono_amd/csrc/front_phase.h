@@ -65,10 +65,10 @@ using GemvC = Gemv<2, 8, 1>;   // 128 rows over K 128: 8 row groups x 2 K-splits
 
 struct FrontScratch {
   // one parity's hand-off buffers (complemented words)
-  static constexpr size_t HA = 0;                                           // f32 [16][2240]
-  static constexpr size_t HW = HA + (size_t)FR_MAXR * FR_HA * 4;            // f32 [7][16][64]
-  static constexpr size_t HN = HW + (size_t)FR_WCH * FR_MAXR * FR_IH * 4;   // bf16 [16][32][128]
-  static constexpr size_t HI = HN + (size_t)FR_MAXR * FR_HEADS * FR_NOPE * 2;  // bf16 [16][8192]
+  static constexpr size_t HA = 0;                                           // f32 [8][2240]
+  static constexpr size_t HW = HA + (size_t)FR_MAXR * FR_HA * 4;            // f32 [7][8][64]
+  static constexpr size_t HN = HW + (size_t)FR_WCH * FR_MAXR * FR_IH * 4;   // bf16 [8][32][128]
+  static constexpr size_t HI = HN + (size_t)FR_MAXR * FR_HEADS * FR_NOPE * 2;  // bf16 [8][8192]
   static constexpr size_t PARITY = (HI + (size_t)FR_MAXR * FR_IQ * 2 + 255) & ~(size_t)255;
   static constexpr size_t BYTES = 2 * PARITY;
 };
@@ -132,19 +132,47 @@ __device__ inline void pow2_ceil(float x, float& sc, float& inv) {
   inv = __uint_as_float((254u - e) << 23);
 }
 
+// one butterfly over lanes l and l ^ M (`up`: lane l holds the upper one): the lower lane
+// gets lo + hi, the upper lo - hi. On the VALU: DPP quad_perm for M = 1, 2, two DPP
+// mirrors for 4 (half-row mirror, then quad reversal) and 8 (row mirror, then half-row
+// mirror), v_permlane16_swap / v_permlane32_swap for 16, 32 (which hand every lane its
+// pair's lower and upper value).
+template <int M>
+__device__ inline float bfly(float v, bool up) {
+  if constexpr (M == 16 || M == 32) {
+    const uint32_t u = __float_as_uint(v);
+    const auto s = M == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const float lo = __uint_as_float(s[0]), hi = __uint_as_float(s[1]);
+    return up ? lo - hi : lo + hi;
+  } else {
+    float p;
+    if constexpr (M == 1) p = dpp_f<DPP_XOR1>(v);
+    else if constexpr (M == 2) p = dpp_f<DPP_XOR2>(v);
+    else if constexpr (M == 4) p = dpp_f<DPP_REV4>(dpp_f<DPP_HALF_MIRROR>(v));
+    else p = dpp_f<DPP_HALF_MIRROR>(dpp_f<DPP_MIRROR>(v));
+    return up ? p - v : v + p;
+  }
+}
+
 // the orthonormal 128-point Sylvester Hadamard transform of the values a wave holds,
 // lane l holding entries 2l and 2l + 1
 __device__ inline void fwht128(float& v0, float& v1, int l) {
   const float a = v0 + v1, b = v0 - v1;
   v0 = a;
   v1 = b;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float p0 = xor_f(v0, m), p1 = xor_f(v1, m);
-    const bool up = (l & m) != 0;
-    v0 = up ? p0 - v0 : v0 + p0;
-    v1 = up ? p1 - v1 : v1 + p1;
-  }
+  auto stage = [&](auto m_c) {
+    constexpr int M = decltype(m_c)::value;
+    const bool up = (l & M) != 0;
+    v0 = bfly<M>(v0, up);
+    v1 = bfly<M>(v1, up);
+  };
+  stage(std::integral_constant<int, 1>());
+  stage(std::integral_constant<int, 2>());
+  stage(std::integral_constant<int, 4>());
+  stage(std::integral_constant<int, 8>());
+  stage(std::integral_constant<int, 16>());
+  stage(std::integral_constant<int, 32>());
   constexpr float S = 0.08838834764831845f;  // 128^-1/2
   v0 *= S;
   v1 *= S;
@@ -167,8 +195,8 @@ __device__ inline uint32_t fp4_pair(float v0, float v1, uint32_t& e8) {
 // 4 lanes' bytes (lanes 4k .. 4k + 3) into one word, valid in lane 4k
 __device__ inline uint32_t gather4(uint32_t byte, int l) {
   uint32_t w = byte << (8 * (l & 3));
-  w |= xor_u(w, 1);
-  w |= xor_u(w, 2);
+  w |= dpp_u<DPP_XOR1>(w);
+  w |= dpp_u<DPP_XOR2>(w);
   return w;
 }
 

@@ -114,10 +114,6 @@ __device__ inline int opaque_zero() {
 
 __device__ inline int lane_id() { return __lane_id(); }
 
-__device__ inline float xor_f(float v, int m) { return __shfl_xor(v, m, WAVE); }
-__device__ inline uint32_t xor_u(uint32_t v, int m) {
-  return (uint32_t)__shfl_xor((int)v, m, WAVE);
-}
 
 // Butterfly reductions on the VALU (no LDS crossbar): DPP quad_perm pairs lanes i^1 and
 // i^2, row_half_mirror i <-> 7-i and row_mirror i <-> 15-i within each row of 16 lanes,
@@ -133,6 +129,7 @@ __device__ inline float dpp_f(float v) {
 }
 constexpr int DPP_XOR1 = 0xB1;       // quad_perm [1, 0, 3, 2]
 constexpr int DPP_XOR2 = 0x4E;       // quad_perm [2, 3, 0, 1]
+constexpr int DPP_REV4 = 0x1B;       // quad_perm [3, 2, 1, 0]
 constexpr int DPP_HALF_MIRROR = 0x141;
 constexpr int DPP_MIRROR = 0x140;
 
