@@ -90,6 +90,21 @@ int mono_reset(void* scratch, size_t scratch_bytes, int32_t* guard, mono_stream_
  * :1575-1629 + :4332-4350 (routing), :4352-4999 (up/gate), :5001-5187 (down), and
  * the W == 1 peer_reduce branch :1665-1669. */
 /* On-HBM layouts of FP8 expert weights [.., N, K] */
+/* Index-key caches (the indexer's keys, one per token, read in place):
+ * MONO_INDEX_FP4_PLANE  SGLang's FP4 index plane: plane [pages, 4, 64, 16] E2M1 and
+ *                       plane_scale [pages, 4, 64] E8M0 (the attention launch's layout note)
+ * MONO_INDEX_FP8_PAGE   SGLang's DSA index page on HIP: [pages, 8448] bytes, 64 tokens x 128
+ *                       E4M3 values in 16-token x 16-byte tiles (token t, dim d at (t / 16)
+ *                       * 2048 + (d / 16) * 256 + (t % 16) * 16 + d % 16), then the 64 tokens'
+ *                       power-of-two f32 scales (sgl_amd_mono/glm53/gfx950/kernel.py:534-550);
+ *                       plane_scale unused
+ * MONO_INDEX_FP8_ROWS   the same page with token-major values (t * 128 + d)
+ * With an FP8 page the index query iq is bf16 [R, 64, 128] (rotated, transformed, then
+ * rounded to bf16 once) and iqs is unused. */
+#define MONO_INDEX_FP4_PLANE 0
+#define MONO_INDEX_FP8_PAGE 1
+#define MONO_INDEX_FP8_ROWS 2
+
 #define MONO_LAYOUT_ROWMAJOR 0 /* plain row-major E4M3 */
 #define MONO_LAYOUT_AITER16 1  /* AITER (16, 16) shuffle: [N / 16, K / 32, 2, 16, 16 B],
                                   SGLang's in-place layout on gfx950
@@ -260,6 +275,7 @@ typedef struct {
   int32_t fault_site;        /* test fault injection (MONO_SITE_SCORES/TOPK/SPLIT) */
   int32_t fault_after;
   uint64_t* timeline;
+  int32_t index_format;      /* MONO_INDEX_*: plane / plane_scale and iq / iqs as it says */
 } MonoAttnArgs;
 
 size_t mono_attn_scratch_bytes(int32_t rows_max);
@@ -310,7 +326,11 @@ int mono_post_launch(const MonoPostArgs* args, mono_stream_t stream);
  * after the FWHT: sgl_amd_mono/deepseek_v4/gfx950/kernels/stages/indexer.py:242-254,
  * 330-335). RoPE pairs are interleaved (x0 c - x1 s,
  * x0 s + x1 c) with bf16 tables cos/sin [rope_rows, 32] indexed by position. A slot
- * outside the caches (e.g. -1, a pad row) writes nothing.
+ * outside the caches (e.g. -1, a pad row) writes nothing. With a DSA index page
+ * (MONO_INDEX_FP8_*) the index key's LayerNorm, RoPE and FWHT are not rounded and it is
+ * stored as E4M3 at a power-of-two per-token scale 2^ceil(log2(max(amax, 1e-4) / 448)),
+ * and the index query is rotated and transformed unrounded, then bf16 once
+ * (sgl_amd_mono/glm53/gfx950/kernel.py:2103-2168, 2928-2944).
  * Replaces sgl_amd_mono/glm53/gfx950/kernel.py:1781-2443 (stages qkv_a, q_norm, cache,
  * q_b, index_q, uk) and the FP4 index paths of
  * sgl_amd_mono/deepseek_v4/gfx950/kernels/stages/indexer.py:143-151,311-338,340-408. */
@@ -341,11 +361,11 @@ typedef struct {
   float* kv_scale;           /* optional f32 [kv_slots]: written with a power-of-two per-token
                                 scale; null: raw E4M3 at scale 1 (SGLang's pool layout),
                                 values saturating at +-448 */
-  uint8_t* plane;            /* [plane_pages, 4, 64, 16] */
-  uint8_t* plane_scale;      /* [plane_pages, 4, 64] */
+  uint8_t* plane;            /* [plane_pages, 4, 64, 16], or DSA pages [plane_pages, 8448] */
+  uint8_t* plane_scale;      /* [plane_pages, 4, 64] (FP4 plane only) */
   void* q;                   /* out bf16 [R, 32, 576]: q_lat | q_pe */
-  uint8_t* iq;               /* out [R, 64, 64] E2M1 */
-  uint8_t* iqs;              /* out [R, 4, 16, 4] E8M0 */
+  uint8_t* iq;               /* out [R, 64, 64] E2M1 (DSA pages: bf16 [R, 64, 128]) */
+  uint8_t* iqs;              /* out [R, 4, 16, 4] E8M0 (FP4 plane only) */
   float* iw;                 /* out f32 [R, 64] */
   void* scratch;             /* runtime owned, mono_front_scratch_bytes() */
   int32_t* guard;
@@ -357,6 +377,8 @@ typedef struct {
                                 LayerNorm */
   void* iq_raw;              /* optional out bf16 [R, 64, 128]: the index query W_iq q_an,
                                 before its RoPE */
+  int32_t index_format;      /* MONO_INDEX_*: the index key written as it says, iq / iqs
+                                made for it */
 } MonoFrontArgs;
 
 size_t mono_front_scratch_bytes(void);
@@ -437,6 +459,7 @@ typedef struct {
                                block, MoE */
   int32_t n_group;       /* group-limited routing: 0 or 1 none, else 2..16 groups */
   int32_t topk_group;    /* groups kept (topk_group * 256 / n_group >= 8) */
+  int32_t index_format;  /* MONO_INDEX_* of plane / plane_scale (and so of iq / iqs) */
 } MonoLayerArgs;
 
 size_t mono_layer_scratch_bytes(int32_t rows_max);

@@ -12,11 +12,16 @@
   3638-4123``; softmax scale ``glm53/gfx950/config.py:180-181``): K = V = the cached
   576-value row (latent 512 + rope 64) of each selected token, E4M3 times the token's
   f32 scale; scores = q . k * sm_scale, softmax over the selected tokens, o = P V[:, :512].
+* or the DSA (FP8) indexer scores (``index_scores_fp8``) over SGLang's DSA index pages:
+  [pages, 64 x 128 E4M3 values (16-token x 16-byte tiles, or token-major), 64 f32
+  scales], a bf16 query [64, 128] (``kernel.py:2684-2842``, layout :534-550).
 
 Pinned by ``tests/test_oracle_attn.py``: the scores against a dense dequantisation
 built slot by slot from bit fields and an independent matmul; a scale-code shift
 doubling them exactly; sparse MLA against ``torch.nn.functional.scaled_dot_product_attention``
-in f64; the selection of the chain against ``topk_sort``.
+in f64; the selection of the chain against ``topk_sort``; the DSA (FP8) page keys
+against a byte-by-byte decode through the reference's token formula, and their scores
+against one-hot queries and keys whose scores are closed forms.
 """
 
 from __future__ import annotations
@@ -25,6 +30,7 @@ import numpy as np
 import torch
 
 from . import formats as F
+from .front import dsa_value_offset
 from .topk import topk_sort
 
 PAGE = 64
@@ -71,6 +77,29 @@ def index_scores(q_fp4, q_scale, w, payload, kscale, pages, n, cols=None):
         dot = (k[:, c, :] @ q[:, c, :].T).astype(np.float64)  # [n, H]
         s += dot * np.exp2(ke[:, c].astype(np.float64))[:, None] * np.exp2(qe[:, c].astype(np.float64))[None, :]
     return np.maximum(s, 0.0) @ np.asarray(w, dtype=np.float64)
+
+
+def dsa_keys(pages_u8, pages, n, cols=None, tiled: bool = True):
+    """f64 [n, 128]: the first n keys of a request whose pages are ``pages`` (or the
+    positions ``cols``) from DSA index pages u8 [P, 8448]: each E4M3 value times its
+    token's f32 scale (the page decode of ``sgl_amd_mono/glm53/check.py:58-66``)."""
+    pos = np.arange(n) if cols is None else np.asarray(cols, dtype=np.int64)
+    page = np.asarray(pages)[pos // PAGE].astype(np.int64)
+    off = pos % PAGE
+    pu = np.asarray(pages_u8)
+    vals = pu[page[:, None], dsa_value_offset(off[:, None], np.arange(128)[None], tiled)]
+    sc = pu[page[:, None], 8192 + 4 * off[:, None] + np.arange(4)[None]].copy().view(np.float32)
+    return F.e4m3_to_f32(vals).astype(np.float64) * sc.astype(np.float64)
+
+
+def index_scores_fp8(q, w, pages_u8, pages, n, cols=None, tiled: bool = True):
+    """f64 [n]: the DSA (FP8) indexer score of each of the row's first n tokens (or of the
+    positions ``cols``): s_t = sum_h w_h relu(q_h . k_t), q the bf16 query [64, 128], k_t
+    the page's E4M3 key times its scale (``kernel.py:2784-2842``: a bf16 MFMA of the query
+    against the E4M3 values widened exactly, each head's ReLU times its weight, times the
+    key's power-of-two scale)."""
+    k = dsa_keys(pages_u8, pages, n, cols, tiled)
+    return np.maximum(k @ np.asarray(q, np.float64).T, 0.0) @ np.asarray(w, dtype=np.float64)
 
 
 def kv_rows(kv, kv_scale, slots):

@@ -31,7 +31,11 @@ Reference stages (``sgl_amd_mono/glm53/gfx950/kernel.py``):
   (``indexer.py:311-338``), whose rotated half is ``bf16_round``-ed before the Hadamard
   transform and whose Hadamard output is ``bf16_round``-ed before ``fp4_block``
   (:330-335);
-* the head weights: bf16(w) * 128^-0.5 * 64^-0.5 (``indexer.py:400-406``).
+* the head weights: bf16(w) * 128^-0.5 * 64^-0.5 (``indexer.py:400-406``);
+* the DSA (FP8) index path instead of FP4 (``index_key_fp8``, ``index_query_bf16``): the
+  key's LayerNorm, RoPE and FWHT unrounded, then E4M3 at a power-of-two per-token scale
+  into SGLang's DSA index page (:2103-2168, layout :534-550, ``dsa_value_offset``); the
+  query rotated and transformed unrounded, then bf16 once (:2928-2944).
 
 The f32 / f64 arithmetic here is exact or correctly rounded; the launch uses f32 with
 hardware rsqrt, so bf16 outputs may differ by one rounding and quantised codes only where
@@ -43,7 +47,11 @@ a complex multiplication (and its inverse); the FWHT against scipy's Hadamard ma
 search with ties to even and the pow2 scale against frexp; the index key and query
 chains' bf16 rounding points by constructed inputs whose FP4 codes flip when a rounding
 is dropped (one- or two-hot pre-transform vectors, whose Hadamard outputs are closed
-forms); the GEMVs are ``oracle/dense.py`` (pinned there).
+forms); the DSA page layout against the reference's page decode (``glm53/check.py:
+58-66``), the FP8 key chain by a closed form (a one-hot key's LayerNorm and transform) and
+a scale that drops a power of two when the transform's output is rounded to bf16 first,
+the bf16 query's single rounding by a rotated pair whose early rounding changes its bf16
+transform; the GEMVs are ``oracle/dense.py`` (pinned there).
 """
 
 from __future__ import annotations
@@ -177,7 +185,9 @@ def front(h, g_in, g_q, g_kv, w_qkv_a, s_qkv_a, w_k, s_k, w_w, g_k, b_k, w_qb, s
     (bf16-valued [R, 576] before quantisation), kv_codes u8 [R, 576], kv_scale f32 [R],
     ik (f64 [R, 128] before FP4), ik_codes u8 [R, 128], ik_e8 u8 [R, 4], q bf16 [R, 32,
     576], iq_raw (bf16 [R, 64, 128]), iq_pre (f64 before FP4), iq_codes u8 [R, 64, 128],
-    iq_e8 u8 [R, 64, 4], iw f32 [R, 64]."""
+    iq_e8 u8 [R, 64, 4], iw f32 [R, 64]; and the DSA (FP8) index path's ik8 (f64 [R, 128]
+    before E4M3), ik8_codes u8 [R, 128], ik8_scale f32 [R], iq16 (bf16 values [R, 64,
+    128])."""
     h = np.asarray(torch.as_tensor(h).float(), np.float64)
     R = h.shape[0]
     pos = np.asarray(positions, np.int64)
@@ -203,11 +213,14 @@ def front(h, g_in, g_q, g_kv, w_qkv_a, s_qkv_a, w_k, s_k, w_w, g_k, b_k, w_qb, s
     q = np.concatenate([q_lat, q_pe], -1)
     iq_raw = bf16(D.w8a16_gemv(q_an, w_iq, s_iq)).reshape(R, IHEADS, IDIM)
     iqd = index_query(iq_raw, c, s)
+    ik8 = index_key_fp8(k, f32(g_k), f32(b_k), c, s)
     iw = (bf16(w) * (IDIM ** -0.5 * IHEADS ** -0.5)).astype(np.float32)
     return dict(x=x, q_a=q_a, kv_a=kv_a, k=k, w=w, q_an=q_an, kv_rows=kv_rows,
                 kv_codes=np.stack([a for a, _ in kq]), kv_scale=np.array([b for _, b in kq]),
                 ik=ikd["pre"], ik_codes=ikd["codes"], ik_e8=ikd["e8"], q=q, iq_raw=iq_raw,
-                iq_pre=iqd["pre"], iq_codes=iqd["codes"], iq_e8=iqd["e8"], iw=iw)
+                iq_pre=iqd["pre"], iq_codes=iqd["codes"], iq_e8=iqd["e8"], iw=iw,
+                ik8=ik8["pre"], ik8_codes=ik8["codes"], ik8_scale=ik8["scale"],
+                iq16=index_query_bf16(iq_raw, c, s))
 
 
 def _rope_lead(v, cos, sin):
@@ -251,6 +264,61 @@ def index_query(iq_raw, cos, sin):
     pre = bf16(t)
     codes, e8, _ = fp4_block(pre)
     return dict(rot=r, fwht=t, pre=pre, codes=codes, e8=e8)
+
+
+# ------------------------------------------------------------ the DSA (FP8) index page
+DSA_PAGE_BYTES = 64 * (IDIM + 4)  # 64 tokens x 128 E4M3 values, then 64 f32 scales
+
+
+def dsa_value_offset(off, d, tiled: bool = True):
+    """Byte offset of value ``d`` (0..127) of token ``off`` (0..63) within a DSA index page
+    (``kernel.py:534-543``, ``index_value_word``). Tiled (SGLang's HIP layout,
+    ``index_shuffled``): 16-token x 16-byte tiles, (off // 16) * 2048 + (d // 16) * 256 +
+    (off % 16) * 16 + d % 16; otherwise token-major, off * 128 + d. The token's f32 scale
+    follows the values, at 8192 + 4 off (:545-550)."""
+    off, d = np.asarray(off), np.asarray(d)
+    if tiled:
+        return (off // 16) * 2048 + (d // 16) * 256 + (off % 16) * 16 + d % 16
+    return off * IDIM + d
+
+
+def index_key_fp8(k, g_k, b_k, cos, sin):
+    """The index-key chain into a DSA (FP8) index page (``kernel.py:2103-2168``, its
+    ``index_paged`` branch) for rows k [R, 128] (the W_k outputs) with the rows' RoPE
+    factors cos / sin [R, 32]: LayerNorm (eps 1e-6) times g plus b, RoPE on dims 0..63,
+    the FWHT-128, none of them rounded; then one power-of-two scale a token, scale =
+    2^ceil(log2(max(amax, 1e-4) / 448)) with the quotient rounded to f32 first (the
+    kernel's ``div_rn``), and codes = E4M3(v / scale), round to nearest even.
+
+    Returns dict(pre f64 [R, 128] before quantisation, codes u8 [R, 128], scale f32 [R])."""
+    n = layernorm(k, g_k, b_k)
+    r = np.concatenate([rope(n[..., :ROPE], cos, sin), n[..., ROPE:]], -1)
+    t = fwht128(r)
+    amax = np.maximum(np.abs(t).max(-1), 1e-4).astype(np.float32)
+    sc = pow2_ceil(amax / np.float32(448.0))
+    codes = fp8_codes(t / sc[:, None])
+    return dict(pre=t, codes=codes, scale=sc.astype(np.float32))
+
+
+def index_query_bf16(iq_raw, cos, sin):
+    """The index query of the DSA (FP8) path for iq_raw [R, 64, 128] (bf16 values of W_iq
+    q_an, ``kernel.py:2262-2353``) with the rows' RoPE factors cos / sin [R, 32]: the score
+    stage rotates dims 0..63, applies the FWHT-128 and rounds the result to bf16 once
+    (:2928-2944). Returns f64 [R, 64, 128] of bf16 values."""
+    iq_raw = np.asarray(iq_raw, np.float64)
+    c = np.asarray(cos, np.float64)[:, None]
+    s = np.asarray(sin, np.float64)[:, None]
+    r = np.concatenate([rope(iq_raw[..., :ROPE], c, s), iq_raw[..., ROPE:]], -1)
+    return bf16(fwht128(r))
+
+
+def dsa_page_write(pages, slot, codes, scale, tiled: bool = True):
+    """Write one token's FP8 key (codes [128], f32 scale) into DSA index pages u8 [P, 8448]
+    at ``slot`` (page slot // 64, token slot % 64)."""
+    page, off = divmod(int(slot), 64)
+    pages[page, dsa_value_offset(off, np.arange(IDIM), tiled)] = np.asarray(codes, np.uint8)
+    at = 64 * IDIM + 4 * off
+    pages[page, at:at + 4] = np.frombuffer(np.float32(scale).tobytes(), np.uint8)
 
 
 def iq_bytes(codes, e8):

@@ -33,6 +33,12 @@ GUARD_EXIT = 6
 GUARD_ABORT = 7
 GUARD_WORDS = 16
 
+# index-key caches (MONO_INDEX_*): the FP4 plane, SGLang's DSA page (tiled or token-major)
+INDEX_FP4_PLANE = 0
+INDEX_FP8_PAGE = 1
+INDEX_FP8_ROWS = 2
+DSA_PAGE_BYTES = 64 * (128 + 4)
+
 # on-HBM layouts of expert weights (MONO_LAYOUT_*)
 LAYOUT_ROWMAJOR = 0
 LAYOUT_AITER16 = 1
@@ -162,6 +168,7 @@ class MonoAttnArgs(ctypes.Structure):
         ("fault_site", c_int32),
         ("fault_after", c_int32),
         ("timeline", c_void_p),
+        ("index_format", c_int32),
     ]
 
 
@@ -239,6 +246,7 @@ class MonoFrontArgs(ctypes.Structure):
         ("timeline", c_void_p),
         ("ik_raw", c_void_p),
         ("iq_raw", c_void_p),
+        ("index_format", c_int32),
     ]
 
 
@@ -257,7 +265,8 @@ class MonoLayerArgs(ctypes.Structure):
         "o_lat", "a", "scores", "topk_pos", "y", "moe_scores", "ids", "weights", "scratch",
         "guard", "host_error")]
     _fields_ += [("fault_site", c_int32), ("fault_after", c_int32), ("timeline", c_void_p),
-                 ("phase_timeline", c_void_p), ("n_group", c_int32), ("topk_group", c_int32)]
+                 ("phase_timeline", c_void_p), ("n_group", c_int32), ("topk_group", c_int32),
+                 ("index_format", c_int32)]
 
 
 # name -> (restype, argtypes)

@@ -3,14 +3,14 @@
 
 namespace mono {
 
-template <int SPLIT, bool LONG>
+template <int SPLIT, bool LONG, bool DSA>
 __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[AT_LDS_BYTES];
   __shared__ LaunchShared sh;
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
   const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
-  attn_phase<SPLIT, false, LONG>(p, lds, guard, tag, sh.ok, NoWait());
+  attn_phase<SPLIT, false, LONG, DSA>(p, lds, guard, tag, sh.ok, NoWait());
   stamp(p.timeline, MONO_TL_DOWN);
   launch_end(sh, p.guard, tag, p.scratch, (uint32_t)AttnScratch(p.rows_max).bytes,
              Poison{p.out, (uint32_t)p.rows * AT_HEADS * AT_LAT * 2u, NAN_BF16X2},
@@ -42,8 +42,12 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
   if (a->plane_pages == 0 || a->plane_pages > (1u << 19) || a->kv_slots == 0 ||
       (uint64_t)a->kv_slots * AT_KV > 0x7FFFFFFFull)
     return set_error(MONO_E_ARG, "mono_attn_launch: plane_pages / kv_slots out of range");
-  if (!a->positions || !a->req_ids || !a->page_table || !a->q || !a->iq || !a->iqs || !a->iw ||
-      !a->plane || !a->plane_scale || !a->kv || !a->out || !a->scratch || !a->guard)
+  if (a->index_format < MONO_INDEX_FP4_PLANE || a->index_format > MONO_INDEX_FP8_ROWS)
+    return set_error(MONO_E_ARG, "mono_attn_launch: unknown index_format");
+  const bool fp4 = a->index_format == MONO_INDEX_FP4_PLANE;
+  if (!a->positions || !a->req_ids || !a->page_table || !a->q || !a->iq || !a->iw ||
+      (fp4 && (!a->iqs || !a->plane_scale)) || !a->plane || !a->kv || !a->out || !a->scratch ||
+      !a->guard)
     return set_error(MONO_E_ARG, "mono_attn_launch: null tensor");
   AttnParams p;
   p.rows = a->rows;
@@ -53,6 +57,7 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
   p.pt_rows = a->pt_rows;
   p.sm_scale = a->sm_scale;
   p.plane_pages = a->plane_pages;
+  p.index_fmt = a->index_format;
   p.kv_slots = a->kv_slots;
   p.positions = a->positions;
   p.req_ids = a->req_ids;
@@ -90,8 +95,13 @@ extern "C" int mono_attn_launch(const MonoAttnArgs* a, mono_stream_t stream) {
   // 64-key splits when the rows' 32 splits each take one CTA, else 128-key splits
   // rows that may span more than one top-k block take the multi-block variant
   const bool s64 = p.rows * (AT_TOPK / 64) <= grid, lng = p.ctx_max > AT_TKBLOCK;
-  auto kern = s64 ? (lng ? attn_kernel<64, true> : attn_kernel<64, false>)
-                  : (lng ? attn_kernel<128, true> : attn_kernel<128, false>);
+  // DSA (FP8) index pages take their own instances (their score code holds more registers)
+  using K = void (*)(AttnParams);
+  const K kerns[2][2][2] = {{{attn_kernel<128, false, false>, attn_kernel<128, false, true>},
+                             {attn_kernel<128, true, false>, attn_kernel<128, true, true>}},
+                            {{attn_kernel<64, false, false>, attn_kernel<64, false, true>},
+                             {attn_kernel<64, true, false>, attn_kernel<64, true, true>}}};
+  const K kern = kerns[s64][lng][!fp4];
   rc = check_coresident(kern, AT_THREADS, 0,
                         "mono_attn_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;

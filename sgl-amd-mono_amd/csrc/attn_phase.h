@@ -94,6 +94,7 @@ struct AttnScratch {
 
 struct AttnParams {
   int rows, rows_max, ctx_max, pt_stride, pt_rows;
+  int index_fmt;  // MONO_INDEX_*: the FP4 plane, or a DSA (FP8) page (tiled or token-major)
   float sm_scale;
   uint32_t plane_pages, kv_slots;
   const int64_t* positions;
@@ -135,6 +136,12 @@ __device__ inline v4f mfma_fp4(v4i a, v4i b, int sa, int sb) {
 
 
 // LDS of the attention phase: the top-k arena (carved per stage), then small words
+// a DSA (FP8) index page: 64 x 128 E4M3 values, then 64 f32 scales; the score task's
+// bf16 query in LDS, a head a row of 256 + 16 bytes, then the 64 head weights
+constexpr uint32_t AT_DSA_PAGE = 64 * (128 + 4);
+constexpr int AT_LDS_IQ8 = 8192;
+constexpr int AT_IQ8_ROW = 272;
+static_assert(AT_LDS_IQ8 + 64 * AT_IQ8_ROW + 256 <= TOPK_ARENA_WORDS * 4, "in the arena");
 constexpr int AT_LDS_WSUM = TOPK_ARENA_WORDS * 4;         // int [2][16], 16-byte aligned
 constexpr int AT_LDS_RES = AT_LDS_WSUM + 2 * AT_WAVES * 4;  // int [4]
 constexpr int AT_LDS_MM = AT_LDS_RES + 16;                  // u32 [4]
@@ -144,12 +151,13 @@ constexpr int AT_LDS_BYTES = AT_LDS_LINV + 16;
 
 // The attention phase (stages 1-4) in one CTA of a launch. LONG: rows may span more than
 // one top-k block (a context bound above AT_TKBLOCK); the launch picks it, so a launch
-// within one block carries none of the multi-block code. FUSED: it runs after the front
+// within one block carries none of the multi-block code. DSA: the index keys are DSA (FP8)
+// pages (the launch picks it by its index format). FUSED: it runs after the front
 // in the same launch, so its inputs (q, iq, iqs, iw and the rows' own cache entries) are
 // read device-coherent, after `ready` (the front's barrier), which it calls once, after
 // its first index-page loads are in flight. Always inlined: it is instantiated in more
 // than one kernel, and as a real call it would spill around the call.
-template <int SPLIT, bool FUSED, bool LONG, class Ready>
+template <int SPLIT, bool FUSED, bool LONG, bool DSA, class Ready>
 __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParams& p,
                                                                  uint8_t* lds, Guard& guard,
                                                                  uint32_t tag, int& ok_s,
@@ -227,9 +235,12 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   // A row within one top-k block that keeps fewer keys than it has also gets each chunk's
   // candidate list (chunk_list): the chunk's order keys go through LDS (ckey).
   static_assert(AT_CHUNK == AT_THREADS && TK_NLIST * AT_CHUNK == AT_TKBLOCK, "a key a thread");
+  static_assert((AT_CHUNK + 256 + AT_WAVES) * 4 <= AT_LDS_IQ8, "the query clear of the keys");
+  static_assert(AT_IHEADS * 256 == AT_THREADS * 16, "a DSA row's query: 16 bytes a thread");
   uint32_t* ckey = reinterpret_cast<uint32_t*>(smem);   // [AT_CHUNK]
   uint32_t* chist = ckey + AT_CHUNK;                     // [256]
   int* cwsum = reinterpret_cast<int*>(chist + 256);      // [AT_WAVES]
+  uint8_t* iq8 = smem + AT_LDS_IQ8;                      // a DSA row's bf16 query
   const int nchr = (p.ctx_max + AT_CHUNK - 1) / AT_CHUNK;
   for (int task = b; task < rs8 * nchr; task += nblk) {
     const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
@@ -246,19 +257,51 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     const bool live = pg * AT_PAGE < n;
     float sco[4];  // a listed chunk's scores (lanes < 16), stored after its list
     const int pid = live ? __builtin_amdgcn_readfirstlane(page_of(r, pg)) : 0;
-    // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
-    // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword. Loaded before
-    // the wait for the front: only the row's own key (its last) is written this launch
-    const uint32_t kofs = live ? (uint32_t)pid * 4096u : 0x80000000u;
-    const uint32_t sofs = live ? (uint32_t)pid * 256u : 0x80000000u;
-    v4i kb[4];
+    // token tile nt's sums (one a lane: heads 4 (l / 16) .. of token 16 nt + l % 16) to
+    // the tile's scores: the four lane groups summed, lane l < 16 keeping token l's. A
+    // listed chunk's scores are stored after its list is made (a store in flight would
+    // hold up the list making's waits)
+    float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
+    auto emit = [&](int nt, float acc) {
+      float a, bb;
+      swap16(acc, a, bb);
+      acc = a + bb;
+      swap32(acc, a, bb);
+      acc = a + bb;
+      sco[nt] = acc;
+      if (l < 16) {
+        const int tok = pg * AT_PAGE + 16 * nt + l;
+        if (listed) {
+          const uint32_t k = radix_key(acc);
+          ckey[w * AT_PAGE + 16 * nt + l] = tok < n ? (k > 1u ? k : 1u) : 0u;
+        } else {
+          st_devf(dst + 16 * nt + l, acc);
+          if (p.scores_out && tok < n) p.scores_out[(size_t)r * p.ctx_max + tok] = acc;
+        }
+      }
+    };
+    // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
+    auto load_wv = [&](v4f (&wv)[4]) {
+      const __amdgpu_buffer_rsrc_t rw = rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      kb[nt] = ld16<CP_NT>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
-    int ks = ld4<CP_NT>(rpsc, sofs + (uint32_t)l * 4);
-    enter();
-    if (!ok) break;
-    if (live) {
+      for (int mi = 0; mi < 4; ++mi)
+        wv[mi] = __builtin_bit_cast(v4f, ld16<XCP>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
+    };
+    // The wave's page from the FP4 index plane. False: the launch is failing.
+    auto fp4_page = [&]() -> bool {
+      // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
+      // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword. Loaded before
+      // the wait for the front: only the row's own key (its last) is written this launch
+      const uint32_t kofs = live ? (uint32_t)pid * 4096u : 0x80000000u;
+      const uint32_t sofs = live ? (uint32_t)pid * 256u : 0x80000000u;
+      v4i kb[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        kb[nt] = ld16<CP_NT>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
+      int ks = ld4<CP_NT>(rpsc, sofs + (uint32_t)l * 4);
+      enter();
+      if (!ok) return false;
+      if (!live) return true;
       // the row's own key (the last page of the row) is the front's store of this
       // launch: read it again, device coherent
       if (FUSED && pg == (n - 1) / AT_PAGE) {
@@ -275,17 +318,8 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       for (int mi = 0; mi < 4; ++mi)
         qa[mi] = ld16<XCP>(rq, (uint32_t)((16 * mi + (l & 15)) * 64 + 16 * (l >> 4)));
       const int qs = ld4<XCP>(rsrc(p.iqs + (size_t)r * 256, 256), (uint32_t)l * 4);
-      // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
       v4f wv[4];
-      const __amdgpu_buffer_rsrc_t rw = rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4);
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        wv[mi] = __builtin_bit_cast(
-            v4f, ld16<XCP>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
-      float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
-      // a listed chunk's scores are stored after its list is made: a store in flight would
-      // hold up the list making's waits
-      float sv[4];
+      load_wv(wv);
       auto tile = [&](auto nt_c) {
         constexpr int NT = decltype(nt_c)::value;
         float acc = 0.f;
@@ -299,35 +333,100 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         head_tile(std::integral_constant<int, 1>());
         head_tile(std::integral_constant<int, 2>());
         head_tile(std::integral_constant<int, 3>());
-        // sum the four lane groups (heads 4 (l / 16) ..): lane l keeps token l % 16
-        float a, bb;
-        swap16(acc, a, bb);
-        acc = a + bb;
-        swap32(acc, a, bb);
-        acc = a + bb;
-        sv[NT] = acc;
-        if (l < 16) {
-          const int tok = pg * AT_PAGE + 16 * NT + l;
-          if (listed) {
-            const uint32_t k = radix_key(acc);
-            ckey[w * AT_PAGE + 16 * NT + l] = tok < n ? (k > 1u ? k : 1u) : 0u;
-          } else {
-            st_devf(dst + 16 * NT + l, acc);
-            if (p.scores_out && tok < n) p.scores_out[(size_t)r * p.ctx_max + tok] = acc;
-          }
-        }
+        emit(NT, acc);
       };
       tile(std::integral_constant<int, 0>());
       tile(std::integral_constant<int, 1>());
       tile(std::integral_constant<int, 2>());
       tile(std::integral_constant<int, 3>());
-      if (listed) {
+      return true;
+    };
+    // The wave's page from a DSA (FP8) index page: 64 x 128 E4M3 values (16-token x
+    // 16-byte tiles, or token-major), then 64 f32 scales. Token tile nt, K steps 2 m and
+    // 2 m + 1: lane l's 16 bytes are token 16 nt + l % 16's dims 64 m + 16 (l / 16) .. (the
+    // first 8 for step 2 m, the next 8 for 2 m + 1; the query's A operands take the same
+    // dims). The query is the row's bf16 [64][128], staged in LDS. False: the launch is
+    // failing.
+    auto fp8_page = [&]() -> bool {
+      const bool tiled = p.index_fmt == MONO_INDEX_FP8_PAGE;
+      // a page-table entry outside the pages reads zeros, as the FP4 plane's bounded reads
+      const bool inside = (uint32_t)pid < p.plane_pages;
+      const __amdgpu_buffer_rsrc_t rpg =
+          rsrc(p.plane + (inside ? (size_t)pid * AT_DSA_PAGE : 0), live && inside ? AT_DSA_PAGE : 0u);
+      auto vofs = [&](int nt, int m) -> uint32_t {
+        const int t = 16 * nt + (l & 15), d = 64 * m + 16 * (l >> 4);
+        return (uint32_t)(tiled ? (t >> 4) * 2048 + (d >> 4) * 256 + (t & 15) * 16 : t * 128 + d);
+      };
+      v4i kb[8];
+      int ks[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) sco[nt] = sv[nt];
+      for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) kb[2 * nt + m] = ld16<CP_NT>(rpg, vofs(nt, m));
+        ks[nt] = ld4<CP_NT>(rpg, 8192u + (uint32_t)(16 * nt + (l & 15)) * 4u);
       }
-    } else if (listed) {
-      ckey[w * AT_PAGE + l] = 0u;
-    }
+      enter();
+      if (!ok) return false;
+      // the row's query into LDS rows of AT_IQ8_ROW bytes (A-operand reads conflict free),
+      // its head weights after them
+      *reinterpret_cast<v4i*>(iq8 + (tid >> 4) * AT_IQ8_ROW + (tid & 15) * 16) =
+          ld16<XCP>(rsrc(p.iq + (size_t)r * AT_IHEADS * 256, AT_IHEADS * 256), (uint32_t)tid * 16u);
+      if (tid < AT_IHEADS / 4)
+        *reinterpret_cast<v4i*>(iq8 + AT_IHEADS * AT_IQ8_ROW + tid * 16) =
+            ld16<XCP>(rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4), (uint32_t)tid * 16u);
+      __syncthreads();
+      if (!live) return true;
+      if (FUSED && pg == (n - 1) / AT_PAGE) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+          for (int m = 0; m < 2; ++m) kb[2 * nt + m] = ld16<CP_DEV>(rpg, vofs(nt, m));
+          ks[nt] = ld4<CP_DEV>(rpg, 8192u + (uint32_t)(16 * nt + (l & 15)) * 4u);
+        }
+      }
+      // head tile by head tile: the four token tiles' accumulators over the four K steps,
+      // the keys widened exactly to bf16 as each step takes them (B operands)
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        // one head tile at a time: no loads or conversions hoisted from the next one
+        __builtin_amdgcn_sched_barrier(0);
+        // A operands of head tile mi: head 16 mi + l % 16, K step 2 m + s
+        const uint8_t* qrow = iq8 + (16 * mi + (l & 15)) * AT_IQ8_ROW + 32 * (l >> 4);
+        v4f d[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) d[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const v8bf qa = *reinterpret_cast<const v8bf*>(qrow + 128 * (st >> 1) + 16 * (st & 1));
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) {
+            const v4i& k = kb[2 * nt + (st >> 1)];
+            const v8bf kw = (st & 1) ? fp8x8_bf16((uint32_t)k[2], (uint32_t)k[3])
+                                     : fp8x8_bf16((uint32_t)k[0], (uint32_t)k[1]);
+            d[nt] = mfma_bf16(qa, kw, d[nt]);
+          }
+        }
+        // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
+        const v4f wv = *reinterpret_cast<const v4f*>(iq8 + AT_IHEADS * AT_IQ8_ROW +
+                                                     (16 * mi + 4 * (l >> 4)) * 4);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[nt] = fmaf(fmaxf(d[nt][e], 0.f), wv[e], acc[nt]);
+      }
+      // the key's power-of-two scale after the heads' sums (the ReLU commutes with it)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) emit(nt, acc[nt] * __int_as_float(ks[nt]));
+      return true;
+    };
+    bool going;
+    if constexpr (DSA)
+      going = fp8_page();
+    else
+      going = fp4_page();
+    if (!going) break;
+    if (!live && listed) ckey[w * AT_PAGE + l] = 0u;
     if (listed) {
       __syncthreads();
       const uint32_t cut =
@@ -335,7 +434,6 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
                      rsrc(lists + ((size_t)r * TK_NLIST + c) * TK_LIST, TK_LIST * 8));
       if (tid == 0) st_dev(&cuts[r * TK_NLIST + c], cut);
       if (live && l < 16) {
-        float* dst = scores + (size_t)r * AT_MAXCTX + pg * AT_PAGE;
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
           st_devf(dst + 16 * nt + l, sco[nt]);

@@ -31,14 +31,16 @@ extern "C" int mono_front_launch(const MonoFrontArgs* a, mono_stream_t stream) {
     return set_error(MONO_E_ARG, "mono_front_launch: built for hidden 7168 and 32 heads");
   if (a->layout != MONO_LAYOUT_ROWMAJOR && a->layout != MONO_LAYOUT_AITER16)
     return set_error(MONO_E_ARG, "mono_front_launch: unknown weight layout");
-  if (a->rope_rows < 1 || a->kv_slots < 1 || a->plane_pages < 1 ||
-      (uint64_t)a->kv_slots * FR_KVA > 0x7FFFFFFFull || (uint64_t)a->plane_pages * 4096 > 0x7FFFFFFFull ||
-      (uint64_t)a->rope_rows * 64 > 0x7FFFFFFFull)
+  if (a->index_format < MONO_INDEX_FP4_PLANE || a->index_format > MONO_INDEX_FP8_ROWS)
+    return set_error(MONO_E_ARG, "mono_front_launch: unknown index_format");
+  const bool fp4 = a->index_format == MONO_INDEX_FP4_PLANE;
+  if (a->rope_rows < 1 || a->kv_slots < 1 || a->plane_pages < 1 || a->plane_pages > (1u << 19) ||
+      (uint64_t)a->kv_slots * FR_KVA > 0x7FFFFFFFull || (uint64_t)a->rope_rows * 64 > 0x7FFFFFFFull)
     return set_error(MONO_E_ARG, "mono_front_launch: cache or table sizes out of range");
   if (!a->h || !a->g_in || !a->g_q || !a->g_kv || !a->w_qkv_a || !a->s_qkv_a || !a->w_k ||
       !a->s_k || !a->w_w || !a->g_k || !a->b_k || !a->w_qb || !a->s_qb || !a->w_iq || !a->s_iq ||
       !a->w_uk || !a->s_uk || !a->cos || !a->sin || !a->positions || !a->slots || !a->kv ||
-      !a->plane || !a->plane_scale || !a->q || !a->iq || !a->iqs || !a->iw ||
+      !a->plane || (fp4 && (!a->plane_scale || !a->iqs)) || !a->q || !a->iq || !a->iw ||
       !a->scratch || !a->guard)
     return set_error(MONO_E_ARG, "mono_front_launch: null tensor");
   FrontParams p;
@@ -47,6 +49,7 @@ extern "C" int mono_front_launch(const MonoFrontArgs* a, mono_stream_t stream) {
   p.rope_rows = a->rope_rows;
   p.kv_slots = a->kv_slots;
   p.plane_pages = a->plane_pages;
+  p.index_fmt = a->index_format;
   p.eps = a->eps;
   p.h = static_cast<const uint16_t*>(a->h);
   p.g_in = static_cast<const uint16_t*>(a->g_in);

@@ -46,6 +46,7 @@ constexpr int FR_QB = FR_HEADS * FR_QHD;         // 6144
 constexpr int FR_IQ = FR_IH * FR_IK;             // 8192
 constexpr int FR_LAT = 512;
 constexpr int FR_Q = FR_LAT + FR_PE;             // 576: an attention query row
+constexpr uint32_t FR_DSA_PAGE = 64 * (128 + 4);  // a DSA index page: values, then scales
 constexpr int FR_MAXR = 8;                       // rows: x of all of them fits in LDS
 constexpr int FR_XG = 8;
 constexpr int FR_XS = FR_H + 8;                  // LDS row stride of x (bf16): 16 B of pad
@@ -75,6 +76,7 @@ struct FrontScratch {
 
 struct FrontParams {
   int rows, shuf, rope_rows;
+  int index_fmt;  // MONO_INDEX_*: the index key's cache and the index query's form
   uint32_t kv_slots, plane_pages;
   float eps;
   const uint16_t* h;
@@ -505,7 +507,8 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
             if (live && tid == 0 && p.kv_scale) st_devf(p.kv_scale + slot, sc);
           }
         } else if (kind == 2) {
-          // the index key -> LayerNorm, RoPE, FWHT, FP4 -> the index plane (wave 0)
+          // the index key -> LayerNorm, RoPE, FWHT -> FP4 into the index plane or E4M3
+          // into a DSA page (wave 0)
           const int64_t pos = sld(p.positions, r), slot = sld(p.slots, r);
           const bool on = w == 0;
           const __amdgpu_buffer_rsrc_t rc = rsrc(p.cos, (uint32_t)p.rope_rows * 64u);
@@ -526,32 +529,62 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
             const float mean = wave_sum(k0 + k1) * (1.0f / FR_IK);
             const float c0 = k0 - mean, c1 = k1 - mean;
             const float rstd = __builtin_amdgcn_rsqf(wave_sum(fmaf(c0, c0, c1 * c1)) * (1.0f / FR_IK) + 1e-6f);
-            // bf16 after the norm, after the rotation and after the transform, then FP4
-            // (the reference's FP4 key path, deepseek_v4 indexer.py:242-254)
-            float v0 = bf16_round(fmaf(c0 * rstd, gk[0], bk[0]));
-            float v1 = bf16_round(fmaf(c1 * rstd, gk[1], bk[1]));
-            if (l < FR_PE / 2) {
-              const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
-              v0 = bf16_round(r0);
-              v1 = bf16_round(r1);
-            }
-            fwht128(v0, v1, l);
-            v0 = bf16_round(v0);
-            v1 = bf16_round(v1);
-            uint32_t e8;
-            const uint32_t byte = fp4_pair(v0, v1, e8);
-            const uint32_t word = gather4(byte, l);
             const bool live = slot >= 0 && (uint64_t)slot < (uint64_t)p.plane_pages * 64u;
-            if (live) {
-              const uint32_t page = (uint32_t)(slot >> 6), s = (uint32_t)(slot & 63), c = (uint32_t)(l >> 4);
-              if ((l & 3) == 0)
-                __builtin_amdgcn_raw_buffer_store_b32(
-                    (int)word, rsrc(p.plane, p.plane_pages * 4096u),
-                    ((page * 4 + c) * 64 + s) * 16 + (uint32_t)(l & 15), 0, CP_DEV);
-              if ((l & 15) == 0)
-                __builtin_amdgcn_raw_buffer_store_b8(
-                    (uint8_t)e8, rsrc(p.plane_scale, p.plane_pages * 256u),
-                    (page * 4 + c) * 64 + (s % 16) * 4 + s / 16, 0, CP_DEV);
+            if (p.index_fmt == MONO_INDEX_FP4_PLANE) {
+              // bf16 after the norm, after the rotation and after the transform, then FP4
+              // (the reference's FP4 key path, deepseek_v4 indexer.py:242-254)
+              float v0 = bf16_round(fmaf(c0 * rstd, gk[0], bk[0]));
+              float v1 = bf16_round(fmaf(c1 * rstd, gk[1], bk[1]));
+              if (l < FR_PE / 2) {
+                const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
+                v0 = bf16_round(r0);
+                v1 = bf16_round(r1);
+              }
+              fwht128(v0, v1, l);
+              v0 = bf16_round(v0);
+              v1 = bf16_round(v1);
+              uint32_t e8;
+              const uint32_t byte = fp4_pair(v0, v1, e8);
+              const uint32_t word = gather4(byte, l);
+              if (live) {
+                const uint32_t page = (uint32_t)(slot >> 6), s = (uint32_t)(slot & 63), c = (uint32_t)(l >> 4);
+                if ((l & 3) == 0)
+                  __builtin_amdgcn_raw_buffer_store_b32(
+                      (int)word, rsrc(p.plane, p.plane_pages * 4096u),
+                      ((page * 4 + c) * 64 + s) * 16 + (uint32_t)(l & 15), 0, CP_DEV);
+                if ((l & 15) == 0)
+                  __builtin_amdgcn_raw_buffer_store_b8(
+                      (uint8_t)e8, rsrc(p.plane_scale, p.plane_pages * 256u),
+                      (page * 4 + c) * 64 + (s % 16) * 4 + s / 16, 0, CP_DEV);
+              }
+            } else {
+              // a DSA index page (kernel.py:2103-2168): the norm, the rotation and the
+              // transform in f32, then E4M3 at a power-of-two per-token scale
+              float v0 = fmaf(c0 * rstd, gk[0], bk[0]);
+              float v1 = fmaf(c1 * rstd, gk[1], bk[1]);
+              if (l < FR_PE / 2) {
+                const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
+                v0 = r0;
+                v1 = r1;
+              }
+              fwht128(v0, v1, l);
+              float sc, inv;
+              pow2_ceil(__fdiv_rn(fmaxf(wave_max(fmaxf(fabsf(v0), fabsf(v1))), 1e-4f), 448.0f), sc, inv);
+              // lanes 2 k, 2 k + 1 hold dims 4 k .. 4 k + 3: one dword of codes
+              const uint32_t c2 =
+                  (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0 * inv, v1 * inv, 0, false) & 0xFFFFu;
+              const uint32_t word = c2 | (dpp_u<DPP_XOR1>(c2) << 16);
+              if (live) {
+                const uint32_t s = (uint32_t)(slot & 63), d = 2u * (uint32_t)l;
+                const __amdgpu_buffer_rsrc_t rp =
+                    rsrc(p.plane + (size_t)(slot >> 6) * FR_DSA_PAGE, FR_DSA_PAGE);
+                const uint32_t at = p.index_fmt == MONO_INDEX_FP8_PAGE
+                                        ? (s >> 4) * 2048u + (d >> 4) * 256u + (s & 15u) * 16u + (d & 15u)
+                                        : s * 128u + d;
+                if ((l & 1) == 0) __builtin_amdgcn_raw_buffer_store_b32((int)word, rp, at, 0, CP_DEV);
+                if (l == 0)
+                  __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(sc), rp, 8192u + 4u * s, 0, CP_DEV);
+              }
             }
           }
         } else {
@@ -717,7 +750,20 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
       return __all(xw != 0u);
     });
     ok = cta_all(ok, ok_s);
-    if (ok) {
+    if (ok && p.index_fmt != MONO_INDEX_FP4_PLANE) {
+      // a DSA index page's query (kernel.py:2928-2944): the rotation and the transform in
+      // f32, then bf16 once, into iq bf16 [R, 64, 128]
+      const uint32_t pr = ~xw;
+      float v0 = bf16_lo(pr), v1 = bf16_hi(pr);
+      if (rp) {
+        const float r0 = v0 * cs - v1 * sn, r1 = v0 * sn + v1 * cs;
+        v0 = r0;
+        v1 = r1;
+      }
+      fwht128(v0, v1, l);
+      st_dev(reinterpret_cast<uint32_t*>(p.iq) + (r * FR_IH + hi) * 64 + l,
+             bf16_bits(v0) | (bf16_bits(v1) << 16));
+    } else if (ok) {
       const uint32_t pr = ~xw;
       float v0 = bf16_lo(pr), v1 = bf16_hi(pr);
       // the rotated half rounded to bf16 before the transform, the transform's output

@@ -44,7 +44,7 @@ struct LayerScratch {
     moe = at_align(post + PostScratch::BYTES);
     q = at_align(moe + MoeFp8Geom<LY_H, LY_I>::BYTES);
     iq = at_align(q + (size_t)rm * AT_HEADS * AT_KV * 2);
-    iqs = at_align(iq + (size_t)rm * AT_IHEADS * 64);
+    iqs = at_align(iq + (size_t)rm * AT_IHEADS * 256);  // FP4 codes, or a DSA page's bf16 query
     iw = at_align(iqs + (size_t)rm * 256);
     o_lat = at_align(iw + (size_t)rm * AT_IHEADS * 4);
     a = at_align(o_lat + (size_t)rm * AT_HEADS * AT_LAT * 2);
@@ -68,7 +68,7 @@ struct LayerParams {
 // layer timeline marks: start, each phase's end, exit
 constexpr int LY_TL_FRONT = 1, LY_TL_ATTN = 2, LY_TL_POST = 3, LY_TL_MOE = 4, LY_TL_END = 5;
 
-template <bool SHUF, int SPLIT, bool LONG>
+template <bool SHUF, int SPLIT, bool LONG, bool DSA>
 __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[LY_LDS_BYTES];
   __shared__ LaunchShared sh;
@@ -78,7 +78,7 @@ __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
   front_phase(p.f, lds, guard, tag, sh.ok);
   p.bar[0].arrive(tag);
   stamp(p.timeline, LY_TL_FRONT);
-  attn_phase<SPLIT, true, LONG>(p.at, lds, guard, tag, sh.ok,
+  attn_phase<SPLIT, true, LONG, DSA>(p.at, lds, guard, tag, sh.ok,
                           BarrierWait{&p.bar[0], &guard, tag, MONO_SITE_PHASE, &sh.ok});
   stamp(p.timeline, LY_TL_ATTN);
   // no barrier: the merge ran W_UV, and o's complemented words are their own hand-off
@@ -129,8 +129,11 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
       (uint64_t)a->kv_slots * AT_KV > 0x7FFFFFFFull || a->plane_pages == 0 ||
       a->plane_pages > (1u << 19))
     return set_error(MONO_E_ARG, "mono_layer_launch: cache or table sizes out of range");
+  if (a->index_format < MONO_INDEX_FP4_PLANE || a->index_format > MONO_INDEX_FP8_ROWS)
+    return set_error(MONO_E_ARG, "mono_layer_launch: unknown index_format");
+  const bool fp4 = a->index_format == MONO_INDEX_FP4_PLANE;
   if (!a->h || !a->out || !a->positions || !a->slots || !a->req_ids || !a->page_table ||
-      !a->kv || !a->plane || !a->plane_scale || !a->g_in || !a->g_q || !a->g_kv ||
+      !a->kv || !a->plane || (fp4 && !a->plane_scale) || !a->g_in || !a->g_q || !a->g_kv ||
       !a->w_qkv_a || !a->s_qkv_a || !a->w_k || !a->s_k || !a->w_w || !a->g_k || !a->b_k ||
       !a->w_qb || !a->s_qb || !a->w_iq || !a->s_iq || !a->w_uk || !a->s_uk || !a->cos ||
       !a->sin || !a->w_uv || !a->s_uv || !a->w_o || !a->s_o || !a->g_post || !a->w_r ||
@@ -163,6 +166,7 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   f.rope_rows = a->rope_rows;
   f.kv_slots = a->kv_slots;
   f.plane_pages = a->plane_pages;
+  f.index_fmt = a->index_format;
   f.eps = a->eps;
   f.h = static_cast<const uint16_t*>(a->h);
   f.g_in = static_cast<const uint16_t*>(a->g_in);
@@ -210,6 +214,7 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   at.pt_rows = a->pt_rows;
   at.sm_scale = a->sm_scale;
   at.plane_pages = a->plane_pages;
+  at.index_fmt = a->index_format;
   at.kv_slots = a->kv_slots;
   at.positions = a->positions;
   at.req_ids = a->req_ids;
@@ -310,13 +315,18 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   const bool s64 = R * (AT_TOPK / 64) <= grid;
   // rows that may span more than one top-k block take the multi-block variant
   const bool lng = a->ctx_max > AT_TKBLOCK;
+  // DSA (FP8) index pages take their own instances (their score code holds more registers)
   using K = void (*)(LayerParams);
-  const K kerns[2][2][2] = {
-      {{layer_kernel<false, 128, false>, layer_kernel<false, 128, true>},
-       {layer_kernel<false, 64, false>, layer_kernel<false, 64, true>}},
-      {{layer_kernel<true, 128, false>, layer_kernel<true, 128, true>},
-       {layer_kernel<true, 64, false>, layer_kernel<true, 64, true>}}};
-  const K kern = kerns[shuf][s64][lng];
+  const K kerns[2][2][2][2] = {
+      {{{layer_kernel<false, 128, false, false>, layer_kernel<false, 128, false, true>},
+        {layer_kernel<false, 128, true, false>, layer_kernel<false, 128, true, true>}},
+       {{layer_kernel<false, 64, false, false>, layer_kernel<false, 64, false, true>},
+        {layer_kernel<false, 64, true, false>, layer_kernel<false, 64, true, true>}}},
+      {{{layer_kernel<true, 128, false, false>, layer_kernel<true, 128, false, true>},
+        {layer_kernel<true, 128, true, false>, layer_kernel<true, 128, true, true>}},
+       {{layer_kernel<true, 64, false, false>, layer_kernel<true, 64, false, true>},
+        {layer_kernel<true, 64, true, false>, layer_kernel<true, 64, true, true>}}}};
+  const K kern = kerns[shuf][s64][lng][!fp4];
   rc = check_coresident(kern, 1024, 0, "mono_layer_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);

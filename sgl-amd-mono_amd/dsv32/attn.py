@@ -38,23 +38,42 @@ class AttnInputs:
     plane uint8 [pages, 4, 64, 16] and plane_scale uint8 [pages, 4, 64] (SGLang's FP4 index
     plane); kv uint8/E4M3 [slots, 576] with kv_scale f32 [slots] (None: raw E4M3 rows at
     scale 1, SGLang's FP8 MLA pool); positions i64 [R]; req_ids i32 [R]; page_table i32
-    [requests, pages_per_request]."""
+    [requests, pages_per_request]. With ``index_format`` a DSA page (``_lib.INDEX_FP8_PAGE``
+    or ``INDEX_FP8_ROWS``): plane uint8 [pages, 8448] (SGLang's DSA index pages), iq bf16
+    [R, 64, 128], plane_scale and iqs None."""
 
     q: torch.Tensor
     iq: torch.Tensor
-    iqs: torch.Tensor
+    iqs: Optional[torch.Tensor]
     iw: torch.Tensor
     plane: torch.Tensor
-    plane_scale: torch.Tensor
+    plane_scale: Optional[torch.Tensor]
     kv: torch.Tensor
     kv_scale: Optional[torch.Tensor]
     positions: torch.Tensor
     req_ids: torch.Tensor
     page_table: torch.Tensor
+    index_format: int = _lib.INDEX_FP4_PLANE
 
     @property
     def rows(self) -> int:
         return self.q.shape[0]
+
+
+def check_index_inputs(cfg: LayerConfig, dev, r: int, fmt: int, iq, iqs, plane, plane_scale):
+    """The index query and key cache for ``fmt`` (``_lib.INDEX_*``): the FP4 plane with
+    E2M1 queries, or DSA pages with bf16 queries (``ValueError`` otherwise)."""
+    if fmt == _lib.INDEX_FP4_PLANE:
+        _need(iq, "iq", U8, (r, cfg.index_heads, cfg.index_dim // 2), dev)
+        _need(iqs, "iqs", U8, (r, 4, 16, 4), dev)
+        pages = plane.shape[0]
+        _need(plane, "plane", U8, (pages, 4, cfg.page, 16), dev)
+        _need(plane_scale, "plane_scale", U8, (pages, 4, cfg.page), dev)
+    elif fmt in (_lib.INDEX_FP8_PAGE, _lib.INDEX_FP8_ROWS):
+        _need(iq, "iq", torch.bfloat16, (r, cfg.index_heads, cfg.index_dim), dev)
+        _need(plane, "plane", U8, (plane.shape[0], _lib.DSA_PAGE_BYTES), dev)
+    else:
+        raise ValueError(f"index_format {fmt}: not one of _lib.INDEX_*")
 
 
 class AttnOp:
@@ -86,12 +105,8 @@ class AttnOp:
             raise ValueError(f"rows {r}: needs 1..{self.max_rows}")
         kvd = cfg.kv_lora + cfg.rope_dim
         _need(x.q, "q", torch.bfloat16, (r, cfg.heads, kvd), dev)
-        _need(x.iq, "iq", U8, (r, cfg.index_heads, cfg.index_dim // 2), dev)
-        _need(x.iqs, "iqs", U8, (r, 4, 16, 4), dev)
         _need(x.iw, "iw", torch.float32, (r, cfg.index_heads), dev)
-        pages = x.plane.shape[0]
-        _need(x.plane, "plane", U8, (pages, 4, cfg.page, 16), dev)
-        _need(x.plane_scale, "plane_scale", U8, (pages, 4, cfg.page), dev)
+        check_index_inputs(cfg, dev, r, x.index_format, x.iq, x.iqs, x.plane, x.plane_scale)
         kv = x.kv if x.kv.dtype == U8 else x.kv.view(U8)
         _need(kv, "kv", U8, (kv.shape[0], kvd), dev)
         if x.kv_scale is not None:
@@ -131,13 +146,13 @@ class AttnOp:
             pt_rows=x.page_table.shape[0], plane_pages=x.plane.shape[0], kv_slots=kv.shape[0],
             sm_scale=self.sm_scale, positions=x.positions.data_ptr(),
             req_ids=x.req_ids.data_ptr(), page_table=x.page_table.data_ptr(),
-            q=x.q.data_ptr(), iq=x.iq.data_ptr(), iqs=x.iqs.data_ptr(), iw=x.iw.data_ptr(),
-            plane=x.plane.data_ptr(), plane_scale=x.plane_scale.data_ptr(), kv=kv.data_ptr(),
+            q=x.q.data_ptr(), iq=x.iq.data_ptr(), iqs=ptr(x.iqs), iw=x.iw.data_ptr(),
+            plane=x.plane.data_ptr(), plane_scale=ptr(x.plane_scale), kv=kv.data_ptr(),
             kv_scale=ptr(x.kv_scale), out=out.data_ptr(), scores=ptr(scores),
             topk_pos=ptr(topk), scratch=self.rt.scratch.data_ptr(),
             guard=self.rt.guard.data_ptr(), host_error=self.rt.host_error.data_ptr(),
             fault_site=int(self.fault[0]), fault_after=int(self.fault[1]),
-            timeline=ptr(timeline))
+            timeline=ptr(timeline), index_format=int(x.index_format))
         with torch.cuda.device(self.device):
             _lib.check(_lib.lib().mono_attn_launch(ctypes.byref(args), _lib.stream_handle(stream)),
                        "mono_attn_launch")

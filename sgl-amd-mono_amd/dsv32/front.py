@@ -23,6 +23,7 @@ import torch
 from .. import _lib, layouts
 from ..runtime import MonoRuntime, shared_or_new
 from .config import DSV32, LayerConfig
+from .attn import check_index_inputs
 from .moe import FP8, _need
 
 FRONT_MAX_ROWS = 8
@@ -94,19 +95,22 @@ class FrontWeights:
 class FrontCaches:
     """The layer's caches the front writes: kv E4M3 (uint8) [slots, 576] + kv_scale f32
     [slots] (None: raw E4M3 rows at scale 1, SGLang's FP8 MLA pool layout); the FP4 index
-    plane [pages, 4, 64, 16] + its scales [pages, 4, 64]."""
+    plane [pages, 4, 64, 16] + its scales [pages, 4, 64], or with ``index_format`` a DSA
+    page format (``_lib.INDEX_FP8_PAGE`` / ``INDEX_FP8_ROWS``) SGLang's DSA index pages
+    uint8 [pages, 8448] as ``plane`` and no ``plane_scale``."""
 
     kv: torch.Tensor
     kv_scale: Optional[torch.Tensor]
     plane: torch.Tensor
-    plane_scale: torch.Tensor
+    plane_scale: Optional[torch.Tensor]
+    index_format: int = _lib.INDEX_FP4_PLANE
 
 
 @dataclass
 class FrontOut:
     q: torch.Tensor    # bf16 [R, 32, 576]
-    iq: torch.Tensor   # uint8 [R, 64, 64]
-    iqs: torch.Tensor  # uint8 [R, 4, 16, 4]
+    iq: torch.Tensor   # uint8 [R, 64, 64] (DSA pages: bf16 [R, 64, 128])
+    iqs: Optional[torch.Tensor]  # uint8 [R, 4, 16, 4] (DSA pages: None)
     iw: torch.Tensor   # f32 [R, 64]
 
 
@@ -131,6 +135,9 @@ class FrontOp:
             iqs=torch.empty(max_rows, 4, 16, 4, dtype=U8, device=d),
             iw=torch.empty(max_rows, cfg.index_heads, dtype=torch.float32, device=d))
             for _ in range(2)]
+        # a DSA page's bf16 query, by parity
+        self.iq16 = [torch.empty(max_rows, cfg.index_heads, cfg.index_dim, dtype=BF16, device=d)
+                     for _ in range(2)]
         self.parity = 0
 
     def launch(self, h: torch.Tensor, caches: FrontCaches, positions: torch.Tensor,
@@ -150,16 +157,16 @@ class FrontOp:
         _need(kv, "kv", U8, (kv.shape[0], cfg.kv_row), dev)
         if caches.kv_scale is not None:
             _need(caches.kv_scale, "kv_scale", torch.float32, (kv.shape[0],), dev)
+        fmt = caches.index_format
         pages = caches.plane.shape[0]
-        _need(caches.plane, "plane", U8, (pages, 4, cfg.page, 16), dev)
-        _need(caches.plane_scale, "plane_scale", U8, (pages, 4, cfg.page), dev)
         if out is None:
             o = self.outs[self.parity]
-            out = FrontOut(q=o.q[:r], iq=o.iq[:r], iqs=o.iqs[:r], iw=o.iw[:r])
+            out = (FrontOut(q=o.q[:r], iq=o.iq[:r], iqs=o.iqs[:r], iw=o.iw[:r])
+                   if fmt == _lib.INDEX_FP4_PLANE else
+                   FrontOut(q=o.q[:r], iq=self.iq16[self.parity][:r], iqs=None, iw=o.iw[:r]))
             self.parity ^= 1
+        check_index_inputs(cfg, dev, r, fmt, out.iq, out.iqs, caches.plane, caches.plane_scale)
         _need(out.q, "q", BF16, (r, cfg.heads, cfg.kv_row), dev)
-        _need(out.iq, "iq", U8, (r, cfg.index_heads, cfg.index_dim // 2), dev)
-        _need(out.iqs, "iqs", U8, (r, 4, 16, 4), dev)
         _need(out.iw, "iw", torch.float32, (r, cfg.index_heads), dev)
         if timeline is not None:
             _need(timeline, "timeline", torch.int64, (self.rt.grid, _lib.TL_COLS), dev)
@@ -180,12 +187,12 @@ class FrontOp:
             s_iq=w.s_iq.data_ptr(), w_uk=w.w_uk.data_ptr(), s_uk=w.s_uk.data_ptr(),
             cos=w.cos.data_ptr(), sin=w.sin.data_ptr(), positions=positions.data_ptr(),
             slots=slots.data_ptr(), kv=kv.data_ptr(), kv_scale=ptr(caches.kv_scale),
-            plane=caches.plane.data_ptr(), plane_scale=caches.plane_scale.data_ptr(),
-            q=out.q.data_ptr(), iq=out.iq.data_ptr(), iqs=out.iqs.data_ptr(), iw=out.iw.data_ptr(),
+            plane=caches.plane.data_ptr(), plane_scale=ptr(caches.plane_scale),
+            q=out.q.data_ptr(), iq=out.iq.data_ptr(), iqs=ptr(out.iqs), iw=out.iw.data_ptr(),
             scratch=self.rt.scratch.data_ptr(), guard=self.rt.guard.data_ptr(),
             host_error=self.rt.host_error.data_ptr(), fault_site=int(self.fault[0]),
             fault_after=int(self.fault[1]), timeline=ptr(timeline), ik_raw=ptr(ik_raw),
-            iq_raw=ptr(iq_raw))
+            iq_raw=ptr(iq_raw), index_format=int(fmt))
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().mono_front_launch(ctypes.byref(args), _lib.stream_handle(stream)),
                        "mono_front_launch")

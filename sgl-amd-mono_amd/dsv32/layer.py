@@ -103,7 +103,7 @@ class LayerOp:
         inp = AttnInputs(q=f.q, iq=f.iq, iqs=f.iqs, iw=f.iw, plane=caches.plane,
                          plane_scale=caches.plane_scale, kv=caches.kv, kv_scale=caches.kv_scale,
                          positions=step.positions, req_ids=step.req_ids,
-                         page_table=step.page_table)
+                         page_table=step.page_table, index_format=caches.index_format)
         o_lat = self.attn.launch(inp, stream=stream)
         a = self.post.launch(o_lat, h, stream=stream)
         return self.moe.launch(a, out=out, stream=stream)
@@ -112,8 +112,8 @@ class LayerOp:
 @dataclass
 class LayerDebug:
     """Optional views into a layer launch (each None or a tensor of the named shape, rows
-    [R]): the phases' hand-offs q bf16 [R, 32, 576], iq u8 [R, 64, 64], iqs u8 [R, 4, 16,
-    4], iw f32 [R, 64], o_lat bf16 [R, 32, 512], a bf16 [R, 7168]; and outputs scores f32
+    [R]): the phases' hand-offs q bf16 [R, 32, 576], iq u8 [R, 64, 64] (a DSA index
+    page's: bf16 [R, 64, 128]), iqs u8 [R, 4, 16, 4] (FP4 plane only), iw f32 [R, 64], o_lat bf16 [R, 32, 512], a bf16 [R, 7168]; and outputs scores f32
     [R, ctx_max], topk i32 [R, 2048], y f32 [R, 7168], moe_scores f32 [R, 256], ids i32
     [R, 9], weights f32 [R, 9]."""
 
@@ -130,9 +130,14 @@ class LayerDebug:
     ids: Optional[torch.Tensor] = None
     weights: Optional[torch.Tensor] = None
 
-    def check(self, r: int, ctx_max: int, cfg: LayerConfig, device) -> None:
+    def check(self, r: int, ctx_max: int, cfg: LayerConfig, device,
+              index_format: int = _lib.INDEX_FP4_PLANE) -> None:
+        fp4 = index_format == _lib.INDEX_FP4_PLANE
+        if not fp4 and self.iqs is not None:
+            raise ValueError("iqs: a DSA index page's query has no E8M0 scales")
         shapes = dict(q=(torch.bfloat16, (r, cfg.heads, cfg.kv_row)),
-                      iq=(torch.uint8, (r, cfg.index_heads, cfg.index_dim // 2)),
+                      iq=(torch.uint8, (r, cfg.index_heads, cfg.index_dim // 2)) if fp4 else
+                      (torch.bfloat16, (r, cfg.index_heads, cfg.index_dim)),
                       iqs=(torch.uint8, (r, 4, 16, 4)),
                       iw=(torch.float32, (r, cfg.index_heads)),
                       o_lat=(torch.bfloat16, (r, cfg.heads, cfg.kv_lora)),
@@ -215,14 +220,20 @@ class FusedLayerOp:
         if caches.kv_scale is not None:
             _need(caches.kv_scale, "kv_scale", torch.float32, (kv.shape[0],), dev)
         pages = caches.plane.shape[0]
-        _need(caches.plane, "plane", torch.uint8, (pages, 4, cfg.page, 16), dev)
-        _need(caches.plane_scale, "plane_scale", torch.uint8, (pages, 4, cfg.page), dev)
+        fmt = caches.index_format
+        if fmt == _lib.INDEX_FP4_PLANE:
+            _need(caches.plane, "plane", torch.uint8, (pages, 4, cfg.page, 16), dev)
+            _need(caches.plane_scale, "plane_scale", torch.uint8, (pages, 4, cfg.page), dev)
+        elif fmt in (_lib.INDEX_FP8_PAGE, _lib.INDEX_FP8_ROWS):
+            _need(caches.plane, "plane", torch.uint8, (pages, _lib.DSA_PAGE_BYTES), dev)
+        else:
+            raise ValueError(f"index_format {fmt}: not one of _lib.INDEX_*")
         if out is None:
             out = self.outs[self.parity][:r]
             self.parity ^= 1
         _need(out, "out", torch.bfloat16, (r, cfg.hidden), dev)
         d = debug or LayerDebug()
-        d.check(r, self.ctx_max, cfg, dev)
+        d.check(r, self.ctx_max, cfg, dev, fmt)
         if timeline is not None:
             _need(timeline, "timeline", torch.int64, (self.rt.grid, _lib.TL_COLS), dev)
         if phase_timeline is not None:
@@ -242,7 +253,7 @@ class FusedLayerOp:
             out=out.data_ptr(), positions=step.positions.data_ptr(), slots=step.slots.data_ptr(),
             req_ids=step.req_ids.data_ptr(), page_table=pt.data_ptr(), kv=kv.data_ptr(),
             kv_scale=ptr(caches.kv_scale), plane=caches.plane.data_ptr(),
-            plane_scale=caches.plane_scale.data_ptr(), g_in=f.g_in.data_ptr(),
+            plane_scale=ptr(caches.plane_scale), g_in=f.g_in.data_ptr(),
             g_q=f.g_q.data_ptr(), g_kv=f.g_kv.data_ptr(), w_qkv_a=f.w_qkv_a.data_ptr(),
             s_qkv_a=f.s_qkv_a.data_ptr(), w_k=f.w_k.data_ptr(), s_k=f.s_k.data_ptr(),
             w_w=f.w_w.data_ptr(), g_k=f.g_k.data_ptr(), b_k=f.b_k.data_ptr(),
@@ -258,7 +269,7 @@ class FusedLayerOp:
             scratch=self.rt.scratch.data_ptr(), guard=self.rt.guard.data_ptr(),
             host_error=self.rt.host_error.data_ptr(), fault_site=int(self.fault[0]),
             fault_after=int(self.fault[1]), timeline=ptr(timeline),
-            phase_timeline=ptr(phase_timeline))
+            phase_timeline=ptr(phase_timeline), index_format=int(fmt))
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().mono_layer_launch(ctypes.byref(args), _lib.stream_handle(stream)),
                        "mono_layer_launch")

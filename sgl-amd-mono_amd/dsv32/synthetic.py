@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import layouts
+from .. import _lib, layouts
 from .config import DSV32, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
 from .moe import MoeFp8Weights, MoeMxfp4Weights
 from .post import PostWeights
@@ -105,13 +105,25 @@ def logits_f32(rows: int, experts: int, device, seed: int = 0) -> torch.Tensor:
     return torch.randn(rows, experts, generator=g, device=device)
 
 
+def dsa_pages(pages: int, device, seed: int = 0) -> torch.Tensor:
+    """DSA index pages uint8 [pages, 8448] with random contents: E4M3 values (no NaN
+    codes), then per-token power-of-two f32 scales 2^-10 .. 2^-6."""
+    dev = torch.device(device)
+    g = _gen(dev, seed, 24)
+    vals = torch.randint(0, 256, (pages, 8192), generator=g, device=dev, dtype=torch.uint8)
+    vals[(vals & 0x7F) == 0x7F] ^= 1
+    sc = torch.exp2(torch.randint(-10, -5, (pages, 64), generator=g, device=dev).float())
+    return torch.cat([vals, sc.view(torch.uint8).view(pages, 256)], 1).contiguous()
+
+
 def attention_inputs(rows: int, ctx: int, device, seed: int = 0, positions=None,
-                     extra_pages: int = 3):
+                     extra_pages: int = 3, index_format: int = _lib.INDEX_FP4_PLANE):
     """Config 3: each row its own request seeing ``ctx`` keys (position ctx - 1 unless
     ``positions`` is given), its pages a random permutation of the plane (as
     ``test/kernels/test_deepseek_v41_k2i.py:109-119``). Index plane: random E2M1 bytes,
     E8M0 scales in [123, 129]; index query likewise; head weights 0.05 N(0, 1); q bf16
-    N(0, 1); KV rows E4M3 of N(0, 1) with per-token scales U(0.5, 1.5)."""
+    N(0, 1); KV rows E4M3 of N(0, 1) with per-token scales U(0.5, 1.5). With a DSA
+    ``index_format``: DSA pages (``dsa_pages``) and a bf16 N(0, 1) index query."""
     from .attn import AttnInputs
 
     dev = torch.device(device)
@@ -125,6 +137,9 @@ def attention_inputs(rows: int, ctx: int, device, seed: int = 0, positions=None,
     page_table = perm[: rows * ppr].view(rows, ppr).contiguous()
     iq = torch.randint(0, 256, (rows, 64, 64), **u8)
     iqs = torch.randint(123, 130, (rows, 4, 16, 4), **u8)
+    if index_format != _lib.INDEX_FP4_PLANE:
+        plane, plane_scale, iqs = dsa_pages(pages, dev, seed), None, None
+        iq = torch.randn(rows, 64, 128, generator=_gen(dev, seed, 25), device=dev).to(torch.bfloat16)
     gq = _gen(dev, seed, 22)
     iw = torch.randn(rows, 64, generator=gq, device=dev) * 0.05
     q = torch.randn(rows, 32, 576, generator=gq, device=dev).to(torch.bfloat16)
@@ -141,7 +156,7 @@ def attention_inputs(rows: int, ctx: int, device, seed: int = 0, positions=None,
     req_ids = torch.arange(rows, dtype=torch.int32, device=dev)
     return AttnInputs(q=q, iq=iq, iqs=iqs, iw=iw, plane=plane, plane_scale=plane_scale, kv=kv,
                       kv_scale=kv_scale, positions=positions, req_ids=req_ids,
-                      page_table=page_table)
+                      page_table=page_table, index_format=index_format)
 
 
 def post_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
@@ -230,31 +245,37 @@ def rowmajor_front(w: FrontWeights) -> dict:
                 cos=w.cos.cpu(), sin=w.sin.cpu())
 
 
-def front_caches(device, slots: int, pages: int, seed: int = 0) -> FrontCaches:
+def front_caches(device, slots: int, pages: int, seed: int = 0,
+                 index_format: int = _lib.INDEX_FP4_PLANE) -> FrontCaches:
     """Caches with random prior contents (so untouched slots can be checked)."""
     dev = torch.device(device)
     g = _gen(dev, seed, 64)
     kv = torch.randint(0, 256, (slots, 576), generator=g, device=dev, dtype=torch.uint8)
     kv[(kv & 0x7F) == 0x7F] = 0  # no NaN codes
     kv_scale = torch.rand(slots, generator=g, device=dev)
+    if index_format != _lib.INDEX_FP4_PLANE:
+        return FrontCaches(kv=kv, kv_scale=kv_scale, plane=dsa_pages(pages, dev, seed),
+                           plane_scale=None, index_format=index_format)
     plane = torch.randint(0, 256, (pages, 4, 64, 16), generator=g, device=dev, dtype=torch.uint8)
     plane_scale = torch.randint(120, 130, (pages, 4, 64), generator=g, device=dev, dtype=torch.uint8)
     return FrontCaches(kv=kv, kv_scale=kv_scale, plane=plane, plane_scale=plane_scale)
 
 
-def layer(rows: int, ctx: int, device, seed: int = 0, layout: str = layouts.AITER16):
+def layer(rows: int, ctx: int, device, seed: int = 0, layout: str = layouts.AITER16,
+          index_format: int = _lib.INDEX_FP4_PLANE):
     """Config 5, one layer: its weights (front, output block, FP8 MoE), caches as config 3
-    (each row its own request at position ctx - 1 over shuffled pages), the step's
-    tables (each row's slot the page-table entry of its position) and the input rows h.
-    Returns (LayerWeights, FrontCaches, LayerStep, h)."""
+    (each row its own request at position ctx - 1 over shuffled pages; the index keys in
+    ``index_format``), the step's tables (each row's slot the page-table entry of its
+    position) and the input rows h. Returns (LayerWeights, FrontCaches, LayerStep, h)."""
     from .layer import LayerStep, LayerWeights
 
     dev = torch.device(device)
     w = LayerWeights(front=front_weights(dev, seed, layout=layout, rope_rows=max(ctx, 1)),
                      post=post_weights(dev, seed, layout=layout),
                      moe=moe_fp8_weights(dev, seed, layout=layout))
-    a = attention_inputs(rows, ctx, dev, seed=seed)
-    caches = FrontCaches(kv=a.kv, kv_scale=a.kv_scale, plane=a.plane, plane_scale=a.plane_scale)
+    a = attention_inputs(rows, ctx, dev, seed=seed, index_format=index_format)
+    caches = FrontCaches(kv=a.kv, kv_scale=a.kv_scale, plane=a.plane, plane_scale=a.plane_scale,
+                         index_format=index_format)
     pos = a.positions
     page = a.page_table.gather(1, (pos // 64).to(torch.int64)[:, None])[:, 0].to(torch.int64)
     step = LayerStep(positions=pos, slots=page * 64 + pos % 64, req_ids=a.req_ids,

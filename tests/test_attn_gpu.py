@@ -13,6 +13,7 @@ import torch
 
 from oracle import attn as A
 from oracle.topk import topk_sort
+from sgl_amd_mono_amd import _lib
 from sgl_amd_mono_amd.dsv32 import synthetic
 from sgl_amd_mono_amd.dsv32.attn import AttnOp
 
@@ -33,8 +34,12 @@ def _check(op, inp, full_score_rows=1, sample=4096, seed=0):
     out, scores, topk = _run(op, inp)
     pos = inp.positions.cpu().numpy()
     pt = inp.page_table.cpu().numpy()
-    plane, psc = inp.plane.cpu().numpy(), inp.plane_scale.cpu().numpy()
-    iq, iqs, iw = inp.iq.cpu().numpy(), inp.iqs.cpu().numpy(), inp.iw.cpu().numpy()
+    fp4 = inp.index_format == _lib.INDEX_FP4_PLANE
+    plane = inp.plane.cpu().numpy()
+    psc = inp.plane_scale.cpu().numpy() if fp4 else None
+    iq = inp.iq.cpu().numpy() if fp4 else inp.iq.float().cpu().numpy().astype(np.float64)
+    iqs = inp.iqs.cpu().numpy() if fp4 else None
+    iw = inp.iw.cpu().numpy()
     kv, ksc = inp.kv.cpu().numpy(), inp.kv_scale.cpu().numpy()
     rng = np.random.default_rng(seed)
     for r in range(inp.rows):
@@ -46,7 +51,9 @@ def _check(op, inp, full_score_rows=1, sample=4096, seed=0):
             continue
         cols = np.arange(n) if (r < full_score_rows or n <= sample) else np.sort(
             rng.choice(n, sample, replace=False))
-        want = A.index_scores(iq[r], iqs[r], iw[r], plane, psc, pages, n, cols=cols)
+        want = (A.index_scores(iq[r], iqs[r], iw[r], plane, psc, pages, n, cols=cols) if fp4 else
+                A.index_scores_fp8(iq[r], iw[r], plane, pages, n, cols=cols,
+                                   tiled=inp.index_format == _lib.INDEX_FP8_PAGE))
         got = scores[r, cols].astype(np.float64)
         assert np.all(np.isfinite(got)), r
         err = np.abs(got - want).max() / max(np.abs(want).max(), 1e-30)
@@ -71,6 +78,24 @@ def test_attention_matches_oracle_at_32k(gpu, rows):
     inp = synthetic.attention_inputs(rows, 32768, gpu, seed=rows)
     op = AttnOp(gpu, max_rows=rows)
     _check(op, inp, full_score_rows=1)
+
+
+@pytest.mark.parametrize("fmt", [_lib.INDEX_FP8_PAGE, _lib.INDEX_FP8_ROWS])
+def test_attention_dsa_pages_at_32k(gpu, fmt):
+    """SGLang's DSA index pages (E4M3 keys with per-token scales, bf16 query): 8 rows at
+    32768 keys, the oracle's ``index_scores_fp8`` to the same bars."""
+    print(f"case attention DSA pages fmt={fmt} rows=8 ctx=32768", flush=True)
+    inp = synthetic.attention_inputs(8, 32768, gpu, seed=80 + fmt, index_format=fmt)
+    _check(AttnOp(gpu, max_rows=8), inp, full_score_rows=1)
+
+
+def test_attention_dsa_pages_ragged_and_long(gpu):
+    """DSA pages on rows seeing 101, 3000 and 40000 keys and a pad row, under a context
+    bound of 65536 (rows ranked over more than one 32768-key block)."""
+    print("case attention DSA pages ragged ctx_max=65536", flush=True)
+    inp = synthetic.attention_inputs(4, 65536, gpu, seed=86, positions=[100, 2999, 39999, -1],
+                                     index_format=_lib.INDEX_FP8_PAGE)
+    _check(AttnOp(gpu, max_rows=4, ctx_max=65536), inp, full_score_rows=2, sample=2048)
 
 
 def test_attention_short_and_ragged_rows(gpu):

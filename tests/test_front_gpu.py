@@ -30,7 +30,7 @@ import torch
 
 from oracle import formats as F
 from oracle import front as Fr
-from sgl_amd_mono_amd import layouts
+from sgl_amd_mono_amd import _lib, layouts
 from sgl_amd_mono_amd.dsv32 import synthetic
 from sgl_amd_mono_amd.dsv32.front import FrontOp
 
@@ -187,6 +187,71 @@ def test_front_unscaled_rows_read_back_without_scales(gpu, front_w):
     """Without a scale array the KV rows go into the cache as raw E4M3 (SGLang's MLA
     pool): read back as plain E4M3 values, with no scale, they match the oracle's rows."""
     _run_case(gpu, front_w, 3, [5, 700, 4095], [17, 700, 4000], seed=12, scaled=False)
+
+
+def _e4m3_near(dev_codes, ora_codes, what, max_frac=0.01):
+    """E4M3 codes equal, but for at most ``max_frac`` of them one step apart (the f32
+    chain against the f64 one at a rounding boundary)."""
+    dv = F.e4m3_to_f32(dev_codes).astype(np.float64)
+    ov = F.e4m3_to_f32(ora_codes).astype(np.float64)
+    diff = dv != ov
+    mag = np.maximum(np.abs(dv), np.abs(ov))
+    step = np.maximum(2.0 ** (np.floor(np.log2(np.maximum(mag, 1e-30))) - 3), 2.0 ** -9)
+    assert np.all(np.abs(dv - ov)[diff] <= step[diff]), what
+    print(f"{what}: {int(diff.sum())} of {diff.size} codes one step apart", flush=True)
+    assert diff.sum() <= max(2, max_frac * diff.size), (what, int(diff.sum()))
+
+
+@pytest.mark.parametrize("fmt", [_lib.INDEX_FP8_PAGE, _lib.INDEX_FP8_ROWS])
+def test_front_dsa_index_pages(gpu, front_w, fmt):
+    """SGLang's DSA index page instead of the FP4 plane: each row's key as E4M3 at a
+    power-of-two per-token scale in its page (tiled or token-major) and the bf16 index
+    query, from the launch's own projections through the oracle's DSA chains
+    (``index_key_fp8`` / ``index_query_bf16``): scales equal, codes equal but for at most
+    1% one step apart, the query's bf16 values equal but for at most 0.1% one ulp apart;
+    every other byte of the pages unchanged, a pad row writing nothing."""
+    w, ws = front_w
+    rows, positions = 8, [0, 1, 63, 64, 100, 2047, 4000, 5]
+    slots = [0, 1, 63, 64, 1000, 2047, -1, 4095]
+    print(f"case front DSA pages fmt={fmt} layout={w.layout}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(21)
+    h = torch.randn(rows, 7168, generator=g, device=gpu).to(torch.bfloat16)
+    caches = synthetic.front_caches(gpu, SLOTS, PAGES, seed=21, index_format=fmt)
+    before = caches.plane.cpu().numpy().copy()
+    pos = torch.tensor(positions, dtype=torch.int64, device=gpu)
+    sl = torch.tensor(slots, dtype=torch.int64, device=gpu)
+    op = FrontOp(w, gpu, max_rows=8)
+    ik_raw = torch.full((rows, 128), float("nan"), device=gpu)
+    iq_raw = torch.full((rows, 64, 128), float("nan"), dtype=torch.bfloat16, device=gpu)
+    out = op.launch(h, caches, pos, sl, ik_raw=ik_raw, iq_raw=iq_raw)
+    op.rt.check()
+    assert out.iqs is None and out.iq.dtype == torch.bfloat16
+    ikr = ik_raw.cpu().numpy().astype(np.float64)
+    iqr = iq_raw.float().cpu().numpy().astype(np.float64)
+    cs = ws["cos"].float().numpy().astype(np.float64)[np.array(positions)]
+    sn = ws["sin"].float().numpy().astype(np.float64)[np.array(positions)]
+    # the query: one bf16 rounding after the rotation and the transform
+    want = Fr.index_query_bf16(iqr, cs, sn)
+    got = out.iq.float().cpu().numpy().astype(np.float64)
+    diff = got != want
+    assert np.all(np.abs(got - want)[diff] <= 2.0 ** -7 * np.abs(want)[diff]), "iq ulp"
+    assert diff.sum() <= max(2, 1e-3 * diff.size), int(diff.sum())
+    # the keys
+    kd = Fr.index_key_fp8(ikr, ws["g_k"], ws["b_k"], cs, sn)
+    pages = caches.plane.cpu().numpy()
+    expect = before.copy()
+    tiled = fmt == _lib.INDEX_FP8_PAGE
+    for r, s in enumerate(slots):
+        if s < 0:
+            continue
+        page, off = divmod(s, 64)
+        at = Fr.dsa_value_offset(off, np.arange(128), tiled)
+        scale = pages[page, 8192 + 4 * off: 8192 + 4 * off + 4].copy().view(np.float32)[0]
+        assert scale == kd["scale"][r], (r, scale, kd["scale"][r])
+        _e4m3_near(pages[page, at], kd["codes"][r], f"DSA key {r}")
+        expect[page, at] = pages[page, at]
+        expect[page, 8192 + 4 * off: 8192 + 4 * off + 4] = pages[page, 8192 + 4 * off: 8192 + 4 * off + 4]
+    assert np.array_equal(pages, expect), "bytes outside the rows' keys changed"
 
 
 def test_front_deterministic_and_graph_replay(gpu, front_w):

@@ -18,6 +18,7 @@ from oracle import dense as D
 from oracle import front as Fr
 from oracle import moe as M
 from oracle.topk import topk_sort
+from sgl_amd_mono_amd import _lib
 from sgl_amd_mono_amd.dsv32 import synthetic
 from sgl_amd_mono_amd.dsv32.attn import AttnInputs
 from sgl_amd_mono_amd.dsv32.layer import FusedLayerOp, LayerDebug, LayerOp, LayerStep
@@ -55,15 +56,25 @@ def test_layer_eight_rows_at_32k(gpu):
     _layer_case(gpu, 8, 32768, None, seed=32)
 
 
-def _layer_case(gpu, rows, ctx, positions, seed):
-    w, caches, step, h = synthetic.layer(rows, ctx, gpu, seed=seed)
+def test_layer_dsa_index_pages(gpu):
+    """The layer over SGLang's DSA index pages (E4M3 keys at per-token scales, bf16 index
+    query): 8 ragged rows, the chain against the oracle and the one launch bit-equal."""
+    print("case layer DSA pages rows=8 ctx<=8192 ragged", flush=True)
+    _layer_case(gpu, 8, 8192, [8191, 5000, 2048, 2047, 100, 7000, 2999, 0], seed=5,
+                index_format=_lib.INDEX_FP8_PAGE)
+
+
+def _layer_case(gpu, rows, ctx, positions, seed, index_format=0):
+    w, caches, step, h = synthetic.layer(rows, ctx, gpu, seed=seed, index_format=index_format)
+    fp4 = index_format == _lib.INDEX_FP4_PLANE
     if positions is not None:
         step = _ragged(step, positions)
     op = LayerOp(w, gpu, max_rows=rows, ctx_max=ctx)
     f = op.front.launch(h, caches, step.positions, step.slots)
     inp = AttnInputs(q=f.q, iq=f.iq, iqs=f.iqs, iw=f.iw, plane=caches.plane,
                      plane_scale=caches.plane_scale, kv=caches.kv, kv_scale=caches.kv_scale,
-                     positions=step.positions, req_ids=step.req_ids, page_table=step.page_table)
+                     positions=step.positions, req_ids=step.req_ids, page_table=step.page_table,
+                     index_format=index_format)
     scores = torch.full((rows, ctx), float("nan"), device=gpu)
     topk = torch.full((rows, TOPK), -7, dtype=torch.int32, device=gpu)
     o_lat = op.attn.launch(inp, scores=scores, topk=topk)
@@ -78,7 +89,7 @@ def _layer_case(gpu, rows, ctx, positions, seed):
     # bytes at the same slots): bit-equal at every hand-off and at its output
     fused = FusedLayerOp(w, gpu, max_rows=rows, ctx_max=ctx)
     dbg = LayerDebug(q=torch.empty_like(f.q), iq=torch.empty_like(f.iq),
-                     iqs=torch.empty_like(f.iqs), iw=torch.empty_like(f.iw),
+                     iqs=torch.empty_like(f.iqs) if fp4 else None, iw=torch.empty_like(f.iw),
                      o_lat=torch.empty_like(o_lat), a=torch.empty_like(a),
                      scores=torch.full_like(scores, float("nan")),
                      topk=torch.full_like(topk, -7), y=torch.empty_like(y),
@@ -86,7 +97,8 @@ def _layer_case(gpu, rows, ctx, positions, seed):
                      weights=torch.empty_like(rt.weights))
     fout = fused.launch(h, caches, step, debug=dbg)
     fused.check()
-    for name, got, want in (("q", dbg.q, f.q), ("iq", dbg.iq, f.iq), ("iqs", dbg.iqs, f.iqs),
+    for name, got, want in (("q", dbg.q, f.q), ("iq", dbg.iq, f.iq),
+                            ("iqs", dbg.iqs if fp4 else f.iq, f.iqs if fp4 else f.iq),
                             ("iw", dbg.iw, f.iw), ("topk", dbg.topk, topk),
                             ("o_lat", dbg.o_lat, o_lat), ("a", dbg.a, a), ("y", dbg.y, y),
                             ("moe scores", dbg.moe_scores, rt.scores), ("ids", dbg.ids, rt.ids),
@@ -100,8 +112,12 @@ def _layer_case(gpu, rows, ctx, positions, seed):
     _close(f.q.float().cpu(), fr["q"], "front q")
 
     sc, tk = scores.cpu().numpy(), topk.cpu().numpy()
-    iq, iqs, iw = f.iq.cpu().numpy(), f.iqs.cpu().numpy(), f.iw.cpu().numpy()
-    plane, psc = caches.plane.cpu().numpy(), caches.plane_scale.cpu().numpy()
+    iw = f.iw.cpu().numpy()
+    plane = caches.plane.cpu().numpy()
+    if fp4:
+        iq, iqs, psc = f.iq.cpu().numpy(), f.iqs.cpu().numpy(), caches.plane_scale.cpu().numpy()
+    else:
+        iq = f.iq.float().cpu().numpy().astype(np.float64)
     kv, ksc = caches.kv.cpu().numpy(), caches.kv_scale.cpu().numpy()
     pt = step.page_table.cpu().numpy()
     rng = np.random.default_rng(seed)
@@ -109,7 +125,8 @@ def _layer_case(gpu, rows, ctx, positions, seed):
         n = int(pos[r]) + 1
         pages = pt[r]
         cols = np.arange(n) if n <= 3000 else np.sort(rng.choice(n, 3000, replace=False))
-        want = A.index_scores(iq[r], iqs[r], iw[r], plane, psc, pages, n, cols=cols)
+        want = (A.index_scores(iq[r], iqs[r], iw[r], plane, psc, pages, n, cols=cols) if fp4
+                else A.index_scores_fp8(iq[r], iw[r], plane, pages, n, cols=cols))
         err = np.abs(sc[r, cols] - want).max() / max(np.abs(want).max(), 1e-30)
         assert err <= 1e-5, (r, err)
         k = min(n, TOPK)
