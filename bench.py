@@ -66,6 +66,10 @@ def parse():
     p.add_argument("--layout", default="aiter16", choices=("aiter16", "rowmajor"),
                    help="on-HBM layout of the expert weights (SGLang's gfx950 MoE load "
                         "leaves them in AITER's (16, 16) shuffle)")
+    p.add_argument("--index-format", default="fp4", choices=("fp4", "dsa"),
+                   help="layer / attn: the index keys in the FP4 index plane (BASELINE "
+                        "configs[2], the default) or in SGLang's DSA pages (E4M3 + per-token "
+                        "scales, 16x16 tiles; bf16 index query)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device-to-device copy 5 times (the reference "
                         "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -333,6 +337,7 @@ def cpu_baseline_attn(inp, sm_scale, rows):
 def bench_attn(args):
     import torch
 
+    from sgl_amd_mono_amd import _lib
     from sgl_amd_mono_amd.dsv32 import synthetic
     from sgl_amd_mono_amd.dsv32.attn import AttnOp
 
@@ -340,28 +345,41 @@ def bench_attn(args):
     rows, L, ctx = args.rows, args.layers, args.ctx
     print(f"bench: generating {L} layers of caches ({rows} rows x {ctx} keys)", file=sys.stderr,
           flush=True)
-    inps = [synthetic.attention_inputs(rows, ctx, dev, seed=400 + i) for i in range(L)]
+    dsa = args.index_format == "dsa"
+    fmt = _lib.INDEX_FP8_PAGE if dsa else _lib.INDEX_FP4_PLANE
+    inps = [synthetic.attention_inputs(rows, ctx, dev, seed=400 + i, index_format=fmt)
+            for i in range(L)]
     ops = [AttnOp(dev, max_rows=rows, ctx_max=ctx) for _ in range(L)]
     outs = [torch.empty(rows, 32, 512, dtype=torch.bfloat16, device=dev) for _ in range(L)]
     n = min(ctx, 1 << 30)
     k = min(n, 2048)
-    # KV rows gathered (576 E4M3 + a 4-byte scale), index keys scanned (64 B + 4 scales),
-    # the queries in (absorbed q bf16, index q + scales + weights) and the latent out
-    bytes_per = rows * (k * 580 + n * 68 + 32 * 576 * 2 + 64 * 64 + 256 + 64 * 4 + 32 * 512 * 2)
+    # KV rows gathered (576 E4M3 + a 4-byte scale), index keys scanned (FP4: 64 B + 4
+    # scales; DSA: 128 B + a scale), the queries in (absorbed q bf16, index q (+ scales) +
+    # weights) and the latent out
+    key, iqb = index_bytes(dsa)
+    bytes_per = rows * (k * 580 + n * key + 32 * 576 * 2 + iqb + 64 * 4 + 32 * 512 * 2)
     us, wall, steps = time_graph(lambda i: ops[i].launch(inps[i], out=outs[i]), L, args.steps,
                                  args.warmup)
     for op in ops:
         op.rt.check()
     print(f"bench: {steps} launches, {us:.1f} us each (wall {wall * 1e3 / steps:.1f} ms/step)",
           file=sys.stderr, flush=True)
-    cpu = None if args.no_cpu else cpu_baseline_attn(inps[0], ops[0].sm_scale, rows)
+    # the CPU baseline leg restates the FP4 indexer (the headline configuration)
+    cpu = None if args.no_cpu or dsa else cpu_baseline_attn(inps[0], ops[0].sm_scale, rows)
     config = {
         "workload": "BASELINE configs[2]: sparse MLA decode, 32 heads, kv_lora 512 + rope 64, "
                     "64-token paged E4M3 KV with per-token scales, FP4 indexer (64 heads x 128, "
-                    "E2M1 + E8M0) top-2048, one persistent launch",
+                    "E2M1 + E8M0) top-2048, one persistent launch" if not dsa else
+                    "configs[2] geometry over SGLang's DSA index pages: sparse MLA decode, 32 "
+                    "heads, 64-token paged E4M3 KV, indexer over E4M3 keys with per-token "
+                    "power-of-two scales (16x16 tiles) and a bf16 query, top-2048, one "
+                    "persistent launch",
         "rows": rows, "context": ctx, "topk": k, "layers_rotated": L,
+        "index_format": args.index_format,
     }
-    return us, steps, bytes_per, "fp4 idx / bf16 x e4m3 attn", config, f"attn_r{rows}", cpu
+    name = f"attn_r{rows}" if not dsa else f"attn_dsa_r{rows}"
+    return (us, steps, bytes_per, "fp4 idx / bf16 x e4m3 attn" if not dsa else
+            "bf16 x e4m3 idx / bf16 x e4m3 attn", config, name, cpu)
 
 
 def cpu_baseline_post(o_lat, h, w):
@@ -419,12 +437,20 @@ FRONT_W_BYTES = (2112 * 7168 + 17 * 56 * 4 + 128 * 7168 + 56 * 4 + 64 * 7168 * 2
 POST_W_BYTES = 32 * 128 * 512 + 7168 * 4096 + (32 * 4 + 56 * 32) * 4
 
 
-def phase_bytes(rows, ctx, distinct):
+def index_bytes(dsa: bool):
+    """(bytes a cached index key, bytes of a row's index query): the FP4 plane's 64 B + 4
+    E8M0 and 64 x 64 B + 256 E8M0, or a DSA page's 128 B + a 4-byte scale and a bf16
+    64 x 128 query."""
+    return (132, 64 * 128 * 2) if dsa else (68, 64 * 64 + 256)
+
+
+def phase_bytes(rows, ctx, distinct, dsa=False):
     """Algorithmic bytes of each phase of one layer (each needed byte counted once)."""
     n, k = ctx, min(ctx, 2048)
-    front = (FRONT_W_BYTES + rows * (7168 * 2 + 580 + 68 + 32 * 576 * 2 + 64 * 64 + 256
+    key, iq = index_bytes(dsa)
+    front = (FRONT_W_BYTES + rows * (7168 * 2 + 580 + key + 32 * 576 * 2 + iq
                                      + 64 * 4 + 64 * 2 * 2))
-    attn = rows * (k * 580 + n * 68 + 32 * 576 * 2 + 64 * 64 + 256 + 64 * 4 + 32 * 512 * 2)
+    attn = rows * (k * 580 + n * key + 32 * 576 * 2 + iq + 64 * 4 + 32 * 512 * 2)
     post = POST_W_BYTES + rows * (32 * 512 * 2 + 7168 * 2 * 2)
     moe = distinct * EXPERT_BYTES + ROUTER_BYTES + rows * 7168 * 2 * 2
     return {"front": front, "attn": attn, "post": post, "moe": moe}
@@ -502,6 +528,7 @@ def bench_layer(args):
     import numpy as np
     import torch
 
+    from sgl_amd_mono_amd import _lib
     from sgl_amd_mono_amd.dsv32 import synthetic
     from sgl_amd_mono_amd.dsv32.attn import AttnInputs
     from sgl_amd_mono_amd.dsv32.layer import FusedLayerOp, LayerDebug, LayerOp, layer_runtime
@@ -512,8 +539,11 @@ def bench_layer(args):
     print(f"bench: generating {L} decoder layers ({rows} rows x {ctx} keys)", file=sys.stderr,
           flush=True)
     layers = []
+    dsa = args.index_format == "dsa"
+    fmt = _lib.INDEX_FP8_PAGE if dsa else _lib.INDEX_FP4_PLANE
     for i in range(L):
-        layers.append(synthetic.layer(rows, ctx, dev, seed=1000 + i, layout=args.layout))
+        layers.append(synthetic.layer(rows, ctx, dev, seed=1000 + i, layout=args.layout,
+                                      index_format=fmt))
         if (i + 1) % 8 == 0:
             print(f"bench: {i + 1} layers", file=sys.stderr, flush=True)
     # the one-launch layers share one runtime, as a served model's layers do
@@ -527,7 +557,7 @@ def bench_layer(args):
         op.launch(h, caches, step, out=outs[i], debug=LayerDebug(ids=ids))
         op.check()
         distinct.append(len(np.unique(ids.cpu().numpy())))
-    per = [phase_bytes(rows, ctx, d) for d in distinct]
+    per = [phase_bytes(rows, ctx, d, dsa) for d in distinct]
     avg = {k: sum(p[k] for p in per) / L for k in per[0]}
     total = sum(avg.values())
     us, wall, steps = time_graph(
@@ -546,7 +576,8 @@ def bench_layer(args):
         f = op.front.launch(h, caches, step.positions, step.slots)
         inp = AttnInputs(q=f.q, iq=f.iq, iqs=f.iqs, iw=f.iw, plane=caches.plane,
                          plane_scale=caches.plane_scale, kv=caches.kv, kv_scale=caches.kv_scale,
-                         positions=step.positions, req_ids=step.req_ids, page_table=step.page_table)
+                         positions=step.positions, req_ids=step.req_ids, page_table=step.page_table,
+                         index_format=caches.index_format)
         o = op.attn.launch(inp).clone()
         a = op.post.launch(o, h).clone()
         op.moe.launch(a, out=outs[i])
@@ -576,8 +607,9 @@ def bench_layer(args):
                   "achieved_GBs": round(avg[k] / (v * 1e-6) / 1e9, 1)} for k, v in phase_us.items()}
     print(f"bench: four launches {chain_us:.1f} us; phases alone {phases}", file=sys.stderr,
           flush=True)
-    cpu = None if args.no_cpu else cpu_baseline_layer(layers[0][3], layers[0][0], layers[0][1],
-                                                      layers[0][2], rows)
+    # the CPU baseline leg restates the FP4 indexer (the headline configuration)
+    cpu = None if args.no_cpu or dsa else cpu_baseline_layer(layers[0][3], layers[0][0],
+                                                             layers[0][1], layers[0][2], rows)
     config = {
         "workload": "BASELINE configs[4]: full DeepSeek-V3.2 DSA decoder layer, one GPU's TP=4 "
                     "share, 8 rows at position 32767 (context 32768), ONE persistent launch a "
@@ -585,14 +617,21 @@ def bench_layer(args):
                     "writes, FP4 index query), FP4 indexer + exact top-2048 + sparse MLA, W_UV + "
                     "o_proj + residual, FP8 MoE (norm, router, top-8 + shared, residual)",
         "rows": rows, "context": ctx, "layers_rotated": L, "launches_per_layer": 1,
-        "weight_layout": args.layout, "distinct_experts": distinct,
+        "weight_layout": args.layout, "index_format": args.index_format,
+        "distinct_experts": distinct,
         "in_launch_phase_ends_us": inside,
         "four_launch_chain_us": round(chain_us, 2), "phases_as_own_launches": phases,
         "bytes_per_layer": int(total), "layer_achieved_GBs": round(total / (us * 1e-6) / 1e9, 1),
         "model_layers": 61, "us_per_token_step_61_layers": round(us * 61, 1),
     }
     # the roofline line is the layer kernel's: the only kernel of the step
-    return us, steps, total, "fp8 / fp4 idx / bf16", config, "layer", cpu, us
+    if dsa:
+        config["workload"] = config["workload"].replace(
+            "KV + FP4 index-key cache writes, FP4 index query), FP4 indexer",
+            "KV + DSA index-page writes (E4M3, per-token scales), bf16 index query), DSA "
+            "indexer")
+    return (us, steps, total, "fp8 / fp4 idx / bf16" if not dsa else "fp8 / e4m3 idx / bf16",
+            config, "layer" if not dsa else "layer_dsa", cpu, us)
 
 
 def main():

@@ -24,7 +24,7 @@ from typing import Optional
 
 import torch
 
-from .. import layouts
+from .. import _lib, layouts
 from .config import DSV32, LayerConfig
 from .front import FrontCaches, FrontWeights
 from .layer import LayerWeights
@@ -181,31 +181,63 @@ def layer_disable_reason(layer, idx: int, cfg: LayerConfig = DSV32) -> Optional[
     return None
 
 
+def index_cache(pool, idx: int, cfg: LayerConfig = DSV32):
+    """The layer's index-key cache in SGLang's pool, in place: ``(plane, plane_scale,
+    index_format)``. A pool with the FP4 index plane gives its pages [pages, 1, 4, 64, 16]
+    and E8M0 scales [pages, 1, 4, 64] (``get_index_k_fp4_payload_buffer`` /
+    ``_scale_buffer``); DeepSeek-V3.2's NSA pool gives its DSA index pages
+    (``get_index_k_with_scale_buffer``: per page 64 tokens x 128 E4M3 values then 64 f32
+    scales, 8448 bytes), bound as 16-token x 16-byte tiles, the layout of SGLang's HIP DSA
+    pool as the reference binds it (``glm53/spec.py:444-466``,
+    ``glm53/gfx950/runner.py:177``). Any other pool raises ``RuntimeError``."""
+    if hasattr(pool, "get_index_k_fp4_payload_buffer"):
+        pay = pool.get_index_k_fp4_payload_buffer(idx)
+        sc = pool.get_index_k_fp4_scale_buffer(idx)
+        if (pay.dtype != torch.uint8 or tuple(pay.shape[1:]) != (1, 4, cfg.page, 16)
+                or not pay.is_contiguous()):
+            raise RuntimeError(f"layer {idx}: FP4 index pages {pay.dtype} {tuple(pay.shape)}; "
+                               f"needs contiguous uint8 [pages, 1, 4, {cfg.page}, 16]")
+        if (sc.dtype != torch.uint8 or tuple(sc.shape) != (pay.shape[0], 1, 4, cfg.page)
+                or not sc.is_contiguous()):
+            raise RuntimeError(f"layer {idx}: FP4 index scales {sc.dtype} {tuple(sc.shape)}; "
+                               f"needs contiguous uint8 [{pay.shape[0]}, 1, 4, {cfg.page}]")
+        pages = pay.shape[0]
+        return (pay.view(pages, 4, cfg.page, 16), sc.view(pages, 4, cfg.page),
+                _lib.INDEX_FP4_PLANE)
+    if hasattr(pool, "get_index_k_with_scale_buffer"):
+        buf = pool.get_index_k_with_scale_buffer(idx)
+        per = cfg.page * (cfg.index_dim + 4)
+        if (buf.dtype != torch.uint8 or buf.dim() < 2 or not buf.is_contiguous()
+                or buf.numel() != buf.shape[0] * per or per != _lib.DSA_PAGE_BYTES):
+            raise RuntimeError(f"layer {idx}: DSA index pages {buf.dtype} {tuple(buf.shape)}; "
+                               f"needs contiguous uint8 [pages, {per}] (64 x (128 + 4) bytes "
+                               f"a page)")
+        return buf.view(buf.shape[0], per), None, _lib.INDEX_FP8_PAGE
+    raise RuntimeError(f"layer {idx}: the KV pool has no index-key cache this build reads "
+                       f"(an FP4 index plane or DSA index pages)")
+
+
+def index_buffers(pool, idx: int) -> list:
+    """The pool's index-key tensors of a layer, page-major (for a caller that saves and
+    restores pages around SGLang's own layer)."""
+    if hasattr(pool, "get_index_k_fp4_payload_buffer"):
+        return [pool.get_index_k_fp4_payload_buffer(idx), pool.get_index_k_fp4_scale_buffer(idx)]
+    return [pool.get_index_k_with_scale_buffer(idx)]
+
+
 def caches(pool, idx: int, cfg: LayerConfig = DSV32) -> FrontCaches:
     """A layer's caches from SGLang's KV pool, in place: the MLA rows E4M3 [slots, 1, 576]
-    (``get_key_buffer``) and the FP4 index pages [pages, 1, 4, 64, 16] with their E8M0
-    scales [pages, 1, 4, 64] (``get_index_k_fp4_payload_buffer`` / ``_scale_buffer``).
-    The pool's MLA rows are raw E4M3 at scale 1 (SGLang's HIP DSA layout, as the
-    reference binds it: ``glm53/spec.py:451-461``), so the launches write and read them
-    with no per-token scale: a row SGLang wrote and a row the front wrote read the same
-    way, whichever path serves the next step."""
+    (``get_key_buffer``) and the index-key cache (``index_cache``: the FP4 index plane or
+    DSA index pages). The pool's MLA rows are raw E4M3 at scale 1 (SGLang's HIP DSA
+    layout, as the reference binds it: ``glm53/spec.py:451-461``), so the launches write
+    and read them with no per-token scale: a row SGLang wrote and a row the front wrote
+    read the same way, whichever path serves the next step."""
     kv = pool.get_key_buffer(idx)
-    pay = pool.get_index_k_fp4_payload_buffer(idx)
-    sc = pool.get_index_k_fp4_scale_buffer(idx)
     row = cfg.kv_row
     if kv.element_size() != 1 or kv.shape[-1] != row or not kv.is_contiguous():
         raise RuntimeError(f"layer {idx}: MLA cache {kv.dtype} {tuple(kv.shape)}; needs "
                            f"contiguous E4M3 [slots, 1, {row}]")
     slots = kv.numel() // row
-    if (pay.dtype != torch.uint8 or tuple(pay.shape[1:]) != (1, 4, cfg.page, 16)
-            or not pay.is_contiguous()):
-        raise RuntimeError(f"layer {idx}: FP4 index pages {pay.dtype} {tuple(pay.shape)}; "
-                           f"needs contiguous uint8 [pages, 1, 4, {cfg.page}, 16]")
-    if (sc.dtype != torch.uint8 or tuple(sc.shape) != (pay.shape[0], 1, 4, cfg.page)
-            or not sc.is_contiguous()):
-        raise RuntimeError(f"layer {idx}: FP4 index scales {sc.dtype} {tuple(sc.shape)}; "
-                           f"needs contiguous uint8 [{pay.shape[0]}, 1, 4, {cfg.page}]")
-    pages = pay.shape[0]
-    return FrontCaches(kv=kv.view(torch.uint8).view(slots, row), kv_scale=None,
-                       plane=pay.view(pages, 4, cfg.page, 16),
-                       plane_scale=sc.view(pages, 4, cfg.page))
+    plane, plane_scale, fmt = index_cache(pool, idx, cfg)
+    return FrontCaches(kv=kv.view(torch.uint8).view(slots, row), kv_scale=None, plane=plane,
+                       plane_scale=plane_scale, index_format=fmt)

@@ -22,6 +22,8 @@ import os
 
 import torch
 
+from .binding import index_buffers
+
 logger = logging.getLogger(__name__)
 
 SHARED_EXPERT = 256  # SGLang's id of the fused shared expert
@@ -85,10 +87,9 @@ def reference(L, positions, h_rows: torch.Tensor, forward_batch, S: int, cfg, po
     kv = pool.get_key_buffer(L.i)
     kv_rows = kv.view(kv.shape[0], -1)
     saved_kv = kv_rows[slots].clone()
-    pay = pool.get_index_k_fp4_payload_buffer(L.i)
-    sc = pool.get_index_k_fp4_scale_buffer(L.i)
+    index = index_buffers(pool, L.i)
     pages = (slots // 64).unique()
-    saved_pay, saved_sc = pay[pages].clone(), sc[pages].clone()
+    saved_index = [t[pages].clone() for t in index]
     seen, hooks = _route_in_f32(L.module.mlp, cfg)
     try:
         hidden = set_written(h_rows.clone(), forward_batch)
@@ -100,8 +101,8 @@ def reference(L, positions, h_rows: torch.Tensor, forward_batch, S: int, cfg, po
         for hk in hooks:
             hk.remove()
         kv_rows[slots] = saved_kv
-        pay[pages] = saved_pay
-        sc[pages] = saved_sc
+        for t, saved in zip(index, saved_index):
+            t[pages] = saved
     return {"out": stream, "ids": seen.get("ids"), "topk": topk}
 
 

@@ -129,6 +129,27 @@ def test_caches_bind_in_place_and_refuse_other_layouts():
         binding.caches(paged, 7)
 
 
+def test_dsa_index_pages_bind_in_place():
+    """DeepSeek-V3.2's NSA pool keeps its index keys in DSA pages
+    (``get_index_k_with_scale_buffer``, [pages, 64 x (128 + 4)] uint8): bound in place as
+    the tiled DSA format, with no scale plane; a page of another size is refused."""
+    from sgl_amd_mono_amd import _lib
+
+    kv = torch.zeros(256, 1, DSV32.kv_row, dtype=FP8)
+    buf = torch.zeros(4, 64 * 132, dtype=torch.uint8)
+    pool = NS(get_key_buffer=lambda i: kv, get_index_k_with_scale_buffer=lambda i: buf)
+    c = binding.caches(pool, 3)
+    assert c.index_format == _lib.INDEX_FP8_PAGE and c.plane_scale is None
+    assert c.plane.data_ptr() == buf.data_ptr() and c.plane.shape == (4, 8448)
+    assert binding.index_buffers(pool, 3) == [buf]
+    odd = NS(get_key_buffer=lambda i: kv,
+             get_index_k_with_scale_buffer=lambda i: torch.zeros(4, 64 * 130, dtype=torch.uint8))
+    with pytest.raises(RuntimeError, match="DSA index pages"):
+        binding.caches(odd, 3)
+    with pytest.raises(RuntimeError, match="no index-key cache"):
+        binding.caches(NS(get_key_buffer=lambda i: kv), 3)
+
+
 def test_a_reused_slot_reads_back_unscaled():
     """A slot the front wrote (raw E4M3 of the row, oracle.front.kv_quant unscaled), then
     freed and rewritten by SGLang with another row: the attention's reader (oracle.attn
