@@ -242,13 +242,16 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   int* cwsum = reinterpret_cast<int*>(chist + 256);      // [AT_WAVES]
   uint8_t* iq8 = smem + AT_LDS_IQ8;                      // a DSA row's bf16 query
   const int nchr = (p.ctx_max + AT_CHUNK - 1) / AT_CHUNK;
+  // chunk lists only while every CTA holds at most one score task: a list costs its task
+  // ~2 us of VALU work, which several tasks a CTA would pay in series
+  const bool lists_on = !LONG && rs8 * nchr <= nblk;
   for (int task = b; task < rs8 * nchr; task += nblk) {
     const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
     const int r = task % rs8, c = task / rs8;
     if (r >= R) continue;
     const int n = row_n(r);
     if (c * AT_CHUNK >= n) continue;
-    const bool listed = !LONG && n > AT_TOPK;
+    const bool listed = lists_on && n > AT_TOPK;
     if (listed) {
       if (tid < 64) reinterpret_cast<v4i*>(chist)[tid] = v4i{0, 0, 0, 0};
       if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = v4i{-1, 0, 0, 0};
@@ -476,21 +479,26 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         // topk_lists' / topk_select's minimum, maximum and flag words, set before a barrier
         if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = v4i{-1, 0, 0, 0};
         __syncthreads();
-        // each wave waits for its own chunks' done words, then loads their lists at once
+        // each wave waits for its own chunks' done words (then loads their lists at once)
         const uint32_t* dw = score_done + r * AT_NCHUNK;
-        int32_t* sel = topk_lists(
-            tid, rsrc(lists + (size_t)r * TK_NLIST * TK_LIST, (uint32_t)(nch * TK_LIST * 8)),
-            rsrc(cuts + r * TK_NLIST, (uint32_t)nch * 4u), nch, smem, wsum, mm_s, res_s,
-            [&](int c0, int c1) {
-              return wait_until(guard, MONO_SITE_SCORES, [&]() {
-                return __all((c0 >= nch || ld_dev(&dw[c0]) == tag) &&
-                             (c1 >= nch || ld_dev(&dw[c1]) == tag));
-              });
-            },
-            ok);
+        auto wait_chunks = [&](int c0, int c1) {
+          return wait_until(guard, MONO_SITE_SCORES, [&]() {
+            return __all((c0 >= nch || ld_dev(&dw[c0]) == tag) &&
+                         (c1 >= nch || ld_dev(&dw[c1]) == tag));
+          });
+        };
+        int32_t* sel = nullptr;
+        if (lists_on) {
+          sel = topk_lists(
+              tid, rsrc(lists + (size_t)r * TK_NLIST * TK_LIST, (uint32_t)(nch * TK_LIST * 8)),
+              rsrc(cuts + r * TK_NLIST, (uint32_t)nch * 4u), nch, smem, wsum, mm_s, res_s,
+              wait_chunks, ok);
+        } else {
+          ok = cta_all(wait_chunks(2 * w, 2 * w + 1) && ok, ok_s);
+        }
         if (ok) {
-          // where the lists cannot decide it (every chunk is done: each wave saw its own),
-          // every score
+          // without lists, or where they cannot decide it (every chunk is done: each wave
+          // saw its own), every score
           if (!sel) {
             if (tid == 0) {
               mm_s[0] = 0xFFFFFFFFu;
