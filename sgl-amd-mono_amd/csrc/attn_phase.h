@@ -245,12 +245,91 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   // chunk lists only while every CTA holds at most one score task: a list costs its task
   // ~2 us of VALU work, which several tasks a CTA would pay in series
   const bool lists_on = !LONG && rs8 * nchr <= nblk;
-  for (int task = b; task < rs8 * nchr; task += nblk) {
+  // This CTA's score tasks: with XCD-local rows, tasks b, b + nblk, .. (all of row b % 8);
+  // otherwise a contiguous run of the row-major task list (task t: row t / nchr, chunk
+  // t % nchr), so that consecutive tasks mostly share a row and its query
+  const int ntask = rs8 * nchr;
+  int t_first = b, t_step = nblk, t_count = b < ntask ? (ntask - 1 - b) / nblk + 1 : 0;
+  if (!xcd) {
+    const int q = ntask / nblk, rem = ntask % nblk;
+    t_first = b * q + (b < rem ? b : rem);
+    t_step = 1;
+    t_count = q + (b < rem ? 1 : 0);
+  }
+  auto task_rc = [&](int t, int& r, int& c) {
+    r = xcd ? t % rs8 : t / nchr;
+    c = xcd ? t / rs8 : t % nchr;
+  };
+  // the keys each row sees, lane r holding row r's, loaded ahead of every key (a later
+  // read would wait for the keys in flight)
+  static_assert(AT_MAXR <= 64, "a lane a row");
+  const int nrow = l < R ? row_n(l) : 0;
+  // FP4 plane: the page ids of this CTA's tasks, one a lane (lane i: the wave's page of
+  // its task i; -1: none), loaded at once, so that a task's keys are requested while the
+  // task before computes
+  static_assert(AT_MAXR * ((AT_MAXCTX + AT_CHUNK - 1) / AT_CHUNK) <= 64 * 256, "a lane a task");
+  int tpage = -1;
+  if constexpr (!DSA) {
+    int ri, ci;
+    task_rc(t_first + l * t_step, ri, ci);
+    const int pgi = ci * (AT_CHUNK / AT_PAGE) + w;
+    if (l < t_count && ri < R && pgi * AT_PAGE < row_n(ri)) tpage = page_of(ri, pgi);
+  }
+  // task i's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims 32 (l / 16)
+  // ..; the key scales of the four tiles: bytes of one dword
+  auto fp4_keys = [&](int i, v4i (&kb)[4], int& ks, bool dev) {
+    const int pid = __builtin_amdgcn_readlane(tpage, i < 64 ? i : 63);
+    const uint32_t kofs = pid >= 0 ? (uint32_t)pid * 4096u : 0x80000000u;
+    const uint32_t sofs = pid >= 0 ? (uint32_t)pid * 256u : 0x80000000u;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const uint32_t o = kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16);
+      kb[nt] = dev ? ld16<CP_DEV>(rplane, o) : ld16<CP_NT>(rplane, o);
+    }
+    ks = dev ? ld4<CP_DEV>(rpsc, sofs + (uint32_t)l * 4) : ld4<CP_NT>(rpsc, sofs + (uint32_t)l * 4);
+  };
+  // the next task's keys (FP4 plane), in flight while a task computes
+  v4i kbn[4];
+  int ksn = 0;
+  if constexpr (!DSA) fp4_keys(0, kbn, ksn, false);
+  // the row whose query (FP4: in registers; DSA: in LDS) the CTA holds
+  int qrow = -1;
+  v4i qa[4];
+  int qs = 0;
+  v4f wv[4];
+  // row r's head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
+  auto load_wv = [&](int r, v4f (&wv)[4]) {
+    const __amdgpu_buffer_rsrc_t rw = rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+      wv[mi] = __builtin_bit_cast(v4f, ld16<XCP>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
+  };
+  // One task; false: the launch is failing (every later task skipped).
+  auto score_task = [&](int ti, v4i (&kb)[4], int& ks, v4i (&kbn)[4], int& ksn) -> bool {
     const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
-    const int r = task % rs8, c = task / rs8;
-    if (r >= R) continue;
-    const int n = row_n(r);
-    if (c * AT_CHUNK >= n) continue;
+    int r, c;
+    task_rc(t_first + ti * t_step, r, c);
+    const int n = r < R ? __builtin_amdgcn_readlane(nrow, r) : 0;
+    const bool valid = r < R && c * AT_CHUNK < n;
+    if constexpr (!DSA) {
+      // after the wait for the front: the row's query when the wave's task changes rows,
+      // then the next task's keys (the newest loads: this task's MFMAs wait for neither)
+      enter();
+      if (!ok) return false;
+      if (valid && (c * (AT_CHUNK / AT_PAGE) + w) * AT_PAGE < n && r != qrow) {
+        // the query as A operands: head tile mi, lane l: head 16 mi + l % 16, dims
+        // 32 (l / 16) .. (16 bytes); its scales: the dword of lane l holds tile mi's byte mi
+        const __amdgpu_buffer_rsrc_t rq = rsrc(p.iq + (size_t)r * AT_IHEADS * 64, AT_IHEADS * 64);
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+          qa[mi] = ld16<XCP>(rq, (uint32_t)((16 * mi + (l & 15)) * 64 + 16 * (l >> 4)));
+        qs = ld4<XCP>(rsrc(p.iqs + (size_t)r * 256, 256), (uint32_t)l * 4);
+        load_wv(r, wv);
+        qrow = r;
+      }
+      if (ti + 1 < t_count) fp4_keys(ti + 1, kbn, ksn, false);
+    }
+    if (!valid) return true;
     const bool listed = lists_on && n > AT_TOPK;
     if (listed) {
       if (tid < 64) reinterpret_cast<v4i*>(chist)[tid] = v4i{0, 0, 0, 0};
@@ -259,7 +338,8 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     const int pg = c * (AT_CHUNK / AT_PAGE) + w;
     const bool live = pg * AT_PAGE < n;
     float sco[4];  // a listed chunk's scores (lanes < 16), stored after its list
-    const int pid = live ? __builtin_amdgcn_readfirstlane(page_of(r, pg)) : 0;
+    // (a DSA page's id, looked up by its task)
+    const int pid = DSA && live ? __builtin_amdgcn_readfirstlane(page_of(r, pg)) : 0;
     // token tile nt's sums (one a lane: heads 4 (l / 16) .. of token 16 nt + l % 16) to
     // the tile's scores: the four lane groups summed, lane l < 16 keeping token l's. A
     // listed chunk's scores are stored after its list is made (a store in flight would
@@ -283,46 +363,15 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         }
       }
     };
-    // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
-    auto load_wv = [&](v4f (&wv)[4]) {
-      const __amdgpu_buffer_rsrc_t rw = rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4);
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        wv[mi] = __builtin_bit_cast(v4f, ld16<XCP>(rw, (uint32_t)(16 * mi + 4 * (l >> 4)) * 4));
-    };
     // The wave's page from the FP4 index plane. False: the launch is failing.
+    // The wave's page from the FP4 index plane (its keys requested a task ahead, before
+    // the wait for the front: only the row's own key, its last, is written this launch).
+    // False: the launch is failing.
     auto fp4_page = [&]() -> bool {
-      // the page's key tiles (B operands): tile nt, lane l: slot 16 nt + l % 16, dims
-      // 32 (l / 16) ..; the key scales of the four tiles: bytes of one dword. Loaded before
-      // the wait for the front: only the row's own key (its last) is written this launch
-      const uint32_t kofs = live ? (uint32_t)pid * 4096u : 0x80000000u;
-      const uint32_t sofs = live ? (uint32_t)pid * 256u : 0x80000000u;
-      v4i kb[4];
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        kb[nt] = ld16<CP_NT>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
-      int ks = ld4<CP_NT>(rpsc, sofs + (uint32_t)l * 4);
-      enter();
-      if (!ok) return false;
       if (!live) return true;
       // the row's own key (the last page of the row) is the front's store of this
       // launch: read it again, device coherent
-      if (FUSED && pg == (n - 1) / AT_PAGE) {
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          kb[nt] = ld16<CP_DEV>(rplane, kofs + (uint32_t)((l >> 4) * 1024 + (16 * nt + (l & 15)) * 16));
-        ks = ld4<CP_DEV>(rpsc, sofs + (uint32_t)l * 4);
-      }
-      // the row's query as A operands: head tile mi, lane l: head 16 mi + l % 16, dims
-      // 32 (l / 16) .. (16 bytes); its scales: the dword of lane l holds tile mi's byte mi
-      const __amdgpu_buffer_rsrc_t rq = rsrc(p.iq + (size_t)r * AT_IHEADS * 64, AT_IHEADS * 64);
-      v4i qa[4];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        qa[mi] = ld16<XCP>(rq, (uint32_t)((16 * mi + (l & 15)) * 64 + 16 * (l >> 4)));
-      const int qs = ld4<XCP>(rsrc(p.iqs + (size_t)r * 256, 256), (uint32_t)l * 4);
-      v4f wv[4];
-      load_wv(wv);
+      if (FUSED && pg == (n - 1) / AT_PAGE) fp4_keys(ti, kb, ks, true);
       auto tile = [&](auto nt_c) {
         constexpr int NT = decltype(nt_c)::value;
         float acc = 0.f;
@@ -371,13 +420,18 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       enter();
       if (!ok) return false;
       // the row's query into LDS rows of AT_IQ8_ROW bytes (A-operand reads conflict free),
-      // its head weights after them
-      *reinterpret_cast<v4i*>(iq8 + (tid >> 4) * AT_IQ8_ROW + (tid & 15) * 16) =
-          ld16<XCP>(rsrc(p.iq + (size_t)r * AT_IHEADS * 256, AT_IHEADS * 256), (uint32_t)tid * 16u);
-      if (tid < AT_IHEADS / 4)
-        *reinterpret_cast<v4i*>(iq8 + AT_IHEADS * AT_IQ8_ROW + tid * 16) =
-            ld16<XCP>(rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4), (uint32_t)tid * 16u);
-      __syncthreads();
+      // its head weights after them, when the CTA's task changes rows (after the last
+      // task's readers)
+      if (r != qrow) {
+        __syncthreads();
+        *reinterpret_cast<v4i*>(iq8 + (tid >> 4) * AT_IQ8_ROW + (tid & 15) * 16) =
+            ld16<XCP>(rsrc(p.iq + (size_t)r * AT_IHEADS * 256, AT_IHEADS * 256), (uint32_t)tid * 16u);
+        if (tid < AT_IHEADS / 4)
+          *reinterpret_cast<v4i*>(iq8 + AT_IHEADS * AT_IQ8_ROW + tid * 16) =
+              ld16<XCP>(rsrc(p.iw + (size_t)r * AT_IHEADS, AT_IHEADS * 4), (uint32_t)tid * 16u);
+        __syncthreads();
+        qrow = r;
+      }
       if (!live) return true;
       if (FUSED && pg == (n - 1) / AT_PAGE) {
 #pragma unroll
@@ -428,7 +482,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       going = fp8_page();
     else
       going = fp4_page();
-    if (!going) break;
+    if (!going) return false;
     if (!live && listed) ckey[w * AT_PAGE + l] = 0u;
     if (listed) {
       __syncthreads();
@@ -445,11 +499,29 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         }
       }
     }
-    drain();
-    __syncthreads();
-    if (tid == 0) st_dev(&score_done[r * AT_NCHUNK + c], tag);
+    // a listed chunk's LDS is reused by the next task
+    if (listed) __syncthreads();
+    return true;
+  };
+  for (int ti = 0; ti < t_count; ++ti) {
+    v4i kb[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) kb[nt] = kbn[nt];
+    int ks = ksn;
+    if (!score_task(ti, kb, ks, kbn, ksn)) break;
   }
   enter();  // a CTA without a score task
+  // every task's stores acknowledged, then their done words (one drain a CTA, not a task)
+  if (ok && t_count > 0) {
+    drain();
+    __syncthreads();
+    const int tid = opaque_v((int)threadIdx.x);
+    if (tid < t_count) {
+      int r, c;
+      task_rc(t_first + tid * t_step, r, c);
+      if (r < R) st_dev(&score_done[r * AT_NCHUNK + c], tag);
+    }
+  }
 
   // ---------------------------------------------------------------- 2: top-k
   stamp(p.timeline, MONO_TL_STAGED);
