@@ -52,7 +52,7 @@ struct MoeFp8Geom {
   static constexpr int KCW = NKC / QW;     // chunks a K slice holds
   static constexpr int NUG = I / 16;       // up/gate tasks per expert
   static constexpr int NKB = I / 128;      // 128-blocks of the intermediate
-  static constexpr int DNT = 32;           // output rows of a down task
+  static constexpr int DNT = 16;           // output rows of a down task
   static constexpr int NDN = H / DNT;
   static_assert(NKC % QW == 0, "hidden must split into 8 slices of 128-chunks");
   static_assert(I % 128 == 0, "intermediate must be whole 128-blocks");
@@ -782,8 +782,11 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
 
   // ---------------------------------------------------------------- stage 4
   stamp(p.timeline, MONO_TL_MIDQ);
-  // down: task f = output rows [32 f, 32 f + 32); waves 0-7 the first 16 rows, 8-15 the
-  // next 16; wave wq takes experts u = wq, wq + 8, ... in order. The (expert, row) mid
+  // down: task f = output rows [16 f, 16 f + 16); wave w takes experts u = w, w + 16, ...
+  // in order. CTA b runs task b, then tasks from a device-wide counter (nblk, nblk + 1,
+  // ...): its second is grabbed on arrival here, each later one in its wave 0's last step
+  // of the task before, so a CTA that leaves up/gate early takes two tasks and one that
+  // leaves late takes one, and the stage ends together. The (expert, row) mid
   // rows are copied into LDS over the dead activation operands, so the expert loop
   // streams weights with no poll and no other global load: first those of the experts
   // already quantised when the CTA gets here (one pass over the ready words, the first
@@ -791,6 +794,8 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   // after one wait, the others. Each wave still takes its experts in the same order.
   {
     const int ntask = ok ? G::NDN : 0;
+    constexpr int DW = G::WAVES;  // a wave's expert stride
+    static_assert(G::NDN >= 256, "a first task for every CTA of a full grid");
     uint8_t* mql = reinterpret_cast<uint8_t*>(xq_lds);  // [9 R slots][I] E4M3
     float* mcl = reinterpret_cast<float*>(mql + MOE_MAXR * MOE_SLOTS * I);  // [slots][NKB]
     static_assert(MOE_MAXR * MOE_SLOTS * (I + NKB * 4) <= LO::XS - LO::XQ, "mid slots");
@@ -802,13 +807,13 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     auto src_of = [&](int f, int u, uint32_t& so) {
       const bool live = f < ntask && u < nd;
       const int e = __builtin_amdgcn_readfirstlane(rl.uexp[live ? u : 0]);
-      const int row0 = (live ? f : 0) * G::DNT + 16 * half;
+      const int row0 = (live ? f : 0) * G::DNT;
       so = SHUF ? (uint32_t)((row0 / 16) * (I / 32) * 512) : (uint32_t)row0 * I;
       return rsrc(p.w2 + (size_t)e * H * I, live ? (uint32_t)H * I : 0u);
     };
     {
       uint32_t so;
-      const __amdgpu_buffer_rsrc_t r = src_of(b, wq, so);
+      const __amdgpu_buffer_rsrc_t r = src_of(b, w, so);
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         buf[kb][0] = ld16s<CP_NT>(r, vo, so + kb * CS);
@@ -849,6 +854,11 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     if (tid == 0) n1_s = nd;
     __syncthreads();
     if (ntask) {
+      // the second task, with the ready words' round trip
+      if (tid == 0) {
+        const uint32_t g = add_dev(&queue[2], 1u);
+        next_s = nblk + (int)g < ntask ? nblk + (int)g : ntask;
+      }
       const int i = tid;
       static_assert(MOE_NDIST * NKB <= 2 * G::THREADS, "two ready words a thread");
       const uint32_t r0 = ld4<CP_DEV>(rsrc(ready_w, (uint32_t)(nd * NKB) * 4u), (uint32_t)i * 4u);
@@ -859,20 +869,29 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     }
     __syncthreads();
     const int n1 = ntask ? n1_s : nd;
+    int next = ntask ? next_s : 0;
     const int s_split = n1 < nd ? rl.uslot[n1] : nsl;
     if (ok && ntask) copy_slots(0, s_split);
     __syncthreads();
     bool rest = n1 < nd;  // the experts from n1 on are still to be copied
-    for (int f = b; f < (ok ? ntask : 0); f += nblk) {
-      const int rg0 = f * G::DNT + 16 * half;
+    for (int f = b; f < (ok ? ntask : 0);) {
+      const int rg0 = f * G::DNT;
       v4f acc = {0.f, 0.f, 0.f, 0.f};
-      int u = wq;
+      int u = w;
+      uint32_t grabbed = 0;
       auto step = [&]() {
-        int fn = f, un = u + QW;
-        if (un >= nd) {
-          fn = f + nblk;
-          un = wq;
+        int fn = f, un = u + DW;
+        const bool last = un >= nd;
+        if (last) {
+          fn = next;
+          un = w;
         }
+        // the task after next: lane 0 of wave 0 in its last step (wave 0 has the most
+        // steps); the other lanes and steps are out of range, with no branch (a branch
+        // around the atomic would make the compiler wait for its reply right after it)
+        const bool grab_on = last && next < ntask;
+        grabbed = (uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
+            1, rsrc(queue + 2, grab_on ? 4u : 0u), tid == 0 ? 0u : 0x80000000u, 0, 0);
         uint32_t son;
         const __amdgpu_buffer_rsrc_t rn = src_of(fn, un, son);
         const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
@@ -894,7 +913,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
           acc += d * (sld(p.s2, s2b + kb) * cf);
           __builtin_amdgcn_sched_barrier(0);
         }
-        u += QW;
+        u += DW;
       };
       while (u < (rest ? n1 : nd)) step();
       if (rest) {
@@ -912,16 +931,17 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
         if (!ok) break;
         while (u < nd) step();
       }
-      // fixed-order reduction over each half's 8 waves, then the residual add
+      // fixed-order reduction over the 16 waves, then the residual add
       red[w][l] = acc;
+      if (tid == 0) next_s = next < ntask ? nblk + (int)grabbed : ntask;
       __syncthreads();
-      if (tid < 512) {
-        const int row = tid & 31, tok = tid >> 5;  // 32 rows x 16 columns, rows fastest
-        const int h = row >> 4, rr = row & 15;
-        const int L = tok + 16 * (rr >> 2), v = rr & 3;
+      const int after = next_s < ntask ? next_s : ntask;
+      if (tid < 256) {
+        const int row = tid & 15, tok = tid >> 4;  // 16 rows x 16 columns, rows fastest
+        const int L = tok + 16 * (row >> 2), v = row & 3;
         float ys = 0.f;
 #pragma unroll
-        for (int i = 0; i < QW; ++i) ys += red[h * QW + i][L][v];
+        for (int i = 0; i < G::WAVES; ++i) ys += red[i][L][v];
         if (tok < R) {
           const int col = f * G::DNT + row;
           const float av = bf16_lo((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
@@ -937,6 +957,8 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
         }
       }
       __syncthreads();
+      f = next;
+      next = after;
     }
   }
 
