@@ -451,6 +451,25 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
       if (ok && c < 2 * G::NKC) xs_lds[c >> 1][l & 15] = __uint_as_float(~sv[h]);
     }
   }
+  // Up/gate task b (b < NUG) is the shared expert's and CTA b's first, whatever the
+  // routing: its weights are pulled into L2 now, while the rows are routed (buffer -> LDS
+  // copies into the reduction buffer, idle until stage 2's first epilogue; stage 2's
+  // image check waits for them, long done by then), so that task's ring loads hit L2
+  if (b < NUG && !routes_row) {
+    const uint32_t vo = SHUF ? (uint32_t)(grp * 512 + t * 16) : (uint32_t)(t * H + 32 * grp);
+    constexpr uint32_t HO = SHUF ? 256 : 16, CS = SHUF ? 2048 : 128;
+    const int row0 = half * I + b * 16;
+    const uint32_t so = SHUF ? (uint32_t)((row0 / 16) * (H / 32) * 512 + wq * KCW * CS)
+                             : (uint32_t)(row0 * H + wq * KCW * 128);
+    const __amdgpu_buffer_rsrc_t r =
+        rsrc(p.w13 + (size_t)MOE_SHARED * (2 * I) * H, ok ? 2u * I * H : 0u);
+    auto* dst = (__attribute__((address_space(3))) void*)(&red[w][0]);
+#pragma unroll
+    for (int j = 0; j < KCW; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, vo, so + j * CS, 0, CP_NONE);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, vo + HO, so + j * CS, 0, CP_NONE);
+    }
+  }
   // Row r is routed once, by wave 0 of CTA (NTASK0 + r) mod grid: its 256 logits (the
   // 14 partials summed in a fixed order; a poll that finds an unwritten word is
   // discarded whole), sigmoid, bias top-8; the 8 ids and weights go out as
