@@ -453,8 +453,9 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   }
   // Up/gate task b (b < NUG) is the shared expert's and CTA b's first, whatever the
   // routing: its weights are pulled into L2 now, while the rows are routed (buffer -> LDS
-  // copies into the reduction buffer, idle until stage 2's first epilogue; stage 2's
-  // image check waits for them, long done by then), so that task's ring loads hit L2
+  // copies, every wave's into the first 1 KB of the reduction buffer, idle until stage
+  // 2's first epilogue and below 128 KB like every copy target here; stage 2's image
+  // check waits for them, long done by then), so that task's ring loads hit L2
   if (b < NUG && !routes_row) {
     const uint32_t vo = SHUF ? (uint32_t)(grp * 512 + t * 16) : (uint32_t)(t * H + 32 * grp);
     constexpr uint32_t HO = SHUF ? 256 : 16, CS = SHUF ? 2048 : 128;
@@ -463,7 +464,8 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
                              : (uint32_t)(row0 * H + wq * KCW * 128);
     const __amdgpu_buffer_rsrc_t r =
         rsrc(p.w13 + (size_t)MOE_SHARED * (2 * I) * H, ok ? 2u * I * H : 0u);
-    auto* dst = (__attribute__((address_space(3))) void*)(&red[w][0]);
+    auto* dst = (__attribute__((address_space(3))) void*)(&red[0][0]);
+    static_assert(LO::RED + 1024 <= 128 * 1024, "the pull's copies below 128 KB");
 #pragma unroll
     for (int j = 0; j < KCW; ++j) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, vo, so + j * CS, 0, CP_NONE);
