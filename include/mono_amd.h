@@ -167,7 +167,10 @@ int mono_moe_fp8_launch(const MonoMoeFp8Args* args, mono_stream_t stream);
  * calls that overlap on one GPU (two streams, no ordering) race; calls ordered on one
  * stream are safe. The waits use the library's default 10 s deadline. A timed-out call
  * leaves the block unusable: pass a pinned host_error word, and a call seeing it
- * non-zero is refused with MONO_E_FAILED. */
+ * non-zero is refused with MONO_E_FAILED. That refusal happens on the host, when the
+ * call is made: a launch captured in a HIP graph is not refused at replay, so after a
+ * timeout every replay runs on the aborted block and only fills out (and y) with NaN.
+ * Nothing resets the static block short of ending the process. */
 int mono_moe_fp8_launch_static(const MonoMoeFp8Args* args, mono_stream_t stream);
 
 /* ------------------------------------------------------------------------------

@@ -41,13 +41,16 @@ def bf16(x) -> np.ndarray:
     return torch.as_tensor(np.asarray(x, dtype=np.float32)).to(torch.bfloat16).float().numpy()
 
 
-def attn_out(o_lat, h, w_uv, s_uv, w_o, s_o):
+def attn_out(o_lat, h, w_uv, s_uv, w_o, s_o, uv=None):
     """o_lat [R, H, 512] bf16 values; h [R, 7168]; w_uv [H, 128, 512] + s_uv [H, 1, 4];
     w_o [7168, H * 128] + s_o [56, H]. Returns dict(o bf16-rounded f32 [R, H * 128],
-    y f64 [R, 7168] = W_o o, a bf16-rounded f32 = h + y)."""
+    y f64 [R, 7168] = W_o o, a bf16-rounded f32 = h + y). ``uv(o_lat_h [R, 512], h) ->
+    [R, 128]`` replaces the W_UV GEMV (w_uv / s_uv may then be None)."""
     o_lat = np.asarray(torch.as_tensor(o_lat).float())
     heads = o_lat.shape[1]
-    o = np.concatenate([w8a16_gemv(o_lat[:, i], w_uv[i], s_uv[i]) for i in range(heads)], -1)
+    if uv is None:
+        uv = lambda x, i: w8a16_gemv(x, w_uv[i], s_uv[i])  # noqa: E731
+    o = np.concatenate([np.asarray(uv(o_lat[:, i], i), np.float64) for i in range(heads)], -1)
     o = bf16(o)
     y = w8a16_gemv(o, w_o, s_o)
     a = bf16(np.asarray(torch.as_tensor(h).float()) + y)

@@ -177,9 +177,11 @@ def kv_quant(row, scaled: bool = True):
 
 
 def front(h, g_in, g_q, g_kv, w_qkv_a, s_qkv_a, w_k, s_k, w_w, g_k, b_k, w_qb, s_qb,
-          w_iq, s_iq, w_uk, s_uk, cos, sin, positions, eps=1e-6, kv_scaled=True):
+          w_iq, s_iq, w_uk, s_uk, cos, sin, positions, eps=1e-6, kv_scaled=True, absorb=None):
     """One step's front for rows h [R, 7168] (bf16 values) at ``positions``; row-major
     weights (numpy E4M3 codes, f32 scales; w_w bf16 values); cos/sin [pos, 32].
+    ``absorb(q_nope_h [R, 128], h) -> [R, 512]`` replaces the W_UK GEMV (w_uk / s_uk may
+    then be None): a caller holding W_UK in another orientation states its product.
 
     Returns dict with x, q_a, kv_a, k, w (f64 GEMV outputs), q_an (bf16), kv_rows
     (bf16-valued [R, 576] before quantisation), kv_codes u8 [R, 576], kv_scale f32 [R],
@@ -208,7 +210,9 @@ def front(h, g_in, g_q, g_kv, w_qkv_a, s_qkv_a, w_k, s_k, w_w, g_k, b_k, w_qb, s
     qb =D.w8a16_gemv(q_an, w_qb, s_qb).reshape(R, HEADS, NOPE + ROPE)
     q_nope = bf16(qb[..., :NOPE])
     q_pe = bf16(rope(qb[..., NOPE:], c[:, None], s[:, None]))
-    q_lat = np.stack([bf16(D.w8a16_gemv(q_nope[:, hh], w_uk[hh], s_uk[hh]))
+    if absorb is None:
+        absorb = lambda qn, hh: D.w8a16_gemv(qn, w_uk[hh], s_uk[hh])  # noqa: E731
+    q_lat = np.stack([bf16(np.asarray(absorb(q_nope[:, hh], hh), np.float64))
                       for hh in range(HEADS)], 1)
     q = np.concatenate([q_lat, q_pe], -1)
     iq_raw = bf16(D.w8a16_gemv(q_an, w_iq, s_iq)).reshape(R, IHEADS, IDIM)

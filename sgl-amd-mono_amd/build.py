@@ -47,10 +47,7 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every ``csrc/*.hip`` into ``libmono_amd.so`` (always recompiles)."""
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *map(str, sources()), "-o", str(tmp)]
+def _run(cmd: list, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -62,6 +59,26 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if verbose and err:
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int = 0) -> Path:
+    """Compile every ``csrc/*.hip`` into ``libmono_amd.so`` (always recompiles): each
+    source to an object of its own, in parallel, then one link."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
+    srcs = sources()
+    jobs = jobs or min(len(srcs), os.cpu_count() or 1, 16)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="mono_build_") as tmpdir:
+        objs = [Path(tmpdir) / (src.stem + ".o") for src in srcs]
+        cmds = [[hipcc(), *flags, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+                for src, obj in zip(srcs, objs)]
+        with ThreadPoolExecutor(jobs) as pool:
+            list(pool.map(lambda c: _run(c, verbose), cmds))
+        tmp = LIB.with_suffix(".so.tmp")
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o",
+              str(tmp)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

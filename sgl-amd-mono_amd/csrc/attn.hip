@@ -5,8 +5,9 @@ namespace mono {
 
 template <int SPLIT, bool LONG, bool DSA>
 __global__ void __launch_bounds__(AT_THREADS, 1) attn_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[AT_LDS_BYTES];
-  __shared__ LaunchShared sh;
+  using Arena = LdsArena<AT_LDS_BYTES>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[Arena::TOTAL];
+  LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
   const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);

@@ -4,8 +4,9 @@
 namespace mono {
 
 __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[FR_LDS_BYTES];
-  __shared__ LaunchShared sh;
+  using Arena = LdsArena<FR_LDS_BYTES>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[Arena::TOTAL];
+  LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
   const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);

@@ -307,6 +307,7 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
       const __amdgpu_buffer_rsrc_t rh = rsrc(p.h, (uint32_t)R * FR_H * 2u);
       // rows g 8 .. g 8 + 7 of h straight into LDS (buffer -> LDS, no registers): a row
       // is 14 chunks of 1 KiB, a wave copies 7 of the group's 112
+      static_assert(FR_LDS_XS + FR_XG * FR_XS * 2 <= LDS_DMA_END, "x rows' copies below 128 KB");
       auto dma_rows = [&](int g) {
 #pragma unroll
         for (int i = 0; i < 7; ++i) {

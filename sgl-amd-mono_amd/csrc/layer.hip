@@ -70,8 +70,9 @@ constexpr int LY_TL_FRONT = 1, LY_TL_ATTN = 2, LY_TL_POST = 3, LY_TL_MOE = 4, LY
 
 template <bool SHUF, int SPLIT, bool LONG, bool DSA>
 __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[LY_LDS_BYTES];
-  __shared__ LaunchShared sh;
+  using Arena = LdsArena<LY_LDS_BYTES>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[Arena::TOTAL];
+  LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
   uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
@@ -311,22 +312,20 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   // CTA of its own, at most two B tiles a CTA
   if (grid > FR_MAX_GRID || grid < FR_ATASKS + 4 * R || grid < FR_CT || 2 * grid < FR_BT)
     return set_error(MONO_E_DEVICE, "mono_layer_launch: needs 224..1024 CUs (and 168 + 4 rows)");
-  // 64-key splits when the rows' 32 splits each take one CTA, else 128-key splits
-  const bool s64 = R * (AT_TOPK / 64) <= grid;
+  // 64-key splits, the rows' 32 splits each on a CTA of its own (8 rows: 256 CTAs)
+  if (R * (AT_TOPK / 64) > grid)
+    return set_error(MONO_E_DEVICE, "mono_layer_launch: needs a CTA for each of the rows' "
+                                    "32 attention splits (32 x rows CUs)");
   // rows that may span more than one top-k block take the multi-block variant
   const bool lng = a->ctx_max > AT_TKBLOCK;
   // DSA (FP8) index pages take their own instances (their score code holds more registers)
   using K = void (*)(LayerParams);
-  const K kerns[2][2][2][2] = {
-      {{{layer_kernel<false, 128, false, false>, layer_kernel<false, 128, false, true>},
-        {layer_kernel<false, 128, true, false>, layer_kernel<false, 128, true, true>}},
-       {{layer_kernel<false, 64, false, false>, layer_kernel<false, 64, false, true>},
-        {layer_kernel<false, 64, true, false>, layer_kernel<false, 64, true, true>}}},
-      {{{layer_kernel<true, 128, false, false>, layer_kernel<true, 128, false, true>},
-        {layer_kernel<true, 128, true, false>, layer_kernel<true, 128, true, true>}},
-       {{layer_kernel<true, 64, false, false>, layer_kernel<true, 64, false, true>},
-        {layer_kernel<true, 64, true, false>, layer_kernel<true, 64, true, true>}}}};
-  const K kern = kerns[shuf][s64][lng][!fp4];
+  const K kerns[2][2][2] = {
+      {{layer_kernel<false, 64, false, false>, layer_kernel<false, 64, false, true>},
+       {layer_kernel<false, 64, true, false>, layer_kernel<false, 64, true, true>}},
+      {{layer_kernel<true, 64, false, false>, layer_kernel<true, 64, false, true>},
+       {layer_kernel<true, 64, true, false>, layer_kernel<true, 64, true, true>}}};
+  const K kern = kerns[shuf][lng][!fp4];
   rc = check_coresident(kern, 1024, 0, "mono_layer_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);

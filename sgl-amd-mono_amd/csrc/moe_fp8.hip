@@ -5,8 +5,9 @@ namespace mono {
 
 template <int H, int I, bool SHUF>
 __global__ void __launch_bounds__(1024, 1) moe_fp8_kernel(MoeFp8Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[MoeLds<H, I>::BYTES];
-  __shared__ LaunchShared sh;
+  using Arena = LdsArena<MoeLds<H, I>::BYTES>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[Arena::TOTAL];
+  LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
   uint32_t tag = 0;

@@ -404,6 +404,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   // before all of its words were written holds zeros, which the check below finds;
   // the re-copy then reads device-coherent (sc1) data.
   static_assert(G::SZ_XQ / 1024 == 2 * G::NKC, "two 1 KiB chunks a 128-K chunk");
+  static_assert(LO::XQ + (int)G::SZ_XQ <= LDS_DMA_END, "the image's copies below 128 KB");
   const __amdgpu_buffer_rsrc_t rxq = rsrc(hxq, (uint32_t)G::SZ_XQ);
   auto copy_image = [&](int w0, int nw, bool coherent) {
     for (int c = w - w0; c < (int)(G::SZ_XQ / 1024); c += nw) {
@@ -465,7 +466,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     const __amdgpu_buffer_rsrc_t r =
         rsrc(p.w13 + (size_t)MOE_SHARED * (2 * I) * H, ok ? 2u * I * H : 0u);
     auto* dst = (__attribute__((address_space(3))) void*)(&red[0][0]);
-    static_assert(LO::RED + 1024 <= 128 * 1024, "the pull's copies below 128 KB");
+    static_assert(LO::RED + 1024 <= LDS_DMA_END, "the pull's copies below 128 KB");
 #pragma unroll
     for (int j = 0; j < KCW; ++j) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, vo, so + j * CS, 0, CP_NONE);
@@ -820,6 +821,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     uint8_t* mql = reinterpret_cast<uint8_t*>(xq_lds);  // [9 R slots][I] E4M3
     float* mcl = reinterpret_cast<float*>(mql + MOE_MAXR * MOE_SLOTS * I);  // [slots][NKB]
     static_assert(MOE_MAXR * MOE_SLOTS * (I + NKB * 4) <= LO::XS - LO::XQ, "mid slots");
+    static_assert(LO::XQ + MOE_MAXR * MOE_SLOTS * I <= LDS_DMA_END, "mid copies below 128 KB");
     // one tile of weight chunks a wave; each chunk is refilled with the next step's as
     // soon as its MFMA issued, the last expert of a task running into the next task
     v4i buf[NKB][2];

@@ -152,16 +152,29 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   const int R = p.rows;
   const int nblk = gridDim.x, b = blockIdx.x;
 
-  __shared__ RouteLds rl;
-  __shared__ v4f red[2][G::WAVES][64];  // up/gate: by task parity; down: [0]
-  // up/gate: the rows as MFMA B operands, [step][d][lane] (16 B: 8 bf16 of row lane % 16
-  // at K 128 step + 32 (lane / 16) + 8 d); down: the mid slot rows, bf16 [R x 9][I]
-  __shared__ __attribute__((aligned(16))) uint8_t mid_lds[MOE_MAXR * MOE_SLOTS * I * 2];
-  static_assert(G::NKS * 4 * 64 * 16 <= (int)sizeof(mid_lds), "B operand staging");
-  __shared__ float wslot[MOE_MAXR * MOE_SLOTS];  // route weight of each (expert, row) slot
-  __shared__ uint32_t head_s[4];
-  __shared__ LaunchShared sh;  // the launch end's role word
-  __shared__ int ok_s;
+  // One arena (the kernel's only LDS variable, at LDS address 0), carved here:
+  //   MID   up/gate: the rows as MFMA B operands, [step][d][lane] (16 B: 8 bf16 of row
+  //         lane % 16 at K 128 step + 32 (lane / 16) + 8 d); down: the mid slot rows,
+  //         bf16 [R x 9][I], copied by buffer -> LDS copies, so first and below 128 KB
+  //   RL    RouteLds;  RED  v4f [2][16][64] (up/gate: by task parity; down: [0])
+  //   WS    f32 [R x 9]: route weight of each (expert, row) slot;  HEAD  u32 [4];  OK  int
+  constexpr int MID = 0, MID_BYTES = MOE_MAXR * MOE_SLOTS * I * 2;
+  constexpr int RL = (MID + MID_BYTES + 15) & ~15;
+  constexpr int RED = (RL + (int)sizeof(RouteLds) + 15) & ~15;
+  constexpr int WS = RED + 2 * G::WAVES * 64 * 16;
+  constexpr int HEAD = (WS + MOE_MAXR * MOE_SLOTS * 4 + 15) & ~15;
+  constexpr int OK = HEAD + 16;
+  using Arena = LdsArena<OK + 4>;
+  static_assert(MID + MID_BYTES <= LDS_DMA_END, "the mid copies below 128 KB");
+  static_assert(G::NKS * 4 * 64 * 16 <= MID_BYTES, "B operand staging");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[Arena::TOTAL];
+  uint8_t* const mid_lds = lds + MID;
+  RouteLds& rl = *reinterpret_cast<RouteLds*>(lds + RL);
+  v4f (*red)[G::WAVES][64] = reinterpret_cast<v4f (*)[G::WAVES][64]>(lds + RED);
+  float* const wslot = reinterpret_cast<float*>(lds + WS);
+  uint32_t* const head_s = reinterpret_cast<uint32_t*>(lds + HEAD);
+  int& ok_s = *reinterpret_cast<int*>(lds + OK);
+  LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
 
   uint16_t* mid = reinterpret_cast<uint16_t*>(p.scratch + G::OFF_MID);
   uint32_t* done = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_DONE);

@@ -27,6 +27,16 @@ struct LaunchShared {
   int role;
 };
 
+// A kernel's LDS: ONE arena of BYTES (the phases' carving) with the launch's shared words
+// after it. As the kernel's only LDS variable the arena starts at LDS address 0, so an
+// offset into it is the LDS address a buffer -> LDS copy writes (see LDS_DMA_END).
+template <int BYTES>
+struct LdsArena {
+  static constexpr int BODY = (BYTES + 15) & ~15;
+  static constexpr int TOTAL = BODY + (int)sizeof(LaunchShared);
+  static_assert(TOTAL <= 160 * 1024, "gfx950 LDS");
+};
+
 // The launch tag after `epoch`. Tags run 1 .. 0xFFFFFFFE and then start again at 1:
 // never 0 (the tag of a pair nobody wrote or the scrub cleared), and the cycle is even,
 // so the buffers indexed by the tag's parity keep alternating across the wrap.

@@ -9,10 +9,11 @@ another format, and each copy is logged in ``copies`` under (what, layer, name):
 
 * W_UK / W_UV: SGLang's per-tensor FP8 ``w_kc`` [heads, 128, 512] / ``w_vc`` [heads,
   512, 128] transposed to the launches' [head][out][in] rows, with the scalar ``w_scale``
-  as every block scale (``weights.py:145-184``);
+  as every block scale (``weights.py:145-184``), each packed once a layer;
 * the index key LayerNorm weight and bias in f32 (``weights.py:187-210``);
 * the RoPE table: SGLang's f32 ``cos_sin_cache`` [positions, 64] (cos | sin) as the
-  bf16 [positions, 32] pair the front reads.
+  bf16 [positions, 32] pair the front reads, made once for all covered layers
+  (``rope_table``: every layer's MLA and indexer rotary must hold the same cache).
 
 Mismatches raise ``ValueError`` naming the tensor, before anything launches; a cache
 that does not have the launches' layout raises ``RuntimeError`` (``spec.py:446-461``).
@@ -73,47 +74,88 @@ def _shuffled(t: torch.Tensor, layout: str) -> torch.Tensor:
     return t.contiguous()
 
 
-def absorbed(attn, idx: int, copies: dict, layout: str, cfg: LayerConfig = DSV32):
-    """W_UK [heads, 512, 128] and W_UV [heads, 128, 512] (E4M3, ``layout`` per head) with
-    their block scales, from ``w_kc`` / ``w_vc`` and the scalar ``w_scale``."""
+def _per_tensor(attn, cfg: LayerConfig):
+    """SGLang's per-tensor E4M3 ``w_kc`` [heads, nope, latent], ``w_vc`` [heads, latent,
+    v] and the scalar ``w_scale`` they share, checked."""
     w_kc, w_vc, w_scale = attn.w_kc, attn.w_vc, getattr(attn, "w_scale", None)
-    hh, nope, c, v = cfg.heads, cfg.nope_dim, cfg.kv_lora, cfg.v_dim
     if w_kc.dtype != FP8 or w_scale is None or w_scale.numel() != 1:
         raise ValueError(
             f"w_kc / w_vc: needs per-tensor E4M3 with a scalar w_scale, got {w_kc.dtype} and "
             f"{None if w_scale is None else tuple(w_scale.shape)}")
-    _same("w_kc", w_kc, (hh, nope, c), FP8)
-    _same("w_vc", w_vc, (hh, c, v), FP8)
-    scale = float(w_scale.float().reshape(()).item())
-    uk = w_kc.transpose(1, 2).contiguous()  # [h][c][nope]: latent rows over the nope dims
-    uv = w_vc.transpose(1, 2).contiguous()  # [h][v][c]: value rows over the latent
+    _same("w_kc", w_kc, (cfg.heads, cfg.nope_dim, cfg.kv_lora), FP8)
+    _same("w_vc", w_vc, (cfg.heads, cfg.kv_lora, cfg.v_dim), FP8)
+    return w_kc, w_vc, float(w_scale.float().reshape(()).item())
+
+
+def pack_uk(attn, idx: int, copies: dict, layout: str, cfg: LayerConfig = DSV32):
+    """W_UK [heads, 512, 128] (E4M3, ``layout`` per head) and its block scales. SGLang
+    absorbs as ``q_lat[h] = q_nope[h] @ w_kc[h]`` (w_kc [heads, 128, 512]); the front's
+    GEMV computes y[c] = sum_n W[c][n] x[n], so W_UK[h] = w_kc[h] transposed, with the
+    scalar w_scale as every block scale (``weights.py:145-184``)."""
+    w_kc, _, scale = _per_tensor(attn, cfg)
+    hh = cfg.heads
+    uk = w_kc.transpose(1, 2).contiguous()  # [h][latent c][nope n]
     w_uk = torch.stack([_shuffled(uk[h], layout) for h in range(hh)])
+    s_uk = torch.full((hh, cfg.kv_lora // 128, (cfg.nope_dim + 127) // 128), scale,
+                      dtype=torch.float32, device=w_kc.device)
+    copies["W_UK / W_UV packed", idx, "w_uk"] = w_uk
+    copies["W_UK / W_UV packed", idx, "s_uk"] = s_uk
+    return w_uk, s_uk
+
+
+def pack_uv(attn, idx: int, copies: dict, layout: str, cfg: LayerConfig = DSV32):
+    """W_UV [heads, 128, 512] (E4M3, ``layout`` per head) and its block scales. SGLang
+    maps the latent back as ``o[h] = o_lat[h] @ w_vc[h]`` (w_vc [heads, 512, 128]); as the
+    output block's GEMV rows, W_UV[h] = w_vc[h] transposed, at the scalar w_scale."""
+    _, w_vc, scale = _per_tensor(attn, cfg)
+    hh = cfg.heads
+    uv = w_vc.transpose(1, 2).contiguous()  # [h][v][latent c]
     w_uv = torch.stack([_shuffled(uv[h], layout) for h in range(hh)])
-    f32 = dict(dtype=torch.float32, device=w_kc.device)
-    s_uk = torch.full((hh, c // 128, (nope + 127) // 128), scale, **f32)
-    s_uv = torch.full((hh, v // 128, c // 128), scale, **f32)
-    for name, t in (("w_uk", w_uk), ("s_uk", s_uk), ("w_uv", w_uv), ("s_uv", s_uv)):
-        copies["W_UK / W_UV packed", idx, name] = t
-    return w_uk, s_uk, w_uv, s_uv
+    s_uv = torch.full((hh, cfg.v_dim // 128, cfg.kv_lora // 128), scale,
+                      dtype=torch.float32, device=w_vc.device)
+    copies["W_UK / W_UV packed", idx, "w_uv"] = w_uv
+    copies["W_UK / W_UV packed", idx, "s_uv"] = s_uv
+    return w_uv, s_uv
 
 
-def rope_table(rotary, idx: int, copies: dict):
-    """bf16 cos / sin [positions, 32] from SGLang's f32 ``cos_sin_cache`` [positions, 64]
-    (cos in the first half, sin in the second)."""
+def _cos_sin_cache(rotary, what: str) -> torch.Tensor:
     cache = getattr(rotary, "cos_sin_cache", None)
     if cache is None or cache.dim() != 2 or cache.shape[1] != DSV32.rope_dim:
         got = None if cache is None else tuple(cache.shape)
-        raise ValueError(f"rotary_emb.cos_sin_cache: needs [positions, {DSV32.rope_dim}], got {got}")
+        raise ValueError(f"{what}.cos_sin_cache: needs [positions, {DSV32.rope_dim}], got {got}")
+    return cache
+
+
+def rope_table(layers: dict, copies: dict):
+    """The bf16 cos / sin [positions, 32] that every covered layer's front reads, made once
+    from the first layer's MLA rotary: SGLang's f32 ``cos_sin_cache`` [positions, 64]
+    (rotating with ``cos, sin = cache[pos].chunk(2, -1)``). The front rotates the index
+    key and query with the same table, so each layer's MLA rotary and its indexer's (when
+    it keeps its own) must hold the same cache (``glm53/gfx950/weights.py:323-344``).
+    ``layers``: {layer index: SGLang decoder layer}."""
+    first = min(layers)
+    cache = _cos_sin_cache(layers[first].self_attn.rotary_emb, f"layer {first} rotary_emb")
+    for i, layer in sorted(layers.items()):
+        attn = layer.self_attn
+        mine = _cos_sin_cache(attn.rotary_emb, f"layer {i} rotary_emb")
+        ind = getattr(getattr(attn, "indexer", None), "rotary_emb", None)
+        others = [mine] + ([_cos_sin_cache(ind, f"layer {i} indexer.rotary_emb")] if ind else [])
+        for other in others:
+            if other is not cache and (other.shape != cache.shape or not torch.equal(other, cache)):
+                raise ValueError(f"layer {i}: the indexer's and every layer's rotary table "
+                                 f"must equal layer {first}'s MLA one (one table is read)")
     half = DSV32.rope_dim // 2
     cos = cache[:, :half].to(torch.bfloat16).contiguous()
     sin = cache[:, half:].to(torch.bfloat16).contiguous()
-    copies["RoPE table bf16", idx, "cos"] = cos
-    copies["RoPE table bf16", idx, "sin"] = sin
+    copies["RoPE table bf16", first, "cos"] = cos
+    copies["RoPE table bf16", first, "sin"] = sin
     return cos, sin
 
 
-def front_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> FrontWeights:
-    """The attention front of a loaded layer (``self_attn`` with its indexer)."""
+def front_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32,
+                  rope=None) -> FrontWeights:
+    """The attention front of a loaded layer (``self_attn`` with its indexer); ``rope``:
+    the (cos, sin) table shared by the covered layers (made from this layer if None)."""
     attn = layer.self_attn
     ind = getattr(attn, "indexer", None)
     if ind is None:
@@ -136,8 +178,8 @@ def front_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> Fr
     b_k = ind.k_norm.bias.detach().float().contiguous()
     copies["indexer k LayerNorm f32", idx, "weight"] = g_k
     copies["indexer k LayerNorm f32", idx, "bias"] = b_k
-    w_uk, s_uk, _, _ = absorbed(attn, idx, copies, layout, cfg)
-    cos, sin = rope_table(attn.rotary_emb, idx, copies)
+    w_uk, s_uk = pack_uk(attn, idx, copies, layout, cfg)
+    cos, sin = rope if rope is not None else rope_table({idx: layer}, copies)
     return FrontWeights(g_in=g_in, g_q=g_q, g_kv=g_kv, w_qkv_a=w_qkv_a, s_qkv_a=s_qkv_a,
                         w_k=w_k, s_k=s_k, w_w=w_w, g_k=g_k, b_k=b_k, w_qb=w_qb, s_qb=s_qb,
                         w_iq=w_iq, s_iq=s_iq, w_uk=w_uk, s_uk=s_uk, cos=cos, sin=sin,
@@ -148,7 +190,7 @@ def post_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> Pos
     """The attention output block: ``o_proj`` in place, W_UV packed in its layout."""
     attn = layer.self_attn
     w_o, s_o, layout = _linear("o_proj", attn.o_proj, cfg.hidden, cfg.heads * cfg.v_dim)
-    _, _, w_uv, s_uv = absorbed(attn, idx, copies, layout, cfg)
+    w_uv, s_uv = pack_uv(attn, idx, copies, layout, cfg)
     return PostWeights(w_uv=w_uv, s_uv=s_uv, w_o=w_o, s_o=s_o, layout=layout)
 
 
@@ -166,9 +208,11 @@ def moe_weights(layer) -> MoeFp8Weights:
     )
 
 
-def layer_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32) -> LayerWeights:
-    """Every weight of a covered layer's four launches."""
-    return LayerWeights(front=front_weights(layer, idx, copies, cfg),
+def layer_weights(layer, idx: int, copies: dict, cfg: LayerConfig = DSV32,
+                  rope=None) -> LayerWeights:
+    """Every weight of a covered layer's four launches; ``rope``: the covered layers'
+    shared (cos, sin) table (``rope_table``; made from this layer if None)."""
+    return LayerWeights(front=front_weights(layer, idx, copies, cfg, rope),
                         post=post_weights(layer, idx, copies, cfg), moe=moe_weights(layer))
 
 

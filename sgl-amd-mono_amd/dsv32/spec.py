@@ -48,7 +48,7 @@ except ModuleNotFoundError:  # SGLang before sgl-project/sglang#45389
     )
 
 from .config import DSV32
-from .runner import StepRows, page_table
+from .runner import StepRows
 
 MAX_ROWS = 8  # the front builds x of at most 8 rows in LDS
 WIDTHS = tuple(range(1, MAX_ROWS + 1))  # one build serves every row count up to 8
@@ -65,6 +65,11 @@ NUMERICS = Numerics(
         "layer.out.rel": 1e-2,
         "router.ids.mismatch": 0.0,
         "indexer.topk.mismatch": 0.0,
+        # the cache rows the launch writes against SGLang's (floors)
+        "layer.kv.cosine": 0.995,
+        "layer.index.cosine": 0.999,
+        # the selection is exactly the top-k of the launch's own scores
+        "layer.topk_exact.max_abs": 0.0,
     },
 )
 
@@ -185,13 +190,19 @@ def _config_disable_reasons(cfg, hf_config) -> list:
 
 def _model_disable_reasons(model, hf_config, copies) -> list:
     """Why the loaded model cannot be read in place (an empty list: it can)."""
-    from .binding import layer_disable_reason
+    from .binding import layer_disable_reason, rope_table
 
     reasons = []
-    for i in covered_layers(hf_config):
-        why = layer_disable_reason(model.model.layers[i], i)
+    layers = {i: model.model.layers[i] for i in covered_layers(hf_config)}
+    for i, layer in layers.items():
+        why = layer_disable_reason(layer, i)
         if why is not None:
             reasons.append(why)
+    if layers and not reasons:
+        try:
+            rope_table(layers, {})
+        except (ValueError, AttributeError) as e:
+            reasons.append(str(e))
     return reasons
 
 
@@ -216,7 +227,7 @@ class _Built:
         self.last = max(layers) if layers else None
         self.max_rows = MAX_ROWS
         self.max_position = context_len - 1
-        self.steps = {w: StepRows.empty(w, device) for w in WIDTHS}
+        self.steps = {w: StepRows.empty(w, device, context_len) for w in WIDTHS}
         self.pad_h = {w: torch.zeros(w, DSV32.hidden, dtype=torch.bfloat16, device=device)
                       for w in WIDTHS}
 
@@ -299,43 +310,58 @@ class _Built:
         return set_written(out[:S], forward_batch)
 
     def _checked(self, L: _Layer, positions, h, caches, lstep, forward_batch, S: int):
-        """The launch, with SGLang's layer run first on the same rows (check mode)."""
+        """The launch, with SGLang's layer run first on the same rows (check mode). The
+        one launch also hands out its routed ids, index scores and selection, which
+        ``check.compare`` scores against SGLang's and against the exact top-k."""
         from . import check
         from .layer import FusedLayerOp, LayerDebug
 
         ref = check.reference(L, positions, h[:S], forward_batch, S, self.cfg,
                               forward_batch.token_to_kv_pool)
-        ids = topk = None
+        extra = {}
         if isinstance(L.op, FusedLayerOp):
-            W, dev = h.shape[0], h.device
-            dbg = LayerDebug(ids=torch.empty(W, self.cfg.top_k + 1, dtype=torch.int32, device=dev),
-                             topk=torch.empty(W, self.cfg.index_topk, dtype=torch.int32,
-                                              device=dev))
+            W, dev, cfg = h.shape[0], h.device, self.cfg
+            dbg = LayerDebug(
+                ids=torch.empty(W, cfg.top_k + 1, dtype=torch.int32, device=dev),
+                topk=torch.empty(W, cfg.index_topk, dtype=torch.int32, device=dev),
+                scores=torch.empty(W, L.op.ctx_max, dtype=torch.float32, device=dev))
             out = L.op.launch(h, caches, lstep, debug=dbg)
-            ids = dbg.ids[:, 1:]
             pos = dbg.topk[:S].long()
             pages = lstep.page_table[lstep.req_ids[:S].long()[:, None],
-                                     (pos.clamp_min(0) // self.cfg.page)].long()
-            topk = torch.where(pos >= 0, pages * self.cfg.page + pos % self.cfg.page, -1)
+                                     pos.clamp_min(0) // cfg.page].long()
+            counts = torch.where(lstep.slots[:S] >= 0, lstep.positions[:S] + 1, 0)
+            extra = dict(ids=dbg.ids[:, 1:],
+                         topk_slots=torch.where(pos >= 0, pages * cfg.page + pos % cfg.page, -1),
+                         scores=dbg.scores[:S], topk_pos=pos, counts=counts.tolist())
         else:
             out = L.op.launch(h, caches, lstep)
-        check.compare(L, out[:S], ref, S, ids=ids, topk_slots=topk, numerics=NUMERICS.bounds)
+        check.compare(L, out[:S], ref, S, numerics=NUMERICS.bounds, **extra)
         return out
 
     def step(self, plan, positions, forward_batch):
-        """The step's row tables, written once a step (in the graph when captured)."""
+        """The step's row tables, written once a step (in the graph when captured). The
+        page table is the attention backend's ``real_page_table`` in place when it covers
+        the served context (the launches read a row's pages up to ``ctx_max``); the DSA
+        backend sizes that table by the batch's longest sequence, so a narrower one is
+        replaced by the step's own full-width table, filled from ``req_to_token``."""
         if "step" not in plan.state:
             S = plan.key.rows
             st = self.steps[_width(S)]
             md = getattr(getattr(forward_batch, "attn_backend", None), "forward_metadata", None)
             pt = getattr(md, "real_page_table", None)
-            if pt is None:
-                pt = page_table(forward_batch.req_to_token_pool.req_to_token,
-                                forward_batch.req_pool_indices, S, self.max_position + 1)
+            if not self.page_table_covers(pt):
+                pt = st.fill_pages(forward_batch.req_to_token_pool.req_to_token,
+                                   forward_batch.req_pool_indices, S)
             st.write(positions, forward_batch.out_cache_loc, S, self.max_position,
                      page_table=pt)
             plan.state["step"] = _Step(st)
         return plan.state["step"]
+
+    def page_table_covers(self, pt) -> bool:
+        """Whether a backend page table can be read in place: int32 [requests, pages]
+        with contiguous rows and pages for every key up to the served context."""
+        return (pt is not None and pt.dtype == torch.int32 and pt.dim() == 2
+                and pt.stride(1) == 1 and pt.shape[1] * PAGE_SIZE >= self.max_position + 1)
 
     @staticmethod
     def _caches(L: _Layer, forward_batch):
@@ -371,7 +397,7 @@ def _build(model, hf_config, ctx):
     projections SGLang left in mixed FP8 layouts runs as the four launches instead.
     ``SGLANG_AMD_MONO_FAULT_INJECT`` (``rank:site[:after]``) arms a test stall."""
     from ..guard import fault_injection, watchdog_deadline
-    from .binding import layer_weights
+    from .binding import layer_weights, rope_table
     from .layer import FusedLayerOp, LayerOp, LayerRuntimes, layer_runtime
 
     deadline = watchdog_deadline(getattr(ctx, "deadline_s", 120.0) * 2)
@@ -383,9 +409,10 @@ def _build(model, hf_config, ctx):
     cfg = dataclasses.replace(DSV32, n_group=n_group, topk_group=topk_group)
     fault = fault_injection(int(getattr(ctx, "tp_rank", 0) or 0)) or (0, 0)
     layers, rt, chained, device = {}, None, None, None
-    for i in covered_layers(hf_config):
-        mod = model.model.layers[i]
-        w = layer_weights(mod, i, copies)
+    modules = {i: model.model.layers[i] for i in covered_layers(hf_config)}
+    rope = rope_table(modules, copies) if modules else None  # one table for every layer
+    for i, mod in modules.items():
+        w = layer_weights(mod, i, copies, rope=rope)
         device = w.moe.w13.device
         if rt is None:
             rt = layer_runtime(device, MAX_ROWS, deadline)

@@ -208,3 +208,77 @@ def test_a_layer_that_cannot_bind_refuses_the_model_with_its_reason():
     assert len(reasons) == 1 and reasons[0].startswith("layer 2:") and "indexer" in reasons[0]
     assert spec._model_disable_reasons(NS(model=NS(layers=[None, ok])),
                                        NS(first_k_dense_replace=1, num_hidden_layers=2), {}) == []
+
+
+def _sglang_attn(seed, positions=96):
+    """SGLang's MLA tensors drawn on their own (not from the launches' structs): per-tensor
+    E4M3 ``w_kc`` [32, 128, 512] and ``w_vc`` [32, 512, 128] at a scalar ``w_scale``, and
+    a rotary ``cos_sin_cache`` [positions, 64] built as SGLang's rotary embedding builds
+    it (angles pos * theta^(-2i/64), cos then sin)."""
+    g = torch.Generator().manual_seed(seed)
+    codes = lambda *shape: torch.randint(0, 0x7E, shape, generator=g, dtype=torch.uint8) | (
+        torch.randint(0, 2, shape, generator=g, dtype=torch.uint8) << 7)
+    w_kc = codes(DSV32.heads, DSV32.nope_dim, DSV32.kv_lora).view(FP8)
+    w_vc = codes(DSV32.heads, DSV32.kv_lora, DSV32.v_dim).view(FP8)
+    inv = 10000.0 ** (-torch.arange(0, 64, 2, dtype=torch.float64) / 64)
+    ang = torch.arange(positions, dtype=torch.float64)[:, None] * inv[None]
+    cache = torch.cat([ang.cos(), ang.sin()], 1).float()
+    return NS(w_kc=w_kc, w_vc=w_vc, w_scale=torch.tensor(SCALE),
+              rotary_emb=NS(cos_sin_cache=cache))
+
+
+@pytest.mark.parametrize("layout", [layouts.ROWMAJOR, layouts.AITER16])
+def test_packed_absorb_matrices_apply_sglangs_products(layout):
+    """SGLang absorbs with q_lat[h] = q_nope[h] @ w_kc[h], maps the latent back with
+    o[h] = o_lat[h] @ w_vc[h] (both times w_scale) and rotates with cos, sin =
+    cos_sin_cache[pos].chunk(2, -1). The packed W_UK / W_UV rows, applied as the launches'
+    GEMVs apply theirs (``oracle.dense.w8a16_gemv``: y = W x over row-major [out, in]),
+    give exactly those products, and the bf16 table holds the two halves. A W packed
+    without the transpose (the plain reshape of w_kc / w_vc) gives other products: the
+    check tells a transpose slip from the right packing."""
+    from oracle import dense as D
+    from oracle import formats as F
+
+    attn = _sglang_attn(11)
+    copies = {}
+    w_uk, s_uk = binding.pack_uk(attn, 2, copies, layout)
+    w_uv, s_uv = binding.pack_uv(attn, 2, copies, layout)
+    g = torch.Generator().manual_seed(12)
+    q_nope = torch.randn(3, DSV32.heads, DSV32.nope_dim, generator=g).to(torch.bfloat16).double()
+    o_lat = torch.randn(3, DSV32.heads, DSV32.kv_lora, generator=g).to(torch.bfloat16).double()
+    kc = torch.from_numpy(F.e4m3_to_f32(attn.w_kc.view(torch.uint8).numpy())).double() * SCALE
+    vc = torch.from_numpy(F.e4m3_to_f32(attn.w_vc.view(torch.uint8).numpy())).double() * SCALE
+    for h in (0, 17, 31):
+        uk = _rowmajor(w_uk[h], layout).view(torch.uint8).numpy()
+        uv = _rowmajor(w_uv[h], layout).view(torch.uint8).numpy()
+        got_lat = D.w8a16_gemv(q_nope[:, h], uk, s_uk[h].numpy())
+        got_o = D.w8a16_gemv(o_lat[:, h], uv, s_uv[h].numpy())
+        np.testing.assert_allclose(got_lat, (q_nope[:, h] @ kc[h]).numpy(), rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(got_o, (o_lat[:, h] @ vc[h]).numpy(), rtol=1e-12, atol=1e-12)
+        # the negative control: the same bytes read without the transpose
+        wrong = attn.w_kc[h].view(torch.uint8).reshape(DSV32.kv_lora, DSV32.nope_dim).numpy()
+        bad = D.w8a16_gemv(q_nope[:, h], wrong, s_uk[h].numpy())
+        assert not np.allclose(bad, (q_nope[:, h] @ kc[h]).numpy(), rtol=1e-3, atol=1e-3)
+    cos, sin = binding.rope_table({2: NS(self_attn=attn)}, copies)
+    cache = attn.rotary_emb.cos_sin_cache
+    pos = torch.tensor([0, 5, 95])
+    want_cos, want_sin = cache[pos].chunk(2, -1)
+    assert torch.equal(cos[pos], want_cos.to(torch.bfloat16))
+    assert torch.equal(sin[pos], want_sin.to(torch.bfloat16))
+    assert {k[2] for k in copies} == {"w_uk", "s_uk", "w_uv", "s_uv", "cos", "sin"}
+
+
+def test_one_rope_table_serves_every_layer_and_the_indexers_must_agree():
+    """The covered layers share one bf16 table (logged once); a layer's indexer whose
+    rotary holds another cache (a different base) refuses the model."""
+    a, b = _sglang_attn(1), _sglang_attn(2)
+    b.rotary_emb = a.rotary_emb  # SGLang shares the rotary module between layers
+    a.indexer = NS(rotary_emb=NS(cos_sin_cache=a.rotary_emb.cos_sin_cache.clone()))
+    copies = {}
+    cos, sin = binding.rope_table({4: NS(self_attn=b), 3: NS(self_attn=a)}, copies)
+    assert list(copies) == [("RoPE table bf16", 3, "cos"), ("RoPE table bf16", 3, "sin")]
+    other = _sglang_attn(3, positions=96)
+    other.rotary_emb.cos_sin_cache[:, :32] *= 0.5
+    a.indexer = NS(rotary_emb=other.rotary_emb)
+    with pytest.raises(ValueError, match="indexer"):
+        binding.rope_table({3: NS(self_attn=a), 4: NS(self_attn=b)}, {})

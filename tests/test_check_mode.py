@@ -5,9 +5,11 @@ back, and the comparison logs each value and every bound missed."""
 
 import logging
 from collections import namedtuple
+from dataclasses import replace
 from types import SimpleNamespace as NS
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import moe as om
@@ -87,7 +89,9 @@ def test_f32_router_matches_the_oracle_plain_and_grouped():
     mlp = _Mlp(g)
     x = torch.randn(6, 64, generator=g)
     for n_group, topk_group in ((1, 1), (8, 4), (4, 1)):
-        ids, w = check._f32_topk(x, mlp, 8, n_group, topk_group, 2.5)
+        cfg = replace(DSV32, n_group=n_group, topk_group=topk_group)
+        ids, w = check.route_f32(x, mlp.gate.weight.detach(),
+                                 mlp.gate.e_score_correction_bias.detach(), cfg)
         scores = torch.sigmoid(x.float() @ mlp.gate.weight.detach().float().t())
         want, want_w = om.route_topk(scores, mlp.gate.e_score_correction_bias.detach(),
                                      n_group=n_group, topk_group=topk_group)
@@ -105,12 +109,16 @@ def test_reference_runs_the_layer_routes_in_f32_and_restores_the_caches():
     cfg = DSV32
     ref = check.reference(NS(i=5, module=layer), torch.arange(3), h, fb, 3, cfg, pool)
     assert torch.equal(ref["out"], h * 2.0 + 1.0)
-    ids, _ = check._f32_topk(h, layer.mlp, 8, 1, 1, 2.5)
+    ids, _ = check.route_f32(h, layer.mlp.gate.weight.detach(),
+                             layer.mlp.gate.e_score_correction_bias.detach(), cfg)
     assert torch.equal(ref["ids"], ids)
-    # SGLang's routing was replaced by the f32 one (the shared column kept)
+    # SGLang's routing was replaced by the f32 one (the shared column kept), and its own
+    # top-k module is back in place
     assert torch.equal(layer.mlp.routed[:, :8], ids) and torch.all(layer.mlp.routed[:, 8] == 256)
-    # the KV rows and index pages it wrote are back as they were
+    assert isinstance(layer.mlp.topk, _TopK)
+    # the KV rows and index pages it wrote are back as they were, and kept aside
     assert torch.all(pool.kv == 1) and torch.all(pool.pay == 0)
+    assert torch.all(ref["written"]["kv"] == 7) and torch.all(ref["written"]["index"][0] == 9)
 
 
 def test_compare_logs_values_and_violations(caplog):
@@ -142,3 +150,89 @@ def test_check_mode_reads_its_variable(monkeypatch):
     assert not check.enabled()
     monkeypatch.setenv("SGLANG_AMD_MONO_CHECK", "1")
     assert check.enabled()
+
+
+def test_f32_router_ties_go_to_the_lower_id_and_the_lower_group():
+    """Equal candidates: the lower expert id wins; equal group values: the lower group."""
+    cfg = replace(DSV32, n_group=8, topk_group=4)
+    x = torch.zeros(1, 4)
+    w = torch.zeros(256, 4)  # every score sigmoid(0) = 0.5
+    bias = torch.zeros(256)
+    ids, wt = check.route_f32(x, w, bias, replace(DSV32))
+    assert ids.tolist() == [list(range(8))]
+    assert torch.allclose(wt, torch.full((1, 8), 2.5 / 8))
+    # groups 5 and 6 lifted equally: they stay, then the lowest two of the rest (0, 1)
+    bias[5 * 32 + 3] = 0.25
+    bias[6 * 32 + 7] = 0.25
+    ids, _ = check.route_f32(x, w, bias, cfg)
+    want = om.route_topk(torch.full((1, 256), 0.5), bias, n_group=8, topk_group=4)[0]
+    assert ids.tolist() == want.tolist()
+    assert set(ids[0].tolist()) >= {5 * 32 + 3, 6 * 32 + 7}
+
+
+def _fp4_pool(seed):
+    g = torch.Generator().manual_seed(seed)
+    pay = torch.randint(0, 256, (3, 1, 4, 64, 16), generator=g, dtype=torch.uint8)
+    sc = torch.randint(118, 136, (3, 1, 4, 64), generator=g, dtype=torch.uint8)
+    kv = torch.randint(0, 126, (256, 1, 576), generator=g, dtype=torch.uint8)
+    return NS(get_key_buffer=lambda i: kv, get_index_k_fp4_payload_buffer=lambda i: pay,
+              get_index_k_fp4_scale_buffer=lambda i: sc), kv, pay, sc
+
+
+def test_step_entries_decode_the_fp4_plane_and_kv_rows_as_the_oracle_does():
+    from oracle import attn as A
+    from oracle import formats as F
+
+    pool, kv, pay, sc = _fp4_pool(7)
+    loc = torch.tensor([3, 0, 130, 77])  # slot 0: a pad row
+    e = check.StepEntries.of(pool, 2, loc, 4)
+    assert e.slots.tolist() == [3, 130, 77] and e.pages.tolist() == [0, 1, 2]
+    got = e.index_keys()
+    vals, ex = A.index_keys(pay[:, 0].numpy(), sc[:, 0].numpy(), np.arange(3), 192,
+                            cols=[3, 130, 77])
+    want = vals * np.exp2(ex.astype(np.float64))[..., None]
+    np.testing.assert_array_equal(got.numpy(), want.reshape(3, 128))
+    kvv = e.kv_values()
+    np.testing.assert_array_equal(kvv.numpy(), F.e4m3_to_f32(kv[[3, 130, 77], 0].numpy()))
+
+
+def test_step_entries_decode_dsa_pages_as_the_oracle_does():
+    from oracle import attn as A
+
+    g = torch.Generator().manual_seed(8)
+    pages = torch.randint(0, 126, (3, 8448), generator=g, dtype=torch.uint8)
+    scales = torch.exp2(torch.randint(-8, 4, (3, 64), generator=g).float())
+    pages[:, 8192:] = scales.view(torch.uint8).view(3, 256)
+    kv = torch.zeros(256, 1, 576, dtype=torch.uint8)
+    pool = NS(get_key_buffer=lambda i: kv, get_index_k_with_scale_buffer=lambda i: pages)
+    e = check.StepEntries.of(pool, 2, torch.tensor([65, 191, 7]), 3)
+    want = A.dsa_keys(pages.numpy(), np.arange(3), 192, cols=[65, 191, 7])
+    np.testing.assert_array_equal(e.index_keys().double().numpy(), want)
+
+
+def test_compare_scores_the_cache_rows_the_launch_wrote():
+    """SGLang wrote its rows (``reference``'s ``written``); the launch's rows now in the
+    pool give the cosines; rows far from SGLang's miss the floors."""
+    pool, kv, pay, sc = _fp4_pool(9)
+    e = check.StepEntries.of(pool, 2, torch.tensor([3, 130]), 2)
+    written = e.save()  # SGLang's rows
+    b = torch.randn(2, 32)
+    ref = {"out": b, "ids": None, "topk": None, "entries": e, "written": written}
+    bounds = {"layer.kv.cosine": 0.995, "layer.index.cosine": 0.999}
+    v = check.compare(NS(i=1), b, ref, 2, numerics=bounds)
+    assert v["layer.kv.cosine"] == pytest.approx(1.0) and v["layer.index.cosine"] == pytest.approx(1.0)
+    kv[3, 0, :] = torch.randint(0, 126, (576,), dtype=torch.uint8)  # the launch's rows
+    pay[0, 0, :, 3, :] ^= 0x77
+    v = check.compare(NS(i=1), b, ref, 2, numerics=bounds)
+    assert v["layer.kv.cosine"] < 0.995 and v["layer.index.cosine"] < 0.999
+
+
+def test_exact_topk_misses_counts_keys_of_the_own_scores_left_out():
+    scores = torch.tensor([[0.5, 2.0, 2.0, -1.0, 3.0, 0.0],
+                           [1.0, 1.0, 1.0, 1.0, 1.0, 1.0]])
+    # row 0, k 3: 4, then the tie 1 and 2; row 1 (4 keys seen): the lowest positions
+    assert check.exact_topk_misses(scores, torch.tensor([[4, 1, 2], [0, 1, 2]]), [6, 4], 3) == 0
+    assert check.exact_topk_misses(scores, torch.tensor([[4, 1, 0], [0, 1, 3]]), [6, 4], 3) == 1
+    assert check.exact_topk_misses(scores, torch.tensor([[5, 3, -1], [-1, -1, -1]]), [6, 4], 3) == 3
+    # fewer keys than k: every key is selected
+    assert check.exact_topk_misses(scores, torch.tensor([[0, 1, -1]]), [2], 3) == 0

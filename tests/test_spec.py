@@ -110,21 +110,21 @@ def test_each_row_attends_the_keys_up_to_its_position(case):
     st.write(torch.tensor(case["positions"]), torch.tensor(case["slots"]), 4,
              case["context_len"] - 1)
     assert st.positions.tolist() == case["want_positions"]
-    assert st.indptr.tolist() == case["want_indptr"]
+    assert st.indptr().tolist() == case["want_indptr"]
     assert st.slots.tolist() == [s if s != 0 else -1 for s in case["slots"]]
 
 
 def test_a_short_step_pads_the_width():
     st = StepRows.empty(4, "cpu")
     st.write(torch.tensor([5, 9]), torch.tensor([40, 41]), 2, 100)
-    assert st.indptr.tolist() == [0, 6, 16, 16, 16]
+    assert st.indptr().tolist() == [0, 6, 16, 16, 16]
     assert st.slots.tolist() == [40, 41, -1, -1]
     assert st.req_ids.tolist() == [0, 1, 0, 0]
     # a narrower step after a wider one leaves nothing of the wider one behind
     st.write(torch.tensor([3, 4, 5, 6]), torch.tensor([1, 2, 3, 4]), 4, 100)
     st.write(torch.tensor([7]), torch.tensor([9]), 1, 100)
     assert st.positions.tolist() == [7, 0, 0, 0] and st.slots.tolist() == [9, -1, -1, -1]
-    assert st.indptr.tolist() == [0, 8, 8, 8, 8]
+    assert st.indptr().tolist() == [0, 8, 8, 8, 8]
     with pytest.raises(ValueError):
         st.write(torch.tensor([1] * 5), torch.tensor([1] * 5), 5, 100)
 
@@ -190,11 +190,21 @@ def _model(dense, covered, width_rows=8):
     return built, lm, ops
 
 
-def _batch(rows):
+def _batch(rows, table_pages=64):
+    """A decode batch: request r at pool row 2 r, its KV slots r * 4096 + position (64
+    pages of 64), the attention backend's page table ``table_pages`` wide (the served
+    context of ``_model`` is 4096 keys: 64 pages)."""
     pool = NS(get_key_buffer=lambda i: torch.zeros(64, 1, 576, dtype=torch.uint8))
-    md = NS(real_page_table=torch.arange(rows * 2, dtype=torch.int32).reshape(rows, 2))
+    req_to_token = torch.zeros(2 * rows, 4096, dtype=torch.int32)
+    for r in range(rows):
+        req_to_token[2 * r] = r * 4096 + torch.arange(4096, dtype=torch.int32)
+    real = (torch.arange(rows, dtype=torch.int32)[:, None] * 64
+            + torch.arange(table_pages, dtype=torch.int32)[None])
+    md = NS(real_page_table=real)
     return NS(out_cache_loc=torch.arange(1, rows + 1) * 3, token_to_kv_pool=pool,
-              attn_backend=NS(forward_metadata=md), forward_mode=NS(is_idle=lambda: False))
+              attn_backend=NS(forward_metadata=md), forward_mode=NS(is_idle=lambda: False),
+              req_to_token_pool=NS(req_to_token=req_to_token),
+              req_pool_indices=torch.arange(rows) * 2)
 
 
 def test_the_backbone_hands_the_full_stream_to_the_first_launch(monkeypatch):
@@ -220,7 +230,8 @@ def test_the_backbone_hands_the_full_stream_to_the_first_launch(monkeypatch):
     assert torch.equal(h0.float(), full.expand(-1, 7168))
     assert caches0 == ("caches", 2)
     assert step0.positions.tolist() == [10, 20, 30] and step0.slots.tolist() == [3, 6, 9]
-    assert step0.page_table.shape == (3, 2)
+    assert step0.page_table.shape == (3, 64)
+    assert step0.page_table.data_ptr() == fb.attn_backend.forward_metadata.real_page_table.data_ptr()
     h1, _, _ = ops[3].seen[0]
     first = full.to(torch.bfloat16) * 5 + 1  # the launches' bf16 arithmetic
     assert torch.equal(h1, first.expand(-1, 7168))
@@ -275,7 +286,9 @@ def _fake_build(monkeypatch, mixed=()):
             self.w, self.rts, self.sm_scale, self.cfg = w, rts, sm_scale, cfg
 
     monkeypatch.setattr(binding, "layer_weights",
-                        lambda mod, i, copies: NS(moe=NS(w13=NS(device="cpu")), i=i))
+                        lambda mod, i, copies, rope=None: NS(moe=NS(w13=NS(device="cpu")), i=i,
+                                                             rope=rope))
+    monkeypatch.setattr(binding, "rope_table", lambda layers, copies: ("cos", "sin"))
     monkeypatch.setattr(layer, "layer_runtime", _Rt)
     monkeypatch.setattr(layer, "LayerRuntimes", _Rts)
     monkeypatch.setattr(layer, "FusedLayerOp", _Fused)
@@ -367,3 +380,40 @@ def test_check_mode_runs_sglang_first_and_compares(monkeypatch):
     # layer 1's launch is h*5+1: its comparison finds no difference; layer 2's is h*7+1
     assert [c[:2] for c in calls] == [("ref", 1), ("cmp", 1), ("ref", 2), ("cmp", 2)]
     assert calls[1][2] == 0.0 and calls[3][2] > 0.0
+
+
+def test_a_page_table_narrower_than_the_context_is_rebuilt_full_width(monkeypatch):
+    """The DSA backend sizes ``real_page_table`` by the batch's longest sequence. One
+    narrower than the served context (4096 keys: 64 pages) is not read in place: the step
+    fills its own full-width table from ``req_to_token`` (request r's page p is
+    r * 64 + p), and the launch's page-table checks see every page of the context."""
+    from sgl_amd_mono_amd.dsv32 import binding
+    from sgl_amd_mono_amd.dsv32.layer import FusedLayerOp
+
+    monkeypatch.setattr(binding, "caches", lambda pool, i: ("caches", i))
+    built, _, ops = _model([2], [5])
+    fb = _batch(3, table_pages=2)
+    plan = registry.Plan(key=registry.ShapeKey("decode", 3, 1))
+    built.forward(plan, torch.tensor([1, 2, 3]), torch.tensor([10, 20, 30]), fb)
+    _, _, step = ops[1].seen[0]
+    pt = step.page_table
+    assert pt.shape == (3, 64) and pt.dtype == torch.int32 and pt.stride(1) == 1
+    want = torch.arange(3, dtype=torch.int32)[:, None] * 64 + torch.arange(64, dtype=torch.int32)
+    assert torch.equal(pt, want)
+    assert pt.data_ptr() != fb.attn_backend.forward_metadata.real_page_table.data_ptr()
+    # the one launch's argument check: a table of 2 pages a request is refused, the
+    # rebuilt one passes the width check (it stops at the device, this is the CPU)
+    op = FusedLayerOp.__new__(FusedLayerOp)
+    op.cfg, op.device, op.max_rows, op.ctx_max = dsv32.DSV32, torch.device("cpu"), 8, 4096
+    op.w = None
+    h = torch.zeros(3, 7168, dtype=torch.bfloat16)
+    from sgl_amd_mono_amd.dsv32.layer import LayerStep
+    narrow = LayerStep(positions=step.positions[:3], slots=step.slots[:3],
+                       req_ids=step.req_ids[:3],
+                       page_table=fb.attn_backend.forward_metadata.real_page_table)
+    with pytest.raises(ValueError, match="cannot hold"):
+        op.launch(h, None, narrow)
+    wide = LayerStep(positions=step.positions[:3], slots=step.slots[:3],
+                     req_ids=step.req_ids[:3], page_table=pt)
+    with pytest.raises(AttributeError):  # past the page-table check: the caches (None)
+        op.launch(h, None, wide)
