@@ -248,7 +248,8 @@ def test_layer_bound_from_sglang_modules_matches_the_oracle(gpu):
     args.update(w_uk=None, s_uk=None, cos=cos_h.to(torch.bfloat16), sin=sin_h.to(torch.bfloat16))
     pos = step.positions.cpu().numpy()
     fr = Fr.front(h.cpu(), positions=pos, kv_scaled=caches.kv_scale is not None,
-                  absorb=lambda qn, hh: (torch.from_numpy(qn) @ kc[hh]).numpy(), **args)
+                  absorb=lambda qn, hh: (torch.from_numpy(np.asarray(qn, np.float64)) @ kc[hh]).numpy(),
+                  **args)
     _close(dbg.q.float().cpu(), fr["q"], "q under SGLang's w_kc")
     # the cache rows the front wrote (latent + rotated key), read back: within an E4M3
     # step of the oracle's bf16 row, plus 2^-7 of the row's rms for one-ulp upstream
@@ -277,7 +278,7 @@ def test_layer_bound_from_sglang_modules_matches_the_oracle(gpu):
         _close(dbg.o_lat[r].float().cpu(), o, f"o_lat row {r}")
     _, _, w_o, s_o = synthetic.rowmajor_post(po)
     pr = D.attn_out(dbg.o_lat.cpu(), h.cpu(), None, None, w_o, s_o,
-                    uv=lambda x, hh: (torch.from_numpy(x).double() @ vc[hh]).numpy())
+                    uv=lambda x, hh: (torch.from_numpy(np.asarray(x, np.float64)) @ vc[hh]).numpy())
     _close(dbg.a.float().cpu(), pr["a"], "a under SGLang's w_vc")
     ids = dbg.ids.cpu().numpy()
     sel8, _ = M.route_topk(dbg.moe_scores.cpu(), m.bias.cpu())
