@@ -545,7 +545,9 @@ def bench_layer(args):
         layers.append(synthetic.layer(rows, ctx, dev, seed=1000 + i, layout=args.layout,
                                       index_format=fmt))
         if (i + 1) % 8 == 0:
-            print(f"bench: {i + 1} layers", file=sys.stderr, flush=True)
+            torch.cuda.synchronize()
+            print(f"bench: {i + 1} layers ({torch.cuda.memory_allocated() / 2**30:.0f} GiB)",
+                  file=sys.stderr, flush=True)
     # the one-launch layers share one runtime, as a served model's layers do
     rt = layer_runtime(dev, max_rows=rows)
     fused = [FusedLayerOp(w, dev, max_rows=rows, ctx_max=ctx, rt=rt) for w, _, _, _ in layers]
@@ -569,6 +571,22 @@ def bench_layer(args):
           flush=True)
     inside = layer_timeline(fused[0], layers[0][3], layers[0][1], layers[0][2], rt.grid)
     print(f"bench: in-launch phase ends {inside}", file=sys.stderr, flush=True)
+    if L > 8:
+        # a model step: one graph replay runs all L distinct layers back to back, so the
+        # step's time is measured, not scaled from a rotation of a few layers
+        config = {
+            "workload": f"a decode step through {L} stacked random-init DSA decoder layers "
+                        f"(BASELINE configs[4]), one persistent launch a layer, {rows} rows at "
+                        f"context {ctx}, every layer's weights and caches distinct in HBM",
+            "rows": rows, "context": ctx, "layers": L, "launches_per_layer": 1,
+            "weight_layout": args.layout, "index_format": args.index_format,
+            "distinct_experts": distinct, "in_launch_phase_ends_us": inside,
+            "bytes_per_layer": int(total),
+            "layer_achieved_GBs": round(total / (us * 1e-6) / 1e9, 1),
+            "us_per_token_step_measured": round(us * L, 1),
+        }
+        return (us, steps, total, "fp8 / fp4 idx / bf16" if not dsa else "fp8 / e4m3 idx / bf16",
+                config, "layer" if not dsa else "layer_dsa", None, us)
     # each phase as its own launch (the four-launch chain), for the per-phase figures
     chain = [LayerOp(w, dev, max_rows=rows, ctx_max=ctx) for w, _, _, _ in layers]
     fr_out, att_in, olat, a_in = [], [], [], []
@@ -622,7 +640,6 @@ def bench_layer(args):
         "in_launch_phase_ends_us": inside,
         "four_launch_chain_us": round(chain_us, 2), "phases_as_own_launches": phases,
         "bytes_per_layer": int(total), "layer_achieved_GBs": round(total / (us * 1e-6) / 1e9, 1),
-        "model_layers": 61, "us_per_token_step_61_layers": round(us * 61, 1),
     }
     # the roofline line is the layer kernel's: the only kernel of the step
     if dsa:
@@ -664,6 +681,7 @@ def main():
         "data": "synthetic",
         "config": config,
         # rows a second through one launch, or (layer) through the 61 layers of the model
+        # (the per-layer time x 61; ``--layers 61`` measures such a step whole)
         "rows_per_s": round(args.rows / (us * 1e-6 * (61 if args.workload == "layer" else 1)), 1),
         "roofline": {
             "bound": "hbm",
