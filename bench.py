@@ -45,6 +45,8 @@ EXPERT_BYTES = 7_340_032 + 1_792 + 3_670_016 + 896  # w13 + s13 + w2 + s2 of one
 ROUTER_BYTES = 3_670_016
 # MXFP4 expert of config 4: w13 768 x 1536 B + 768 x 96 scales, w2 3072 x 192 B + 3072 x 12
 MX_EXPERT_BYTES = 1_179_648 + 73_728 + 589_824 + 36_864
+# MXFP4 expert at the layer's geometry: w13 1024 x 3584 B + 1024 x 224, w2 7168 x 256 + 7168 x 16
+MX_LAYER_EXPERT_BYTES = 3_670_016 + 229_376 + 1_835_008 + 114_688
 
 
 def parse():
@@ -70,6 +72,9 @@ def parse():
                    help="layer / attn: the index keys in the FP4 index plane (BASELINE "
                         "configs[2], the default) or in SGLang's DSA pages (E4M3 + per-token "
                         "scales, 16x16 tiles; bf16 index query)")
+    p.add_argument("--experts", default="fp8", choices=("fp8", "mxfp4"),
+                   help="layer: the MoE's experts, FP8 W8A8 (BASELINE configs[4]) or MXFP4 "
+                        "A16W4 (E2M1 + E8M0 per 32) in the same one launch")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a 1 GiB device-to-device copy 5 times (the reference "
                         "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -444,15 +449,16 @@ def index_bytes(dsa: bool):
     return (132, 64 * 128 * 2) if dsa else (68, 64 * 64 + 256)
 
 
-def phase_bytes(rows, ctx, distinct, dsa=False):
-    """Algorithmic bytes of each phase of one layer (each needed byte counted once)."""
+def phase_bytes(rows, ctx, distinct, dsa=False, mx=False):
+    """Algorithmic bytes of each phase of one layer (each needed byte counted once); ``mx``:
+    MXFP4 experts."""
     n, k = ctx, min(ctx, 2048)
     key, iq = index_bytes(dsa)
     front = (FRONT_W_BYTES + rows * (7168 * 2 + 580 + key + 32 * 576 * 2 + iq
                                      + 64 * 4 + 64 * 2 * 2))
     attn = rows * (k * 580 + n * key + 32 * 576 * 2 + iq + 64 * 4 + 32 * 512 * 2)
     post = POST_W_BYTES + rows * (32 * 512 * 2 + 7168 * 2 * 2)
-    moe = distinct * EXPERT_BYTES + ROUTER_BYTES + rows * 7168 * 2 * 2
+    moe = distinct * (MX_LAYER_EXPERT_BYTES if mx else EXPERT_BYTES) + ROUTER_BYTES + rows * 7168 * 2 * 2
     return {"front": front, "attn": attn, "post": post, "moe": moe}
 
 
@@ -540,10 +546,11 @@ def bench_layer(args):
           flush=True)
     layers = []
     dsa = args.index_format == "dsa"
+    mx = args.experts == "mxfp4"
     fmt = _lib.INDEX_FP8_PAGE if dsa else _lib.INDEX_FP4_PLANE
     for i in range(L):
         layers.append(synthetic.layer(rows, ctx, dev, seed=1000 + i, layout=args.layout,
-                                      index_format=fmt))
+                                      index_format=fmt, experts=args.experts))
         if (i + 1) % 8 == 0:
             torch.cuda.synchronize()
             print(f"bench: {i + 1} layers ({torch.cuda.memory_allocated() / 2**30:.0f} GiB)",
@@ -559,7 +566,7 @@ def bench_layer(args):
         op.launch(h, caches, step, out=outs[i], debug=LayerDebug(ids=ids))
         op.check()
         distinct.append(len(np.unique(ids.cpu().numpy())))
-    per = [phase_bytes(rows, ctx, d, dsa) for d in distinct]
+    per = [phase_bytes(rows, ctx, d, dsa, mx) for d in distinct]
     avg = {k: sum(p[k] for p in per) / L for k in per[0]}
     total = sum(avg.values())
     us, wall, steps = time_graph(
@@ -571,6 +578,23 @@ def bench_layer(args):
           flush=True)
     inside = layer_timeline(fused[0], layers[0][3], layers[0][1], layers[0][2], rt.grid)
     print(f"bench: in-launch phase ends {inside}", file=sys.stderr, flush=True)
+    dtype = ("mxfp4" if mx else "fp8") + (" / e4m3 idx / bf16" if dsa else " / fp4 idx / bf16")
+    prof = "layer" + ("_dsa" if dsa else "") + ("_mx" if mx else "")
+    if mx:
+        # MXFP4 experts run in the one launch only (no four-launch chain to time beside it)
+        config = {
+            "workload": "BASELINE configs[4]'s decoder layer with MXFP4 experts: one GPU's "
+                        "TP=4 share, 8 rows at position 32767 (context 32768), ONE persistent "
+                        "launch a layer: the FP8 front, FP4 indexer + exact top-2048 + sparse "
+                        "MLA, W_UV + o_proj + residual, then the MoE over MXFP4 (E2M1 + E8M0 "
+                        "per 32) A16W4 experts (norm, router, top-8 + shared, residual)",
+            "rows": rows, "context": ctx, "layers_rotated": L, "launches_per_layer": 1,
+            "weight_layout": args.layout, "index_format": args.index_format,
+            "experts": "mxfp4", "distinct_experts": distinct, "in_launch_phase_ends_us": inside,
+            "bytes_per_layer": int(total), "moe_bytes_per_layer": int(avg["moe"]),
+            "layer_achieved_GBs": round(total / (us * 1e-6) / 1e9, 1),
+        }
+        return us, steps, total, dtype, config, prof, None, us
     if L > 8:
         # a model step: one graph replay runs all L distinct layers back to back, so the
         # step's time is measured, not scaled from a rotation of a few layers
@@ -585,8 +609,7 @@ def bench_layer(args):
             "layer_achieved_GBs": round(total / (us * 1e-6) / 1e9, 1),
             "us_per_token_step_measured": round(us * L, 1),
         }
-        return (us, steps, total, "fp8 / fp4 idx / bf16" if not dsa else "fp8 / e4m3 idx / bf16",
-                config, "layer" if not dsa else "layer_dsa", None, us)
+        return us, steps, total, dtype, config, prof, None, us
     # each phase as its own launch (the four-launch chain), for the per-phase figures
     chain = [LayerOp(w, dev, max_rows=rows, ctx_max=ctx) for w, _, _, _ in layers]
     fr_out, att_in, olat, a_in = [], [], [], []
@@ -647,8 +670,7 @@ def bench_layer(args):
             "KV + FP4 index-key cache writes, FP4 index query), FP4 indexer",
             "KV + DSA index-page writes (E4M3, per-token scales), bf16 index query), DSA "
             "indexer")
-    return (us, steps, total, "fp8 / fp4 idx / bf16" if not dsa else "fp8 / e4m3 idx / bf16",
-            config, "layer" if not dsa else "layer_dsa", cpu, us)
+    return us, steps, total, dtype, config, prof, cpu, us
 
 
 def main():

@@ -105,6 +105,19 @@ int mono_reset(void* scratch, size_t scratch_bytes, int32_t* guard, mono_stream_
 #define MONO_INDEX_FP8_PAGE 1
 #define MONO_INDEX_FP8_ROWS 2
 
+/* Expert weights of the layer launch (the reference's MoE modes W8A8 and A16W4,
+ * sgl_amd_mono/glm53/gfx950/config.py:15-21,88-93):
+ * MONO_EXPERTS_FP8    E4M3 w13 [257, 1024, 7168] + f32 s13 [257, 8, 56] and w2 [257, 7168,
+ *                     512] + s2 [257, 56, 4] (128 x 128 blocks), W8A8 on per-128 E4M3 rows
+ * MONO_EXPERTS_MXFP4  E2M1 codes (two a byte, the even K index in the low nibble) w13
+ *                     [257, 1024, 3584] + E8M0 e13 [257, 1024, 224] and w2 [257, 7168, 256] +
+ *                     e2 [257, 7168, 16] (one scale per 32 values), A16W4: the bf16 rows,
+ *                     mid = bf16(silu(gate) up), the route weight on each expert's f32 down
+ *                     sum; at most 8 rows. Layout AITER16: codes in the (16, 16) byte shuffle,
+ *                     scales in the e8m0 shuffle (the MXFP4 MoE launch's layout note) */
+#define MONO_EXPERTS_FP8 0
+#define MONO_EXPERTS_MXFP4 1
+
 #define MONO_LAYOUT_ROWMAJOR 0 /* plain row-major E4M3 */
 #define MONO_LAYOUT_AITER16 1  /* AITER (16, 16) shuffle: [N / 16, K / 32, 2, 16, 16 B],
                                   SGLang's in-place layout on gfx950
@@ -160,7 +173,7 @@ int mono_moe_fp8_launch(const MonoMoeFp8Args* args, mono_stream_t stream);
 /* mono_moe_fp8_launch without any allocation, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. The scratch and the guard block live in
- * a static device array of this library (18.9 MiB a GPU, held until the process ends,
+ * a static device array of this library (20.9 MiB a GPU, held until the process ends,
  * its address looked up once per device on the first call there): args->scratch and
  * args->guard must be null; hidden 7168, inter 512, 256 experts and at most 16 rows,
  * else MONO_E_ARG. Every call on one GPU shares that GPU's block and its launch tags, so
@@ -389,7 +402,8 @@ int mono_front_launch(const MonoFrontArgs* args, mono_stream_t stream);
 
 /* ------------------------------------------------------------------------------
  * The whole decoder layer as ONE persistent launch: the front, the attention phase, the
- * output block and the FP8 MoE above, run back to back in every CTA of one launch with a
+ * output block and the MoE above (FP8 or MXFP4 experts: expert_format), run back to
+ * back in every CTA of one launch with a
  * deadline-guarded grid barrier between phases (each phase's input-independent loads,
  * weights and index pages, issued before it waits). out = the layer's output stream
  * (h + attention block + MoE), bf16 [R, 7168].
@@ -463,6 +477,10 @@ typedef struct {
   int32_t n_group;       /* group-limited routing: 0 or 1 none, else 2..16 groups */
   int32_t topk_group;    /* groups kept (topk_group * 256 / n_group >= 8) */
   int32_t index_format;  /* MONO_INDEX_* of plane / plane_scale (and so of iq / iqs) */
+  int32_t expert_format; /* MONO_EXPERTS_*: FP8 (w13, s13, w2, s2) or MXFP4 (w13, e13, w2,
+                            e2; s13 / s2 unused) experts */
+  const uint8_t* e13;    /* MXFP4: E8M0 scales of w13 */
+  const uint8_t* e2;     /* MXFP4: E8M0 scales of w2 */
 } MonoLayerArgs;
 
 size_t mono_layer_scratch_bytes(int32_t rows_max);

@@ -43,6 +43,10 @@ DSA_PAGE_BYTES = 64 * (128 + 4)
 LAYOUT_ROWMAJOR = 0
 LAYOUT_AITER16 = 1
 
+# expert weights of the layer launch (MONO_EXPERTS_*): FP8 W8A8 or MXFP4 A16W4
+EXPERTS_FP8 = 0
+EXPERTS_MXFP4 = 1
+
 # timeline marks of the MoE launch (MONO_TL_*), u64 [grid, TL_COLS]
 TL_MARKS = ("start", "staged", "routed", "upgate", "midq", "down", "end")
 TL_COLS = 8
@@ -266,7 +270,8 @@ class MonoLayerArgs(ctypes.Structure):
         "guard", "host_error")]
     _fields_ += [("fault_site", c_int32), ("fault_after", c_int32), ("timeline", c_void_p),
                  ("phase_timeline", c_void_p), ("n_group", c_int32), ("topk_group", c_int32),
-                 ("index_format", c_int32)]
+                 ("index_format", c_int32), ("expert_format", c_int32), ("e13", c_void_p),
+                 ("e2", c_void_p)]
 
 
 # name -> (restype, argtypes)

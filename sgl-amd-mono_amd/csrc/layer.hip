@@ -1,108 +1,6 @@
-// The whole decoder layer as one persistent gfx950 launch: the front, the attention phase,
-// the output block and the FP8 MoE run back to back in every CTA of one 256-CTA launch.
-//
-// Before the attention and before the MoE sits a grid barrier (phase.h): a phase's stores
-// are device coherent and drained before its CTA arrives, the last arrival raises the
-// barrier's flag to the launch tag, and the next phase waits for the flag only after
-// issuing the loads that do not depend on the phase before it:
-//   attention  the index pages of its first score task (the rows' own keys, written by the
-//              front in this launch, are read again device coherent after the wait);
-//   MoE        the norm weight and its router tile's weights.
-// The output block needs none: the attention's merge runs W_UV on the latents it merges
-// and stores o as complemented words, which o_proj's loads poll (zero: not written yet).
-// Every wait is deadline guarded; a failing wait lets every CTA run to the end of the
-// launch. The launch tag is the guard's epoch + 1, shared by the four phases (each keeps
-// its own scratch region), and the last CTA out zeroes the barrier counts and advances the
-// epoch.
-//
-// Replaces the reference's one-launch layer kernel, sgl_amd_mono/glm53/gfx950/kernel.py:
-// 171-5282 (launch arguments :5191-5234), driven per layer by Glm53LayerOp.launch
-// (sgl_amd_mono/glm53/gfx950/runner.py:240-321).
-#include "attn_phase.h"
-#include "front_phase.h"
-#include "moe_fp8_phase.h"
-#include "post_phase.h"
-
-namespace mono {
-
-constexpr int LY_H = 7168, LY_I = 512;
-constexpr int LY_MAXR = FR_MAXR;  // the front builds x of at most 8 rows in LDS
-
-constexpr int cmax(int a, int b) { return a > b ? a : b; }
-constexpr int LY_LDS_BYTES =
-    cmax(cmax(FR_LDS_BYTES, AT_LDS_BYTES), cmax(PO_LDS_BYTES, MoeLds<LY_H, LY_I>::BYTES));
-
-// scratch of the layer launch for `rm` rows: the barriers, each phase's scratch, and the
-// hand-offs between phases that the caller does not ask to see
-struct LayerScratch {
-  static constexpr size_t BARRIERS = 0;  // count k at 256 k, flag k at 256 k + 128
-  size_t front, attn, post, moe, q, iq, iqs, iw, o_lat, a, bytes;
-  __host__ __device__ explicit LayerScratch(int rm) {
-    front = 1024;
-    attn = at_align(front + FrontScratch::BYTES);
-    post = at_align(attn + AttnScratch(rm).bytes);
-    moe = at_align(post + PostScratch::BYTES);
-    q = at_align(moe + MoeFp8Geom<LY_H, LY_I>::BYTES);
-    iq = at_align(q + (size_t)rm * AT_HEADS * AT_KV * 2);
-    iqs = at_align(iq + (size_t)rm * AT_IHEADS * 256);  // FP4 codes, or a DSA page's bf16 query
-    iw = at_align(iqs + (size_t)rm * 256);
-    o_lat = at_align(iw + (size_t)rm * AT_IHEADS * 4);
-    a = at_align(o_lat + (size_t)rm * AT_HEADS * AT_LAT * 2);
-    bytes = at_align(a + (size_t)rm * LY_H * 2);
-  }
-};
-
-struct LayerParams {
-  FrontParams f;
-  AttnParams at;
-  PostParams po;
-  MoeFp8Params m;
-  PhaseBarrier bar[2];  // front -> attention, output block -> MoE
-  uint8_t* scratch;
-  int32_t* guard;
-  uint32_t* host_err;
-  int fault_site, fault_after;
-  uint64_t* timeline;
-};
-
-// layer timeline marks: start, each phase's end, exit
-constexpr int LY_TL_FRONT = 1, LY_TL_ATTN = 2, LY_TL_POST = 3, LY_TL_MOE = 4, LY_TL_END = 5;
-
-template <bool SHUF, int SPLIT, bool LONG, bool DSA>
-__global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
-  using Arena = LdsArena<LY_LDS_BYTES>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[Arena::TOTAL];
-  LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
-  stamp(p.timeline, MONO_TL_START);
-  Guard guard;
-  uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
-  front_phase(p.f, lds, guard, tag, sh.ok);
-  p.bar[0].arrive(tag);
-  stamp(p.timeline, LY_TL_FRONT);
-  attn_phase<SPLIT, true, LONG, DSA>(p.at, lds, guard, tag, sh.ok,
-                          BarrierWait{&p.bar[0], &guard, tag, MONO_SITE_PHASE, &sh.ok});
-  stamp(p.timeline, LY_TL_ATTN);
-  // no barrier: the merge ran W_UV, and o's complemented words are their own hand-off
-  post_phase<true>(p.po, lds, guard, tag, sh.ok, NoWait{});
-  p.bar[1].arrive(tag);
-  stamp(p.timeline, LY_TL_POST);
-  moe_phase<LY_H, LY_I, SHUF, true>(p.m, lds, guard, tag, sh.ok,
-                                    BarrierWait{&p.bar[1], &guard, tag, MONO_SITE_PHASE, &sh.ok});
-  stamp(p.timeline, LY_TL_MOE);
-  launch_end(sh, p.guard, tag, p.scratch,
-             (uint32_t)LayerScratch(p.at.rows_max).bytes,
-             Poison{p.m.out, (uint32_t)p.m.rows * LY_H * 2u, NAN_BF16X2},
-             Poison{p.m.y, (uint32_t)p.m.rows * LY_H * 4u, NAN_F32},
-             [&]() {
-               moe_reset_queues<LY_H, LY_I>(p.m);
-#pragma unroll
-               for (int k = 0; k < 2; ++k) p.bar[k].reset();
-             });
-  stamp(p.timeline, LY_TL_END);
-}
-
-}  // namespace mono
-
+// The C ABI of the one-launch decoder layer (the kernel: layer_kernel.h): argument
+// checks, the phases' parameters, instance choice and the launch.
+#include "layer_kernel.h"
 using namespace mono;
 
 extern "C" size_t mono_layer_scratch_bytes(int32_t rows_max) {
@@ -133,12 +31,16 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   if (a->index_format < MONO_INDEX_FP4_PLANE || a->index_format > MONO_INDEX_FP8_ROWS)
     return set_error(MONO_E_ARG, "mono_layer_launch: unknown index_format");
   const bool fp4 = a->index_format == MONO_INDEX_FP4_PLANE;
+  if (a->expert_format != MONO_EXPERTS_FP8 && a->expert_format != MONO_EXPERTS_MXFP4)
+    return set_error(MONO_E_ARG, "mono_layer_launch: unknown expert_format");
+  const bool mx = a->expert_format == MONO_EXPERTS_MXFP4;
   if (!a->h || !a->out || !a->positions || !a->slots || !a->req_ids || !a->page_table ||
       !a->kv || !a->plane || (fp4 && !a->plane_scale) || !a->g_in || !a->g_q || !a->g_kv ||
       !a->w_qkv_a || !a->s_qkv_a || !a->w_k || !a->s_k || !a->w_w || !a->g_k || !a->b_k ||
       !a->w_qb || !a->s_qb || !a->w_iq || !a->s_iq || !a->w_uk || !a->s_uk || !a->cos ||
       !a->sin || !a->w_uv || !a->s_uv || !a->w_o || !a->s_o || !a->g_post || !a->w_r ||
-      !a->bias || !a->w13 || !a->s13 || !a->w2 || !a->s2 || !a->scratch || !a->guard)
+      !a->bias || !a->w13 || !a->w2 || (!mx && (!a->s13 || !a->s2)) ||
+      (mx && (!a->e13 || !a->e2)) || !a->scratch || !a->guard)
     return set_error(MONO_E_ARG, "mono_layer_launch: null tensor");
   uint32_t* host_err = nullptr;
   if (a->host_error) {
@@ -276,6 +178,8 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   m.s13 = a->s13;
   m.w2 = a->w2;
   m.s2 = a->s2;
+  m.e13 = mx ? a->e13 : nullptr;
+  m.e2 = mx ? a->e2 : nullptr;
   m.y = a->y;
   m.scores = a->moe_scores;
   m.ids = a->ids;
@@ -319,13 +223,14 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   // rows that may span more than one top-k block take the multi-block variant
   const bool lng = a->ctx_max > AT_TKBLOCK;
   // DSA (FP8) index pages take their own instances (their score code holds more registers)
-  using K = void (*)(LayerParams);
+  // MXFP4 experts: instances of their own (layer_mx.hip)
+  using K = LayerKernel;
   const K kerns[2][2][2] = {
-      {{layer_kernel<false, 64, false, false>, layer_kernel<false, 64, false, true>},
-       {layer_kernel<false, 64, true, false>, layer_kernel<false, 64, true, true>}},
-      {{layer_kernel<true, 64, false, false>, layer_kernel<true, 64, false, true>},
-       {layer_kernel<true, 64, true, false>, layer_kernel<true, 64, true, true>}}};
-  const K kern = kerns[shuf][lng][!fp4];
+      {{layer_kernel<false, 64, false, false, false>, layer_kernel<false, 64, false, true, false>},
+       {layer_kernel<false, 64, true, false, false>, layer_kernel<false, 64, true, true, false>}},
+      {{layer_kernel<true, 64, false, false, false>, layer_kernel<true, 64, false, true, false>},
+       {layer_kernel<true, 64, true, false, false>, layer_kernel<true, 64, true, true, false>}}};
+  const K kern = mx ? layer_kernel_mx(shuf, lng, !fp4) : kerns[shuf][lng][!fp4];
   rc = check_coresident(kern, 1024, 0, "mono_layer_launch: one 1024-thread CTA per CU does not fit");
   if (rc) return rc;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);

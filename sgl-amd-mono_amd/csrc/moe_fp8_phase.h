@@ -39,13 +39,18 @@
 
 #include "moe_common.h"
 #include "mono_abi.h"
+#include "mx_common.h"
 #include "phase.h"
 
 namespace mono {
 
-template <int H, int I>
+// MX: MXFP4 experts (A16W4: E2M1 + E8M0 per 32 weights on bf16 rows, the layer launch
+// only, at most MXR rows), else FP8 W8A8 experts
+template <int H, int I, bool MX = false>
 struct MoeFp8Geom {
   static constexpr int WAVES = 16;
+  static constexpr int MXR = 8;            // rows of an MXFP4-expert launch, at most
+  static constexpr int MQB = MX ? 2 : 1;   // bytes of a mid value as the down stage reads it
   static constexpr int THREADS = WAVES * WAVE;
   static constexpr int QW = 8;             // waves that own a K slice (stage 0, B operands)
   static constexpr int NKC = H / 128;      // 128-K chunks of the hidden dim
@@ -62,7 +67,9 @@ struct MoeFp8Geom {
   static constexpr size_t OFF_MID = 0;
   static constexpr size_t SZ_MID = (size_t)MOE_NDIST * MOE_MAXR * I * 8;
   static constexpr size_t OFF_MQ = OFF_MID + SZ_MID;
-  static constexpr size_t SZ_MQ = (size_t)MOE_NDIST * MOE_MAXR * I;
+  // room for bf16 mids whichever the format: both formats keep one scratch layout, so
+  // launches of either kind can share a runtime (counters and hand-off words line up)
+  static constexpr size_t SZ_MQ = (size_t)MOE_NDIST * MOE_MAXR * I * 2;
   static constexpr size_t OFF_MCOEF = OFF_MQ + SZ_MQ;
   static constexpr size_t SZ_MCOEF = (size_t)MOE_NDIST * MOE_MAXR * NKB * 4;
   static constexpr size_t OFF_READY = OFF_MCOEF + SZ_MCOEF;
@@ -82,6 +89,9 @@ struct MoeFp8Geom {
   static constexpr int NREP = 8;
   static constexpr size_t REP_STRIDE = 4096;
   static constexpr size_t SZ_XQ = (size_t)NKC * 2 * 64 * 16;
+  // MX: the image is bf16 rows as MFMA B operands, [chunk][d][K group][row < MXR] x 16 B
+  // (8 bf16 of the row at K 128 chunk + 32 group + 8 d), the same size
+  static_assert(!MX || (size_t)NKC * 4 * 4 * MXR * 16 == SZ_XQ, "the bf16 image's size");
   static constexpr size_t SZ_XS = (size_t)NKC * 16 * 4;
   static constexpr size_t SZ_RP = (size_t)NKS * MOE_MAXR * MOE_NEXP * 4;
   static constexpr size_t SZ_RT = NREP * REP_STRIDE;
@@ -105,6 +115,8 @@ struct MoeFp8Params {
   const float* s13;
   const uint8_t* w2;
   const float* s2;
+  const uint8_t* e13;  // MX: E8M0 scales of w13 / w2 (w13, w2 then E2M1 codes)
+  const uint8_t* e2;
   float* y;
   float* scores;
   int32_t* ids;
@@ -135,9 +147,9 @@ __device__ inline v8i cat8(v4i a, v4i b) {
 // (what SGLang's gfx950 MoE load leaves in place): a 16-row x 128-K MFMA tile is then one
 // contiguous 2 KB, and each load instruction reads 8 whole cache lines
 // LDS of the MoE phase (offsets in bytes)
-template <int H, int I>
+template <int H, int I, bool MX = false>
 struct MoeLds {
-  using G = MoeFp8Geom<H, I>;
+  using G = MoeFp8Geom<H, I, MX>;
   static constexpr int RL = 0;  // RouteLds
   static constexpr int XQ = (int)((sizeof(RouteLds) + 15) & ~(size_t)15);  // v4i [QW KCW 2 64]
   static constexpr int XS = XQ + G::QW * G::KCW * 2 * 64 * 16;   // f32 [QW KCW][16]
@@ -157,13 +169,15 @@ struct MoeLds {
 // (`guard` and `tag` given): it issues the norm weight and its router tile's weights,
 // waits at `ready` (the output block's barrier), then reads the stream `a` the output
 // block stored, device coherent.
-template <int H, int I, bool SHUF, bool FUSED, class Ready>
+template <int H, int I, bool SHUF, bool FUSED, bool MX = false, class Ready>
 __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Params& p,
                                                                 uint8_t* lds, Guard& guard,
                                                                 uint32_t& tag, int& ok_s,
                                                                 Ready ready) {
-  using G = MoeFp8Geom<H, I>;
-  using LO = MoeLds<H, I>;
+  using G = MoeFp8Geom<H, I, MX>;
+  using LO = MoeLds<H, I, MX>;
+  using W13 = MxOperand<SHUF, H>;  // MX: w13 [2 I, H] and w2 [H, I] as E2M1 + E8M0
+  using W2 = MxOperand<SHUF, I>;
   constexpr int KCW = G::KCW, NUG = G::NUG, NKB = G::NKB, QW = G::QW;
   // the stream a is read through L2 in both forms: fused, its lines are only stored
   // (write-through) before the barrier in this launch, so no cache holds a stale copy
@@ -351,6 +365,21 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
         for (int ww = 0; ww < G::WAVES; ++ww) sum += red[ww][L][v];
         if (r < R) st_dev(&hrp[(ks * MOE_MAXR + r) * MOE_NEXP + et * 16 + i], enc_word(__float_as_uint(sum)));
       }
+    } else if constexpr (MX) {
+      // the bf16 image: thread tid the 8 values of row r at K 128 kc + 8 m (rows past R
+      // read zeros), the MFMA B operand of K group m / 4, d = m % 4
+      const int pt = task - G::NROUTER;
+      const int kc = pt * 8 + (tid >> 7), r = (tid >> 4) & 7, m = tid & 15;
+      float fg[8], fa[8];
+      bf16x8(g_lds[kc * 16 + m], fg);
+      bf16x8(pa[0], fa);
+      const float rs = rstd_s[r];
+      v4i o;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        o[d] = (int)enc_word(bf16x2_bits(fa[2 * d] * rs * fg[2 * d], fa[2 * d + 1] * rs * fg[2 * d + 1]));
+      st16<CP_DEV>(rsrc(hxq, (uint32_t)G::SZ_XQ),
+                   (uint32_t)((((kc * 4 + (m & 3)) * 4 + (m >> 2)) * G::MXR + r) * 16), o);
     } else {
       const int pt = task - G::NROUTER;
       const int kc = pt * 8 + (tid >> 7), r = (tid >> 4) & 7, m = tid & 15;
@@ -419,8 +448,21 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   // the copy's would hold up the router's own LDS traffic
   bool routes_row = false;
   for (int row = 0; row < R; ++row) routes_row |= (G::NTASK0 + row) % nblk == b;
-  if (w >= 1) {
-    constexpr int NCW = (int)(G::SZ_XQ / 1024) / (G::WAVES - 1) + 1;  // chunks a wave, at most
+  constexpr int NCW = (int)(G::SZ_XQ / 1024) / (G::WAVES - 1) + 1;  // chunks a wave, at most
+  if (MX && w >= 1) {
+    // no scale words: lanes 2 j and 2 j + 1 poll the first and the last word of the wave's
+    // chunk j (written by the publisher's two waves of that chunk)
+    static_assert(2 * NCW <= WAVE, "a lane a polled word");
+    const __amdgpu_buffer_rsrc_t rxw = rsrc(hxq, (uint32_t)G::SZ_XQ);
+    ok = wait_until(guard, MONO_SITE_LOGITS, [&]() {
+      const int c = (w - 1) + (G::WAVES - 1) * (l >> 1);
+      const bool on = l < 2 * NCW && c < 2 * G::NKC;
+      const uint32_t v = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+          rxw, on ? (uint32_t)(c * 1024 + (l & 1) * 1020) : 0x80000000u, 0, CP_DEV);
+      return !__any(on && v == 0u);
+    });
+    if (!routes_row) copy_image(1, G::WAVES - 1, false);
+  } else if (w >= 1) {
     const __amdgpu_buffer_rsrc_t rxs = rsrc(hxs, (uint32_t)G::SZ_XS);
     static_assert(NCW * 16 <= 2 * WAVE, "a wave's scale words fit two loads a lane");
     // lane l: the scale word of chunk (w - 1) + 15 (l / 16 + 4 h), row l % 16
@@ -457,7 +499,19 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   // copies, every wave's into the first 1 KB of the reduction buffer, idle until stage
   // 2's first epilogue and below 128 KB like every copy target here; stage 2's image
   // check waits for them, long done by then), so that task's ring loads hit L2
-  if (b < NUG && !routes_row) {
+  if (MX && b < NUG && !routes_row) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(p.w13 + (size_t)MOE_SHARED * W13::code_bytes(2 * I),
+                                          ok ? W13::code_bytes(2 * I) : 0u);
+    auto* dst = (__attribute__((address_space(3))) void*)(&red[0][0]);
+    static_assert(LO::RED + 1024 <= LDS_DMA_END, "the pull's copies below 128 KB");
+    const int rg = half * (I / 16) + b;
+    const uint32_t cv = W13::code_v(l);
+#pragma unroll
+    for (int j = 0; j < KCW; ++j) {
+      const uint32_t cs = W13::code_s(rg, wq * KCW + j);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, cv, cs, 0, CP_NONE);
+    }
+  } else if (b < NUG && !routes_row) {
     const uint32_t vo = SHUF ? (uint32_t)(grp * 512 + t * 16) : (uint32_t)(t * H + 32 * grp);
     constexpr uint32_t HO = SHUF ? 256 : 16, CS = SHUF ? 2048 : 128;
     const int row0 = half * I + b * 16;
@@ -586,7 +640,9 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   // a slot is refilled with the next task's chunk as soon as its MFMA issued.
   {
     int ntask = ok ? nd * NUG : 0;
-    v4i ring[KCW][2];
+    // FP8: a chunk is 32 bytes a lane; MX: a 128-K step is 16 code bytes and a scale byte
+    v4i ring[KCW][MX ? 1 : 2];
+    uint32_t rsc[MX ? KCW : 1];
     // this lane's row and K group; the second 16 bytes of a lane's 32 sit 16 bytes on
     // (row major) or a 16-row half-tile on (shuffled); a 128-K chunk is CS bytes on
     const uint32_t vo = SHUF ? (uint32_t)(grp * 512 + t * 16) : (uint32_t)(t * H + 32 * grp);
@@ -603,6 +659,21 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
                 : (uint32_t)(row0 * H + wq * KCW * 128);
       return rsrc(p.w13 + (size_t)e * (2 * I) * H, live ? 2u * I * H : 0u);
     };
+    // MX: the codes and scales of the task's 16-row group rg of expert uexp[u]
+    // MX: task `task`'s 128-K step j of its 16-row group of expert uexp[u]: codes, scale
+    auto mx_issue = [&](int task, int j) {
+      const bool live = task < ntask;
+      const int tk = live ? task : 0;
+      const int u = tk / NUG, cc = tk % NUG;
+      const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
+      const int rg = half * (I / 16) + cc, st = wq * KCW + j;
+      ring[j][0] = ld16s<CP_NT>(
+          rsrc(p.w13 + (size_t)e * W13::code_bytes(2 * I), live ? W13::code_bytes(2 * I) : 0u),
+          W13::code_v(l), W13::code_s(rg, st));
+      rsc[j] = ld1(
+          rsrc(p.e13 + (size_t)e * W13::scale_bytes(2 * I), live ? W13::scale_bytes(2 * I) : 0u),
+          W13::scale_v(l), W13::scale_s(rg, st));
+    };
     // Task hand-out: CTA b runs tasks b and b + nblk first; later tasks come from a
     // device-wide counter in order (2 nblk, 2 nblk + 1, ...), each grabbed one task ahead
     // so the ring can be refilled with the next task while this one runs. The first grab
@@ -612,7 +683,10 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     // retire in order). Tasks run the same arithmetic on whichever CTA takes them, so
     // results do not depend on the hand-out.
     int task = b;
-    {
+    if constexpr (MX) {
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) mx_issue(task, j);
+    } else {
       uint32_t so;
       const __amdgpu_buffer_rsrc_t r = task_src(task, so);
 #pragma unroll
@@ -704,24 +778,39 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
       const bool grab_on = next < ntask;
       const uint32_t grabbed = (uint32_t)__builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
           1, rsrc(queue, grab_on ? 4u : 0u), tid == 0 ? 0u : 0x80000000u, 0, 0);
-      uint32_t son;
-      const __amdgpu_buffer_rsrc_t rn = task_src(next, son);
-      // B operands and scales: the same LDS words every task, read through an opaque
-      // base so they are not hoisted out of the loop (they would hold 56 VGPRs)
-      const int xb = opaque_v(wq * KCW * 2 * 64 + l);
-      const int sb = opaque_v(wq * KCW * 16 + t);
       v4f acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (MX) {
+        // B operands of row t (rows t >= 8 reread row t - 8: their output columns are
+        // never stored), through an opaque base as below
+        const int xo = opaque_v(wq * KCW * 128 + grp * G::MXR + (t & (G::MXR - 1)));
 #pragma unroll
-      for (int j = 0; j < KCW; ++j) {
-        const v8i B = cat8(xq_lds[xb + j * 128], xq_lds[xb + j * 128 + 64]);
-        const v4f zero = {0.f, 0.f, 0.f, 0.f};
-        const v4f d = mfma_fp8(cat8(ring[j][0], ring[j][1]), B, zero);
-        // the slot is free once its MFMA issued: refill it with the next task's chunk
-        ring[j][0] = ld16s<CP_NT>(rn, vo, son + j * CS);
-        ring[j][1] = ld16s<CP_NT>(rn, vo + HO, son + j * CS);
-        acc += d * (sld(p.s13, sbase + j) * ((&xs_lds[0][0])[sb + j * 16] * tok_on));
-        // one chunk per scheduling region keeps the live set to the ring
-        __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < KCW; ++j) {
+          v4i B[4];
+#pragma unroll
+          for (int d = 0; d < 4; ++d) B[d] = xq_lds[xo + j * 128 + d * 32];
+          acc = fp4_step(ring[j][0], rsc[j], B, acc);
+          mx_issue(next, j);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        uint32_t son;
+        const __amdgpu_buffer_rsrc_t rn = task_src(next, son);
+        // B operands and scales: the same LDS words every task, read through an opaque
+        // base so they are not hoisted out of the loop (they would hold 56 VGPRs)
+        const int xb = opaque_v(wq * KCW * 2 * 64 + l);
+        const int sb = opaque_v(wq * KCW * 16 + t);
+#pragma unroll
+        for (int j = 0; j < KCW; ++j) {
+          const v8i B = cat8(xq_lds[xb + j * 128], xq_lds[xb + j * 128 + 64]);
+          const v4f zero = {0.f, 0.f, 0.f, 0.f};
+          const v4f d = mfma_fp8(cat8(ring[j][0], ring[j][1]), B, zero);
+          // the slot is free once its MFMA issued: refill it with the next task's chunk
+          ring[j][0] = ld16s<CP_NT>(rn, vo, son + j * CS);
+          ring[j][1] = ld16s<CP_NT>(rn, vo + HO, son + j * CS);
+          acc += d * (sld(p.s13, sbase + j) * ((&xs_lds[0][0])[sb + j * 16] * tok_on));
+          // one chunk per scheduling region keeps the live set to the ring
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
       red[w][l] = acc;
       if (tid == 0) next_s = grab_on ? 2 * nblk + (int)grabbed : ntask;
@@ -776,7 +865,15 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
           p1 = ld_dev64(&mid_pairs[base + 1]);
           return __all((uint32_t)(p0 >> 32) == tag && (uint32_t)(p1 >> 32) == tag);
         });
-        if (ok) {
+        if (MX && ok) {
+          // A16W4: the mid rounds to bf16; its down coefficient is the route weight
+          const float v0 = __uint_as_float((uint32_t)p0), v1 = __uint_as_float((uint32_t)p1);
+          st_dev(reinterpret_cast<uint32_t*>(
+                     mq + (((size_t)u * MOE_MAXR + tok) * I + kb * 128 + 2 * l) * 2),
+                 bf16x2_bits(v0, v1));
+          if (l == 0)
+            st_devf(&mcoef[((size_t)u * MOE_MAXR + tok) * NKB + kb], route_weight(rl, tok, e));
+        } else if (ok) {
           const float v0 = __uint_as_float((uint32_t)p0), v1 = __uint_as_float((uint32_t)p1);
           const float am = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
           const bool nz = am > 0.f;
@@ -818,13 +915,17 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     const int ntask = ok ? G::NDN : 0;
     constexpr int DW = G::WAVES;  // a wave's expert stride
     static_assert(G::NDN >= 256, "a first task for every CTA of a full grid");
-    uint8_t* mql = reinterpret_cast<uint8_t*>(xq_lds);  // [9 R slots][I] E4M3
-    float* mcl = reinterpret_cast<float*>(mql + MOE_MAXR * MOE_SLOTS * I);  // [slots][NKB]
-    static_assert(MOE_MAXR * MOE_SLOTS * (I + NKB * 4) <= LO::XS - LO::XQ, "mid slots");
-    static_assert(LO::XQ + MOE_MAXR * MOE_SLOTS * I <= LDS_DMA_END, "mid copies below 128 KB");
+    // [9 R slots][I] E4M3 (MX: bf16, at most MXR rows), then f32 [slots][NKB]
+    constexpr int SLOTR = MX ? G::MXR : MOE_MAXR, ROWB = I * G::MQB;
+    uint8_t* mql = reinterpret_cast<uint8_t*>(xq_lds);
+    float* mcl = reinterpret_cast<float*>(mql + SLOTR * MOE_SLOTS * ROWB);
+    static_assert(SLOTR * MOE_SLOTS * (ROWB + NKB * 4) <= LO::XS - LO::XQ, "mid slots");
+    static_assert(LO::XQ + SLOTR * MOE_SLOTS * ROWB <= LDS_DMA_END, "mid copies below 128 KB");
     // one tile of weight chunks a wave; each chunk is refilled with the next step's as
     // soon as its MFMA issued, the last expert of a task running into the next task
-    v4i buf[NKB][2];
+    // (MX: a 128-K step is 16 code bytes and a scale byte a lane)
+    v4i buf[NKB][MX ? 1 : 2];
+    uint32_t bsc[MX ? NKB : 1];
     const uint32_t vo = SHUF ? (uint32_t)(grp * 512 + t * 16) : (uint32_t)t * I + 32 * grp;
     constexpr uint32_t HO = SHUF ? 256 : 16, CS = SHUF ? 2048 : 128;
     auto src_of = [&](int f, int u, uint32_t& so) {
@@ -834,7 +935,21 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
       so = SHUF ? (uint32_t)((row0 / 16) * (I / 32) * 512) : (uint32_t)row0 * I;
       return rsrc(p.w2 + (size_t)e * H * I, live ? (uint32_t)H * I : 0u);
     };
-    {
+    // MX: step kb of expert uexp[u]'s 16-row group f: codes, scale
+    auto mx_issue = [&](int f, int u, int kb) {
+      const bool live = f < ntask && u < nd;
+      const int e = __builtin_amdgcn_readfirstlane(rl.uexp[live ? u : 0]);
+      const int fr = live ? f : 0;
+      buf[kb][0] = ld16s<CP_NT>(
+          rsrc(p.w2 + (size_t)e * W2::code_bytes(H), live ? W2::code_bytes(H) : 0u),
+          W2::code_v(l), W2::code_s(fr, kb));
+      bsc[kb] = ld1(rsrc(p.e2 + (size_t)e * W2::scale_bytes(H), live ? W2::scale_bytes(H) : 0u),
+                    W2::scale_v(l), W2::scale_s(fr, kb));
+    };
+    if constexpr (MX) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) mx_issue(b, w, kb);
+    } else {
       uint32_t so;
       const __amdgpu_buffer_rsrc_t r = src_of(b, w, so);
 #pragma unroll
@@ -848,11 +963,17 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     // registers), the coefficients one a thread; then every wave drains (the copies
     // land behind its weight tile in flight, which its next MFMA waits for anyway)
     const int nsl = R * MOE_SLOTS;
-    static_assert(I == 512, "a wave's 1 KiB copy is two mid rows");
+    static_assert(I == 512, "a wave's 1 KiB copy is two mid rows (MX: one)");
     auto copy_slots = [&](int s0, int s1) {
       const __amdgpu_buffer_rsrc_t rmq = rsrc(mq, (uint32_t)G::SZ_MQ);
       const __amdgpu_buffer_rsrc_t rmc = rsrc(mcoef, (uint32_t)G::SZ_MCOEF);
-      for (int c = w; 2 * c < s1 - s0; c += G::WAVES) {
+      for (int c = w; MX && c < s1 - s0; c += G::WAVES) {
+        const int ut = rl.slot_ut[s0 + c];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rmq, (__attribute__((address_space(3))) void*)(mql + (s0 + c) * ROWB), 16,
+            (uint32_t)((((ut >> 8) * MOE_MAXR + (ut & 255)) * I) * 2 + l * 16), 0, 0, CP_DEV);
+      }
+      for (int c = w; !MX && 2 * c < s1 - s0; c += G::WAVES) {
         const int sl = s0 + 2 * c + (l >> 5);
         if (sl < s1) {  // an odd count: the last copy's upper half-wave writes nothing
           const int ut = rl.slot_ut[sl];
@@ -920,6 +1041,27 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
         const int e = __builtin_amdgcn_readfirstlane(rl.uexp[u]);
         const int sl = slot_of(rl, u, rl.umask[u], t);
         const bool on = sl >= 0;
+        if constexpr (MX) {
+          // lane l: the mid row's bf16 at K 128 kb + 32 (l / 16) + 8 d, d < 4
+          const uint8_t* mrow = mql + (on ? sl : 0) * ROWB + 64 * grp;
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) {
+            v4i B[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const v4i z = {0, 0, 0, 0};
+              B[d] = on ? *reinterpret_cast<const v4i*>(mrow + kb * 256 + d * 16) : z;
+            }
+            const float cf = on ? mcl[(on ? sl : 0) * NKB + kb] : 0.f;
+            const v4f zero = {0.f, 0.f, 0.f, 0.f};
+            const v4f d = fp4_step(buf[kb][0], bsc[kb], B, zero);
+            mx_issue(fn, un, kb);
+            acc += d * cf;
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          u += DW;
+          return;
+        }
         const int bb = (on ? sl : 0) * I + 32 * grp;
         const int s2b =
             __builtin_amdgcn_readfirstlane((e * (H / 128) + rg0 / 128) * (I / 128));

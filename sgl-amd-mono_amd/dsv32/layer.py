@@ -1,7 +1,8 @@
 """One GPU's TP=4 share of a DeepSeek-V3.2 DSA decoder layer on gfx950: the front (norms,
 projections, RoPE, KV and index-key cache writes), the attention phase (FP4 indexer,
-exact top-2048, sparse MLA), the output block (W_UV, o_proj, residual) and the FP8 MoE
-(post-norm, router, top-8 + shared experts, residual).
+exact top-2048, sparse MLA), the output block (W_UV, o_proj, residual) and the MoE
+(post-norm, router, top-8 + shared experts, residual) over FP8 or, in the one launch,
+MXFP4 (A16W4) experts.
 
 ``FusedLayerOp.launch(h, caches, step) -> x_out`` runs the layer as ONE persistent launch
 (``mono_layer_launch``); ``LayerOp`` runs the same four phases as four launches on one
@@ -17,7 +18,7 @@ local residual adds of the output block and the MoE (``kernel.py:1665-1669``).
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Optional
+from typing import Optional, Union
 
 import torch
 
@@ -28,7 +29,7 @@ from ..runtime import MonoRuntime, shared_or_new
 from .attn import MAX_CTX, AttnInputs, AttnOp
 from .config import DSV32, LayerConfig
 from .front import FrontCaches, FrontOp, FrontWeights
-from .moe import MoeFp8Op, MoeFp8Weights, _need
+from .moe import MoeFp8Op, MoeFp8Weights, MoeMxfp4LayerWeights, _need
 from .post import PostOp, PostWeights
 
 
@@ -36,7 +37,7 @@ from .post import PostOp, PostWeights
 class LayerWeights:
     front: FrontWeights
     post: PostWeights
-    moe: MoeFp8Weights
+    moe: Union[MoeFp8Weights, MoeMxfp4LayerWeights]
 
 
 @dataclass
@@ -78,6 +79,8 @@ class LayerOp:
                  max_rows: int = 8, ctx_max: int = 32768, deadline_s: float = 10.0,
                  sm_scale: Optional[float] = None):
         rts = device_or_rts
+        if isinstance(weights.moe, MoeMxfp4LayerWeights):
+            raise ValueError("MXFP4 experts run in the one-launch layer (FusedLayerOp) only")
         if not isinstance(rts, LayerRuntimes):
             rts = LayerRuntimes(rts, cfg, max_rows, ctx_max, deadline_s)
         device, max_rows, ctx_max = rts.device, rts.max_rows, rts.ctx_max
@@ -165,7 +168,9 @@ def layer_runtime(device, max_rows: int = 8, deadline_s: float = 10.0) -> MonoRu
 
 class FusedLayerOp:
     """The layer as one persistent launch for up to ``max_rows`` rows (<= 8) seeing at most
-    ``ctx_max`` keys, with a runtime of its own or a shared one (``rt``)."""
+    ``ctx_max`` keys, with a runtime of its own or a shared one (``rt``; FP8- and
+    MXFP4-expert layers can share one). ``weights.moe`` is ``MoeFp8Weights`` (W8A8) or
+    ``MoeMxfp4LayerWeights`` (A16W4)."""
 
     def __init__(self, weights: LayerWeights, device, cfg: LayerConfig = DSV32,
                  max_rows: int = 8, ctx_max: int = 32768, deadline_s: float = 10.0,
@@ -176,12 +181,15 @@ class FusedLayerOp:
             raise ValueError("max_rows must be 1..8")
         if not 1 <= ctx_max <= MAX_CTX:
             raise ValueError(f"ctx_max must be 1..{MAX_CTX}")
+        self.mx = isinstance(weights.moe, MoeMxfp4LayerWeights)
+        if self.mx:
+            weights = LayerWeights(weights.front, weights.post, weights.moe.bytes_view())
         weights.front.validate(cfg, self.device)
         weights.post.validate(cfg, self.device)
         weights.moe.validate(cfg, self.device)
         lays = {weights.front.layout, weights.post.layout, weights.moe.layout}
         if len(lays) != 1:
-            raise ValueError(f"one FP8 layout for the whole layer, got {sorted(lays)}")
+            raise ValueError(f"one weight layout for the whole layer, got {sorted(lays)}")
         self.w, self.layout = weights, lays.pop()
         nbytes = _lib.lib().mono_layer_scratch_bytes(max_rows)
         self.rt = shared_or_new(rt, nbytes, self.device, deadline_s)
@@ -262,7 +270,10 @@ class FusedLayerOp:
             cos=f.cos.data_ptr(), sin=f.sin.data_ptr(), w_uv=po.w_uv.data_ptr(),
             s_uv=po.s_uv.data_ptr(), w_o=po.w_o.data_ptr(), s_o=po.s_o.data_ptr(),
             g_post=m.g_post.data_ptr(), w_r=m.w_r.data_ptr(), bias=m.bias.data_ptr(),
-            w13=m.w13.data_ptr(), s13=m.s13.data_ptr(), w2=m.w2.data_ptr(), s2=m.s2.data_ptr(),
+            w13=m.w13.data_ptr(), w2=m.w2.data_ptr(),
+            s13=None if self.mx else m.s13.data_ptr(), s2=None if self.mx else m.s2.data_ptr(),
+            expert_format=_lib.EXPERTS_MXFP4 if self.mx else _lib.EXPERTS_FP8,
+            e13=m.s13.data_ptr() if self.mx else None, e2=m.s2.data_ptr() if self.mx else None,
             q=ptr(d.q), iq=ptr(d.iq), iqs=ptr(d.iqs), iw=ptr(d.iw), o_lat=ptr(d.o_lat),
             a=ptr(d.a), scores=ptr(d.scores), topk_pos=ptr(d.topk), y=ptr(d.y),
             moe_scores=ptr(d.moe_scores), ids=ptr(d.ids), weights=ptr(d.weights),

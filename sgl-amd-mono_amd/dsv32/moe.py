@@ -188,6 +188,44 @@ class MoeMxfp4Weights:
         _need(self.s2, "s2", U8, (e + 1, h, cols(i // 32)), device)
 
 
+@dataclass
+class MoeMxfp4LayerWeights:
+    """One layer's FFN with MXFP4 (A16W4) experts, for the one-launch layer: the router and
+    norm as ``MoeFp8Weights`` (g_post bf16 [H], w_r bf16 [E, H], bias f32 [E]) and the
+    experts as ``MoeMxfp4Weights`` at the layer's geometry: w13 E2M1 codes uint8
+    [E + 1, 2 I, H / 2], s13 E8M0 uint8 [E + 1, 2 I, H / 32], w2 [E + 1, H, I / 2], s2
+    [E + 1, H, I / 32] (``aiter16``: the (16, 16) code shuffle and the e8m0 scale shuffle,
+    what aiter's MXFP4 MoE method leaves in place). The reference's A16W4 mode
+    (``sgl_amd_mono/glm53/gfx950/config.py:15-21,88-93``)."""
+
+    g_post: torch.Tensor
+    w_r: torch.Tensor
+    bias: torch.Tensor
+    w13: torch.Tensor
+    s13: torch.Tensor
+    w2: torch.Tensor
+    s2: torch.Tensor
+    layout: str = layouts.ROWMAJOR
+
+    def bytes_view(self) -> "MoeMxfp4LayerWeights":
+        v = lambda t: t if t.dtype == U8 else t.view(U8)
+        return MoeMxfp4LayerWeights(self.g_post, self.w_r, self.bias, v(self.w13), v(self.s13),
+                                    v(self.w2), v(self.s2), self.layout)
+
+    def validate(self, cfg: LayerConfig, device) -> None:
+        h, i, e = cfg.hidden, cfg.inter, cfg.experts
+        if self.layout not in layouts.LAYOUTS:
+            raise ValueError(f"layout {self.layout!r}: one of {layouts.LAYOUTS}")
+        cols = (lambda c: layouts.e8m0_cols(c)) if self.layout == layouts.AITER16 else (lambda c: c)
+        _need(self.g_post, "g_post", torch.bfloat16, (h,), device)
+        _need(self.w_r, "w_r", torch.bfloat16, (e, h), device)
+        _need(self.bias, "bias", torch.float32, (e,), device)
+        _need(self.w13, "w13", U8, (e + 1, 2 * i, h // 2), device)
+        _need(self.s13, "s13", U8, (e + 1, 2 * i, cols(h // 32)), device)
+        _need(self.w2, "w2", U8, (e + 1, h, i // 2), device)
+        _need(self.s2, "s2", U8, (e + 1, h, cols(i // 32)), device)
+
+
 class MoeMxfp4Op:
     """The MXFP4 (A16W4) routed-MoE launch on one device for up to ``max_rows`` rows:
     x bf16 [R, H] and gate logits f32 [R, E] -> bf16(res + y) (``bf16(y)`` without a

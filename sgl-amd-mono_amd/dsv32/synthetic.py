@@ -14,7 +14,7 @@ import torch
 
 from .. import _lib, layouts
 from .config import DSV32, MXFP4_MOE, LayerConfig, Mxfp4MoeConfig
-from .moe import MoeFp8Weights, MoeMxfp4Weights
+from .moe import MoeFp8Weights, MoeMxfp4LayerWeights, MoeMxfp4Weights
 from .post import PostWeights
 from .front import FrontCaches, FrontWeights
 
@@ -25,6 +25,16 @@ def _gen(device, seed: int, family: int) -> torch.Generator:
     return torch.Generator(device=device).manual_seed(1_000_003 * seed + 7919 * family + 17)
 
 
+def _router(dev, seed: int, cfg: LayerConfig):
+    """The router w_r bf16 [E, H], its bias f32 [E] and the post-attention norm bf16 [H]."""
+    h, e = cfg.hidden, cfg.experts
+    g = _gen(dev, seed, 1)
+    w_r = (torch.randn(e, h, generator=g, device=dev) * (2.0 / h ** 0.5)).to(torch.bfloat16)
+    bias = torch.randn(e, generator=_gen(dev, seed, 2), device=dev) * 0.1
+    g_post = (1 + 0.1 * torch.randn(h, generator=_gen(dev, seed, 3), device=dev)).to(torch.bfloat16)
+    return w_r, bias, g_post
+
+
 def moe_fp8_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
                     experts: int | None = None, layout: str = layouts.ROWMAJOR) -> MoeFp8Weights:
     """Config 2 weights; ``experts`` limits how many expert slots get random values
@@ -33,10 +43,7 @@ def moe_fp8_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
     dev = torch.device(device)
     h, i, e = cfg.hidden, cfg.inter, cfg.experts
     n = e + 1
-    g = _gen(dev, seed, 1)
-    w_r = (torch.randn(e, h, generator=g, device=dev) * (2.0 / h ** 0.5)).to(torch.bfloat16)
-    bias = torch.randn(e, generator=_gen(dev, seed, 2), device=dev) * 0.1
-    g_post = (1 + 0.1 * torch.randn(h, generator=_gen(dev, seed, 3), device=dev)).to(torch.bfloat16)
+    w_r, bias, g_post = _router(dev, seed, cfg)
     w13 = torch.zeros(n, 2 * i, h, dtype=FP8, device=dev)
     w2 = torch.zeros(n, h, i, dtype=FP8, device=dev)
     gw = _gen(dev, seed, 4)
@@ -70,7 +77,8 @@ def rows_bf16(rows: int, hidden: int, device, seed: int = 0) -> torch.Tensor:
 
 
 def mxfp4_moe_weights(device, seed: int = 0, cfg: Mxfp4MoeConfig = MXFP4_MOE,
-                      layout: str = layouts.ROWMAJOR) -> MoeMxfp4Weights:
+                      layout: str = layouts.ROWMAJOR, e13=(119, 122),
+                      e2=(119, 122)) -> MoeMxfp4Weights:
     """Config 4: E2M1 codes (random bytes, even index in the low nibble) with E8M0
     scales per 32 in [119, 122]; w13 [E+1, 2I, H/2] + [E+1, 2I, H/32], w2 [E+1, H, I/2] +
     [E+1, H, I/32]; router bias f32 0.01*N(0,1). ``layout`` "aiter16" stores the same
@@ -80,9 +88,9 @@ def mxfp4_moe_weights(device, seed: int = 0, cfg: Mxfp4MoeConfig = MXFP4_MOE,
     g = _gen(dev, seed, 11)
     u8 = dict(dtype=torch.uint8, device=dev, generator=g)
     w13 = torch.randint(0, 256, (n, 2 * i, h // 2), **u8)
-    s13 = torch.randint(119, 123, (n, 2 * i, h // 32), **u8)
+    s13 = torch.randint(e13[0], e13[1] + 1, (n, 2 * i, h // 32), **u8)
     w2 = torch.randint(0, 256, (n, h, i // 2), **u8)
-    s2 = torch.randint(119, 123, (n, h, i // 32), **u8)
+    s2 = torch.randint(e2[0], e2[1] + 1, (n, h, i // 32), **u8)
     bias = torch.randn(cfg.experts, generator=_gen(dev, seed, 12), device=dev) * 0.01
     if layout == layouts.AITER16:
         w13, w2 = layouts.shuffle_16x16(w13), layouts.shuffle_16x16(w2)
@@ -90,7 +98,27 @@ def mxfp4_moe_weights(device, seed: int = 0, cfg: Mxfp4MoeConfig = MXFP4_MOE,
     return MoeMxfp4Weights(bias=bias, w13=w13, s13=s13, w2=w2, s2=s2, layout=layout)
 
 
-def rowmajor_mxfp4_expert(w: MoeMxfp4Weights, e: int, cfg: Mxfp4MoeConfig = MXFP4_MOE):
+# MXFP4 experts at the layer's geometry (hidden 7168, expert intermediate 512)
+MXFP4_LAYER_MOE = Mxfp4MoeConfig(hidden=DSV32.hidden, inter=DSV32.inter)
+
+
+def moe_mxfp4_layer_weights(device, seed: int = 0, cfg: LayerConfig = DSV32,
+                            layout: str = layouts.ROWMAJOR) -> MoeMxfp4LayerWeights:
+    """The layer's FFN with MXFP4 experts: the router and norm as ``moe_fp8_weights``
+    draws them, the experts as ``mxfp4_moe_weights`` at the layer's geometry with E8M0
+    exponents around the variance-preserving scale (weight rms ~ 1/sqrt(K); random E2M1
+    codes have rms 2.93): 2^(e - 127) 2.93 sqrt(7168) ~ 1 at e = 119 for w13 and
+    2.93 sqrt(512) ~ 2^6 at e = 121 for w2, each +-1, so the rows' MoE sum is O(1)."""
+    dev = torch.device(device)
+    w_r, bias, g_post = _router(dev, seed, cfg)
+    x = mxfp4_moe_weights(dev, seed, Mxfp4MoeConfig(hidden=cfg.hidden, inter=cfg.inter,
+                                                    experts=cfg.experts), layout=layout,
+                          e13=(118, 120), e2=(120, 122))
+    return MoeMxfp4LayerWeights(g_post=g_post, w_r=w_r, bias=bias, w13=x.w13, s13=x.s13,
+                                w2=x.w2, s2=x.s2, layout=layout)
+
+
+def rowmajor_mxfp4_expert(w, e: int, cfg: Mxfp4MoeConfig = MXFP4_MOE):
     """Expert e's (w13, s13, w2, s2) bytes on the host as numpy, row-major."""
     w13, s13, w2, s2 = w.w13[e], w.s13[e], w.w2[e], w.s2[e]
     if w.layout == layouts.AITER16:
@@ -262,8 +290,9 @@ def front_caches(device, slots: int, pages: int, seed: int = 0,
 
 
 def layer(rows: int, ctx: int, device, seed: int = 0, layout: str = layouts.AITER16,
-          index_format: int = _lib.INDEX_FP4_PLANE):
-    """Config 5, one layer: its weights (front, output block, FP8 MoE), caches as config 3
+          index_format: int = _lib.INDEX_FP4_PLANE, experts: str = "fp8"):
+    """Config 5, one layer: its weights (front, output block, MoE with ``experts`` "fp8" or
+    "mxfp4"), caches as config 3
     (each row its own request at position ctx - 1 over shuffled pages; the index keys in
     ``index_format``), the step's tables (each row's slot the page-table entry of its
     position) and the input rows h. Returns (LayerWeights, FrontCaches, LayerStep, h)."""
@@ -272,7 +301,10 @@ def layer(rows: int, ctx: int, device, seed: int = 0, layout: str = layouts.AITE
     dev = torch.device(device)
     w = LayerWeights(front=front_weights(dev, seed, layout=layout, rope_rows=max(ctx, 1)),
                      post=post_weights(dev, seed, layout=layout),
-                     moe=moe_fp8_weights(dev, seed, layout=layout))
+                     moe=moe_fp8_weights(dev, seed, layout=layout) if experts == "fp8" else
+                     moe_mxfp4_layer_weights(dev, seed, layout=layout))
+    if experts not in ("fp8", "mxfp4"):
+        raise ValueError(f"experts {experts!r}: 'fp8' or 'mxfp4'")
     a = attention_inputs(rows, ctx, dev, seed=seed, index_format=index_format)
     caches = FrontCaches(kv=a.kv, kv_scale=a.kv_scale, plane=a.plane, plane_scale=a.plane_scale,
                          index_format=index_format)
