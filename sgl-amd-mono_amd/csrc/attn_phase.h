@@ -332,8 +332,8 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
     if (!valid) return true;
     const bool listed = lists_on && n > AT_TOPK;
     if (listed) {
-      if (tid < 64) reinterpret_cast<v4i*>(chist)[tid] = v4i{0, 0, 0, 0};
-      if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = v4i{-1, 0, 0, 0};
+      if (tid < 64) reinterpret_cast<v4i*>(chist)[tid] = opaque_v4(0, 0, 0, 0);
+      if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = opaque_v4(-1, 0, 0, 0);
     }
     const int pg = c * (AT_CHUNK / AT_PAGE) + w;
     const bool live = pg * AT_PAGE < n;
@@ -441,36 +441,50 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
           ks[nt] = ld4<CP_DEV>(rpg, 8192u + (uint32_t)(16 * nt + (l & 15)) * 4u);
         }
       }
-      // head tile by head tile: the four token tiles' accumulators over the four K steps,
-      // the keys widened exactly to bf16 as each step takes them (B operands)
+      // two head tiles at a time: the four token tiles' accumulators of both over the four
+      // K steps, each key step widened exactly to bf16 (B operand) once for the pair. The
+      // second pair widens the keys again: an opaque copy of the raw keys keeps the
+      // compiler from reusing the first pair's widened keys, whose 64 registers beside
+      // the raw keys and accumulators would spill
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
-        // one head tile at a time: no loads or conversions hoisted from the next one
+      for (int hp = 0; hp < 2; ++hp) {
         __builtin_amdgcn_sched_barrier(0);
-        // A operands of head tile mi: head 16 mi + l % 16, K step 2 m + s
-        const uint8_t* qrow = iq8 + (16 * mi + (l & 15)) * AT_IQ8_ROW + 32 * (l >> 4);
-        v4f d[4];
+        if (hp == 1) {
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) d[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+          for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(kb[i]));
+        }
+        // A operands of head tile 2 hp + j: head 16 (2 hp + j) + l % 16, K step 2 m + s
+        const uint8_t* qrow = iq8 + (32 * hp + (l & 15)) * AT_IQ8_ROW + 32 * (l >> 4);
+        v4f d[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) d[0][nt] = d[1][nt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-          const v8bf qa = *reinterpret_cast<const v8bf*>(qrow + 128 * (st >> 1) + 16 * (st & 1));
+          const int qo = 128 * (st >> 1) + 16 * (st & 1);
+          const v8bf qa0 = *reinterpret_cast<const v8bf*>(qrow + qo);
+          const v8bf qa1 = *reinterpret_cast<const v8bf*>(qrow + 16 * AT_IQ8_ROW + qo);
 #pragma unroll
           for (int nt = 0; nt < 4; ++nt) {
             const v4i& k = kb[2 * nt + (st >> 1)];
             const v8bf kw = (st & 1) ? fp8x8_bf16((uint32_t)k[2], (uint32_t)k[3])
                                      : fp8x8_bf16((uint32_t)k[0], (uint32_t)k[1]);
-            d[nt] = mfma_bf16(qa, kw, d[nt]);
+            d[0][nt] = mfma_bf16(qa0, kw, d[0][nt]);
+            d[1][nt] = mfma_bf16(qa1, kw, d[1][nt]);
           }
         }
-        // head weights of the lane's D rows: heads 16 mi + 4 (l / 16) + e
-        const v4f wv = *reinterpret_cast<const v4f*>(iq8 + AT_IHEADS * AT_IQ8_ROW +
-                                                     (16 * mi + 4 * (l >> 4)) * 4);
+        // head weights of the lane's D rows: heads 16 (2 hp + j) + 4 (l / 16) + e, the
+        // tiles summed in head order
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
+        for (int j = 0; j < 2; ++j) {
+          const v4f wv = *reinterpret_cast<const v4f*>(iq8 + AT_IHEADS * AT_IQ8_ROW +
+                                                       (16 * (2 * hp + j) + 4 * (l >> 4)) * 4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[nt] = fmaf(fmaxf(d[nt][e], 0.f), wv[e], acc[nt]);
+          for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[nt] = fmaf(fmaxf(d[j][nt][e], 0.f), wv[e], acc[nt]);
+        }
       }
       // the key's power-of-two scale after the heads' sums (the ReLU commutes with it)
 #pragma unroll
@@ -549,7 +563,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
       } else {
         const int nch = (n + AT_CHUNK - 1) / AT_CHUNK;
         // topk_lists' / topk_select's minimum, maximum and flag words, set before a barrier
-        if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = v4i{-1, 0, 0, 0};
+        if (tid == 0) *reinterpret_cast<v4i*>(mm_s) = opaque_v4(-1, 0, 0, 0);
         __syncthreads();
         // each wave waits for its own chunks' done words (then loads their lists at once)
         const uint32_t* dw = score_done + r * AT_NCHUNK;

@@ -68,6 +68,13 @@ __device__ inline int opaque_v(int v) {
   asm volatile("" : "+v"(v));
   return v;
 }
+// a constant vector made where it is stored: the compiler would otherwise build it once,
+// ahead of the loops around the store, and hold (or spill) its registers meanwhile
+__device__ inline v4i opaque_v4(int a, int b, int c, int d) {
+  v4i v{a, b, c, d};
+  asm volatile("" : "+v"(v));
+  return v;
+}
 template <int CP>
 __device__ inline v2i ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP);

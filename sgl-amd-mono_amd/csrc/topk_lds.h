@@ -93,7 +93,7 @@ __device__ inline void select_pass(int tid, const uint32_t (&key)[NK], uint32_t 
   constexpr int G = NB / AT_THREADS;
   v4i* mine = reinterpret_cast<v4i*>(hist + NB - G * (tid + 1));
   const v4i h4 = *mine;
-  *mine = v4i{0, 0, 0, 0};
+  *mine = opaque_v4(0, 0, 0, 0);
   const int s = h4[0] + h4[1] + h4[2] + h4[3];
   int tot;
   const int pre = block_scan(s, wsum, phase, tot);
@@ -248,7 +248,7 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_select(
   v4i raw[NLD];
 #pragma unroll
   for (int q = 0; q < NLD; ++q) raw[q] = ld16<CP_NONE>(rs, (uint32_t)(4 * (tid + AT_THREADS * q)) * 4);
-  reinterpret_cast<v4i*>(hist)[tid] = v4i{0, 0, 0, 0};  // select_pass expects it zero
+  reinterpret_cast<v4i*>(hist)[tid] = opaque_v4(0, 0, 0, 0);  // select_pass expects it zero
   // a position past the row holds key 0, below every real key (a score keeps key >= 1:
   // only the all-ones NaN would map to 0, and it ranks next to it)
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
@@ -331,7 +331,7 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_final(
   v2i raw[NK];
 #pragma unroll
   for (int j = 0; j < NK; ++j) raw[j] = ld8<CP_DEV>(rc, (uint32_t)(NK * tid + j) * 8u);
-  reinterpret_cast<v4i*>(hist)[tid] = v4i{0, 0, 0, 0};  // select_pass expects it zero
+  reinterpret_cast<v4i*>(hist)[tid] = opaque_v4(0, 0, 0, 0);  // select_pass expects it zero
   uint32_t key[NK];
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
@@ -398,7 +398,7 @@ __device__ inline uint32_t chunk_list(int tid, uint32_t k, int pos0, uint32_t* h
       if (w == 0) {
         // lane l: bins 255 - 4 l .. 252 - 4 l (from the top), then an inclusive scan
         const v4i h4 = reinterpret_cast<const v4i*>(hist)[63 - l];
-        reinterpret_cast<v4i*>(hist)[63 - l] = v4i{0, 0, 0, 0};
+        reinterpret_cast<v4i*>(hist)[63 - l] = opaque_v4(0, 0, 0, 0);
         const int c4 = h4[0] + h4[1] + h4[2] + h4[3];
         int above = above0 + wave_scan(c4) - c4;  // keys above the lane's four bins
         int bin = -1, ab = 0, nb = 0;
@@ -499,7 +499,7 @@ __device__ __attribute__((always_inline)) inline int32_t* topk_lists(
   const uint32_t mycut =
       (uint32_t)ld4<CP_NONE>(rcut, ch < nch && tid % (TK_LIST / NK) == 0 ? (uint32_t)ch * 4u
                                                                           : 0x80000000u);
-  reinterpret_cast<v4i*>(hist)[tid] = v4i{0, 0, 0, 0};  // select_pass expects it zero
+  reinterpret_cast<v4i*>(hist)[tid] = opaque_v4(0, 0, 0, 0);  // select_pass expects it zero
   uint32_t key[NK];
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
   int cnt = 0;
