@@ -54,6 +54,9 @@ struct GemvJob {
   // yet" stores the complement); out_plain, if given, gets the plain pairs as well
   uint32_t out_xor;
   uint16_t* out_plain;
+  // with bf16 outputs: each output row's sum of the squares of a 16-column tile's bf16
+  // values, ssq[column tile][16] (f32, device coherent), if given
+  float* ssq;
 };
 
 template <int KS, int RG, int STEPS>
@@ -167,6 +170,16 @@ struct Gemv {
       if (tok < R && (row & 1) == 0) {
         st_dev(reinterpret_cast<uint32_t*>(j.out_bf + at), pair ^ j.out_xor);
         if (j.out_plain) st_dev(reinterpret_cast<uint32_t*>(j.out_plain + at), pair);
+      }
+      if (j.ssq) {
+        // the squares of the stored bf16 values (exact in f32), summed over the row of
+        // 16 lanes (the tile's 16 columns of one output row) in a fixed butterfly order
+        const float hv = bf16_lo(h);
+        const float sq = red16(tok < R ? hv * hv : 0.f, OpAdd());
+        if (tok < R && row == 0)
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __float_as_uint(sq), rsrc(j.ssq, (uint32_t)j.N * 4u),
+              (uint32_t)(((tile * RG + rge) * 16 + tok) * 4), 0, CP_DEV);
       }
     }
   }

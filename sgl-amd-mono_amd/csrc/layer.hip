@@ -156,6 +156,7 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   po.s_o = a->s_o;
   po.out = st;
   po.o = nullptr;
+  po.ssq = reinterpret_cast<float*>(sc + S.ssq);
   po.scratch = sc + S.post;
   po.guard = a->guard;
   po.host_err = host_err;
@@ -170,6 +171,7 @@ extern "C" int mono_layer_launch(const MonoLayerArgs* a, mono_stream_t stream) {
   m.n_group = a->n_group;
   m.topk_group = a->topk_group;
   m.a = st;
+  m.ssq = reinterpret_cast<const float*>(sc + S.ssq);
   m.out = static_cast<uint16_t*>(a->out);
   m.g_post = static_cast<const uint16_t*>(a->g_post);
   m.w_r = static_cast<const uint16_t*>(a->w_r);

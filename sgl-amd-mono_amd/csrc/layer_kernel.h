@@ -35,6 +35,7 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 constexpr int LY_LDS_BYTES =
     cmax(cmax(FR_LDS_BYTES, AT_LDS_BYTES),
          cmax(PO_LDS_BYTES, cmax(MoeLds<LY_H, LY_I>::BYTES, MoeLds<LY_H, LY_I, true>::BYTES)));
+static_assert(PO_HID == LY_H, "the output block's 16-column tiles cover the MoE's rows");
 static_assert(MoeFp8Geom<LY_H, LY_I>::BYTES == MoeFp8Geom<LY_H, LY_I, true>::BYTES,
               "FP8 and MXFP4 layers share one scratch layout");
 
@@ -42,7 +43,7 @@ static_assert(MoeFp8Geom<LY_H, LY_I>::BYTES == MoeFp8Geom<LY_H, LY_I, true>::BYT
 // hand-offs between phases that the caller does not ask to see
 struct LayerScratch {
   static constexpr size_t BARRIERS = 0;  // count k at 256 k, flag k at 256 k + 128
-  size_t front, attn, post, moe, q, iq, iqs, iw, o_lat, a, bytes;
+  size_t front, attn, post, moe, q, iq, iqs, iw, o_lat, a, ssq, bytes;
   __host__ __device__ explicit LayerScratch(int rm) {
     front = 1024;
     attn = at_align(front + FrontScratch::BYTES);
@@ -54,7 +55,8 @@ struct LayerScratch {
     iw = at_align(iqs + (size_t)rm * 256);
     o_lat = at_align(iw + (size_t)rm * AT_IHEADS * 4);
     a = at_align(o_lat + (size_t)rm * AT_HEADS * AT_LAT * 2);
-    bytes = at_align(a + (size_t)rm * LY_H * 2);
+    ssq = at_align(a + (size_t)rm * LY_H * 2);            // f32 [LY_H / 16][16]
+    bytes = at_align(ssq + (size_t)(LY_H / 16) * 16 * 4);
   }
 };
 

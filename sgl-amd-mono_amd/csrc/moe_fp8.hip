@@ -54,6 +54,7 @@ static int moe_fp8_launch_on(const MonoMoeFp8Args* a, mono_stream_t stream, void
   p.n_group = a->n_group;
   p.topk_group = a->topk_group;
   p.a = static_cast<const uint16_t*>(a->a);
+  p.ssq = nullptr;
   p.out = static_cast<uint16_t*>(a->out);
   p.g_post = static_cast<const uint16_t*>(a->g_post);
   p.w_r = static_cast<const uint16_t*>(a->w_r);

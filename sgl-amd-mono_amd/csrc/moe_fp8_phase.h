@@ -107,6 +107,9 @@ struct MoeFp8Params {
   float eps, route_scale;
   int n_group, topk_group;  // group-limited routing (n_group <= 1: none)
   const uint16_t* a;
+  // fused: a's per-row sums of squares per 16-column tile, f32 [H / 16][16], stored by
+  // the output block before its barrier (the norm then reads no whole row of a)
+  const float* ssq;
   uint16_t* out;
   const uint16_t* g_post;
   const uint16_t* w_r;
@@ -154,8 +157,7 @@ struct MoeLds {
   static constexpr int XQ = (int)((sizeof(RouteLds) + 15) & ~(size_t)15);  // v4i [QW KCW 2 64]
   static constexpr int XS = XQ + G::QW * G::KCW * 2 * 64 * 16;   // f32 [QW KCW][16]
   static constexpr int RED = XS + G::QW * G::KCW * 16 * 4;       // v4f [16][64]
-  static constexpr int RSM = RED + G::WAVES * 64 * 16;           // f32 [2][2][16]
-  static constexpr int RSTD = RSM + 2 * 2 * 16 * 4;              // f32 [16]
+  static constexpr int RSTD = RED + G::WAVES * 64 * 16;          // f32 [16]
   static constexpr int NEXT = RSTD + MOE_MAXR * 4;               // int
   static constexpr int N1 = NEXT + 4;                            // int
   static constexpr int ORW = N1 + 4;                             // int: a CTA-wide OR
@@ -195,7 +197,6 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   v4i* xq_lds = reinterpret_cast<v4i*>(lds + LO::XQ);
   float (*xs_lds)[16] = reinterpret_cast<float (*)[16]>(lds + LO::XS);  // scale per (chunk, row)
   v4f (*red)[64] = reinterpret_cast<v4f (*)[64]>(lds + LO::RED);
-  float (*red_small)[2][16] = reinterpret_cast<float (*)[2][16]>(lds + LO::RSM);
   int& next_s = *reinterpret_cast<int*>(lds + LO::NEXT);
   float* rstd_s = reinterpret_cast<float*>(lds + LO::RSTD);
   uint32_t* head_s = reinterpret_cast<uint32_t*>(lds + LO::HEAD);
@@ -206,19 +207,35 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   uint32_t* ready_w = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_READY);
   uint32_t* queue = reinterpret_cast<uint32_t*>(p.scratch + G::OFF_QUEUE);
 
-  // the first eight rows: two waves a row, lane l the 8 values at q * 512 + l * 8 of its
-  // half's 7 slices; issued first (standalone) so they fly with the staging and guard loads
-  constexpr int NQ0 = H / 1024;
-  v4i av0[NQ0];
-  auto load_rows0 = [&]() {
-    const int r = w / 2, ch = w % 2;
-    const bool live = r < R;
-    const __amdgpu_buffer_rsrc_t rar = rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
-    const uint32_t base = (uint32_t)(ch * NQ0 * 512 + l * 8) * 2;
+  // The rows' sums of squares, in one order whichever the form, so a fused launch's rstd
+  // has the bits of a launch of its own: per 16-column tile of a row the balanced
+  // pairwise tree of its 16 squares (the output block's 16-lane butterfly, in the fused
+  // form), tile t on thread t (H / 16 of them; the rest add zeros), the wave's tiles
+  // summed by the wave butterfly, then the 16 waves in order. Fused, the output block
+  // stored the tile sums (rows 0-7, f32 [H / 16][16]); standalone, thread t loads its
+  // tile of rows row0 .. row0 + 7 (32 bytes a row), issued first so they fly with the
+  // staging and guard loads.
+  constexpr int NSQT = H / 16;
+  static_assert(NSQT <= G::THREADS, "a tile a thread");
+  v4i sq0 = {0, 0, 0, 0}, sq1 = {0, 0, 0, 0};  // fused: tile tid's sums of rows 0-7
+  v4i at[8][2];                                 // standalone: tile tid of 8 rows
+  auto load_tiles = [&](int row0) {
 #pragma unroll
-    for (int q = 0; q < NQ0; ++q) av0[q] = ld16<XCP>(rar, base + q * 1024);
+    for (int rr = 0; rr < 8; ++rr) {
+      const int r = row0 + rr;
+      const bool live = r < R && tid < NSQT;
+      const __amdgpu_buffer_rsrc_t rar = rsrc(p.a + (size_t)(r < R ? r : 0) * H, live ? H * 2 : 0);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) at[rr][hh] = ld16<XCP>(rar, (uint32_t)(tid * 16 + 8 * hh) * 2u);
+    }
   };
-  if constexpr (!FUSED) load_rows0();
+  auto load_ssq = [&]() {
+    const __amdgpu_buffer_rsrc_t rq = rsrc(p.ssq, (uint32_t)NSQT * 16u * 4u);
+    const uint32_t o = tid < NSQT ? (uint32_t)tid * 64u : 0x80000000u;
+    sq0 = ld16<XCP>(rq, o);
+    sq1 = ld16<XCP>(rq, o + 16u);
+  };
+  if constexpr (!FUSED) load_tiles(0);
   // the post-attention norm weight, the same for every row, goes to LDS (over the
   // reduction buffer, idle until stage 2); every load of the prologue is issued before
   // the first is waited on, none under a branch (absent ones read through an empty
@@ -262,7 +279,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   wa0 = router_w(b);
   if constexpr (FUSED) {
     ok = ready();
-    load_rows0();
+    load_ssq();
     xa0 = router_x(b);
     pub_loads(b, pa0);
     if (tid < H / 8) g_lds[tid] = gv;
@@ -292,39 +309,50 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   uint32_t* hrt = reinterpret_cast<uint32_t*>(hcur + G::OFF_RT);
 
   // ---------------------------------------------------------------- stage 0
-  // the rows' rstd: two waves a row, one round trip (a second pass for rows 8-15)
+  // the rows' rstd (the sums' order above; a second pass for rows 8-15, standalone)
   {
-    auto ss_pass = [&](int row0, v4i* av) {
-      const int r = row0 + w / 2, ch = w % 2;
-      // the squares of bf16 pairs by v_dot2c_f32_bf16: 4 instructions for 8 values
-      float ss = 0.f;
+    float* ssr = &xs_lds[0][0];  // [16 waves][8 rows], over the scale table (idle until stage 1)
+    static_assert(G::QW * G::KCW * 16 >= G::WAVES * 8, "the row sums fit the scale table");
+    // v[rr]: this thread's tile sum of row row0 + rr
+    auto reduce_rows = [&](int row0, float (&v)[8]) {
 #pragma unroll
-      for (int q = 0; q < NQ0; ++q)
+      for (int r = 0; r < 8; ++r) v[r] = wave_sum(v[r]);
+      if (l == 0)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ss = dot2_bf16_sq((uint32_t)av[q][i], ss);
-      ss = wave_sum(ss);
-      if (l == 0) red_small[0][ch][r] = ss;
+        for (int r = 0; r < 8; ++r) ssr[w * 8 + r] = v[r];
       __syncthreads();
       if (tid < 8) {
+        float tot = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < G::WAVES; ++ww) tot += ssr[ww * 8 + tid];
         const int rr = row0 + tid;
-        const float tot = red_small[0][0][rr] + red_small[0][1][rr];
         rstd_s[rr] = rr < R ? 1.0f / sqrtf(tot / (float)H + p.eps) : 0.f;
       }
       __syncthreads();
     };
-    ss_pass(0, av0);
-    if (R > 8) {
-      const int r = 8 + w / 2, ch = w % 2;
-      const bool live = r < R;
-      const __amdgpu_buffer_rsrc_t rar =
-          rsrc(p.a + (size_t)(live ? r : 0) * H, live ? H * 2 : 0);
-      const uint32_t base = (uint32_t)(ch * NQ0 * 512 + l * 8) * 2;
-      v4i av1[NQ0];
+    auto tree_pass = [&](int row0) {
+      float v[8];
 #pragma unroll
-      for (int q = 0; q < NQ0; ++q) av1[q] = ld16<XCP>(rar, base + q * 1024);
-      ss_pass(8, av1);
-    } else if (tid >= 8 && tid < 16) {
-      rstd_s[tid] = 0.f;
+      for (int rr = 0; rr < 8; ++rr) v[rr] = sq_tree16(at[rr][0], at[rr][1]);
+      reduce_rows(row0, v);
+    };
+    if constexpr (FUSED) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = __int_as_float(sq0[i]);
+        v[4 + i] = __int_as_float(sq1[i]);
+      }
+      reduce_rows(0, v);
+      if (tid >= 8 && tid < 16) rstd_s[tid] = 0.f;
+    } else {
+      tree_pass(0);
+      if (R > 8) {
+        load_tiles(8);
+        tree_pass(8);
+      } else if (tid >= 8 && tid < 16) {
+        rstd_s[tid] = 0.f;
+      }
     }
   }
   // the task(s): router tiles publish partial logits, publishers the B image and scales

@@ -244,6 +244,26 @@ __device__ inline uint32_t bf16x2_bits(float lo, float hi) {
   const v2f f = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));
 }
+// The squares of 16 bf16 values (lo: values 0-7, hi: 8-15, two a dword, the low half
+// first; each square exact in f32) summed as a balanced pairwise tree, ((s0 + s1) +
+// (s2 + s3)) + ...: the bits a 16-lane butterfly (red16) gives summing one square a lane
+__device__ inline float sq_tree16(v4i lo, v4i hi) {
+  float s[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float a = bf16_lo((uint32_t)lo[q]), b = bf16_hi((uint32_t)lo[q]);
+    const float c = bf16_lo((uint32_t)hi[q]), d = bf16_hi((uint32_t)hi[q]);
+    s[2 * q] = a * a;
+    s[2 * q + 1] = b * b;
+    s[8 + 2 * q] = c * c;
+    s[8 + 2 * q + 1] = d * d;
+  }
+#pragma unroll
+  for (int n = 8; n >= 1; n /= 2)
+#pragma unroll
+    for (int k = 0; k < n; ++k) s[k] = s[2 * k] + s[2 * k + 1];
+  return s[0];
+}
 // acc + w.lo^2 + w.hi^2 for a bf16 pair w, by v_dot2c_f32_bf16
 __device__ inline float dot2_bf16_sq(uint32_t w, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, w), __builtin_bit_cast(v2bf, w),

@@ -47,6 +47,7 @@ extern "C" int mono_post_launch(const MonoPostArgs* a, mono_stream_t stream) {
   p.out = static_cast<uint16_t*>(a->out);
   p.scratch = static_cast<uint8_t*>(a->scratch);
   p.o = static_cast<uint16_t*>(a->o);
+  p.ssq = nullptr;
   p.guard = a->guard;
   p.host_err = nullptr;
   if (a->host_error) {

@@ -52,6 +52,9 @@ struct PostParams {
   const float* s_o;
   uint16_t* out;
   uint16_t* o;  // bf16 [R][4096]: the caller's, or scratch
+  // the one-launch layer: each row's sum of squares of out's bf16 values per 16-column
+  // tile, f32 [448][16], for the MoE phase's RMSNorm (null: not written)
+  float* ssq;
   uint8_t* scratch;
   int32_t* guard;
   uint32_t* host_err;
@@ -90,6 +93,7 @@ __device__ __attribute__((always_inline)) inline void post_phase(const PostParam
   jo.out_stride = PO_HID;
   jo.res = p.h;
   jo.res_stride = PO_HID;
+  jo.ssq = FUSED ? p.ssq : nullptr;  // a launch of its own has no MoE to feed
   const GemvO go(tid);
   const __amdgpu_buffer_rsrc_t rh = rsrc(p.h, (uint32_t)R * PO_HID * 2u);
   const int etok = (tid >> 4) & 15, erow = tid & 15;     // o_proj epilogue coordinates
