@@ -586,10 +586,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
           // without lists, or where they cannot decide it (every chunk is done: each wave
           // saw its own), every score
           if (!sel) {
-            if (tid == 0) {
-              mm_s[0] = 0xFFFFFFFFu;
-              mm_s[1] = 0u;
-            }
+            if (tid == 0) *reinterpret_cast<v2i*>(mm_s) = opaque_v2(-1, 0);
             __syncthreads();
             const __amdgpu_buffer_rsrc_t rs = rsrc(scores + (size_t)r * AT_MAXCTX, (uint32_t)n * 4);
             sel = topk_select(tid, rs, n, smem, wsum, mm_s, res_s);
@@ -630,10 +627,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
             ok = wait_until(guard, MONO_SITE_SCORES, [&]() {
               return __all(l >= nch || ld_dev(&score_done[r * AT_NCHUNK + c0 + l]) == tag);
             });
-          if (tid == 0) {
-            mm_s[0] = 0xFFFFFFFFu;
-            mm_s[1] = 0u;
-          }
+          if (tid == 0) *reinterpret_cast<v2i*>(mm_s) = opaque_v2(-1, 0);
           ok = cta_all(ok, ok_s);
           if (!ok) break;
           const __amdgpu_buffer_rsrc_t rs =
@@ -672,10 +666,7 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
           ok = wait_until(guard, MONO_SITE_BLOCKS, [&]() {
             return __all(l >= nb || ld_dev(&blk_done[r * AT_MAXBLK + l]) == tag);
           });
-        if (tid == 0) {
-          mm_s[0] = 0xFFFFFFFFu;
-          mm_s[1] = 0u;
-        }
+        if (tid == 0) *reinterpret_cast<v2i*>(mm_s) = opaque_v2(-1, 0);
         ok = cta_all(ok, ok_s);
         if (!ok) break;
         const __amdgpu_buffer_rsrc_t rc =

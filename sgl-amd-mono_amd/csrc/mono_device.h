@@ -75,6 +75,11 @@ __device__ inline v4i opaque_v4(int a, int b, int c, int d) {
   asm volatile("" : "+v"(v));
   return v;
 }
+__device__ inline v2i opaque_v2(int a, int b) {
+  v2i v{a, b};
+  asm volatile("" : "+v"(v));
+  return v;
+}
 template <int CP>
 __device__ inline v2i ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP);
@@ -298,45 +303,50 @@ __device__ inline v4f mfma_fp4_scaled(v8i a, v8i b, v4f c, int sa, int sb) {
 
 // ------------------------------------------------------------------ guard
 // The guard block (int32 words, runtime owned): see mono_amd.h MONO_GUARD_*.
+// Every field is CTA-uniform and kept in scalar registers (the LDS-read ones through
+// readfirstlane): vector registers held for the whole launch would crowd every phase.
 struct Guard {
   int32_t* words;
   uint32_t* host_err;  // pinned host mirror of the first error (may be null)
   uint64_t deadline;   // ticks of the 100 MHz clock
   int fault_site;      // test fault injection: this wait site never completes
   uint64_t slack;      // deadline multiple of the other waits while a fault is injected
-  uint64_t t0;
 
   // `head` = guard words 0-3 as read once by the CTA (one coherent load, shared in LDS:
   // every thread reading the block itself would pile thousands of requests on one line)
   __device__ void init(int32_t* w, uint32_t* he, int fsite, const uint32_t* head, uint32_t fafter) {
     words = w;
     host_err = he;
-    const uint32_t epoch = head[MONO_GUARD_EPOCH];
-    deadline = ((uint64_t)head[MONO_GUARD_DEADLINE_HI] << 32) | head[MONO_GUARD_DEADLINE_LO];
+    const uint32_t epoch = __builtin_amdgcn_readfirstlane(head[MONO_GUARD_EPOCH]);
+    deadline = ((uint64_t)__builtin_amdgcn_readfirstlane(head[MONO_GUARD_DEADLINE_HI]) << 32) |
+               __builtin_amdgcn_readfirstlane(head[MONO_GUARD_DEADLINE_LO]);
     // a block nobody set a deadline on (the library's static block starts zeroed): 10 s
     if (deadline == 0) deadline = 10ull * MONO_CLOCK_HZ;
     fault_site = (fsite > 0 && epoch >= fafter) ? fsite : 0;
     // the injected wait times out first: waits downstream of it (which stall as a
     // consequence) get four times as long, so the error word names the injected site
     slack = fault_site ? 4 : 1;
-    t0 = 0;
   }
   __device__ bool aborted() const {
     return ld_dev(reinterpret_cast<uint32_t*>(words) + MONO_GUARD_ABORT) != 0;
   }
   // a wait at `site` passed its deadline: record 1 + site (first failure sticks),
   // raise the abort flag every other wait checks, mirror the word to the host
+  // (its stored constants are made here, opaque: hoisted to the launch's top they would
+  // hold registers through every phase for a path that runs at most once)
   __device__ void fail(int site) {
     uint32_t* w = reinterpret_cast<uint32_t*>(words);
-    uint32_t expect = 0;
-    __hip_atomic_compare_exchange_strong(w + MONO_GUARD_ERR_DEADLINE, &expect, (uint32_t)(site + 1),
+    uint32_t expect = (uint32_t)opaque_v(0);
+    const uint32_t one = (uint32_t)opaque_v(1), code = (uint32_t)opaque_v(site + 1);
+    __hip_atomic_compare_exchange_strong(w + MONO_GUARD_ERR_DEADLINE, &expect, code,
                                          __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
-    if (fault_site) st_dev(w + MONO_GUARD_ERR_FAULT, 1u);
-    st_dev(w + MONO_GUARD_ABORT, 1u);
+    int fs = fault_site;
+    asm volatile("" : "+s"(fs));
+    if (fs) st_dev(w + MONO_GUARD_ERR_FAULT, one);
+    st_dev(w + MONO_GUARD_ABORT, one);
     if (host_err)
-      __hip_atomic_store(host_err, (uint32_t)(site + 1), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(host_err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     drain();
   }
 };

@@ -165,12 +165,16 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
     if (floor_out) *floor_out = lo;
   }
   __syncthreads();
-  uint32_t pick = 0;  // bit j: key[j] is selected
+  // bit j: key[j] is selected. Masks are built a shift at a time from the top bit down:
+  // a constant 1 << j would be a literal each, which gfx9's VOP3 forms cannot encode, so
+  // the compiler would hold them in registers through the stage.
+  uint32_t pick = 0;
+#pragma unroll
+  for (int j = NK - 1; j >= 0; --j) pick = (pick << 1) | (uint32_t)(key[j] > hi);
   if (cnt <= CAND) {
-    // keys above the bin, and the bin's candidates gathered in one pass
+    // the bin's candidates gathered in one pass
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      pick |= (uint32_t)(key[j] > hi) << j;
       if (key[j] >= lo && key[j] <= hi) {
         const int at = atomicAdd(&res_s[0], 1);
         ck[at] = key[j];
@@ -194,18 +198,21 @@ __device__ inline void topk_refine(int tid, const uint32_t (&key)[NK], PosF pos_
     // one key value (lo == hi) shared by many positions: the first kk of them
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < NK; ++j) {
-      pick |= (uint32_t)(key[j] > hi) << j;
-      c += key[j] == lo;
-    }
+    for (int j = 0; j < NK; ++j) c += key[j] == lo;
     int tot;
     int seen = block_scan(c, wsum, phase, tot);
+    // the tied keys taken, in index order (seen counts them), then their mask top down
+    bool take[NK];
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
       const bool e = key[j] == lo;
-      pick |= (uint32_t)(e && seen < kk) << j;
+      take[j] = e && seen < kk;
       seen += e;
     }
+    uint32_t tmask = 0;
+#pragma unroll
+    for (int j = NK - 1; j >= 0; --j) tmask = (tmask << 1) | (uint32_t)take[j];
+    pick |= tmask;
   }
   __syncthreads();
   pick |= pmask[tid];
@@ -463,7 +470,7 @@ __device__ inline uint32_t chunk_list(int tid, uint32_t k, int pos0, uint32_t* h
     __builtin_amdgcn_raw_buffer_store_b64(v2i{pos0 + tid, (int32_t)k}, rout,
                                           (uint32_t)(base + pre) * 8u, 0, CP_DEV);
   if (tid >= tot && tid < TK_LIST)
-    __builtin_amdgcn_raw_buffer_store_b64(v2i{0, 0}, rout, (uint32_t)tid * 8u, 0, CP_DEV);
+    __builtin_amdgcn_raw_buffer_store_b64(opaque_v2(0, 0), rout, (uint32_t)tid * 8u, 0, CP_DEV);
   return cut;
 }
 
