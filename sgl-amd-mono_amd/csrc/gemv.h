@@ -166,16 +166,19 @@ struct Gemv {
       const uint32_t hn = dpp_u<DPP_XOR1>(h);  // the next row's bits (same token)
       uint32_t pair = h | (hn << 16);
       if (pair == 0xFFFFFFFFu) pair = 0xFFC0FFC0u;  // two NaNs; keeps ~pair nonzero
-      const size_t at = (size_t)g * j.out_gstride + tok * j.out_stride + n;
+      // through buffer resources (scalar bases; device coherent like st_dev): a 64-bit
+      // per-lane address would be built ahead of the phase and held in registers
+      const uint32_t at = (uint32_t)(g * j.out_gstride + tok * j.out_stride + n) * 2u;
       if (tok < R && (row & 1) == 0) {
-        st_dev(reinterpret_cast<uint32_t*>(j.out_bf + at), pair ^ j.out_xor);
-        if (j.out_plain) st_dev(reinterpret_cast<uint32_t*>(j.out_plain + at), pair);
+        __builtin_amdgcn_raw_buffer_store_b32(pair ^ j.out_xor, rsrc(j.out_bf, 0xFFFFFFFFu), at, 0,
+                                              CP_DEV);
+        if (j.out_plain)
+          __builtin_amdgcn_raw_buffer_store_b32(pair, rsrc(j.out_plain, 0xFFFFFFFFu), at, 0, CP_DEV);
       }
       if (j.ssq) {
-        // the squares of the stored bf16 values (exact in f32), summed over the row of
-        // 16 lanes (the tile's 16 columns of one output row) in a fixed butterfly order
-        const float hv = bf16_lo(h);
-        const float sq = red16(tok < R ? hv * hv : 0.f, OpAdd());
+        // the squares of the stored bf16 values over the row of 16 lanes (the tile's 16
+        // columns of one output row), in the pairwise tree of `pair_sq_tree`
+        const float sq = pair_sq_tree(h, tok < R);
         if (tok < R && row == 0)
           __builtin_amdgcn_raw_buffer_store_b32(
               __float_as_uint(sq), rsrc(j.ssq, (uint32_t)j.N * 4u),

@@ -313,18 +313,23 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   {
     float* ssr = &xs_lds[0][0];  // [16 waves][8 rows], over the scale table (idle until stage 1)
     static_assert(G::QW * G::KCW * 16 >= G::WAVES * 8, "the row sums fit the scale table");
+    // the waves holding tiles (the others' zeros would add nothing); rows past R skipped
+    constexpr int SQW = (NSQT + WAVE - 1) / WAVE;
     // v[rr]: this thread's tile sum of row row0 + rr
     auto reduce_rows = [&](int row0, float (&v)[8]) {
+      if (w < SQW) {
 #pragma unroll
-      for (int r = 0; r < 8; ++r) v[r] = wave_sum(v[r]);
-      if (l == 0)
+        for (int r = 0; r < 8; ++r)
+          if (row0 + r < R) v[r] = wave_sum(v[r]);
+        if (l == 0)
 #pragma unroll
-        for (int r = 0; r < 8; ++r) ssr[w * 8 + r] = v[r];
+          for (int r = 0; r < 8; ++r) ssr[w * 8 + r] = v[r];
+      }
       __syncthreads();
       if (tid < 8) {
         float tot = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < G::WAVES; ++ww) tot += ssr[ww * 8 + tid];
+        for (int ww = 0; ww < SQW; ++ww) tot += ssr[ww * 8 + tid];
         const int rr = row0 + tid;
         rstd_s[rr] = rr < R ? 1.0f / sqrtf(tot / (float)H + p.eps) : 0.f;
       }
@@ -333,7 +338,8 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
     auto tree_pass = [&](int row0) {
       float v[8];
 #pragma unroll
-      for (int rr = 0; rr < 8; ++rr) v[rr] = sq_tree16(at[rr][0], at[rr][1]);
+      for (int rr = 0; rr < 8; ++rr)
+        v[rr] = w < SQW && row0 + rr < R ? sq_tree16(at[rr][0], at[rr][1]) : 0.f;
       reduce_rows(row0, v);
     };
     if constexpr (FUSED) {

@@ -249,30 +249,44 @@ __device__ inline uint32_t bf16x2_bits(float lo, float hi) {
   const v2f f = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));
 }
-// The squares of 16 bf16 values (lo: values 0-7, hi: 8-15, two a dword, the low half
-// first; each square exact in f32) summed as a balanced pairwise tree, ((s0 + s1) +
-// (s2 + s3)) + ...: the bits a 16-lane butterfly (red16) gives summing one square a lane
-__device__ inline float sq_tree16(v4i lo, v4i hi) {
-  float s[16];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float a = bf16_lo((uint32_t)lo[q]), b = bf16_hi((uint32_t)lo[q]);
-    const float c = bf16_lo((uint32_t)hi[q]), d = bf16_hi((uint32_t)hi[q]);
-    s[2 * q] = a * a;
-    s[2 * q + 1] = b * b;
-    s[8 + 2 * q] = c * c;
-    s[8 + 2 * q + 1] = d * d;
-  }
-#pragma unroll
-  for (int n = 8; n >= 1; n /= 2)
-#pragma unroll
-    for (int k = 0; k < n; ++k) s[k] = s[2 * k] + s[2 * k + 1];
-  return s[0];
-}
 // acc + w.lo^2 + w.hi^2 for a bf16 pair w, by v_dot2c_f32_bf16
 __device__ inline float dot2_bf16_sq(uint32_t w, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, w), __builtin_bit_cast(v2bf, w),
                                         acc, false);
+}
+// The squares of 16 bf16 values (lo: values 0-7, hi: 8-15, two a dword, the low half
+// first) summed as a balanced pairwise tree: each adjacent pair (a dword) by
+// v_dot2c_f32_bf16 with a zero accumulator, then ((p0 + p1) + (p2 + p3)) + ... The same
+// bits as `pair_sq_tree` summing one value a lane over a 16-lane row (the dot2 rounds a
+// pair's sum once, which two separately rounded squares do not match when a square is
+// denormal, so both forms take the pair through it).
+__device__ inline float sq_tree16(v4i lo, v4i hi) {
+  float s[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    s[q] = dot2_bf16_sq((uint32_t)lo[q], 0.f);
+    s[4 + q] = dot2_bf16_sq((uint32_t)hi[q], 0.f);
+  }
+#pragma unroll
+  for (int n = 4; n >= 1; n /= 2)
+#pragma unroll
+    for (int k = 0; k < n; ++k) s[k] = s[2 * k] + s[2 * k + 1];
+  return s[0];
+}
+// One bf16 value a lane (bits h, low half), a 16-lane row holding 16 consecutive values:
+// the sum of their squares in `sq_tree16`'s order and bits (lanes 2k, 2k + 1 form the
+// pair's dword, low half first, for v_dot2c_f32_bf16; then the butterfly over the
+// pairs). `live` (uniform over the row): false gives the row zero. Every lane of the
+// row ends with its sum; call from every lane of the wave.
+__device__ inline float pair_sq_tree(uint32_t h, bool live) {
+  h &= 0xFFFFu;
+  const uint32_t hn = dpp_u<DPP_XOR1>(h);
+  const uint32_t w = (lane_id() & 1) ? (hn | (h << 16)) : (h | (hn << 16));
+  float v = live ? dot2_bf16_sq(w, 0.f) : 0.f;
+  v += dpp_f<DPP_XOR2>(v);
+  v += dpp_f<DPP_HALF_MIRROR>(v);
+  v += dpp_f<DPP_MIRROR>(v);
+  return v;
 }
 // acc + bf16(a) * w.lo + bf16(b) * w.hi, with a, b rounded to bf16 (nearest even) by
 // v_cvt_pk_bf16_f32 and the products summed by v_dot2c_f32_bf16
