@@ -213,7 +213,8 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   const __amdgpu_buffer_rsrc_t rplane = rsrc(p.plane, p.plane_pages * 4096u);
   const __amdgpu_buffer_rsrc_t rpsc = rsrc(p.plane_scale, p.plane_pages * 256u);
 
-  // XCD-local placement (up to 8 rows on 256 CTAs; the hardware hands CTA b to XCD b % 8):
+  // XCD-local placement (up to 8 rows on 256 CTAs; the hardware hands CTA b to XCD
+  // (b + c) % 8 for a launch-wide c, so CTAs b and b + 8 share an XCD):
   // row r's score tasks, its top-k tasks, its 32 splits and its 32 merges all run on XCD r,
   // so the scores, the row's q and the split partials each cross HBM once and are then read
   // from that XCD's L2: task t of a stage belongs to row t % 8 (`rs8` = 8). Otherwise task
