@@ -56,6 +56,7 @@ typedef void* mono_stream_t;
 #define MONO_SITE_QB 10      /* W_UK / the index query wait on q_b / W_iq outputs */
 #define MONO_SITE_PHASE 11   /* a phase of the layer launch waits for the phase before it */
 #define MONO_SITE_BLOCKS 12  /* a long row's final top-k waits on its blocks' selections */
+#define MONO_SITE_X 13       /* a stage-A task waits on the normalised input rows x */
 
 int mono_version(void);
 const char* mono_last_error(void);
@@ -386,7 +387,7 @@ typedef struct {
   void* scratch;             /* runtime owned, mono_front_scratch_bytes() */
   int32_t* guard;
   uint32_t* host_error;
-  int32_t fault_site;        /* test fault injection (MONO_SITE_FRONT_A / QAN / QB) */
+  int32_t fault_site;        /* test fault injection (MONO_SITE_FRONT_A / QAN / QB / X) */
   int32_t fault_after;
   uint64_t* timeline;
   float* ik_raw;             /* optional out f32 [R, 128]: the index key W_k x, before its

@@ -53,7 +53,7 @@ TL_COLS = 8
 
 # wait sites (the deadline error word holds 1 + site)
 SITES = {1: "logits", 2: "mid", 3: "mq", 4: "scores", 5: "topk", 6: "split", 7: "o",
-         8: "front_a", 9: "q_an", 10: "q_b", 11: "phase", 12: "blocks"}
+         8: "front_a", 9: "q_an", 10: "q_b", 11: "phase", 12: "blocks", 13: "x"}
 SITE_PHASE = 11
 # timeline marks of the layer launch (same columns)
 TL_LAYER_MARKS = ("start", "front", "attn", "post", "moe", "end")

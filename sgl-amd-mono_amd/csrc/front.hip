@@ -9,8 +9,10 @@ __global__ void __launch_bounds__(1024, 1) front_kernel(FrontParams p) {
   LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
-  const uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
-  front_phase(p, lds, guard, tag, sh.ok);
+  const v4i hd = launch_head_issue(p.guard);
+  const uint32_t tag = front_phase(p, lds, guard, sh.ok, [&]() {
+    return launch_begin_from(sh, guard, hd, p.guard, p.host_err, p.fault_site, p.fault_after);
+  });
   stamp(p.timeline, MONO_TL_MIDQ);
   launch_end(sh, p.guard, tag, p.scratch, (uint32_t)FrontScratch::BYTES,
              Poison{p.q, (uint32_t)p.rows * FR_HEADS * FR_Q * 2u, NAN_BF16X2},

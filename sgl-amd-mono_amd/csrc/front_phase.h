@@ -1,7 +1,8 @@
 // The front of the layer as one persistent gfx950 launch: from the layer input h to the
 // attention launch's inputs, with the row's KV and index-key cache writes.
-//   A   x = bf16(rmsnorm(h) g_in) of the (up to 8) rows built in LDS by every CTA of
-//       the stage; q_a | kv_a (W_qkv_a [2112, 7168]) and the index key (W_k [128, 7168]) as
+//   X   x = bf16(rmsnorm(h) g_in) of row r built once, by CTA 168 + r (a CTA with no
+//       stage-A task), and handed to every stage-A CTA as complemented bf16 pairs;
+//   A   q_a | kv_a (W_qkv_a [2112, 7168]) and the index key (W_k [128, 7168]) as
 //       140 FP8 16-row tiles over the whole K, the head weights (W_w [64, 7168] bf16) as
 //       28 tasks of 16 rows x 1024 K (partials summed in a fixed order by their reader)
 //       (sgl_amd_mono/glm53/gfx950/kernel.py:1781-1970, stage_x_rmsnorm :1367-1402);
@@ -60,6 +61,10 @@ constexpr int FR_QBT = FR_QB / 32;               // 192
 constexpr int FR_CT = FR_HEADS * 4;              // 128 W_UK tiles
 constexpr int FR_HA = FR_QKVA + FR_IK;           // 2240 stage A outputs a row
 constexpr int FR_MAX_GRID = 1024;
+// timeline marks of the front beyond MONO_TL_STAGED (A / A' done) and MONO_TL_ROUTED (B
+// done): a stage-A CTA's guard set up (its weights issued), x in its LDS, its MFMAs done;
+// a B CTA's q_a in, its MFMAs done
+constexpr int FR_TL_BEGUN = 3, FR_TL_XIN = 4, FR_TL_AMFMA = 5, FR_TL_QAIN = 6, FR_TL_BMFMA = 7;
 
 using GemvB = Gemv<8, 2, 3>;   // 32 rows over K 1536: 2 row groups x 8 K-splits of 192
 using GemvC = Gemv<2, 8, 1>;   // 128 rows over K 128: 8 row groups x 2 K-splits of 64
@@ -70,7 +75,8 @@ struct FrontScratch {
   static constexpr size_t HW = HA + (size_t)FR_MAXR * FR_HA * 4;            // f32 [7][8][64]
   static constexpr size_t HN = HW + (size_t)FR_WCH * FR_MAXR * FR_IH * 4;   // bf16 [8][32][128]
   static constexpr size_t HI = HN + (size_t)FR_MAXR * FR_HEADS * FR_NOPE * 2;  // bf16 [8][8192]
-  static constexpr size_t PARITY = (HI + (size_t)FR_MAXR * FR_IQ * 2 + 255) & ~(size_t)255;
+  static constexpr size_t HX = HI + (size_t)FR_MAXR * FR_IQ * 2;            // bf16 [8][7168]
+  static constexpr size_t PARITY = (HX + (size_t)FR_MAXR * FR_H * 2 + 255) & ~(size_t)255;
   static constexpr size_t BYTES = 2 * PARITY;
 };
 
@@ -225,23 +231,35 @@ static_assert(FR_LDS_RED % 16 == 0, "16-byte aligned reduction tiles");
 
 // The front in one CTA of a launch (the layer launch's first phase: nothing to wait for).
 // Its outputs (q, iq, iqs, iw, the rows' KV and index-key cache entries) are stored
-// device coherent, so the attention phase of the same launch can read them.
-__device__ __attribute__((always_inline)) inline void front_phase(const FrontParams& p,
-                                                                  uint8_t* lds, Guard& guard,
-                                                                  uint32_t tag, int& ok_s) {
+// device coherent, so the attention phase of the same launch can read them. `begin`
+// (every thread, once) sets up the guard and returns the launch tag: it is called after
+// the CTA's first loads are issued, so they are in flight while the guard head arrives.
+// Returns the tag.
+template <class Begin>
+__device__ __attribute__((always_inline)) inline uint32_t front_phase(const FrontParams& p,
+                                                                      uint8_t* lds,
+                                                                      Guard& guard, int& ok_s,
+                                                                      Begin begin) {
   const int b = blockIdx.x, G = gridDim.x, R = p.rows;
   uint16_t* xs = reinterpret_cast<uint16_t*>(lds + FR_LDS_XS);
   v4f (*red)[64] = reinterpret_cast<v4f (*)[64]>(lds + FR_LDS_RED);
   float* sred = reinterpret_cast<float*>(lds + FR_LDS_SRED);
   float* rs_s = reinterpret_cast<float*>(lds + FR_LDS_RS);
 
-  uint8_t* cur = p.scratch + (tag & 1u) * FrontScratch::PARITY;
-  uint8_t* nxt = p.scratch + ((tag + 1u) & 1u) * FrontScratch::PARITY;
+  uint32_t tag = 0;
+  uint8_t* cur = nullptr;
+  uint8_t* nxt = nullptr;
+  auto start = [&]() {
+    tag = begin();
+    cur = p.scratch + (tag & 1u) * FrontScratch::PARITY;
+    nxt = p.scratch + ((tag + 1u) & 1u) * FrontScratch::PARITY;
+  };
   // the hand-off buffers of this launch
   auto rHA = [&]() { return rsrc(cur + FrontScratch::HA, FR_MAXR * FR_HA * 4); };
   auto rHW = [&]() { return rsrc(cur + FrontScratch::HW, FR_WCH * FR_MAXR * FR_IH * 4); };
   auto rHN = [&]() { return rsrc(cur + FrontScratch::HN, FR_MAXR * FR_HEADS * FR_NOPE * 2); };
   auto rHI = [&]() { return rsrc(cur + FrontScratch::HI, FR_MAXR * FR_IQ * 2); };
+  auto rHX = [&]() { return rsrc(cur + FrontScratch::HX, FR_MAXR * FR_H * 2); };
   // the RoPE factors of row r's position, pair j, from the bf16 tables (as A' kind 1)
   auto rope_at = [&](int r, int j, float& cs, float& sn) {
     const int64_t pos = p.positions[r];
@@ -297,29 +315,13 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
       gc.issue(jC, cidx / 4, cidx % 4, wc, sc_, cidx >= 0 && cidx < FR_CT);
     };
     if (is_a) {
-      // ------------------------------------------ stage A: the task's loads, in order:
-      // x's rows and g_in (group 0), the task's weights, then stage B and C's weights
+      // ------------------------------------------ stage A: the task's weights first,
+      // then x (polled), then stage B and C's weights
       const bool a8 = b < FR_A8, qkv = b < FR_QKT;
       const int ta = qkv ? b : b - FR_QKT;          // FP8 16-row tile
       const int tw = (b - FR_A8) / FR_WCH, cw = (b - FR_A8) % FR_WCH;  // bf16 task
       const int ck = tid < FR_H / 8 ? tid : 0;       // thread's 8-K chunk of x
       const bool xk = tid < FR_H / 8;
-      const __amdgpu_buffer_rsrc_t rh = rsrc(p.h, (uint32_t)R * FR_H * 2u);
-      // rows g 8 .. g 8 + 7 of h straight into LDS (buffer -> LDS, no registers): a row
-      // is 14 chunks of 1 KiB, a wave copies 7 of the group's 112
-      static_assert(FR_LDS_XS + FR_XG * FR_XS * 2 <= LDS_DMA_END, "x rows' copies below 128 KB");
-      auto dma_rows = [&](int g) {
-#pragma unroll
-        for (int i = 0; i < 7; ++i) {
-          const int q = w * 7 + i, t = q / 14, c = q % 14, r = g * FR_XG + t;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rh, (__attribute__((address_space(3))) void*)(&xs[t * FR_XS + c * 512]), 16,
-              r < R ? (uint32_t)((r * FR_H + c * 512) * 2 + l * 16) : 0x80000000u, 0, 0, CP_NONE);
-        }
-      };
-      dma_rows(0);
-      asm volatile("" ::: "memory");  // the 15 loads below stay behind the copies
-      const v4i gv = ld16<CP_NONE>(rsrc(p.g_in, FR_H * 2), (uint32_t)(8 * ck) * 2u);
       // the task's weights: an FP8 tile's 7 steps of the wave's K range, or a bf16 task's
       // two 16-byte pieces (rows 16 tw + t16, K c 1024 + 64 w + 16 grp + 8 m) in steps 0-1
       const uint8_t* wa = qkv ? p.w_qkv_a : p.w_k;
@@ -350,59 +352,37 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
               ld4<CP_NONE>(rsa, (uint32_t)((ta / 8) * (FR_H / 128) + k0 / 128) * 4u));
         }
       }
+      start();
+      stamp(p.timeline, FR_TL_BEGUN);
 
-      // x of rows g 8 .. g 8 + 7 into LDS, then the MFMAs over it and the outputs
+      // x of the rows into LDS (built once a row by CTA FR_ATASKS + r as complemented bf16
+      // pairs: the loads are the wait; rows past R are zeros), then the MFMAs over it and
+      // the outputs
       auto run_group = [&](int g) {
-        // x = bf16(h rstd g_in) in place: the rows' sums of squares, then the products.
-        // The copies into LDS are loads the compiler does not track: they are older than
-        // the 15 loads issued after them (g_in, the weights and their scales)
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(15));
-        __syncthreads();
-        float ss[FR_XG];
+        {
+          const __amdgpu_buffer_rsrc_t rx = rHX();
+          v4i xv[FR_XG];
+          bool okx = wait_until(guard, MONO_SITE_X, [&]() {
+            uint32_t mn = 0xFFFFFFFFu;
 #pragma unroll
-        for (int t = 0; t < FR_XG; ++t) {
-          float s = 0.f;
-          if (xk) {
-            const v4i hw = *reinterpret_cast<const v4i*>(&xs[t * FR_XS + 8 * ck]);
+            for (int t = 0; t < FR_XG; ++t) {
+              const bool on = xk && g * FR_XG + t < R;
+              xv[t] = ld16<CP_DEV>(rx, on ? (uint32_t)(((g * FR_XG + t) * FR_H + 8 * ck) * 2) : 0x80000000u);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) s = dot2_bf16_sq((uint32_t)hw[q], s);
-          }
-          ss[t] = wave_sum(s);
-        }
-        if (l == 0)
-#pragma unroll
-          for (int t = 0; t < FR_XG; ++t) sred[w * FR_XG + t] = ss[t];
-        __syncthreads();
-        if (tid < FR_XG) {  // row tid's rstd, the waves' sums in order
-          float s = 0.f;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) s += sred[i * FR_XG + tid];
-          rs_s[tid] = __builtin_amdgcn_rsqf(s * (1.0f / FR_H) + p.eps);
-        }
-        __syncthreads();
-        float gf[8];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          gf[2 * q] = bf16_lo((uint32_t)gv[q]);
-          gf[2 * q + 1] = bf16_hi((uint32_t)gv[q]);
-        }
-#pragma unroll
-        for (int t = 0; t < FR_XG; ++t) {
-          const float rs = rs_s[t];
-          if (xk) {
-            v4i* px = reinterpret_cast<v4i*>(&xs[t * FR_XS + 8 * ck]);
-            const v4i hw = *px;
-            v4i o;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t hq = (uint32_t)hw[q];
-              o[q] = (int)bf16x2_bits(bf16_lo(hq) * rs * gf[2 * q], bf16_hi(hq) * rs * gf[2 * q + 1]);
+              for (int q = 0; q < 4; ++q) mn = on ? min(mn, (uint32_t)xv[t][q]) : mn;
             }
-            *px = o;
-          }
+            return __all(mn != 0u);
+          });
+          if (!cta_all(okx, ok_s)) return;
+#pragma unroll
+          for (int t = 0; t < FR_XG; ++t)
+            if (xk)
+              *reinterpret_cast<v4i*>(&xs[t * FR_XS + 8 * ck]) =
+                  g * FR_XG + t < R ? ~xv[t] : v4i{0, 0, 0, 0};
         }
-        issue_b0();  // the rows are in: stage B's first tile now
         __syncthreads();
+        stamp(p.timeline, FR_TL_XIN);
+        issue_b0();  // the rows are in: stage B's first tile now
         // MFMAs: lanes t16 < 8 take row t16 of the group; the others multiply zeros
         v4f acc = {0.f, 0.f, 0.f, 0.f};
         if (a8) {
@@ -431,6 +411,7 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
         }
         issue_b1c();  // this stage's weights are consumed: B's second tile and C's
         red[w][l] = acc;
+        stamp(p.timeline, FR_TL_AMFMA);
         __syncthreads();
         if (tid < 256) {
           const int row = tid & 15, tok = (tid >> 4) & 15;
@@ -455,6 +436,40 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
       };
       run_group(0);
     } else {
+      // ------------------------------------------ x of row xr = b - FR_ATASKS, once for
+      // every stage-A task: bf16(rmsnorm(h) g_in), the sum of squares in the order each
+      // task used when it built x itself (a thread's 8 values by dot2, the wave, the 16
+      // waves in order), as complemented bf16 pairs
+      const int xr = b - FR_ATASKS;
+      const bool xb = xr >= 0 && xr < R;
+      const int ck = tid < FR_H / 8 ? tid : 0;
+      const bool xk = tid < FR_H / 8;
+      const v4i hw = ld16<CP_NONE>(rsrc(p.h, (uint32_t)R * FR_H * 2u),
+                                   xb && xk ? (uint32_t)((xr * FR_H + 8 * ck) * 2) : 0x80000000u);
+      const v4i gv = ld16<CP_NONE>(rsrc(p.g_in, xb ? FR_H * 2 : 0u), (uint32_t)(8 * ck) * 2u);
+      start();
+      if (xb) {
+        float s = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s = dot2_bf16_sq((uint32_t)hw[q], s);
+        s = wave_sum(s);
+        if (l == 0) sred[w] = s;
+        __syncthreads();
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ss += sred[i];
+        const float rs = __builtin_amdgcn_rsqf(ss * (1.0f / FR_H) + p.eps);
+        if (xk) {
+          v4i o;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t hq = (uint32_t)hw[q], gq = (uint32_t)gv[q];
+            o[q] = (int)enc_pair(bf16x2_bits(bf16_lo(hq) * rs * bf16_lo(gq), bf16_hi(hq) * rs * bf16_hi(gq)));
+          }
+          st16<CP_DEV>(rHX(), (uint32_t)((xr * FR_H + 8 * ck) * 2), o);
+        }
+        __syncthreads();  // sred is reused
+      }
       if (is_ap) {
         // ------------------------------------------ A': task (row, kind)
         const int u = b - (G - nap), r = u >> 2, kind = u & 3;
@@ -666,6 +681,7 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
       return __all(!qon || mn != 0u);
     });
     okb = cta_all(okb, ok_s);
+    stamp(p.timeline, FR_TL_QAIN);
     v4i xa[3][2];
     if (okb) {
       float a[12], s = 0.f;
@@ -703,6 +719,7 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
       if (jb0 < FR_BT) gb.dot(wb0, sb0, xa, red);
       if (two) gb.dot(wb1, sb1, xa, red + 16);
       __syncthreads();
+      stamp(p.timeline, FR_TL_BMFMA);
       const bool mine = tid < 512 ? jb0 < FR_BT : two;
       if (mine) {
         v4f (*rd)[64] = red + (tid < 512 ? 0 : 16);
@@ -823,7 +840,7 @@ __device__ __attribute__((always_inline)) inline void front_phase(const FrontPar
       __syncthreads();
     }
   }
-
+  return tag;
 }
 
 }  // namespace mono

@@ -84,8 +84,10 @@ __global__ void __launch_bounds__(1024, 1) layer_kernel(LayerParams p) {
   LaunchShared& sh = *reinterpret_cast<LaunchShared*>(lds + Arena::BODY);
   stamp(p.timeline, MONO_TL_START);
   Guard guard;
-  uint32_t tag = launch_begin(sh, guard, p.guard, p.host_err, p.fault_site, p.fault_after);
-  front_phase(p.f, lds, guard, tag, sh.ok);
+  const v4i hd = launch_head_issue(p.guard);
+  uint32_t tag = front_phase(p.f, lds, guard, sh.ok, [&]() {
+    return launch_begin_from(sh, guard, hd, p.guard, p.host_err, p.fault_site, p.fault_after);
+  });
   p.bar[0].arrive(tag);
   stamp(p.timeline, LY_TL_FRONT);
   attn_phase<SPLIT, true, LONG, DSA>(p.at, lds, guard, tag, sh.ok,

@@ -59,12 +59,19 @@ struct Poison {
   uint32_t fill;
 };
 
-// Read the guard head (one coherent load, shared in LDS) and set up the guard; returns
-// the launch tag (epoch + 1). Every thread calls it.
-__device__ __attribute__((always_inline)) inline uint32_t launch_begin(LaunchShared& sh, Guard& guard, int32_t* gw,
-                                        uint32_t* host_err, int fault_site, int fault_after) {
+// The guard head's one coherent load (thread 0; zeros elsewhere). A launch issues it
+// first, ahead of its first weight loads, so that the wait for it in launch_begin_from
+// does not queue behind them.
+__device__ inline v4i launch_head_issue(int32_t* gw) {
+  return threadIdx.x == 0 ? ld16<CP_DEV>(rsrc(gw, 16), 0) : v4i{0, 0, 0, 0};
+}
+
+// Share the guard head `hd` (launch_head_issue) in LDS and set up the guard; returns the
+// launch tag (epoch + 1). Every thread calls it.
+__device__ __attribute__((always_inline)) inline uint32_t launch_begin_from(
+    LaunchShared& sh, Guard& guard, v4i hd, int32_t* gw, uint32_t* host_err, int fault_site,
+    int fault_after) {
   if (threadIdx.x == 0) {
-    const v4i hd = ld16<CP_DEV>(rsrc(gw, 16), 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) sh.head[i] = (uint32_t)hd[i];
     sh.ok = 1;
@@ -72,6 +79,13 @@ __device__ __attribute__((always_inline)) inline uint32_t launch_begin(LaunchSha
   __syncthreads();
   guard.init(gw, host_err, fault_site, sh.head, (uint32_t)fault_after);
   return tag_after(sh.head[MONO_GUARD_EPOCH]);
+}
+
+// Read the guard head and set up the guard; returns the launch tag. Every thread calls it.
+__device__ __attribute__((always_inline)) inline uint32_t launch_begin(LaunchShared& sh, Guard& guard, int32_t* gw,
+                                        uint32_t* host_err, int fault_site, int fault_after) {
+  return launch_begin_from(sh, guard, launch_head_issue(gw), gw, host_err, fault_site,
+                           fault_after);
 }
 
 // The CTA leaves the launch. The last CTA out (every other CTA has drained its stores

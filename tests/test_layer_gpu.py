@@ -324,10 +324,10 @@ def test_one_launch_layer_graph_replay_matches_eager(gpu):
     op.check()
 
 
-@pytest.mark.parametrize("site", [11, 5, 2])
+@pytest.mark.parametrize("site", [11, 13, 5, 2])
 def test_one_launch_layer_deadline_stops_and_reports(gpu, site):
-    """A wait forced to stall from the host (the phase barrier, a split's top-k wait, a mid
-    quant's wait): it times out after 5 ms, every CTA runs to the end of the launch, the
+    """A wait forced to stall from the host (the phase barrier, the stage-A wait for x, a
+    split's top-k wait, a mid quant's wait): it times out after 5 ms, every CTA runs to the end of the launch, the
     output is all NaN, the host raises naming the site, and a reset runtime launches
     cleanly."""
     from sgl_amd_mono_amd import _lib
