@@ -145,9 +145,7 @@ static_assert(AT_LDS_IQ8 + 64 * AT_IQ8_ROW + 256 <= TOPK_ARENA_WORDS * 4, "in th
 constexpr int AT_LDS_WSUM = TOPK_ARENA_WORDS * 4;         // int [2][16], 16-byte aligned
 constexpr int AT_LDS_RES = AT_LDS_WSUM + 2 * AT_WAVES * 4;  // int [4]
 constexpr int AT_LDS_MM = AT_LDS_RES + 16;                  // u32 [4]
-constexpr int AT_LDS_WSP = AT_LDS_MM + 16;                  // f32 [NSPLIT]
-constexpr int AT_LDS_LINV = AT_LDS_WSP + AT_NSPLIT * 4;     // f32
-constexpr int AT_LDS_BYTES = AT_LDS_LINV + 16;
+constexpr int AT_LDS_BYTES = AT_LDS_MM + 16;
 
 // The attention phase (stages 1-4) in one CTA of a launch. LONG: rows may span more than
 // one top-k block (a context bound above AT_TKBLOCK); the launch picks it, so a launch
@@ -917,17 +915,13 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
   // ---------------------------------------------------------------- 4: merge
   stamp(p.timeline, MONO_TL_UPGATE);
   {
-    float* red = reinterpret_cast<float*>(smem);  // [NSPLIT][512]
-    float* wsp_s = reinterpret_cast<float*>(lds + AT_LDS_WSP);
-    float& linv_s = *reinterpret_cast<float*>(lds + AT_LDS_LINV);
     static_assert(AT_HEADS == 32, "32 merge tasks a row");
+    static_assert(AT_NSPLIT <= WAVE, "a split's (m, l) a lane");
     constexpr bool uv = FUSED;  // the one-launch layer sets uv_w
-    v4f (*uvred)[64] = reinterpret_cast<v4f (*)[64]>(red + AT_NSPLIT * AT_LAT);  // [16][64]
-    uint16_t* uvx = reinterpret_cast<uint16_t*>(uvred + 16);                      // [512] x
-    uint16_t* uob = uvx + AT_LAT;                                                 // [128] rows
-    static_assert(AT_NSPLIT * AT_LAT * 4 + 16 * 64 * 16 + (AT_LAT + 128) * 2 <=
-                      TOPK_ARENA_WORDS * 4,
-                  "merge LDS");
+    v4f (*uvred)[64] = reinterpret_cast<v4f (*)[64]>(smem);  // [16][64]
+    uint16_t* uvx = reinterpret_cast<uint16_t*>(uvred + 16);  // [512] x
+    uint16_t* uob = uvx + AT_LAT;                             // [128] rows
+    static_assert(16 * 64 * 16 + (AT_LAT + 128) * 2 <= TOPK_ARENA_WORDS * 4, "merge LDS");
     uint16_t* obuf = p.uv_obuf[tag & 1u];
     for (int task = b; task < ntask32; task += nblk) {
       const int tid = opaque_v((int)threadIdx.x), l = tid & 63;
@@ -947,57 +941,39 @@ __device__ __attribute__((always_inline)) inline void attn_phase(const AttnParam
         });
       ok = cta_all(ok, ok_s);
       if (!ok) break;
-      // the split partials and their (m, l) in one round trip: TPS threads a split, VPT
-      // values a thread
-      constexpr int TPS = AT_THREADS / NSP, VPT = AT_LAT / TPS;
-      static_assert(VPT % 8 == 0, "merge thread map");
-      const int sp = tid / TPS, dv = tid % TPS;
-      v4i a[VPT / 8];
-      {
-        const __amdgpu_buffer_rsrc_t ra = rsrc(
-            accs + ((size_t)(r * AT_NSPLIT + (sp < nsp ? sp : 0)) * AT_HEADS + h) * AT_LAT,
-            sp < nsp ? AT_LAT * 2 : 0);
-#pragma unroll
+      // thread d < 512: output dim d. Its 32 split terms (bf16, a wave's 64 dims of a split
+      // are 128 contiguous bytes) and, in every wave, the splits' (m, l) (lane s: split s)
+      // in one round trip; each wave forms the weights exp(m_s - M) itself (no LDS round
+      // trip), then the terms scaled and summed in split order.
+      if (tid < AT_LAT) {
         // through L2: within the launch the partials are only stored (write-through) before
         // the done words this CTA waited for, so no L2 holds a stale copy
-        for (int i = 0; i < VPT / 8; ++i) a[i] = ld16<CP_NONE>(ra, (uint32_t)(dv * VPT * 2 + 16 * i));
-      }
-      if (w == 0) {
+        const __amdgpu_buffer_rsrc_t ra =
+            rsrc(accs + ((size_t)r * AT_NSPLIT * AT_HEADS + h) * AT_LAT,
+                 (uint32_t)(nsp * AT_HEADS * AT_LAT * 2));
+        uint32_t v[AT_NSPLIT];
+#pragma unroll
+        for (int sp = 0; sp < AT_NSPLIT; ++sp)
+          v[sp] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+              ra, (uint32_t)(tid + sp * AT_HEADS * AT_LAT) * 2u, 0, CP_NONE);
         const float* ml = mls + (size_t)r * AT_NSPLIT * AT_HEADS * 2;
         const bool on = l < nsp;
-        const v2i mlv = ld8<CP_NONE>(rsrc(ml, on ? AT_NSPLIT * AT_HEADS * 8 : 0),
-                                    (uint32_t)((l * AT_HEADS + h) * 8));
+        const v2i mlv = ld8<CP_NONE>(rsrc(ml, AT_NSPLIT * AT_HEADS * 8),
+                                    on ? (uint32_t)((l * AT_HEADS + h) * 8) : 0x80000000u);
         const float m = on ? __int_as_float(mlv[0]) : -INFINITY;
         const float ls = on ? __int_as_float(mlv[1]) : 0.f;
         const float M = wave_max(m);
         const float ws = on ? expf(m - M) : 0.f;
         const float L = wave_sum(ws * ls);
-        if (l < AT_NSPLIT) wsp_s[l] = ws;
-        if (l == 0) linv_s = L > 0.f ? 1.0f / L : 0.f;
-      }
-      __syncthreads();
-      {
-        const float ws = sp < nsp ? wsp_s[sp] : 0.f;
+        const float linv = L > 0.f ? 1.0f / L : 0.f;
+        float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < VPT / 8; ++i) {
-          const uint32_t u0 = a[i][0], u1 = a[i][1], u2 = a[i][2], u3 = a[i][3];
-          const v4f v0 = {bf16_lo(u0), bf16_hi(u0), bf16_lo(u1), bf16_hi(u1)};
-          const v4f v1 = {bf16_lo(u2), bf16_hi(u2), bf16_lo(u3), bf16_hi(u3)};
-          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + VPT * dv + 8 * i]) = v0 * ws;
-          *reinterpret_cast<v4f*>(&red[sp * AT_LAT + VPT * dv + 8 * i + 4]) = v1 * ws;
+        for (int sp = 0; sp < AT_NSPLIT; ++sp) {
+          const float wsp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ws), sp));
+          const float term = __fmul_rn(bf16_lo(v[sp]), wsp);
+          acc = sp < nsp ? __fadd_rn(acc, term) : acc;
         }
-      }
-      __syncthreads();
-      if (tid < AT_LAT) {
-        // every split's term read at once (independent LDS reads), then summed in split
-        // order over the row's splits
-        float v[AT_NSPLIT];
-#pragma unroll
-        for (int sp = 0; sp < AT_NSPLIT; ++sp) v[sp] = red[sp * AT_LAT + tid];
-        float s = 0.f;
-#pragma unroll
-        for (int sp = 0; sp < AT_NSPLIT; ++sp) s = sp < nsp ? s + v[sp] : s;
-        const uint32_t ob = bf16_bits(s * linv_s);
+        const uint32_t ob = bf16_bits(acc * linv);
         // device coherent: in the layer launch the output block reads it next
         __builtin_amdgcn_raw_buffer_store_b16(
             (uint16_t)ob, rsrc(p.out, (uint32_t)R * AT_HEADS * AT_LAT * 2u),
