@@ -13,11 +13,13 @@
 //      wave keeps three tasks of weights in flight. Wave 0 reduces each task and stores
 //      mid = bf16(silu(g) * u) by slot (row, pick); only after the CTA's last task does
 //      it wait for those stores, then the CTA's done word gets the launch tag.
-//   2  down: task f = 16 output rows over every distinct expert, wave w taking experts
-//      u = w mod 16. Its first four experts' weights are in flight before the wait for
-//      every CTA's done word; the R x 9 mid slot rows are then copied into LDS. Each
-//      expert's partial is scaled by the row's route weight; a fixed-order reduction
-//      over the 16 waves and out = bf16(res + y).
+//   2  down: task f = 16 output rows over every distinct expert, run by CTA grid - 1 - f
+//      (the CTAs with the fewest up/gate tasks), wave w < 15 taking the experts
+//      u = w (mod 15). Its first four experts' weights are in flight before wave 15,
+//      which has no loads of its own, polls every CTA's done word and copies the R x 9
+//      mid slot rows into LDS; each expert is computed as soon as its weights are in.
+//      Each expert's partial is scaled by the row's route weight; a fixed-order
+//      reduction over the waves and out = bf16(res + y).
 // The tag of a launch is the guard block's epoch + 1; the last CTA out advances it.
 //
 // Reference: A16W4 operands sgl_amd_mono/minimax_m31/a16w4.py:26-92 (lane = one row's
@@ -43,7 +45,7 @@ struct MoeMxGeom {
   static constexpr int KSW = NKS / QK;  // steps of a wave's K slice
   static constexpr int NUG = I / 32;    // up/gate tasks per expert (32 gate + 32 up rows)
   static constexpr int NDS = I / 128;   // 128-K steps of the intermediate
-  static constexpr int NDN = H / 16;    // down tasks
+  static constexpr int NDN = H / 16;    // down tasks (one a CTA: the grid must hold them)
   static constexpr int DW = WAVES - 1;  // down: waves that stream weights (the last one waits)
   static constexpr int RING = 4;        // experts of down weights a wave keeps in flight
   static_assert(NKS % QK == 0, "hidden must split into 4 slices of 128-steps");
@@ -86,6 +88,8 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   using G = MoeMxGeom<H, I>;
   using W13 = MxOperand<SHUF, H>;  // [2 I, H]
   using W2 = MxOperand<SHUF, I>;   // [H, I]
+  using S13 = MxScales<SHUF, H>;
+  using S2 = MxScales<SHUF, I>;
   constexpr int KSW = G::KSW, NUG = G::NUG, NDS = G::NDS, QK = G::QK, RING = G::RING;
   constexpr int THREADS = G::THREADS, DW = G::DW;
   const int tid = threadIdx.x, l = tid & 63;
@@ -181,9 +185,11 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   stamp(p.timeline, MONO_TL_ROUTED);
   {
     const int ntask = nd * NUG;
-    const uint32_t cv = W13::code_v(l), sv = W13::scale_v(l);
+    const uint32_t cv = W13::code_v(l);
     // operands of a task for this wave; a task past the end reads through empty
-    // buffers (loads return 0, no memory traffic), so refills need no branch
+    // buffers (loads return 0, no memory traffic), so refills need no branch. Step j's
+    // scale word sits in slot S13::slot(j) (a wave's K slice starts at an even step)
+    static_assert(KSW % 2 == 0, "paired scale words within a wave's K slice");
     auto issue = [&](int task, int j, v4i& wv, uint32_t& code) {
       const bool live = task < ntask;
       const int tk = live ? task : 0;
@@ -196,7 +202,7 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
       const __amdgpu_buffer_rsrc_t rs =
           rsrc(p.s13 + (size_t)e * W13::scale_bytes(2 * I), live ? W13::scale_bytes(2 * I) : 0u);
       wv = ld16s<CP_NT>(rc, cv, W13::code_s(rg, s));
-      code = ld1(rs, sv, W13::scale_s(rg, s));
+      if (S13::loads(j, KSW)) code = S13::load(rs, l, rg, s);
     };
     // two tasks of weights in flight per wave
     v4i w0[KSW], w1[KSW];
@@ -230,7 +236,7 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
         v4i B[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) B[d] = x_lds[xo + (j * 4 + d) * 64];
-        acc = fp4_step(wv[j], code[j], B, acc);
+        acc = fp4_step(wv[j], S13::of(code[S13::slot(j, KSW)], rsub, j), B, acc);
         issue(task + 2 * nblk, j, wv[j], code[j]);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -272,105 +278,113 @@ __global__ void __launch_bounds__(1024, 1) moe_mxfp4_kernel(MoeMxParams p) {
   stamp(p.timeline, MONO_TL_UPGATE);
   bool ok = true;
   {
-    const uint32_t cv = W2::code_v(l), sv = W2::scale_v(l);
-    // the NDS steps of expert u's 16-row group f (an expert past the end: no traffic)
-    auto issue = [&](int f, int u, v4i (&wv)[NDS], uint32_t (&code)[NDS]) {
-      const bool live = u < nd;
+    // CTA b runs down task nblk - 1 - b (the CTAs with the fewest up/gate tasks, the
+    // highest b, take the down tasks first; the host refuses a grid below NDN CTAs)
+    const int f = nblk - 1 - b;
+    const bool has = f < G::NDN;
+    const uint32_t cv = W2::code_v(l);
+    // the NDS steps of distinct expert u's 16-row group f (no task or an expert past the
+    // end: empty buffers, no memory traffic)
+    auto issue = [&](int u, v4i (&wv)[NDS], uint32_t (&code)[NDS]) {
+      const bool live = has && u < nd;
       const int e = __builtin_amdgcn_readfirstlane(rl.uexp[live ? u : 0]);
+      const int fr = live ? f : 0;
       const __amdgpu_buffer_rsrc_t rc =
           rsrc(p.w2 + (size_t)e * W2::code_bytes(H), live ? W2::code_bytes(H) : 0u);
       const __amdgpu_buffer_rsrc_t rs =
           rsrc(p.s2 + (size_t)e * W2::scale_bytes(H), live ? W2::scale_bytes(H) : 0u);
 #pragma unroll
       for (int s = 0; s < NDS; ++s) {
-        wv[s] = ld16s<CP_NT>(rc, cv, W2::code_s(f, s));
-        code[s] = ld1(rs, sv, W2::scale_s(f, s));
+        wv[s] = ld16s<CP_NT>(rc, cv, W2::code_s(fr, s));
+        if (S2::loads(s, NDS)) code[s] = S2::load(rs, l, fr, s);
       }
     };
-    bool first = true;
-    for (int f = b; f < G::NDN; f += nblk) {
-      // waves 0..DW-1 take experts u = w, w + DW, ...; their first RING experts' weights
-      // fly while the last wave, with no load of its own in flight (loads complete in
-      // order), polls the done words; then every wave copies mid rows into LDS
-      v4i dw[RING][NDS];
-      uint32_t dc[RING][NDS];
-      const int wu = w < DW ? w : MOE_NDIST;  // the last wave takes no expert
+    // waves 0..DW-1 take experts u = w, w + DW, ...: their first RING experts' weights
+    // are issued now, with no branch (so each expert waits only for its own loads), and
+    // each expert is computed as soon as its weights are in
+    v4i dw[RING][NDS];
+    uint32_t dc[RING][NDS];
+    const int wu = w < DW ? w : MOE_NDIST;  // the last wave takes no expert
 #pragma unroll
-      for (int q = 0; q < RING; ++q) issue(f, wu + DW * q, dw[q], dc[q]);
-      if (first) {
-        first = false;
-        if (w == DW)
-          ok = wait_until(guard, MONO_SITE_MID, [&]() {
-            bool all = true;
-            for (int i = l; i < nblk; i += WAVE) all &= ld_dev(&done[i]) == tag;
-            return __all(all);
-          });
-        ok = cta_all(ok, ok_s);
-        if (ok) {
-          // every wave copies 1 KiB pieces straight into LDS (a wave's copy lands after
-          // its weight loads, which the compute waits for anyway)
-          const uint32_t nbytes = (uint32_t)R * MOE_SLOTS * I * 2;
-          const __amdgpu_buffer_rsrc_t rm = rsrc(mid, nbytes);
-          for (uint32_t off = (uint32_t)w * 1024; off < nbytes; off += G::WAVES * 1024)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rm, (__attribute__((address_space(3))) void*)(mid_lds + off), 16, l * 16 + off,
-                0, 0, CP_DEV);
-          drain();
-        }
-        __syncthreads();
-        stamp(p.timeline, MONO_TL_MIDQ);
-      }
-      if (!ok) break;
+    for (int q = 0; q < RING; ++q) issue(wu + DW * q, dw[q], dc[q]);
+    // the last wave, with no load of its own in flight (loads complete in order), polls
+    // every CTA's done word, then copies the R x 9 mid slot rows into LDS in 1 KiB pieces
+    // and waits for them; the streaming waves wait at the barrier only, not for their
+    // weights
+    if (w == DW)
+      ok = wait_until(guard, MONO_SITE_MID, [&]() {
+        bool all = true;
+        for (int i = l; i < nblk; i += WAVE) all &= ld_dev(&done[i]) == tag;
+        return __all(all);
+      });
+    ok = cta_all(ok, ok_s);
+    if (ok && has && w == DW) {
+      const uint32_t nbytes = (uint32_t)R * MOE_SLOTS * I * 2;
+      const __amdgpu_buffer_rsrc_t rm = rsrc(mid, nbytes);
+      for (uint32_t off = 0; off < nbytes; off += 1024)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rm, (__attribute__((address_space(3))) void*)(mid_lds + off), 16, l * 16 + off, 0,
+            0, CP_DEV);
+      drain();
+    }
+    __syncthreads();
+    stamp(p.timeline, MONO_TL_MIDQ);
+    if (ok && has) {
       v4f acc = {0.f, 0.f, 0.f, 0.f};
-      for (int k0 = 0; wu + DW * k0 < nd; k0 += RING) {
+      // expert u from its weights in the ring slot (wv, code)
+      auto expert = [&](int u, const v4i (&wv)[NDS], const uint32_t (&code)[NDS]) {
+        const int sl = slot_of(rl, u, rl.umask[u], t);
+        const bool on = sl >= 0;
+        const float wt = on ? wslot[sl] : 0.f;
+        // a row t not routed to u reads slot row 0 (always a written, finite mid): its
+        // output column t is then scaled by wt = 0, which adds exactly nothing
+        const uint8_t* mrow = mid_lds + (on ? sl : 0) * I * 2 + 64 * grp;
+        v4f d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < RING; ++q) {
-          const int u = wu + DW * (k0 + q);
-          if (u < nd) {
-            const int sl = slot_of(rl, u, rl.umask[u], t);
-            const bool on = sl >= 0;
-            const float wt = on ? wslot[sl] : 0.f;
-            const uint8_t* mrow = mid_lds + (on ? sl : 0) * I * 2 + 64 * grp;
-            v4f d = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < NDS; ++s) {
+          v4i B[4];
 #pragma unroll
-            for (int s = 0; s < NDS; ++s) {
-              v4i B[4];
-#pragma unroll
-              for (int dd = 0; dd < 4; ++dd) {
-                const v4i z = {0, 0, 0, 0};
-                B[dd] = on ? *reinterpret_cast<const v4i*>(mrow + s * 256 + dd * 16) : z;
-              }
-              d = fp4_step(dw[q][s], dc[q][s], B, d);
-            }
-            issue(f, u + DW * RING, dw[q], dc[q]);
-            __builtin_amdgcn_sched_barrier(0);
-            acc += d * wt;
-          }
+          for (int dd = 0; dd < 4; ++dd)
+            B[dd] = *reinterpret_cast<const v4i*>(mrow + s * 256 + dd * 16);
+          d = fp4_step(wv[s], S2::of(code[S2::slot(s, NDS)], f, s), B, d);
         }
+        acc += d * wt;
+      };
+      // the first ring in straight-line code (each expert waits for its own loads only),
+      // then rings of RING more experts (over 60 distinct experts), issued and computed
+#pragma unroll
+      for (int q = 0; q < RING; ++q)
+        if (wu + DW * q < nd) expert(wu + DW * q, dw[q], dc[q]);
+      for (int k0 = RING; wu + DW * k0 < nd; k0 += RING) {
+#pragma unroll
+        for (int q = 0; q < RING; ++q) issue(wu + DW * (k0 + q), dw[q], dc[q]);
+#pragma unroll
+        for (int q = 0; q < RING; ++q)
+          if (wu + DW * (k0 + q) < nd) expert(wu + DW * (k0 + q), dw[q], dc[q]);
       }
       red[0][w][l] = acc;
-      __syncthreads();
-      if (w == 0) {
-        v4f ys = red[0][0][l];
-#pragma unroll
-        for (int i = 1; i < DW; ++i) ys += red[0][i][l];
-        if (t < R) {
-          const int col = f * 16 + 4 * grp;
-          uint32_t h[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            h[v] = bf16_bits((p.res ? bf16_lo(p.res[t * H + col + v]) : 0.f) + ys[v]);
-          // write-through: a failed launch's NaN fill must not meet a dirty line
-          const v2i hv = {(int32_t)(h[0] | (h[1] << 16)), (int32_t)(h[2] | (h[3] << 16))};
-          __builtin_amdgcn_raw_buffer_store_b64(hv, rsrc(p.out, (uint32_t)R * H * 2u),
-                                                (uint32_t)(t * H + col) * 2u, 0, CP_DEV);
-          if (p.y)
-            st16<CP_DEV>(rsrc(p.y, (uint32_t)R * H * 4u), (uint32_t)(t * H + col) * 4u,
-                         __builtin_bit_cast(v4i, ys));
-        }
-      }
-      __syncthreads();
     }
+    __syncthreads();
+    if (ok && has && w == 0) {
+      v4f ys = red[0][0][l];
+#pragma unroll
+      for (int i = 1; i < DW; ++i) ys += red[0][i][l];
+      if (t < R) {
+        const int col = f * 16 + 4 * grp;
+        uint32_t h[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          h[v] = bf16_bits((p.res ? bf16_lo(p.res[t * H + col + v]) : 0.f) + ys[v]);
+        // write-through: a failed launch's NaN fill must not meet a dirty line
+        const v2i hv = {(int32_t)(h[0] | (h[1] << 16)), (int32_t)(h[2] | (h[3] << 16))};
+        __builtin_amdgcn_raw_buffer_store_b64(hv, rsrc(p.out, (uint32_t)R * H * 2u),
+                                              (uint32_t)(t * H + col) * 2u, 0, CP_DEV);
+        if (p.y)
+          st16<CP_DEV>(rsrc(p.y, (uint32_t)R * H * 4u), (uint32_t)(t * H + col) * 4u,
+                       __builtin_bit_cast(v4i, ys));
+      }
+    }
+    __syncthreads();
   }
 
   // ---------------------------------------------------------------- exit
@@ -440,6 +454,8 @@ extern "C" int mono_moe_mxfp4_launch(const MonoMoeMxfp4Args* a, mono_stream_t st
   if (rc) return rc;
   if (grid > MoeMxGeom<3072, 384>::MAX_GRID)
     return set_error(MONO_E_DEVICE, "mono_moe_mxfp4_launch: more CUs than done words");
+  if (grid < MoeMxGeom<3072, 384>::NDN)
+    return set_error(MONO_E_DEVICE, "mono_moe_mxfp4_launch: fewer CUs than down tasks");
   if (a->hidden == 3072 && a->inter == 384) {
     auto k = a->layout == MONO_LAYOUT_AITER16 ? moe_mxfp4_kernel<3072, 384, true>
                                               : moe_mxfp4_kernel<3072, 384, false>;
