@@ -35,7 +35,6 @@
 #include <stdio.h>
 
 #include <mutex>
-#include <type_traits>
 
 #include "moe_common.h"
 #include "mono_abi.h"
@@ -180,6 +179,7 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
   using LO = MoeLds<H, I, MX>;
   using W13 = MxOperand<SHUF, H>;  // MX: w13 [2 I, H] and w2 [H, I] as E2M1 + E8M0
   using W2 = MxOperand<SHUF, I>;
+  using S2 = MxScales<SHUF, I>;
   constexpr int KCW = G::KCW, NUG = G::NUG, NKB = G::NKB, QW = G::QW;
   // the stream a is read through L2 in both forms: fused, its lines are only stored
   // (write-through) before the barrier in this launch, so no cache holds a stale copy
@@ -693,8 +693,9 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
                 : (uint32_t)(row0 * H + wq * KCW * 128);
       return rsrc(p.w13 + (size_t)e * (2 * I) * H, live ? 2u * I * H : 0u);
     };
-    // MX: the codes and scales of the task's 16-row group rg of expert uexp[u]
     // MX: task `task`'s 128-K step j of its 16-row group of expert uexp[u]: codes, scale
+    // (one byte load a step: a wave's K slice of KCW = 7 steps starts at either parity,
+    // so paired scale words would need a code path per parity)
     auto mx_issue = [&](int task, int j) {
       const bool live = task < ntask;
       const int tk = live ? task : 0;
@@ -977,8 +978,9 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
       buf[kb][0] = ld16s<CP_NT>(
           rsrc(p.w2 + (size_t)e * W2::code_bytes(H), live ? W2::code_bytes(H) : 0u),
           W2::code_v(l), W2::code_s(fr, kb));
-      bsc[kb] = ld1(rsrc(p.e2 + (size_t)e * W2::scale_bytes(H), live ? W2::scale_bytes(H) : 0u),
-                    W2::scale_v(l), W2::scale_s(fr, kb));
+      if (S2::loads(kb, NKB))
+        bsc[kb] = S2::load(
+            rsrc(p.e2 + (size_t)e * W2::scale_bytes(H), live ? W2::scale_bytes(H) : 0u), l, fr, kb);
     };
     if constexpr (MX) {
 #pragma unroll
@@ -1077,18 +1079,18 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
         const bool on = sl >= 0;
         if constexpr (MX) {
           // lane l: the mid row's bf16 at K 128 kb + 32 (l / 16) + 8 d, d < 4
+          // a row t not routed to u reads slot row 0 (copied before any expert is
+          // computed, a finite mid): its output column is scaled by cf = 0, adding
+          // exactly nothing (no masked LDS reads)
           const uint8_t* mrow = mql + (on ? sl : 0) * ROWB + 64 * grp;
 #pragma unroll
           for (int kb = 0; kb < NKB; ++kb) {
             v4i B[4];
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              const v4i z = {0, 0, 0, 0};
-              B[d] = on ? *reinterpret_cast<const v4i*>(mrow + kb * 256 + d * 16) : z;
-            }
+            for (int d = 0; d < 4; ++d) B[d] = *reinterpret_cast<const v4i*>(mrow + kb * 256 + d * 16);
             const float cf = on ? mcl[(on ? sl : 0) * NKB + kb] : 0.f;
             const v4f zero = {0.f, 0.f, 0.f, 0.f};
-            const v4f d = fp4_step(buf[kb][0], bsc[kb], B, zero);
+            const v4f d = fp4_step(buf[kb][0], S2::of(bsc[S2::slot(kb, NKB)], f, kb), B, zero);
             mx_issue(fn, un, kb);
             acc += d * cf;
             __builtin_amdgcn_sched_barrier(0);
@@ -1101,9 +1103,9 @@ __device__ __attribute__((always_inline)) inline void moe_phase(const MoeFp8Para
             __builtin_amdgcn_readfirstlane((e * (H / 128) + rg0 / 128) * (I / 128));
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-          const v4i z = {0, 0, 0, 0};
-          const v4i b0 = on ? *reinterpret_cast<const v4i*>(mql + bb + kb * 128) : z;
-          const v4i b1 = on ? *reinterpret_cast<const v4i*>(mql + bb + kb * 128 + 16) : z;
+          // a row t not routed to u reads slot row 0, scaled by cf = 0 (as above)
+          const v4i b0 = *reinterpret_cast<const v4i*>(mql + bb + kb * 128);
+          const v4i b1 = *reinterpret_cast<const v4i*>(mql + bb + kb * 128 + 16);
           const float cf = on ? mcl[(on ? sl : 0) * NKB + kb] : 0.f;
           const v4f zero = {0.f, 0.f, 0.f, 0.f};
           const v4f d = mfma_fp8(cat8(buf[kb][0], buf[kb][1]), cat8(b0, b1), zero);

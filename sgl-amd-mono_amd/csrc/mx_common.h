@@ -49,28 +49,39 @@ __device__ inline uint32_t ld1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t
   return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, CP_NT);
 }
 
-// Scale loads of an n-step run of one 16-row group (steps s = 0 .. n - 1 of 128 K).
-// Row-major: one byte load a step. SHUF: steps 2i and 2i + 1 of a lane share one dword
-// (bytes 2 (s % 2) + rg % 2), so one dword load serves both: it is made with step 2i + 1
-// (with step 2i when that is the run's last), and the scale of step s is that dword
-// shifted right by 8 (2 (s % 2) + rg % 2); fp4_step reads the low byte.
+// Scale loads of an n-step run of one 16-row group (steps s = 0 .. n - 1 of 128 K, the
+// first at absolute step parity p0). Row-major: one byte load a step. SHUF: absolute
+// steps 2i and 2i + 1 of a lane share one dword (bytes 2 (step % 2) + rg % 2), so one
+// dword load serves both: it is made with the later of the two that lies in the run (the
+// earlier one consumes the word before that slot is refilled), and the scale of absolute
+// step a is that dword shifted right by 8 (2 (a % 2) + rg % 2); fp4_step reads the low
+// byte.
 template <bool SHUF, int K>
 struct MxScales {
   using Op = MxOperand<SHUF, K>;
-  // the slot holding step s's scale word
-  static constexpr int slot(int s, int n) { return SHUF ? ((s | 1) < n ? (s | 1) : s) : s; }
-  // step s (of group rg) loads a scale word into its own slot
-  static constexpr bool loads(int s, int n) { return slot(s, n) == s; }
-  __device__ static uint32_t load(__amdgpu_buffer_rsrc_t r, int l, int rg, int s) {
+  // the slot holding run step s's scale word
+  static constexpr int slot(int s, int n, int p0 = 0) {
+    return SHUF && ((p0 + s) & 1) == 0 && s + 1 < n ? s + 1 : s;
+  }
+  // run step s loads a scale word into its own slot
+  static constexpr bool loads(int s, int n, int p0 = 0) { return slot(s, n, p0) == s; }
+  // scale loads of a run
+  static constexpr int count(int n, int p0 = 0) {
+    int c = 0;
+    for (int s = 0; s < n; ++s) c += loads(s, n, p0) ? 1 : 0;
+    return c;
+  }
+  // the scale word of absolute step a of group rg
+  __device__ static uint32_t load(__amdgpu_buffer_rsrc_t r, int l, int rg, int a) {
     if constexpr (SHUF)
       return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-          r, (uint32_t)l * 4, (uint32_t)(((rg >> 1) * (Op::CP / 8) + (s >> 1)) * 256), CP_NT);
+          r, (uint32_t)l * 4, (uint32_t)(((rg >> 1) * (Op::CP / 8) + (a >> 1)) * 256), CP_NT);
     else
-      return ld1(r, Op::scale_v(l), Op::scale_s(rg, s));
+      return ld1(r, Op::scale_v(l), Op::scale_s(rg, a));
   }
-  // the scale word of step s, from the word in slot(s)
-  __device__ static uint32_t of(uint32_t word, int rg, int s) {
-    return SHUF ? word >> (8 * (2 * (s & 1) + (rg & 1))) : word;
+  // the scale of absolute step a, from the word in its slot
+  __device__ static uint32_t of(uint32_t word, int rg, int a) {
+    return SHUF ? word >> (8 * (2 * (a & 1) + (rg & 1))) : word;
   }
 };
 
