@@ -201,7 +201,8 @@ int mono_moe_fp8_launch_static(const MonoMoeFp8Args* args, mono_stream_t stream)
  * Layouts: MONO_LAYOUT_ROWMAJOR = codes [E + 1, N, K / 2], scales [E + 1, N, K / 32];
  * MONO_LAYOUT_AITER16 = codes in the AITER (16, 16) byte shuffle and scales in the
  * e8m0 shuffle of sgl_amd_mono/common/mx.py:40-44, [E + 1, N, C] with C = K / 32
- * rounded up to a multiple of 8 (the map groups columns by 8). */
+ * rounded up to a multiple of 8 (the map groups columns by 8). One CTA a CU; the grid
+ * must hold the hidden / 16 = 192 down tasks, one a CTA (MONO_E_DEVICE otherwise). */
 typedef struct {
   int32_t rows;            /* R, 1..16 */
   int32_t hidden;          /* 3072 */
