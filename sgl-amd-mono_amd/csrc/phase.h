@@ -97,7 +97,9 @@ __device__ __attribute__((always_inline)) inline uint32_t launch_begin(LaunchSha
 // store of the launch is device coherent (sc1, write-through), so no L2 of another XCD
 // holds a dirty line that could overwrite the NaN when the kernel ends. Then thread 0
 // runs `last` (state the next launch expects zero), resets the exit counter and
-// advances the epoch to this launch's tag. Every thread calls it.
+// advances the epoch to this launch's tag, without waiting for the scrub or the NaN
+// fill: the end of the launch orders them all before any later reader. Every thread
+// calls it.
 template <class Last>
 __device__ __attribute__((always_inline)) inline void launch_end(LaunchShared& sh, int32_t* gw,
                                                                 uint32_t tag, uint8_t* scratch,
@@ -132,8 +134,10 @@ __device__ __attribute__((always_inline)) inline void launch_end(LaunchShared& s
         st16<CP_DEV>(r, off, v4i{f, f, f, f});
     }
   }
-  drain();
-  __syncthreads();
+  // no drain or barrier ahead of the final stores: nothing in this launch reads these
+  // words again, and the launch's end makes every store visible before the next launch
+  // (or the host) reads the guard words, the scratch or the outputs, so the scrub, the
+  // resets and the epoch complete in one round trip
   if (threadIdx.x == 0) {
     last();
     st_dev(w + MONO_GUARD_EXIT, 0u);
