@@ -5,14 +5,15 @@
 //      registers while waves 0..R-1 route one row each from the given logits: sigmoid,
 //      + bias, top-8 with lowest-id ties, weights raw / sum * scale. Every CTA routes
 //      for itself (the logits are inputs), so nothing is handed off before up/gate.
-//   1  up/gate: task (u, c) = 16 gate + 16 up rows of distinct expert u over all of K;
+//   1  up/gate: task (u, c) = 32 gate + 32 up rows of distinct expert u over all of K;
 //      task t runs on CTA t mod grid. Waves 0-7 take the gate rows, 8-15 the up rows,
-//      each wave a 384-K slice. A lane's 16 code bytes are one row's 32-group, which
-//      shares one E8M0 scale: v_cvt_scalef32_pk_bf16_fp4 dequantises them exactly to 32
-//      bf16 for four 16x16x32 bf16 MFMAs; the B operands (the rows) wait in LDS. Each
-//      wave keeps three tasks of weights in flight. Wave 0 reduces each task and stores
-//      mid = bf16(silu(g) * u) by slot (row, pick); only after the CTA's last task does
-//      it wait for those stores, then the CTA's done word gets the launch tag.
+//      each wave a quarter of K of one 16-row group. A lane's 16 code bytes are one
+//      row's 32-group, which shares one E8M0 scale (in the AITER layout one scale dword
+//      serves two 128-K steps): v_cvt_scalef32_pk_bf16_fp4 dequantises them exactly to
+//      32 bf16 for four 16x16x32 bf16 MFMAs; the B operands (the rows) wait in LDS. Each
+//      wave keeps two tasks of weights in flight. Waves 0 and 1 reduce each task and
+//      store mid = bf16(silu(g) * u) by slot (row, pick); only after the CTA's last task
+//      do they wait for those stores, then the CTA's done word gets the launch tag.
 //   2  down: task f = 16 output rows over every distinct expert, run by CTA grid - 1 - f
 //      (the CTAs with the fewest up/gate tasks), wave w < 15 taking the experts
 //      u = w (mod 15). Its first four experts' weights are in flight before wave 15,
